@@ -1,0 +1,99 @@
+/*
+ * uaii_hip.h — extern "C" HIP launch layer of libuaii_amd.so (gfx950).
+ *
+ * Plain pointers and sizes only. Device pointers come from uaii_hip_malloc (or
+ * any hipMalloc'd memory of the same process); `stream` is a hipStream_t or
+ * NULL for the null stream. Every call returns 0 on success or a hipError_t /
+ * negative validation code (see uaii_hip_error_string).
+ *
+ * Entry point -> reference interface it replaces:
+ *   uaii_hip_weight_create     gguf_load_tensor_raw (libs/uaii-loaders/src/gguf.cpp:558-602)
+ *                              + Session packed weight buffers (session.cpp:342-358):
+ *                              GGUF block rows uploaded and re-laid out for HBM once
+ *   uaii_hip_dequant_rows      dequant_gguf_row (libs/uaii-quant/src/gguf_dequant.cpp:420-439)
+ *   uaii_hip_gemv              quant_gemm_f32 at M=1 (libs/uaii-kernels/src/quant_gemm.cpp:22-70)
+ *   uaii_hip_gemv_rmsnorm      rmsnorm_f32 (norm.cpp:89-130) feeding quant_gemm_f32
+ *   uaii_hip_gemm              quant_gemm_f32 at M>1 (prefill; same file)
+ *   uaii_hip_rmsnorm           rmsnorm_f32 (libs/uaii-kernels/src/norm.cpp:89-130)
+ *   uaii_hip_softmax           softmax_f32 (libs/uaii-kernels/src/softmax.cpp:11-77)
+ *   uaii_hip_argmax            greedy sample_token_f32 (libs/uaii-runtime/src/sampling.cpp:38-50)
+ *   uaii_hip_rope              rope_f32 (libs/uaii-kernels/src/transformer.cpp:144-220)
+ *   uaii_hip_attention_decode  attention_kv_f32, q_seq=1 (transformer.cpp:222-433)
+ *   uaii_hip_add / _silu_mul   add_f32 / silu_f32 + mul_f32 (elementwise.cpp:73-110)
+ * and the reference ROCm stub's launchers it supersedes
+ * (libs/uaii-backends/src/rocm_kernels.hpp:10-14: launch_add_f32, launch_rmsnorm_f32).
+ */
+#ifndef UAII_HIP_H_
+#define UAII_HIP_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define UAII_HIP_API __attribute__((visibility("default")))
+
+typedef struct uaii_hip_weight uaii_hip_weight;
+
+/* ---- device and memory ---------------------------------------------------- */
+UAII_HIP_API int uaii_hip_init(int device);
+UAII_HIP_API int uaii_hip_device_count(int* count);
+UAII_HIP_API const char* uaii_hip_error_string(int code);
+UAII_HIP_API int uaii_hip_malloc(void** ptr, size_t bytes);
+UAII_HIP_API int uaii_hip_free(void* ptr);
+UAII_HIP_API int uaii_hip_memcpy_h2d(void* dst, const void* src, size_t bytes);
+UAII_HIP_API int uaii_hip_memcpy_d2h(void* dst, const void* src, size_t bytes);
+UAII_HIP_API int uaii_hip_memset(void* ptr, int value, size_t bytes);
+UAII_HIP_API int uaii_hip_synchronize(void);
+
+/* ---- weights ---------------------------------------------------------------- */
+/* gguf_type: GGUF tensor type id (0 F32, 1 F16, 2 Q4_0, 3 Q4_1, 6 Q5_0, 7 Q5_1,
+ * 8 Q8_0, 10 Q2_K, 11 Q3_K, 12 Q4_K, 13 Q5_K, 14 Q6_K); host_packed holds `rows`
+ * GGUF rows of `cols` values. */
+UAII_HIP_API int uaii_hip_weight_create(int gguf_type, const void* host_packed, int64_t rows,
+                                        int64_t cols, uaii_hip_weight** out);
+UAII_HIP_API int uaii_hip_weight_destroy(uaii_hip_weight* w);
+UAII_HIP_API int64_t uaii_hip_weight_bytes(const uaii_hip_weight* w);
+
+/* ---- kernels ---------------------------------------------------------------- */
+UAII_HIP_API int uaii_hip_dequant_rows(const uaii_hip_weight* w, int64_t row0, int64_t nrows,
+                                       float* out, void* stream);
+UAII_HIP_API int uaii_hip_gemv(const uaii_hip_weight* w, const float* x, float* y,
+                               void* stream);
+UAII_HIP_API int uaii_hip_gemv_rmsnorm(const uaii_hip_weight* w, const float* x,
+                                       const float* norm_w, float eps, float* y, void* stream);
+UAII_HIP_API int uaii_hip_gemm(const uaii_hip_weight* w, const float* x, int64_t m, float* y,
+                               void* stream);
+UAII_HIP_API int uaii_hip_rmsnorm(const float* x, const float* w, float* y, int64_t rows,
+                                  int64_t n, float eps, void* stream);
+UAII_HIP_API int uaii_hip_softmax(const float* x, float* y, int64_t n, void* stream);
+UAII_HIP_API int uaii_hip_argmax(const float* x, int64_t n, int32_t* out_idx, void* stream);
+/* table: [max_pos][head_dim/2] (cos, sin) float pairs, filled on the host with
+ * the reference's angle formula, uploaded to `table_dev`. */
+UAII_HIP_API int uaii_hip_rope_table(float theta, int head_dim, int64_t max_pos,
+                                     float* table_dev);
+UAII_HIP_API int uaii_hip_rope(float* x, int64_t rows, int64_t dim, int head_dim, int mode,
+                               const int32_t* pos_dev, const float* table_dev, void* stream);
+/* kcache/vcache: head-major [n_kv_heads][max_seq][head_dim], f16 (kv_f16=1) or f32;
+ * attends over keys 0..n_keys-1. */
+UAII_HIP_API int uaii_hip_attention_decode(const float* q, const void* kcache,
+                                           const void* vcache, int kv_f16, int64_t max_seq,
+                                           int n_heads, int n_kv_heads, int head_dim,
+                                           int64_t n_keys, float* out, void* stream);
+
+/* ---- timing (HIP events on `stream`) ---------------------------------------- */
+/* Average device time of `iters` back-to-back uaii_hip_gemv launches, in ms. */
+UAII_HIP_API int uaii_hip_time_gemv(const uaii_hip_weight* w, const float* x, float* y,
+                                    int iters, float* avg_ms);
+UAII_HIP_API int uaii_hip_time_gemm(const uaii_hip_weight* w, const float* x, int64_t m,
+                                    float* y, int iters, float* avg_ms);
+UAII_HIP_API int uaii_hip_time_copy(const void* src, void* dst, size_t bytes, int iters,
+                                    float* avg_ms);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* UAII_HIP_H_ */

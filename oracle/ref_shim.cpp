@@ -1,0 +1,429 @@
+// ref_shim.cpp — extern "C" driver around the reference's own CPU kernels.
+//
+// TEST INFRASTRUCTURE ONLY. Built by `make -C oracle ref` together with the
+// reference kernel sources (compiled in place from the reference tree) into
+// oracle/_ref/libuaii_ref.so. Tests use it to pin the C oracle, and bench.py may
+// time it as the CPU baseline ("kind": "reference"). The product never loads it.
+//
+// Per-op entry points call the reference functions directly. uref_generate
+// re-drives the reference kernels in the order the reference GGUF graph wires
+// them (libs/uaii-loaders/src/gguf.cpp:935-1209) with the dispatch decisions of
+// libs/uaii-kernels/src/dispatch.cpp:82-237 and the token loop of
+// libs/uaii-runtime/src/session.cpp:910-1164. GGUF header parsing is borrowed
+// from the C oracle (uaii_oracle.c), whose own parity is tested separately.
+
+#include "uaii/kernels/kernels.hpp"
+#include "uaii/kernels/quant_gemm.hpp"
+#include "uaii/quant/gguf_dequant.hpp"
+#include "uaii/runtime/kv_cache.hpp"
+#include "uaii/runtime/sampling.hpp"
+
+extern "C" {
+#include "uaii_oracle.h"
+}
+
+#include <cstring>
+#include <memory>
+#include <random>
+#include <string>
+#include <vector>
+
+using namespace uaii;
+using kernels::TensorView;
+
+namespace {
+
+thread_local std::string g_err;
+
+bool map_type(int t, quant::QuantFormat* f) {
+  switch (t) {
+    case 0: *f = quant::QuantFormat::F32; return true;
+    case 1: *f = quant::QuantFormat::F16; return true;
+    case 2: *f = quant::QuantFormat::Q4_0; return true;
+    case 3: *f = quant::QuantFormat::Q4_1; return true;
+    case 6: *f = quant::QuantFormat::Q5_0; return true;
+    case 7: *f = quant::QuantFormat::Q5_1; return true;
+    case 8: *f = quant::QuantFormat::Q8_0; return true;
+    case 10: *f = quant::QuantFormat::Q2_K; return true;
+    case 11: *f = quant::QuantFormat::Q3_K; return true;
+    case 12: *f = quant::QuantFormat::Q4_K; return true;
+    case 13: *f = quant::QuantFormat::Q5_K; return true;
+    case 14: *f = quant::QuantFormat::Q6_K; return true;
+    default: return false;
+  }
+}
+
+// A tensor plus the shape storage its view points at.
+struct Owned {
+  std::int64_t shape[3] = {0, 0, 0};
+  std::vector<float> f32;
+  TensorView view;
+};
+
+std::unique_ptr<Owned> f32_tensor(std::vector<std::int64_t> dims) {
+  auto t = std::make_unique<Owned>();
+  std::size_t n = 1;
+  for (std::size_t i = 0; i < dims.size(); ++i) {
+    t->shape[i] = dims[i];
+    n *= static_cast<std::size_t>(dims[i]);
+  }
+  t->f32.assign(n, 0.0f);
+  t->view.dtype = DType::F32;
+  t->view.shape = t->shape;
+  t->view.rank = dims.size();
+  t->view.data = t->f32.data();
+  t->view.nbytes = n * sizeof(float);
+  return t;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* uref_last_error(void) { return g_err.c_str(); }
+
+int uref_dequant_row(int type, const std::uint8_t* packed, std::int64_t cols, float* out) {
+  quant::QuantFormat f;
+  if (!map_type(type, &f)) return -1;
+  Error e = quant::dequant_gguf_row(f, packed, cols, out);
+  if (!e.ok()) { g_err = e.message(); return -1; }
+  return 0;
+}
+
+int uref_quant_gemm(int type, const float* A, std::int64_t M, std::int64_t K,
+                    const std::uint8_t* B, std::int64_t N, float* C) {
+  quant::QuantFormat f;
+  if (!map_type(type, &f)) return -1;
+  std::int64_t as[2] = {M, K}, bs[2] = {N, K}, cs[2] = {M, N};
+  TensorView a, b, c;
+  a.dtype = DType::F32; a.shape = as; a.rank = 2; a.data = const_cast<float*>(A);
+  a.nbytes = static_cast<std::size_t>(M * K) * 4;
+  b.dtype = DType::Unknown; b.shape = bs; b.rank = 2; b.data = const_cast<std::uint8_t*>(B);
+  b.quant_format = f; b.quant_rows = N; b.quant_cols = K;
+  b.nbytes = quant::packed_nbytes(f, static_cast<std::size_t>(N * K));
+  c.dtype = DType::F32; c.shape = cs; c.rank = 2; c.data = C;
+  c.nbytes = static_cast<std::size_t>(M * N) * 4;
+  Error e = kernels::quant_gemm_f32(a, b, &c, true);
+  if (!e.ok()) { g_err = e.message(); return -1; }
+  return 0;
+}
+
+int uref_rmsnorm(const float* x, const float* w, float* y, std::int64_t n, float eps) {
+  auto in = f32_tensor({1, n}), wt = f32_tensor({n}), out = f32_tensor({1, n});
+  std::memcpy(in->f32.data(), x, n * 4);
+  if (w) std::memcpy(wt->f32.data(), w, n * 4);
+  Error e = kernels::rmsnorm_f32(in->view, w ? &wt->view : nullptr, &out->view, eps);
+  if (!e.ok()) { g_err = e.message(); return -1; }
+  std::memcpy(y, out->f32.data(), n * 4);
+  return 0;
+}
+
+int uref_rope(float* x, std::int64_t dim, std::int64_t head_dim, float pos, float theta,
+              int mode) {
+  auto in = f32_tensor({1, dim}), out = f32_tensor({1, dim}), p = f32_tensor({1});
+  std::memcpy(in->f32.data(), x, dim * 4);
+  p->f32[0] = pos;
+  Error e = kernels::rope_f32(in->view, &p->view, &out->view, theta, head_dim, mode);
+  if (!e.ok()) { g_err = e.message(); return -1; }
+  std::memcpy(x, out->f32.data(), dim * 4);
+  return 0;
+}
+
+int uref_attention_decode(const float* q, const float* kc, const float* vc, std::int64_t past,
+                          const float* kn, const float* vn, float* out, int n_heads,
+                          int n_kv_heads, int hd) {
+  const std::int64_t qd = static_cast<std::int64_t>(n_heads) * hd;
+  const std::int64_t kvd = static_cast<std::int64_t>(n_kv_heads) * hd;
+  auto Q = f32_tensor({1, qd}), K = f32_tensor({1, kvd}), V = f32_tensor({1, kvd});
+  auto O = f32_tensor({1, qd});
+  std::memcpy(Q->f32.data(), q, qd * 4);
+  std::memcpy(K->f32.data(), kn, kvd * 4);
+  std::memcpy(V->f32.data(), vn, kvd * 4);
+  std::unique_ptr<Owned> PK, PV;
+  if (past > 0) {
+    PK = f32_tensor({1, past, kvd});
+    PV = f32_tensor({1, past, kvd});
+    std::memcpy(PK->f32.data(), kc, past * kvd * 4);
+    std::memcpy(PV->f32.data(), vc, past * kvd * 4);
+  }
+  Error e = kernels::attention_kv_f32(Q->view, K->view, V->view, &O->view, n_heads, 0.0f, true,
+                                      PK ? &PK->view : nullptr, PV ? &PV->view : nullptr,
+                                      nullptr, nullptr);
+  if (!e.ok()) { g_err = e.message(); return -1; }
+  std::memcpy(out, O->f32.data(), qd * 4);
+  return 0;
+}
+
+int uref_softmax(const float* x, float* y, std::int64_t n) {
+  auto in = f32_tensor({1, n}), out = f32_tensor({1, n});
+  std::memcpy(in->f32.data(), x, n * 4);
+  Error e = kernels::softmax_f32(in->view, &out->view, -1);
+  if (!e.ok()) { g_err = e.message(); return -1; }
+  std::memcpy(y, out->f32.data(), n * 4);
+  return 0;
+}
+
+int uref_silu(const float* x, float* y, std::int64_t n) {
+  auto in = f32_tensor({1, n}), out = f32_tensor({1, n});
+  std::memcpy(in->f32.data(), x, n * 4);
+  Error e = kernels::silu_f32(in->view, &out->view);
+  if (!e.ok()) { g_err = e.message(); return -1; }
+  std::memcpy(y, out->f32.data(), n * 4);
+  return 0;
+}
+
+std::int64_t uref_argmax(const float* row, std::int64_t n) {
+  runtime::SampleParams greedy;
+  std::mt19937_64 rng{0};
+  std::int64_t tok = -1;
+  Error e = runtime::sample_token_f32(row, static_cast<std::size_t>(n), greedy, {}, &rng, &tok);
+  if (!e.ok()) { g_err = e.message(); return -1; }
+  return tok;
+}
+
+// ------------------------------------------------------------------ generate
+
+namespace {
+
+struct Weight {
+  std::int64_t shape[3] = {0, 0, 0};
+  std::vector<float> f32;
+  TensorView view;
+  bool present = false;
+};
+
+// Path B keeps block-quant weights packed (session.cpp:342-358); Path A and
+// non-block types are dequantized to f32 with the reference's own decoder
+// (gguf.cpp:445-556, which delegates to dequant_gguf_row for K-quants; for Q8_0
+// and Q4_0-ggml layout the values are identical).
+bool bind_weight(orc_model* m, const std::string& name, bool f32_always, bool path_a, Weight* w) {
+  int type = 0;
+  std::int64_t ne[3];
+  const std::uint8_t* data = nullptr;
+  if (orc_model_tensor(m, name.c_str(), &type, ne, &data) != 0) return false;
+  quant::QuantFormat f;
+  if (!map_type(type, &f)) { g_err = "unsupported type for " + name; return false; }
+  int rank = ne[2] > 1 ? 3 : (ne[1] > 1 || !f32_always ? 2 : 1);
+  if (rank == 3) { w->shape[0] = ne[2]; w->shape[1] = ne[1]; w->shape[2] = ne[0]; }
+  else if (rank == 2) { w->shape[0] = ne[1]; w->shape[1] = ne[0]; }
+  else { w->shape[0] = ne[0]; }
+  const std::int64_t rows = ne[1] * ne[2], cols = ne[0];
+  w->view.shape = w->shape;
+  w->view.rank = static_cast<std::size_t>(rank);
+  const bool packed = quant::is_gguf_block_quant(f) && !f32_always && !path_a;
+  if (packed) {
+    w->view.dtype = DType::Unknown;
+    w->view.data = const_cast<std::uint8_t*>(data);
+    w->view.quant_format = f;
+    w->view.quant_rows = rank == 3 ? 0 : rows;
+    w->view.quant_cols = rank == 3 ? 0 : cols;
+    w->view.nbytes = quant::packed_nbytes(f, static_cast<std::size_t>(rows * cols));
+  } else {
+    w->f32.resize(static_cast<std::size_t>(rows * cols));
+    const std::size_t rb = quant::packed_nbytes(f, static_cast<std::size_t>(cols));
+    for (std::int64_t r = 0; r < rows; ++r) {
+      if (f == quant::QuantFormat::F32) {
+        std::memcpy(&w->f32[r * cols], data + r * cols * 4, cols * 4);
+      } else if (f == quant::QuantFormat::F16) {
+        for (std::int64_t c = 0; c < cols; ++c) {
+          std::uint16_t h;
+          std::memcpy(&h, data + (r * cols + c) * 2, 2);
+          w->f32[r * cols + c] = orc_half_to_float(h);
+        }
+      } else {
+        (void)quant::dequant_gguf_row(f, data + r * rb, cols, &w->f32[r * cols]);
+      }
+    }
+    w->view.dtype = DType::F32;
+    w->view.data = w->f32.data();
+    w->view.nbytes = w->f32.size() * 4;
+  }
+  w->present = true;
+  return true;
+}
+
+Error matmul(const TensorView& x, const Weight& w, TensorView* y) {
+  // dispatch.cpp:82-100: packed + transpose_b -> quant_gemm, else f32 matmul
+  if (kernels::supports_quant_gemm(w.view.quant_format)) {
+    return kernels::quant_gemm_f32(x, w.view, y, true);
+  }
+  return kernels::matmul_f32(x, w.view, y, false, true);
+}
+
+}  // namespace
+
+// Greedy generate through the reference kernels. taps_logits (vocab floats) and
+// taps_resid2 (n_layers*dim floats) receive the last run()'s values when non-NULL.
+int uref_generate(const char* path, int max_layers, const std::int64_t* prompt,
+                  std::int64_t n_prompt, std::int64_t max_new, std::int64_t* out,
+                  std::int64_t* out_n, float* taps_logits, float* taps_resid2) {
+  orc_model* m = orc_model_open(path, max_layers);
+  if (!m) { g_err = orc_last_error(); return -1; }
+  std::int64_t hp[12];
+  float fp[2];
+  orc_model_hparams(m, hp);
+  orc_model_fparams(m, fp);
+  const std::int64_t L = hp[0], D = hp[1], H = hp[2], HKV = hp[3], hd = hp[4], V = hp[5];
+  const std::int64_t E = hp[7], topk = hp[8], rope_mode = hp[9], ctx = hp[10];
+  const float theta = fp[0], eps = fp[1];
+  const bool path_a = E > 0;
+  const std::int64_t qd = H * hd, kvd = HKV * hd;
+  int rc = -1;
+  {
+    Weight emb, onorm, lm;
+    std::vector<Weight> W(static_cast<std::size_t>(L * 16));
+    bind_weight(m, "token_embd.weight", false, path_a, &emb);
+    bind_weight(m, "output_norm.weight", true, path_a, &onorm);
+    if (!bind_weight(m, "output.weight", false, path_a, &lm)) {
+      bind_weight(m, "token_embd.weight", false, path_a, &lm);  // tied (gguf.cpp:813-816)
+    }
+    static const char* names[16] = {"attn_norm", "attn_q", "attn_k", "attn_v", "attn_output",
+                                    "ffn_norm", "ffn_gate", "ffn_up", "ffn_down",
+                                    "ffn_gate_inp", "ffn_gate_exps", "ffn_up_exps",
+                                    "ffn_down_exps", "attn_q.bias", "attn_k.bias",
+                                    "attn_v.bias"};
+    for (std::int64_t li = 0; li < L; ++li) {
+      for (int k = 0; k < 16; ++k) {
+        std::string nm = "blk." + std::to_string(li) + "." + names[k];
+        if (k < 13) nm += ".weight";
+        const bool f32_always = (k == 0 || k == 5 || k >= 9);
+        bind_weight(m, nm, f32_always, path_a, &W[li * 16 + k]);
+      }
+    }
+    std::int64_t ff = 1;
+    for (std::int64_t li = 0; li < L; ++li) {
+      const Weight& up = W[li * 16 + 7];
+      const Weight& ge = W[li * 16 + 10];
+      if (up.present) ff = std::max<std::int64_t>(ff, up.shape[0]);
+      if (ge.present) ff = std::max<std::int64_t>(ff, ge.shape[1]);
+    }
+
+    runtime::KvCache kv;
+    const std::int64_t total = n_prompt + max_new;
+    const std::int64_t kv_max = ctx > 0 ? ctx : std::max<std::int64_t>(total, n_prompt + 1);
+    Error e = kv.configure(L, 1, kv_max, kvd, HKV);
+    if (!e.ok()) { g_err = e.message(); orc_model_close(m); return -1; }
+    kernels::set_active_kv_cache(&kv);
+
+    auto tokens = f32_tensor({1, 1});
+    auto x = f32_tensor({1, D}), n1 = f32_tensor({1, D}), res1 = f32_tensor({1, D});
+    auto q = f32_tensor({1, qd}), k = f32_tensor({1, kvd}), v = f32_tensor({1, kvd});
+    auto qb = f32_tensor({1, qd}), kb = f32_tensor({1, kvd}), vb = f32_tensor({1, kvd});
+    auto qr = f32_tensor({1, qd}), kr = f32_tensor({1, kvd});
+    auto att = f32_tensor({1, qd}), ao = f32_tensor({1, D}), n2 = f32_tensor({1, D});
+    auto g = f32_tensor({1, ff}), u = f32_tensor({1, ff}), ga = f32_tensor({1, ff});
+    auto hid = f32_tensor({1, ff}), fo = f32_tensor({1, D}), res2 = f32_tensor({1, D});
+    auto normed = f32_tensor({1, D}), logits = f32_tensor({1, V}), probs = f32_tensor({1, V});
+    auto mp = f32_tensor({1, std::max<std::int64_t>(E, 1)}), mt = f32_tensor({1, 1});
+
+    auto run = [&](std::int64_t token, bool last) -> Error {
+      tokens->f32[0] = static_cast<float>(token);
+      Error err = kernels::embedding_f32(tokens->view, emb.view, &x->view);
+      if (!err.ok()) return err;
+      TensorView feat = x->view;
+      std::vector<float> cur(x->f32);
+      for (std::int64_t li = 0; li < L; ++li) {
+        Weight* w = &W[li * 16];
+        auto fi = f32_tensor({1, D});
+        fi->f32 = cur;
+        fi->view.data = fi->f32.data();
+        err = kernels::rmsnorm_f32(fi->view, &w[0].view, &n1->view, eps);
+        if (!err.ok()) return err;
+        if (!(err = matmul(n1->view, w[1], &q->view)).ok()) return err;
+        if (!(err = matmul(n1->view, w[2], &k->view)).ok()) return err;
+        if (!(err = matmul(n1->view, w[3], &v->view)).ok()) return err;
+        TensorView qq = q->view, kk = k->view, vv = v->view;
+        if (w[13].present) { (void)kernels::add_f32(q->view, w[13].view, &qb->view); qq = qb->view; }
+        if (w[14].present) { (void)kernels::add_f32(k->view, w[14].view, &kb->view); kk = kb->view; }
+        if (w[15].present) { (void)kernels::add_f32(v->view, w[15].view, &vb->view); vv = vb->view; }
+        if (!(err = kernels::rope_f32(qq, nullptr, &qr->view, theta, hd,
+                                      static_cast<int>(rope_mode))).ok()) return err;
+        if (!(err = kernels::rope_f32(kk, nullptr, &kr->view, theta, hd,
+                                      static_cast<int>(rope_mode))).ok()) return err;
+        // Attention with the active KV cache (dispatch.cpp:219-231)
+        TensorView pk = kv.k_view(li), pv = kv.v_view(li);
+        err = kernels::attention_kv_f32(qr->view, kr->view, vv, &att->view,
+                                        static_cast<int>(H), 0.0f, true,
+                                        pk.data ? &pk : nullptr, pv.data ? &pv : nullptr,
+                                        nullptr, nullptr);
+        if (!err.ok()) return err;
+        if (!(err = kv.append_layer(li, kr->view, vv)).ok()) return err;
+        if (!(err = matmul(att->view, w[4], &ao->view)).ok()) return err;
+        if (!(err = kernels::add_f32(fi->view, ao->view, &res1->view)).ok()) return err;
+        TensorView min = res1->view;
+        if (w[5].present) {
+          if (!(err = kernels::rmsnorm_f32(res1->view, &w[5].view, &n2->view, eps)).ok()) return err;
+          min = n2->view;
+        }
+        if (w[9].present && w[10].present) {
+          if (!(err = kernels::moe_router_f32(min, w[9].view, &mp->view, &mt->view)).ok()) return err;
+          err = kernels::moe_experts_swiglu_f32(min, w[10].view, w[11].view, w[12].view,
+                                                mp->view, &fo->view, static_cast<int>(E),
+                                                static_cast<int>(topk));
+          if (!err.ok()) return err;
+        } else {
+          const std::int64_t I = w[7].shape[0];
+          g->shape[1] = u->shape[1] = ga->shape[1] = hid->shape[1] = I;
+          g->view.nbytes = u->view.nbytes = ga->view.nbytes = hid->view.nbytes =
+              static_cast<std::size_t>(I) * 4;
+          if (!(err = matmul(min, w[6], &g->view)).ok()) return err;
+          if (!(err = matmul(min, w[7], &u->view)).ok()) return err;
+          if (!(err = kernels::silu_f32(g->view, &ga->view)).ok()) return err;
+          if (!(err = kernels::mul_f32(ga->view, u->view, &hid->view)).ok()) return err;
+          if (!(err = matmul(hid->view, w[8], &fo->view)).ok()) return err;
+        }
+        if (!(err = kernels::add_f32(res1->view, fo->view, &res2->view)).ok()) return err;
+        cur = res2->f32;
+        if (last && taps_resid2) std::memcpy(taps_resid2 + li * D, res2->f32.data(), D * 4);
+      }
+      auto fin = f32_tensor({1, D});
+      fin->f32 = cur;
+      fin->view.data = fin->f32.data();
+      TensorView fv = fin->view;
+      if (onorm.present) {
+        if (!(err = kernels::rmsnorm_f32(fin->view, &onorm.view, &normed->view, eps)).ok()) return err;
+        fv = normed->view;
+      }
+      if (!(err = matmul(fv, lm, &logits->view)).ok()) return err;
+      if (!(err = kernels::softmax_f32(logits->view, &probs->view, -1)).ok()) return err;
+      if (last && taps_logits) std::memcpy(taps_logits, logits->f32.data(), V * 4);
+      (void)feat;
+      return Error::success();
+    };
+
+    std::vector<std::int64_t> hist;
+    runtime::SampleParams greedy;
+    std::mt19937_64 rng{0};
+    Error err;
+    bool ok = true;
+    for (std::int64_t i = 0; i < n_prompt && ok; ++i) {
+      err = run(prompt[i], max_new <= 1 && i == n_prompt - 1);
+      if (!err.ok()) { ok = false; break; }
+      kv.commit_step();
+      hist.push_back(prompt[i]);
+    }
+    for (std::int64_t t = 0; t < max_new && ok; ++t) {
+      std::int64_t next = 0;
+      err = runtime::sample_token_f32(probs->f32.data(), static_cast<std::size_t>(V), greedy,
+                                      hist, &rng, &next);
+      if (!err.ok()) { ok = false; break; }
+      hist.push_back(next);
+      if (t + 1 >= max_new) break;
+      err = run(next, t + 2 >= max_new);
+      if (!err.ok()) { ok = false; break; }
+      kv.commit_step();
+    }
+    kernels::set_active_kv_cache(nullptr);
+    if (!ok) {
+      g_err = err.message();
+    } else {
+      for (std::size_t i = 0; i < hist.size(); ++i) out[i] = hist[i];
+      *out_n = static_cast<std::int64_t>(hist.size());
+      rc = 0;
+    }
+  }
+  orc_model_close(m);
+  return rc;
+}
+
+}  // extern "C"

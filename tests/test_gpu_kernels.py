@@ -1,0 +1,223 @@
+"""HIP kernel parity against the CPU oracle (through the uaii_hip_* C ABI).
+
+Bars: dequantized weights bit-exact; GEMV within 2e-3 max relative error
+(max |gpu - cpu| / max |cpu|, the tensor-scale relative error) of the oracle's
+per-row dequant + sequential f32 dot; small ops within 1e-5 of the oracle.
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import oracle
+import uaii_amd
+from uaii_amd import synth, DeviceBuffer, DeviceWeight, check_hip
+
+pytestmark = pytest.mark.gpu
+
+ALL_TYPES = [uaii_amd.Q4_0, uaii_amd.Q8_0, uaii_amd.Q4_K, uaii_amd.Q6_K, uaii_amd.Q4_1,
+             uaii_amd.Q5_0, uaii_amd.Q5_1, uaii_amd.Q5_K, uaii_amd.Q2_K, uaii_amd.Q3_K,
+             uaii_amd.F32, uaii_amd.F16]
+
+
+def maxrel(a, b):
+    return float(np.abs(np.asarray(a, np.float64) - b).max() / max(np.abs(b).max(), 1e-30))
+
+
+def random_packed(t, rows, cols, seed):
+    """Seeded weights quantized by the build's writer, plus random raw bytes for
+    the payload formats so every bit pattern is exercised."""
+    x = synth.normals(seed, 0, 0, rows * cols, 0.02)
+    if t in (uaii_amd.F32, uaii_amd.F16):
+        return (x.astype(np.float32 if t == uaii_amd.F32 else np.float16)).view(np.uint8).copy()
+    return synth.quantize(t, x)
+
+
+def raw_random_blocks(t, rows, cols, seed):
+    """Uniformly random block bytes with finite f16 scales (exercises all codes)."""
+    rng = np.random.default_rng(seed)
+    rb = uaii_amd.row_bytes(t, cols)
+    p = rng.integers(0, 256, size=rows * rb, dtype=np.uint8)
+    be, bb = uaii_amd.BLOCK[t]
+    blocks = p.reshape(-1, bb)
+    # keep f16 scale fields finite (exponent < 31) at their offsets
+    offs = {uaii_amd.Q4_0: [0], uaii_amd.Q8_0: [0], uaii_amd.Q4_1: [0, 2], uaii_amd.Q5_0: [0],
+            uaii_amd.Q5_1: [0, 2], uaii_amd.Q4_K: [0, 2], uaii_amd.Q5_K: [0, 2],
+            uaii_amd.Q6_K: [208], uaii_amd.Q2_K: [80, 82], uaii_amd.Q3_K: [108]}[t]
+    for o in offs:
+        blocks[:, o + 1] &= 0x7b  # exponent bits < 0x1f
+    return p
+
+
+@pytest.mark.parametrize("t", ALL_TYPES[:10], ids=lambda t: uaii_amd.TYPE_NAMES[t])
+def test_dequant_bit_exact_random_bytes(hip, t):
+    rows, cols = 24, 512
+    p = raw_random_blocks(t, rows, cols, seed=100 + t)
+    w = DeviceWeight(t, p, rows, cols)
+    out = DeviceBuffer(rows * cols * 4)
+    check_hip(hip.uaii_hip_dequant_rows(w.h, 0, rows, out.ptr, None), "dequant")
+    check_hip(hip.uaii_hip_synchronize())
+    got = out.to_array(np.float32, rows * cols).reshape(rows, cols)
+    want = oracle.dequant(t, p, rows, cols)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), "dequant not bit-exact"
+
+
+@pytest.mark.parametrize("t", ALL_TYPES, ids=lambda t: uaii_amd.TYPE_NAMES[t])
+def test_dequant_bit_exact_row_window(hip, t):
+    rows, cols = 40, 1024
+    p = random_packed(t, rows, cols, seed=7)
+    w = DeviceWeight(t, p, rows, cols)
+    out = DeviceBuffer(8 * cols * 4)
+    check_hip(hip.uaii_hip_dequant_rows(w.h, 17, 8, out.ptr, None), "dequant")
+    got = out.to_array(np.float32, 8 * cols).reshape(8, cols)
+    want = oracle.dequant(t, p, rows, cols)[17:25]
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def run_gemv(hip, t, rows, cols, x, p, norm=None, eps=1e-5):
+    w = DeviceWeight(t, p, rows, cols)
+    dx = DeviceBuffer.from_array(x.astype(np.float32))
+    dy = DeviceBuffer(rows * 4)
+    if norm is None:
+        check_hip(hip.uaii_hip_gemv(w.h, dx.ptr, dy.ptr, None), "gemv")
+    else:
+        dn = DeviceBuffer.from_array(norm.astype(np.float32))
+        check_hip(hip.uaii_hip_gemv_rmsnorm(w.h, dx.ptr, dn.ptr, eps, dy.ptr, None), "gemv_rmsnorm")
+    check_hip(hip.uaii_hip_synchronize())
+    return dy.to_array(np.float32, rows)
+
+
+@pytest.mark.parametrize("t", ALL_TYPES, ids=lambda t: uaii_amd.TYPE_NAMES[t])
+def test_gemv_small_all_formats(hip, t):
+    rows, cols = 96, 1536
+    p = random_packed(t, rows, cols, seed=21)
+    x = synth.normals(99, 1, 0, cols, 1.0)
+    got = run_gemv(hip, t, rows, cols, x, p)
+    want = oracle.quant_gemm(t, x, p, rows)[0]
+    assert maxrel(got, want) < 2e-5
+
+
+@pytest.mark.parametrize("t", [uaii_amd.Q4_0, uaii_amd.Q8_0, uaii_amd.Q4_K],
+                         ids=lambda t: uaii_amd.TYPE_NAMES[t])
+@pytest.mark.parametrize("shape", [(4096, 4096), (4096, 14336), (14336, 4096)],
+                         ids=lambda s: f"{s[0]}x{s[1]}")
+def test_gemv_config_shapes(hip, t, shape):
+    """Config 2 shapes (N x K) at M=1 against the oracle's CPU dequant-matmul."""
+    rows, cols = shape
+    p = random_packed(t, rows, cols, seed=3)
+    x = synth.normals(98, 1, 0, cols, 1.0)
+    got = run_gemv(hip, t, rows, cols, x, p)
+    want = oracle.quant_gemm(t, x, p, rows, nthreads=0)[0]
+    assert maxrel(got, want) < 2e-3
+    assert maxrel(got, want) < 1e-4  # in practice ~1e-6: f32 sums in a different order
+
+
+def test_gemv_bench_pattern_known_answer(hip):
+    """The reference benchmark's Q4_0 pattern (uaii_bench.cpp:505-518): d = 1.0,
+    qs[i] = (i + block) & 0xff, a[i] = 0.01 * ((i % 17) + 1), N=2048, K=4096;
+    compared with the exact f64 sum."""
+    rows, cols = 2048, 4096
+    nb = rows * cols // 32
+    blk = np.zeros((nb, 18), dtype=np.uint8)
+    blk[:, 0], blk[:, 1] = 0x00, 0x3c
+    b = np.arange(nb, dtype=np.int64)[:, None]
+    blk[:, 2:] = ((np.arange(16)[None, :] + b) & 0xff).astype(np.uint8)
+    a = (0.01 * ((np.arange(cols) % 17) + 1)).astype(np.float32)
+    got = run_gemv(hip, uaii_amd.Q4_0, rows, cols, a, blk.reshape(-1))
+    q = blk[:, 2:].astype(np.int64)
+    vals = np.concatenate([(q & 15) - 8, (q >> 4) - 8], axis=1).reshape(rows, cols).astype(np.float64)
+    exact = vals @ a.astype(np.float64)
+    assert maxrel(got, exact) < 1e-5
+
+
+@pytest.mark.parametrize("t", [uaii_amd.Q4_0, uaii_amd.Q4_K, uaii_amd.Q6_K],
+                         ids=lambda t: uaii_amd.TYPE_NAMES[t])
+def test_gemv_rmsnorm_prologue(hip, t):
+    rows, cols = 512, 2048
+    p = random_packed(t, rows, cols, seed=5)
+    x = synth.normals(97, 1, 0, cols, 3.0)
+    nw = 1.0 + synth.normals(96, 1, 0, cols, 0.1)
+    got = run_gemv(hip, t, rows, cols, x, p, norm=nw, eps=1e-5)
+    xn = np.zeros(cols, np.float32)
+    oracle.oracle().orc_rmsnorm(oracle._fp(x), oracle._fp(nw), oracle._fp(xn), cols, 1e-5)
+    want = oracle.quant_gemm(t, xn, p, rows)[0]
+    assert maxrel(got, want) < 1e-4
+
+
+def test_rmsnorm_softmax_argmax(hip):
+    n = 5000
+    x = synth.normals(1, 2, 0, 3 * n, 2.0).reshape(3, n)
+    w = 1.0 + synth.normals(1, 3, 0, n, 0.1)
+    dx, dw, dy = DeviceBuffer.from_array(x), DeviceBuffer.from_array(w), DeviceBuffer(x.nbytes)
+    check_hip(hip.uaii_hip_rmsnorm(dx.ptr, dw.ptr, dy.ptr, 3, n, 1e-5, None))
+    got = dy.to_array(np.float32, 3 * n).reshape(3, n)
+    for r in range(3):
+        want = np.zeros(n, np.float32)
+        oracle.oracle().orc_rmsnorm(oracle._fp(np.ascontiguousarray(x[r])), oracle._fp(w),
+                                    oracle._fp(want), n, 1e-5)
+        assert maxrel(got[r], want) < 1e-6
+    v = np.ascontiguousarray(x[0])
+    dv, dp = DeviceBuffer.from_array(v), DeviceBuffer(v.nbytes)
+    check_hip(hip.uaii_hip_softmax(dv.ptr, dp.ptr, n, None))
+    probs = dp.to_array(np.float32, n)
+    want = np.zeros(n, np.float32)
+    oracle.oracle().orc_softmax(oracle._fp(v), oracle._fp(want), n)
+    assert maxrel(probs, want) < 1e-5
+    assert abs(float(probs.astype(np.float64).sum()) - 1.0) < 1e-5
+    # argmax with a planted tie: lowest index wins (sampling.cpp:38-50)
+    v2 = v.copy()
+    v2[4321] = v2[123] = v2.max() + 1.0
+    dv2, di = DeviceBuffer.from_array(v2), DeviceBuffer(4)
+    check_hip(hip.uaii_hip_argmax(dv2.ptr, n, di.ptr, None))
+    assert int(di.to_array(np.int32, 1)[0]) == 123 == oracle.oracle().orc_argmax(oracle._fp(v2), n)
+
+
+@pytest.mark.parametrize("mode", [0, 2])
+def test_rope(hip, mode):
+    rows, hd, nh = 5, 64, 4
+    dim = hd * nh
+    x = synth.normals(3, 4, 0, rows * dim, 1.0).reshape(rows, dim)
+    pos = np.array([0, 1, 17, 1000, 4095], dtype=np.int32)
+    tab = DeviceBuffer(4096 * hd * 4)
+    check_hip(hip.uaii_hip_rope_table(500000.0, hd, 4096, tab.ptr))
+    dx, dp = DeviceBuffer.from_array(x), DeviceBuffer.from_array(pos)
+    check_hip(hip.uaii_hip_rope(dx.ptr, rows, dim, hd, mode, dp.ptr, tab.ptr, None))
+    got = dx.to_array(np.float32, rows * dim).reshape(rows, dim)
+    for r in range(rows):
+        want = np.ascontiguousarray(x[r]).copy()
+        oracle.oracle().orc_rope(oracle._fp(want), dim, hd, float(pos[r]), 500000.0, mode)
+        assert maxrel(got[r], want) < 1e-6
+    assert np.array_equal(got[0], x[0])  # position 0 is the identity
+
+
+@pytest.mark.parametrize("kv_f16", [0, 1])
+@pytest.mark.parametrize("heads", [(8, 8, 64), (32, 8, 128), (16, 2, 64)], ids=str)
+@pytest.mark.parametrize("n_keys", [1, 7, 100, 1500])
+def test_attention_decode(hip, kv_f16, heads, n_keys):
+    nh, nkv, hd = heads
+    max_seq = 2048
+    rng = np.random.default_rng(n_keys * 7 + nh)
+    q = rng.standard_normal(nh * hd).astype(np.float32)
+    k = rng.standard_normal((nkv, max_seq, hd)).astype(np.float32)
+    v = rng.standard_normal((nkv, max_seq, hd)).astype(np.float32)
+    if kv_f16:
+        k, v = k.astype(np.float16), v.astype(np.float16)
+    dq, dk, dv = DeviceBuffer.from_array(q), DeviceBuffer.from_array(k), DeviceBuffer.from_array(v)
+    do = DeviceBuffer(nh * hd * 4)
+    check_hip(hip.uaii_hip_attention_decode(dq.ptr, dk.ptr, dv.ptr, kv_f16, max_seq, nh, nkv, hd,
+                                            n_keys, do.ptr, None))
+    got = do.to_array(np.float32, nh * hd)
+    # oracle layout: [seq][kv_dim]; past = n_keys - 1, current = the last key
+    kf = k.astype(np.float32).transpose(1, 0, 2).reshape(max_seq, nkv * hd)
+    vf = v.astype(np.float32).transpose(1, 0, 2).reshape(max_seq, nkv * hd)
+    kc, vc = np.ascontiguousarray(kf[: n_keys - 1]), np.ascontiguousarray(vf[: n_keys - 1])
+    kn, vn = np.ascontiguousarray(kf[n_keys - 1]), np.ascontiguousarray(vf[n_keys - 1])
+    want = np.zeros(nh * hd, np.float32)
+    if n_keys == 1:
+        kc = np.zeros((1, nkv * hd), np.float32)
+        vc = np.zeros((1, nkv * hd), np.float32)
+    oracle.oracle().orc_attention_decode(oracle._fp(q), oracle._fp(kc), oracle._fp(vc), n_keys - 1,
+                                         oracle._fp(kn), oracle._fp(vn), oracle._fp(want), nh, nkv, hd)
+    assert maxrel(got, want) < 1e-5
+    if n_keys == 1:  # one key: the output is that key's V for every head of its group
+        assert maxrel(got, np.repeat(vf[0].reshape(nkv, hd), nh // nkv, axis=0).reshape(-1)) < 1e-6

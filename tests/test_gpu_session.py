@@ -1,0 +1,145 @@
+"""End-to-end greedy generate through the C ABI vs the CPU oracle.
+
+Bars (north star): greedy ids identical over the decoded tokens; per-layer hidden
+states (blk.N.resid1 / resid2) and logits within 2e-3 max relative error
+(max |gpu - cpu| / max |cpu| per tensor) of the oracle on the same seeded GGUF
+and prompt. With an f32 KV cache the oracle is the reference's f32 path; with
+the device fp16 cache the oracle also rounds K/V to fp16 (the reference has no
+fp16 cache), and the f32-oracle distance is reported too.
+"""
+import numpy as np
+import pytest
+
+import oracle
+import uaii_amd
+from uaii_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+
+def maxrel(a, b):
+    return float(np.abs(np.asarray(a, np.float64) - b).max() / max(np.abs(b).max(), 1e-30))
+
+
+SMALL = {
+    # GQA 4:1, Q4_0 with Q8_0 V, head_dim 64
+    "gqa_q4_0": synth.ModelConfig(n_layers=3, dim=512, n_heads=8, n_kv_heads=2, ffn=1024,
+                                  vocab=3000, ctx_len=256, type_default=uaii_amd.Q4_0,
+                                  type_attn_v=uaii_amd.Q8_0, seed=31),
+    # K-quant mix of the 1B config (Q4_K, Q6_K attn_v/ffn_down), tied embeddings
+    "kmix_tied": synth.ModelConfig(n_layers=2, dim=512, n_heads=8, n_kv_heads=2, ffn=1536,
+                                   vocab=2048, ctx_len=256, rope_theta=500000.0, tied=True,
+                                   type_default=uaii_amd.Q4_K, type_attn_v=uaii_amd.Q6_K,
+                                   type_ffn_down=uaii_amd.Q6_K, seed=32),
+    # head_dim 128, NeoX RoPE architecture (mode 2), Q8_0
+    "neox_hd128": synth.ModelConfig(n_layers=2, dim=512, n_heads=4, n_kv_heads=2, ffn=1024,
+                                    vocab=1500, ctx_len=256, type_default=uaii_amd.Q8_0,
+                                    arch="qwen2", seed=33),
+    # remaining block formats
+    "q5_mix": synth.ModelConfig(n_layers=2, dim=512, n_heads=8, n_kv_heads=4, ffn=768,
+                                vocab=1024, ctx_len=256, type_default=uaii_amd.Q5_K,
+                                type_attn_v=uaii_amd.Q5_0, type_ffn_down=uaii_amd.Q3_K,
+                                type_embd=uaii_amd.Q5_1, type_output=uaii_amd.Q2_K, seed=34),
+}
+
+
+def prompt_for(cfg, n, seed):
+    return np.random.default_rng(seed).integers(0, cfg.vocab, n).astype(np.int64)
+
+
+def compare(path, cfg, n_prompt, n_new, kv_f16, seed=0):
+    prompt = prompt_for(cfg, n_prompt, cfg.seed + 1 + seed)
+    with uaii_amd.Session(path, kv_f16=kv_f16) as s:
+        ids = s.generate(prompt, n_new)
+        taps = {k: s.get(k) for k in ("hidden", "normed", "logits")}
+        for li in range(cfg.n_layers):
+            taps[f"r1_{li}"] = s.get(f"blk.{li}.resid1")
+            taps[f"r2_{li}"] = s.get(f"blk.{li}.resid2")
+        probs = s.get("probs")
+    m = oracle.Model(path)
+    want_ids, want = m.generate(prompt, n_new, kv_f16=kv_f16)
+    return prompt, ids, taps, probs, want_ids, want
+
+
+@pytest.mark.parametrize("name", list(SMALL))
+def test_generate_small_configs(name):
+    cfg = SMALL[name]
+    path = synth.cached_model(cfg)
+    prompt, ids, taps, probs, want_ids, want = compare(path, cfg, 12, 20, kv_f16=False)
+    print(name, "gpu", ids[12:].tolist())
+    print(name, "cpu", want_ids[12:].tolist())
+    assert np.array_equal(ids, want_ids)
+    assert maxrel(taps["logits"], want["logits"]) < 2e-3
+    assert maxrel(taps["normed"], want["normed"]) < 2e-3
+    assert np.array_equal(taps["hidden"], want["hidden"])  # embedding row is a bit-exact dequant
+    for li in range(cfg.n_layers):
+        assert maxrel(taps[f"r1_{li}"], want["resid1"][li]) < 2e-3
+        assert maxrel(taps[f"r2_{li}"], want["resid2"][li]) < 2e-3
+    assert maxrel(probs, want["probs"]) < 2e-3
+
+
+def test_generate_tiny_config_f32_kv():
+    """tiny Llama GGUF, Q8_0, 32-token prompt + 64 greedy tokens, f32 KV."""
+    cfg = synth.PRESETS["tiny"]
+    path = synth.cached_model(cfg)
+    prompt, ids, taps, probs, want_ids, want = compare(path, cfg, 32, 64, kv_f16=False)
+    assert np.array_equal(ids, want_ids)
+    assert maxrel(taps["logits"], want["logits"]) < 2e-3
+    for li in range(cfg.n_layers):
+        assert maxrel(taps[f"r2_{li}"], want["resid2"][li]) < 2e-3
+
+
+def test_generate_fp16_kv():
+    cfg = SMALL["gqa_q4_0"]
+    path = synth.cached_model(cfg)
+    prompt, ids, taps, probs, want_ids, want = compare(path, cfg, 40, 24, kv_f16=True)
+    assert np.array_equal(ids, want_ids)
+    assert maxrel(taps["logits"], want["logits"]) < 2e-3
+    # distance to the reference's f32-cache path stays inside the same bar
+    ref_ids, ref32 = oracle.Model(path).generate(prompt, 24, kv_f16=False)
+    assert maxrel(taps["logits"], ref32["logits"]) < 2e-3
+
+
+def test_generate_matches_reference_kernels():
+    """Ids and taps against the reference's own compiled kernels (oracle/_ref)."""
+    if oracle.ref() is None:
+        pytest.skip("oracle/_ref not built")
+    cfg = SMALL["gqa_q4_0"]
+    path = synth.cached_model(cfg)
+    prompt = prompt_for(cfg, 10, 77)
+    with uaii_amd.Session(path) as s:
+        ids = s.generate(prompt, 16)
+        logits = s.get("logits")
+    m = oracle.Model(path)
+    rids, rlog, _ = oracle.ref_generate(path, prompt, 16, n_layers=m.n_layers, dim=m.dim, vocab=m.vocab)
+    assert np.array_equal(ids, rids)
+    assert maxrel(logits, rlog) < 2e-3
+
+
+def test_generate_edge_cases():
+    cfg = SMALL["gqa_q4_0"]
+    path = synth.cached_model(cfg)
+    with uaii_amd.Session(path) as s:
+        # max_new = 0 echoes the prompt
+        out = s.generate(np.array([5, 6, 7]), 0)
+        assert out.tolist() == [5, 6, 7]
+        # single-token prompt, one new token
+        out1 = s.generate(np.array([9]), 1)
+        want, _ = oracle.Model(path).generate(np.array([9]), 1)
+        assert out1.tolist() == want.tolist()
+        # context overflow is rejected (session.cpp:947-962)
+        with pytest.raises(uaii_amd.UaiiError, match="invalid_argument"):
+            s.generate(np.arange(200), 100)
+        # empty prompt
+        with pytest.raises(uaii_amd.UaiiError, match="invalid_argument"):
+            s.generate(np.array([], dtype=np.int64), 4)
+        # out-of-range token id
+        with pytest.raises(uaii_amd.UaiiError, match="invalid_argument"):
+            s.generate(np.array([cfg.vocab + 5]), 2)
+        # a full-context run right to max_context
+        full = s.generate(prompt_for(cfg, 200, 5), 56)
+        assert len(full) == 256
+        # repeated generate on one session resets the KV state
+        a = s.generate(np.array([11, 12, 13]), 5)
+        b = s.generate(np.array([11, 12, 13]), 5)
+        assert a.tolist() == b.tolist()

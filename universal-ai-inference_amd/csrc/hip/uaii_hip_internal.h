@@ -1,0 +1,118 @@
+// uaii_hip_internal.h — launch helpers shared by the HIP translation units and
+// the host runtime. Not part of the public C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "common.h"
+
+namespace uaii_hip {
+
+// Bytes per row of the split arrays a, b, c, d for `type` at `cols`.
+void split_row_bytes(int type, int64_t cols, int64_t out[4]);
+
+hipError_t launch_repack(const DevWeight& w, const uint8_t* src_dev, hipStream_t s);
+hipError_t launch_dequant(const DevWeight& w, int64_t row0, int64_t nrows, float* out,
+                          hipStream_t s);
+
+// ---- fused GEMV (decode, M = 1) ----------------------------------------------
+
+enum Epilogue : int {
+  EPI_STORE = 0,   // y[row] = dot
+  EPI_ADD = 1,     // y[row] = y[row] + dot        (residual add)
+  EPI_QKV = 2,     // bias, RoPE pairs, q -> y, k/v -> KV cache at pos
+  EPI_SWIGLU = 3,  // rows (gate i, up i) -> y[i] = silu(g) * u
+  EPI_LOGITS = 4,  // y[row] = dot, fused greedy argmax + token advance
+};
+
+// Persistent decode state shared by the step kernels (device memory).
+struct StepState {
+  int32_t pos;       // position of the token being processed (= KV past_len)
+  int32_t token;     // token id fed at `pos`
+  int32_t n_prompt;  // prompt length
+  int32_t argmax;    // last greedy argmax
+  float max_logit;   // its logit
+  float second;      // runner-up logit (parity margin diagnostics)
+  int32_t pad[2];
+};
+
+struct GemvSeg {
+  DevWeight w;   // for EPI_SWIGLU: gate rows; w2 = up rows
+  DevWeight w2;
+  const float* bias;   // optional per-row bias (EPI_QKV)
+  int64_t rows;        // logical rows in this segment
+  int64_t row_base;    // first logical row in the epilogue's output space
+  int kind;            // EPI_QKV: 0 = q, 1 = k, 2 = v
+  int block0;          // first block of this segment
+};
+
+struct GemvArgs {
+  GemvSeg seg[3];
+  int nseg;
+  int epi;
+  int64_t K;
+  const float* x;        // input vector [K]
+  const float* norm_w;   // RMSNorm weight [K] (prologue) or null
+  float eps;
+  float* y;              // EPI_STORE/ADD/QKV(q)/SWIGLU/LOGITS output
+  float* tap;            // optional copy of each written value (EPI_ADD)
+  float* xtap;           // optional copy of the staged (normalised) input, block 0
+  // EPI_QKV
+  void* kcache;          // layer base, [n_kv][max_seq][hd] (f16 or f32)
+  void* vcache;
+  int kv_f16;
+  int64_t max_seq;
+  int head_dim;
+  int rope_mode;
+  const float2* rope;    // [max_seq][hd/2] (cos, sin)
+  // EPI_LOGITS
+  float* part_val;       // [gridDim]
+  int32_t* part_idx;
+  uint32_t* ticket;
+  int32_t* ids;          // token history [max_seq + 1]
+  // shared
+  StepState* state;
+};
+
+hipError_t launch_gemv(const GemvArgs& a, hipStream_t s);
+// Raise the dynamic-LDS limit of the GEMV kernel (call once per device, outside capture).
+hipError_t prepare_gemv();
+// Number of blocks launch_gemv will use for the given args (for partial buffers).
+int gemv_grid(const GemvArgs& a);
+
+// ---- small ops -------------------------------------------------------------------
+
+hipError_t launch_embed(const DevWeight& w, const StepState* st, float* x, float* tap,
+                        hipStream_t s);
+hipError_t launch_embed_rows(const DevWeight& w, const int32_t* ids, int64_t n, float* x,
+                             hipStream_t s);
+hipError_t launch_advance(StepState* st, int32_t* ids, hipStream_t s);
+hipError_t launch_rmsnorm(const float* x, const float* w, float* y, int64_t rows, int64_t n,
+                          float eps, hipStream_t s);
+hipError_t launch_softmax(const float* x, float* y, int64_t n, hipStream_t s);
+hipError_t launch_argmax(const float* x, int64_t n, int32_t* out_idx, hipStream_t s);
+hipError_t launch_rope(float* x, int64_t rows, int64_t dim, int head_dim, const int32_t* pos,
+                       int64_t pos_stride, const float2* tab, int mode, hipStream_t s);
+
+// ---- attention -----------------------------------------------------------------
+
+struct AttnArgs {
+  const float* q;        // [n_heads * hd] (post-RoPE)
+  const void* kcache;    // layer base [n_kv][max_seq][hd]
+  const void* vcache;
+  int kv_f16;
+  int64_t max_seq;
+  int n_heads, n_kv, hd;
+  const StepState* state;  // keys 0..state->pos inclusive
+  int fixed_len;           // >0: use this key count instead of state->pos + 1
+  float* out;            // [n_heads * hd]
+  float* part;           // [n_kv][splits][group][hd + 2]
+  uint32_t* ticket;      // [n_kv]
+  int splits;
+};
+
+hipError_t launch_attention_decode(const AttnArgs& a, hipStream_t s);
+hipError_t prepare_attention();
+
+}  // namespace uaii_hip

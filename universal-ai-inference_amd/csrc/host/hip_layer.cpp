@@ -1,0 +1,273 @@
+// hip_layer.cpp — the extern "C" HIP launch layer declared in include/uaii_hip.h.
+#include "uaii_hip.h"
+
+#include "program.h"
+
+#include <cmath>
+#include <mutex>
+#include <vector>
+
+using namespace uaii_hip;
+
+struct uaii_hip_weight {
+  uaii::DeviceWeight w;
+};
+
+namespace {
+
+constexpr int kErrArg = -1;      // invalid argument
+constexpr int kErrNotImpl = -2;  // not implemented
+
+std::mutex g_scratch_mu;
+void* g_scratch = nullptr;       // attention partials + tickets for uaii_hip_attention_decode
+size_t g_scratch_bytes = 0;
+
+hipStream_t S(void* s) { return static_cast<hipStream_t>(s); }
+
+int grow_scratch(size_t bytes) {
+  if (bytes <= g_scratch_bytes) return 0;
+  if (g_scratch) {
+    hipError_t e = hipDeviceSynchronize();
+    if (e != hipSuccess) return (int)e;
+    (void)hipFree(g_scratch);
+    g_scratch = nullptr;
+    g_scratch_bytes = 0;
+  }
+  hipError_t e = hipMalloc(&g_scratch, bytes);
+  if (e != hipSuccess) return (int)e;
+  e = hipMemset(g_scratch, 0, bytes);
+  if (e != hipSuccess) return (int)e;
+  g_scratch_bytes = bytes;
+  return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int uaii_hip_init(int device) {
+  hipError_t e = hipSetDevice(device);
+  if (e != hipSuccess) return (int)e;
+  e = prepare_gemv();
+  if (e != hipSuccess) return (int)e;
+  return (int)prepare_attention();
+}
+
+int uaii_hip_device_count(int* count) {
+  if (!count) return kErrArg;
+  return (int)hipGetDeviceCount(count);
+}
+
+const char* uaii_hip_error_string(int code) {
+  if (code == kErrArg) return "invalid argument";
+  if (code == kErrNotImpl) return "not implemented";
+  return hipGetErrorString(static_cast<hipError_t>(code));
+}
+
+int uaii_hip_malloc(void** ptr, size_t bytes) {
+  if (!ptr) return kErrArg;
+  return (int)hipMalloc(ptr, bytes);
+}
+int uaii_hip_free(void* ptr) { return (int)hipFree(ptr); }
+int uaii_hip_memcpy_h2d(void* dst, const void* src, size_t bytes) {
+  return (int)hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice);
+}
+int uaii_hip_memcpy_d2h(void* dst, const void* src, size_t bytes) {
+  return (int)hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost);
+}
+int uaii_hip_memset(void* ptr, int value, size_t bytes) { return (int)hipMemset(ptr, value, bytes); }
+int uaii_hip_synchronize(void) { return (int)hipDeviceSynchronize(); }
+
+int uaii_hip_weight_create(int gguf_type, const void* host_packed, int64_t rows, int64_t cols,
+                           uaii_hip_weight** out) {
+  if (!host_packed || !out || rows <= 0 || cols <= 0) return kErrArg;
+  auto* h = new uaii_hip_weight();
+  uaii::Error err = uaii::upload_weight(gguf_type, static_cast<const uint8_t*>(host_packed), rows,
+                                        cols, nullptr, &h->w);
+  if (!err.ok()) {
+    delete h;
+    return err.code() == uaii::ErrorCode::NotImplemented ? kErrNotImpl : kErrArg;
+  }
+  *out = h;
+  return 0;
+}
+
+int uaii_hip_weight_destroy(uaii_hip_weight* w) {
+  delete w;
+  return 0;
+}
+
+int64_t uaii_hip_weight_bytes(const uaii_hip_weight* w) { return w ? (int64_t)w->w.bytes : 0; }
+
+int uaii_hip_dequant_rows(const uaii_hip_weight* w, int64_t row0, int64_t nrows, float* out,
+                          void* stream) {
+  if (!w || !out || row0 < 0 || nrows < 0 || row0 + nrows > w->w.view.rows) return kErrArg;
+  return (int)launch_dequant(w->w.view, row0, nrows, out, S(stream));
+}
+
+static int gemv_common(const uaii_hip_weight* w, const float* x, const float* norm_w, float eps,
+                       float* y, void* stream) {
+  if (!w || !x || !y) return kErrArg;
+  if (w->w.view.cols % 4) return kErrArg;
+  GemvArgs a{};
+  a.nseg = 1;
+  a.epi = EPI_STORE;
+  a.K = w->w.view.cols;
+  a.x = x;
+  a.norm_w = norm_w;
+  a.eps = eps;
+  a.y = y;
+  a.seg[0].w = w->w.view;
+  a.seg[0].rows = w->w.view.rows;
+  return (int)launch_gemv(a, S(stream));
+}
+
+int uaii_hip_gemv(const uaii_hip_weight* w, const float* x, float* y, void* stream) {
+  return gemv_common(w, x, nullptr, 0.0f, y, stream);
+}
+
+int uaii_hip_gemv_rmsnorm(const uaii_hip_weight* w, const float* x, const float* norm_w,
+                          float eps, float* y, void* stream) {
+  if (!norm_w) return kErrArg;
+  return gemv_common(w, x, norm_w, eps, y, stream);
+}
+
+int uaii_hip_gemm(const uaii_hip_weight* w, const float* x, int64_t m, float* y, void* stream) {
+  if (!w || !x || !y || m <= 0) return kErrArg;
+  // M rows through the GEMV kernel (prefill MFMA path not in this build yet)
+  for (int64_t i = 0; i < m; ++i) {
+    const int rc = gemv_common(w, x + i * w->w.view.cols, nullptr, 0.0f, y + i * w->w.view.rows, stream);
+    if (rc) return rc;
+  }
+  return 0;
+}
+
+int uaii_hip_rmsnorm(const float* x, const float* w, float* y, int64_t rows, int64_t n, float eps,
+                     void* stream) {
+  if (!x || !y || rows < 0 || n <= 0) return kErrArg;
+  return (int)launch_rmsnorm(x, w, y, rows, n, eps, S(stream));
+}
+
+int uaii_hip_softmax(const float* x, float* y, int64_t n, void* stream) {
+  if (!x || !y || n <= 0) return kErrArg;
+  return (int)launch_softmax(x, y, n, S(stream));
+}
+
+int uaii_hip_argmax(const float* x, int64_t n, int32_t* out_idx, void* stream) {
+  if (!x || !out_idx || n <= 0) return kErrArg;
+  return (int)launch_argmax(x, n, out_idx, S(stream));
+}
+
+int uaii_hip_rope_table(float theta, int head_dim, int64_t max_pos, float* table_dev) {
+  if (!table_dev || head_dim <= 0 || head_dim % 2 || max_pos <= 0) return kErrArg;
+  std::vector<float> tab((size_t)max_pos * (size_t)head_dim);
+  for (int p = 0; p < head_dim / 2; ++p) {
+    // transformer.cpp:195-216: freq = 1/powf(theta, 2p/hd), angle = pos*freq
+    const float freq = 1.0f / std::pow(theta, static_cast<float>(2 * p) / static_cast<float>(head_dim));
+    for (int64_t pos = 0; pos < max_pos; ++pos) {
+      const float ang = static_cast<float>(pos) * freq;
+      tab[((size_t)pos * (size_t)(head_dim / 2) + (size_t)p) * 2] = std::cos(ang);
+      tab[((size_t)pos * (size_t)(head_dim / 2) + (size_t)p) * 2 + 1] = std::sin(ang);
+    }
+  }
+  return (int)hipMemcpy(table_dev, tab.data(), tab.size() * 4, hipMemcpyHostToDevice);
+}
+
+int uaii_hip_rope(float* x, int64_t rows, int64_t dim, int head_dim, int mode,
+                  const int32_t* pos_dev, const float* table_dev, void* stream) {
+  if (!x || !pos_dev || !table_dev || head_dim <= 0 || head_dim % 2 || dim % head_dim) return kErrArg;
+  return (int)launch_rope(x, rows, dim, head_dim, pos_dev, 1,
+                          reinterpret_cast<const float2*>(table_dev), mode, S(stream));
+}
+
+int uaii_hip_attention_decode(const float* q, const void* kcache, const void* vcache, int kv_f16,
+                              int64_t max_seq, int n_heads, int n_kv_heads, int head_dim,
+                              int64_t n_keys, float* out, void* stream) {
+  if (!q || !kcache || !vcache || !out || n_heads <= 0 || n_kv_heads <= 0 ||
+      n_heads % n_kv_heads || head_dim <= 0 || n_keys <= 0 || n_keys > max_seq)
+    return kErrArg;
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  const int splits = (int)std::min<int64_t>(64, std::max<int64_t>(1, (max_seq + 63) / 64));
+  const int G = n_heads / n_kv_heads;
+  // tickets first at a fixed offset (re-armed to zero by the kernel), partials after
+  if (n_kv_heads > 1024) return kErrArg;
+  const size_t part = (size_t)n_kv_heads * splits * G * (size_t)(head_dim + 2) * 4;
+  const size_t part_off = 4096;
+  int rc = grow_scratch(part_off + part);
+  if (rc) return rc;
+  AttnArgs a{};
+  a.q = q;
+  a.kcache = kcache;
+  a.vcache = vcache;
+  a.kv_f16 = kv_f16;
+  a.max_seq = max_seq;
+  a.n_heads = n_heads;
+  a.n_kv = n_kv_heads;
+  a.hd = head_dim;
+  a.state = nullptr;
+  a.fixed_len = (int)n_keys;
+  a.out = out;
+  a.part = reinterpret_cast<float*>(static_cast<char*>(g_scratch) + part_off);
+  a.ticket = static_cast<uint32_t*>(g_scratch);
+  a.splits = splits;
+  return (int)launch_attention_decode(a, S(stream));
+}
+
+int uaii_hip_time_gemv(const uaii_hip_weight* w, const float* x, float* y, int iters,
+                       float* avg_ms) {
+  if (!w || !x || !y || iters <= 0 || !avg_ms) return kErrArg;
+  hipEvent_t e0, e1;
+  (void)hipEventCreate(&e0);
+  (void)hipEventCreate(&e1);
+  int rc = uaii_hip_gemv(w, x, y, nullptr);  // warm
+  (void)hipEventRecord(e0, nullptr);
+  for (int i = 0; i < iters && !rc; ++i) rc = uaii_hip_gemv(w, x, y, nullptr);
+  (void)hipEventRecord(e1, nullptr);
+  (void)hipEventSynchronize(e1);
+  float ms = 0.0f;
+  (void)hipEventElapsedTime(&ms, e0, e1);
+  *avg_ms = ms / (float)iters;
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  return rc;
+}
+
+int uaii_hip_time_gemm(const uaii_hip_weight* w, const float* x, int64_t m, float* y, int iters,
+                       float* avg_ms) {
+  if (!w || !x || !y || iters <= 0 || !avg_ms || m <= 0) return kErrArg;
+  hipEvent_t e0, e1;
+  (void)hipEventCreate(&e0);
+  (void)hipEventCreate(&e1);
+  int rc = uaii_hip_gemm(w, x, m, y, nullptr);
+  (void)hipEventRecord(e0, nullptr);
+  for (int i = 0; i < iters && !rc; ++i) rc = uaii_hip_gemm(w, x, m, y, nullptr);
+  (void)hipEventRecord(e1, nullptr);
+  (void)hipEventSynchronize(e1);
+  float ms = 0.0f;
+  (void)hipEventElapsedTime(&ms, e0, e1);
+  *avg_ms = ms / (float)iters;
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  return rc;
+}
+
+int uaii_hip_time_copy(const void* src, void* dst, size_t bytes, int iters, float* avg_ms) {
+  if (!src || !dst || iters <= 0 || !avg_ms) return kErrArg;
+  hipEvent_t e0, e1;
+  (void)hipEventCreate(&e0);
+  (void)hipEventCreate(&e1);
+  int rc = (int)hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, nullptr);
+  (void)hipEventRecord(e0, nullptr);
+  for (int i = 0; i < iters && !rc; ++i)
+    rc = (int)hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, nullptr);
+  (void)hipEventRecord(e1, nullptr);
+  (void)hipEventSynchronize(e1);
+  float ms = 0.0f;
+  (void)hipEventElapsedTime(&ms, e0, e1);
+  *avg_ms = ms / (float)iters;
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  return rc;
+}
+
+}  // extern "C"

@@ -1,0 +1,521 @@
+// program.cpp — see program.h.
+#include "program.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <sstream>
+
+namespace uaii {
+
+using namespace uaii_hip;
+
+namespace {
+
+size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+double gguf_bpw(int type) {
+  const int be = block_elems(type);
+  return be ? (double)block_bytes(type) / (double)be : 0.0;
+}
+
+// Algorithmic bytes of one M=1 GEMV: packed weight + f32 input + f32 output.
+double gemv_bytes(const DevWeight& w) {
+  return (double)w.rows * (double)w.cols * gguf_bpw(w.type) + 4.0 * (double)w.cols +
+         4.0 * (double)w.rows;
+}
+
+// RoPE angle table, computed with the reference's own float expressions
+// (transformer.cpp:195-216): freq = 1/powf(theta, 2p/hd), angle = pos*freq.
+std::vector<float2> rope_table(float theta, int hd, int64_t max_pos) {
+  std::vector<float2> tab((size_t)max_pos * (size_t)(hd / 2));
+  for (int p = 0; p < hd / 2; ++p) {
+    const float freq = 1.0f / std::pow(theta, static_cast<float>(2 * p) / static_cast<float>(hd));
+    for (int64_t pos = 0; pos < max_pos; ++pos) {
+      const float ang = static_cast<float>(pos) * freq;
+      tab[(size_t)pos * (size_t)(hd / 2) + (size_t)p] = make_float2(std::cos(ang), std::sin(ang));
+    }
+  }
+  return tab;
+}
+
+}  // namespace
+
+DeviceWeight::~DeviceWeight() {
+  if (base) (void)hipFree(base);
+}
+
+Error upload_weight(int type, const uint8_t* host, int64_t rows, int64_t cols, hipStream_t s,
+                    DeviceWeight* out) {
+  const int be = block_elems(type);
+  if (be == 0) return Error::make(ErrorCode::NotImplemented, "unsupported GGUF type " + std::to_string(type));
+  if (rows <= 0 || cols <= 0 || cols % be)
+    return Error::make(ErrorCode::InvalidArgument, "weight cols not a multiple of the block size");
+  int64_t rb[4];
+  split_row_bytes(type, cols, rb);
+  if (rb[0] % 16)
+    return Error::make(ErrorCode::InvalidArgument, "weight row payload not a multiple of 16 bytes");
+  size_t off[4], total = 0;
+  for (int k = 0; k < 4; ++k) {
+    off[k] = total;
+    total = align_up(total + (size_t)(rows * rb[k]), 256);
+  }
+  UAII_HIP(hipMalloc(&out->base, total));
+  out->bytes = total;
+  DevWeight& v = out->view;
+  v.type = type;
+  v.rows = rows;
+  v.cols = cols;
+  uint8_t* b = static_cast<uint8_t*>(out->base);
+  v.a = b + off[0]; v.b = b + off[1]; v.c = b + off[2]; v.d = b + off[3];
+  v.a_row = rb[0]; v.b_row = rb[1]; v.c_row = rb[2]; v.d_row = rb[3];
+
+  const int64_t raw_row = (int64_t)gguf_nbytes(type, (uint64_t)cols);
+  const int64_t chunk_rows = std::max<int64_t>(1, std::min<int64_t>(rows, (64ll << 20) / raw_row));
+  void* stage = nullptr;
+  UAII_HIP(hipMalloc(&stage, (size_t)(chunk_rows * raw_row)));
+  Error err;
+  for (int64_t r0 = 0; r0 < rows && err.ok(); r0 += chunk_rows) {
+    const int64_t n = std::min(chunk_rows, rows - r0);
+    hipError_t st = hipMemcpyAsync(stage, host + r0 * raw_row, (size_t)(n * raw_row),
+                                   hipMemcpyHostToDevice, s);
+    if (st == hipSuccess) {
+      DevWeight sub = v;
+      sub.rows = n;
+      sub.a += r0 * v.a_row; sub.b += r0 * v.b_row; sub.c += r0 * v.c_row; sub.d += r0 * v.d_row;
+      st = launch_repack(sub, static_cast<const uint8_t*>(stage), s);
+    }
+    if (st == hipSuccess) st = hipStreamSynchronize(s);
+    err = hip_error(st, "weight upload");
+  }
+  (void)hipFree(stage);
+  return err;
+}
+
+DecoderProgram::~DecoderProgram() {
+  free_dynamic();
+  for (void* p : allocs_) (void)hipFree(p);
+  if (ev0_) (void)hipEventDestroy(ev0_);
+  if (ev1_) (void)hipEventDestroy(ev1_);
+  if (stream_) (void)hipStreamDestroy(stream_);
+}
+
+void DecoderProgram::free_dynamic() {
+  for (auto& g : graph_) {
+    if (g) (void)hipGraphExecDestroy(g);
+    g = nullptr;
+  }
+  for (void* p : {(void*)kv_, (void*)ids_, (void*)rope_, (void*)attn_part_, (void*)attn_ticket_}) {
+    if (p) (void)hipFree(p);
+  }
+  kv_ = nullptr; ids_ = nullptr; rope_ = nullptr; attn_part_ = nullptr; attn_ticket_ = nullptr;
+  max_ctx_ = 0;
+}
+
+Error DecoderProgram::upload_f32(const GgufTensor* t, float** out) {
+  *out = nullptr;
+  if (!t) return Error::success();
+  uint64_t n = 1;
+  for (auto d : t->ne) n *= d;
+  std::vector<float> h(n);
+  if (t->type == T_F32) {
+    std::memcpy(h.data(), t->data, n * 4);
+  } else if (t->type == T_F16) {
+    for (uint64_t i = 0; i < n; ++i) {
+      uint16_t v;
+      std::memcpy(&v, t->data + 2 * i, 2);
+      // exact half -> float (same value as the reference's f16_to_f32)
+      const uint32_t sign = (uint32_t)(v & 0x8000u) << 16;
+      uint32_t e = (v >> 10) & 31u, m = v & 1023u, bits;
+      if (e == 0 && m == 0) bits = sign;
+      else if (e == 0) { int sh = 0; while (!(m & 0x400u)) { m <<= 1; ++sh; } bits = sign | ((uint32_t)(113 - sh) << 23) | ((m & 1023u) << 13); }
+      else if (e == 31) bits = sign | 0x7f800000u | (m << 13);
+      else bits = sign | ((e + 112u) << 23) | (m << 13);
+      std::memcpy(&h[i], &bits, 4);
+    }
+  } else {
+    return Error::make(ErrorCode::NotImplemented, "norm/bias tensor " + t->name + " must be F32 or F16");
+  }
+  void* p = nullptr;
+  UAII_HIP(hipMalloc(&p, n * 4));
+  allocs_.push_back(p);
+  UAII_HIP(hipMemcpy(p, h.data(), n * 4, hipMemcpyHostToDevice));
+  *out = static_cast<float*>(p);
+  return Error::success();
+}
+
+Error DecoderProgram::build(const DecoderSpec& spec, const ProgramOptions& opts) {
+  spec_ = spec;
+  opts_ = opts;
+  UAII_HIP(prepare_gemv());
+  UAII_HIP(prepare_attention());
+  UAII_HIP(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking));
+  UAII_HIP(hipEventCreate(&ev0_));
+  UAII_HIP(hipEventCreate(&ev1_));
+  const DecoderSpec& d = spec_;
+  if (d.n_layers <= 0) return Error::make(ErrorCode::InvalidArgument, "decoder has no layers");
+  if (d.head_dim % 2 || d.head_dim > 256)
+    return Error::make(ErrorCode::NotImplemented, "head_dim must be even and <= 256");
+  if (d.n_heads % d.n_kv_heads)
+    return Error::make(ErrorCode::InvalidArgument, "invalid GQA head grouping");
+  if (d.dim % 4 || d.q_dim % 4)
+    return Error::make(ErrorCode::InvalidArgument, "model dims must be multiples of 4");
+
+  auto up = [&](const GgufTensor* t, DeviceWeight* w) -> Error {
+    return upload_weight(t->type, t->data, t->rows(), t->cols(), stream_, w);
+  };
+  UAII_TRY(up(d.tok_embd, &tok_embd_));
+  if (!d.tied) UAII_TRY(up(d.output, &output_));
+  UAII_TRY(upload_f32(d.out_norm, &out_norm_));
+  for (int64_t li = 0; li < d.n_layers; ++li) {
+    const LayerSpec& s = d.layers[(size_t)li];
+    auto L = std::make_unique<Layer>();
+    if (s.wq->cols() != d.dim || s.wq->rows() != d.q_dim || s.wk->rows() != d.kv_dim ||
+        s.wv->rows() != d.kv_dim || s.wo->cols() != d.q_dim || s.wo->rows() != d.dim)
+      return Error::make(ErrorCode::InvalidArgument, "attention weight shapes do not match hyperparameters");
+    UAII_TRY(up(s.wq, &L->wq));
+    UAII_TRY(up(s.wk, &L->wk));
+    UAII_TRY(up(s.wv, &L->wv));
+    UAII_TRY(up(s.wo, &L->wo));
+    UAII_TRY(upload_f32(s.attn_norm, &L->attn_norm));
+    UAII_TRY(upload_f32(s.ffn_norm, &L->ffn_norm));
+    UAII_TRY(upload_f32(s.bq, &L->bq));
+    UAII_TRY(upload_f32(s.bk, &L->bk));
+    UAII_TRY(upload_f32(s.bv, &L->bv));
+    if (s.ffn == LayerSpec::kSwiGLU) {
+      if (s.w_gate->type != s.w_up->type)
+        return Error::make(ErrorCode::NotImplemented, "ffn_gate and ffn_up must share a quant type");
+      UAII_TRY(up(s.w_gate, &L->gate));
+      UAII_TRY(up(s.w_up, &L->up));
+      UAII_TRY(up(s.w_down, &L->down));
+      ffn_max_ = std::max(ffn_max_, s.inter);
+    } else if (s.ffn == LayerSpec::kNone) {
+      // resid2 = resid1 (gguf.cpp:1171-1173)
+    } else {
+      return Error::make(ErrorCode::NotImplemented,
+                         s.ffn == LayerSpec::kMoE ? "MoE FFN not supported by this build yet"
+                                                  : "GELU FFN not supported by this build yet");
+    }
+    layers_.push_back(std::move(L));
+  }
+
+  // activations and step state
+  auto alloc = [&](size_t bytes, void** p) -> Error {
+    UAII_HIP(hipMalloc(p, std::max<size_t>(bytes, 256)));
+    UAII_HIP(hipMemset(*p, 0, std::max<size_t>(bytes, 256)));
+    allocs_.push_back(*p);
+    return Error::success();
+  };
+  const size_t D = (size_t)d.dim, Q = (size_t)d.q_dim, V = (size_t)d.vocab, L = (size_t)d.n_layers;
+  UAII_TRY(alloc(4 * D, (void**)&x_));
+  UAII_TRY(alloc(4 * Q, (void**)&q_));
+  UAII_TRY(alloc(4 * Q, (void**)&attn_));
+  UAII_TRY(alloc(4 * (size_t)std::max<int64_t>(ffn_max_, 1) * 2, (void**)&h_));
+  UAII_TRY(alloc(4 * V, (void**)&logits_));
+  UAII_TRY(alloc(4 * V, (void**)&probs_));
+  UAII_TRY(alloc(4 * D, (void**)&tap_hidden_));
+  UAII_TRY(alloc(4 * D * L, (void**)&tap_r1_));
+  UAII_TRY(alloc(4 * D * L, (void**)&tap_r2_));
+  UAII_TRY(alloc(4 * D, (void**)&tap_normed_));
+  UAII_TRY(alloc(sizeof(StepState), (void**)&state_));
+  GemvArgs lm{};
+  lm.nseg = 1;
+  lm.seg[0].rows = d.vocab;
+  const int lm_blocks = gemv_grid(lm);
+  UAII_TRY(alloc(4 * (size_t)lm_blocks, (void**)&lm_part_val_));
+  UAII_TRY(alloc(4 * (size_t)lm_blocks, (void**)&lm_part_idx_));
+  UAII_TRY(alloc(4, (void**)&lm_ticket_));
+  UAII_HIP(hipStreamSynchronize(stream_));
+  int64_t want = opts_.max_context > 0 ? opts_.max_context : d.ctx_len;
+  if (want > 0) UAII_TRY(ensure_capacity(want));
+  return Error::success();
+}
+
+Error DecoderProgram::ensure_capacity(int64_t max_seq) {
+  if (max_seq <= max_ctx_ && kv_) return Error::success();
+  UAII_HIP(hipStreamSynchronize(stream_));
+  free_dynamic();
+  const DecoderSpec& d = spec_;
+  const size_t elem = opts_.kv_f16 ? 2 : 4;
+  kv_bytes_ = (size_t)d.n_layers * 2 * (size_t)d.kv_dim * (size_t)max_seq * elem;
+  UAII_HIP(hipMalloc(&kv_, kv_bytes_));
+  UAII_HIP(hipMemsetAsync(kv_, 0, kv_bytes_, stream_));
+  UAII_HIP(hipMalloc((void**)&ids_, sizeof(int32_t) * (size_t)(max_seq + 2)));
+  UAII_HIP(hipMemsetAsync(ids_, 0, sizeof(int32_t) * (size_t)(max_seq + 2), stream_));
+  const int hd = (int)d.head_dim;
+  std::vector<float2> tab = rope_table(d.rope_theta, hd, max_seq);
+  UAII_HIP(hipMalloc((void**)&rope_, tab.size() * sizeof(float2)));
+  UAII_HIP(hipMemcpy(rope_, tab.data(), tab.size() * sizeof(float2), hipMemcpyHostToDevice));
+  attn_splits_ = (int)std::min<int64_t>(64, std::max<int64_t>(1, (max_seq + 63) / 64));
+  const int G = (int)(d.n_heads / d.n_kv_heads);
+  const size_t part = (size_t)d.n_kv_heads * attn_splits_ * G * (size_t)(hd + 2);
+  UAII_HIP(hipMalloc((void**)&attn_part_, part * 4));
+  UAII_HIP(hipMalloc((void**)&attn_ticket_, 4 * (size_t)d.n_kv_heads));
+  UAII_HIP(hipMemsetAsync(attn_ticket_, 0, 4 * (size_t)d.n_kv_heads, stream_));
+  UAII_HIP(hipStreamSynchronize(stream_));
+  max_ctx_ = max_seq;
+  return Error::success();
+}
+
+Error DecoderProgram::begin(const int64_t* prompt, int64_t n_prompt) {
+  if (n_prompt <= 0) return Error::make(ErrorCode::InvalidArgument, "prompt_tokens empty");
+  if (n_prompt > max_ctx_) return Error::make(ErrorCode::InvalidArgument, "prompt exceeds KV capacity");
+  std::vector<int32_t> ids((size_t)n_prompt);
+  for (int64_t i = 0; i < n_prompt; ++i) {
+    if (prompt[i] < 0 || prompt[i] >= tok_embd_.view.rows)
+      return Error::make(ErrorCode::InvalidArgument,
+                         "embedding token id out of range: " + std::to_string(prompt[i]) +
+                             " vocab=" + std::to_string(tok_embd_.view.rows));
+    ids[(size_t)i] = (int32_t)prompt[i];
+  }
+  UAII_HIP(hipStreamSynchronize(stream_));
+  UAII_HIP(hipMemcpy(ids_, ids.data(), ids.size() * 4, hipMemcpyHostToDevice));
+  StepState st{};
+  st.pos = 0;
+  st.token = ids[0];
+  st.n_prompt = (int32_t)n_prompt;
+  st.argmax = 0;
+  UAII_HIP(hipMemcpy(state_, &st, sizeof(st), hipMemcpyHostToDevice));
+  return Error::success();
+}
+
+Error DecoderProgram::set_token(int64_t token) {
+  if (token < 0 || token >= tok_embd_.view.rows)
+    return Error::make(ErrorCode::InvalidArgument, "embedding token id out of range: " + std::to_string(token));
+  const int32_t t = (int32_t)token;
+  UAII_HIP(hipStreamSynchronize(stream_));
+  UAII_HIP(hipMemcpy(&state_->token, &t, 4, hipMemcpyHostToDevice));
+  return Error::success();
+}
+
+Error DecoderProgram::read_state(StepState* st) {
+  UAII_HIP(hipStreamSynchronize(stream_));
+  UAII_HIP(hipMemcpy(st, state_, sizeof(StepState), hipMemcpyDeviceToHost));
+  return Error::success();
+}
+
+Error DecoderProgram::synchronize() {
+  UAII_HIP(hipStreamSynchronize(stream_));
+  return Error::success();
+}
+
+Error DecoderProgram::read_ids(int64_t* out, int64_t n) {
+  if (n > max_ctx_ + 1) return Error::make(ErrorCode::InvalidArgument, "read_ids beyond capacity");
+  std::vector<int32_t> ids((size_t)n);
+  UAII_HIP(hipStreamSynchronize(stream_));
+  UAII_HIP(hipMemcpy(ids.data(), ids_, (size_t)n * 4, hipMemcpyDeviceToHost));
+  for (int64_t i = 0; i < n; ++i) out[i] = ids[(size_t)i];
+  return Error::success();
+}
+
+Error DecoderProgram::encode_step(bool want_logits) {
+  const DecoderSpec& d = spec_;
+  hipStream_t s = stream_;
+  const size_t elem = opts_.kv_f16 ? 2 : 4;
+  const size_t layer_kv = (size_t)d.kv_dim * (size_t)max_ctx_ * elem;
+
+  // Each launch optionally bracketed by events (profiling mode only).
+  auto timed = [&](const char* name, double bytes, auto&& launch) -> Error {
+    if (!opts_.profile) {
+      UAII_HIP(launch());
+      return Error::success();
+    }
+    UAII_HIP(hipEventRecord(ev0_, s));
+    UAII_HIP(launch());
+    UAII_HIP(hipEventRecord(ev1_, s));
+    UAII_HIP(hipEventSynchronize(ev1_));
+    float ms = 0.0f;
+    UAII_HIP(hipEventElapsedTime(&ms, ev0_, ev1_));
+    KernelTiming& t = timing_[name];
+    t.total_ms += ms;
+    t.launches += 1;
+    t.bytes += bytes;
+    return Error::success();
+  };
+
+  UAII_TRY(timed("embed", 0.0, [&] { return launch_embed(tok_embd_.view, state_, x_, tap_hidden_, s); }));
+  int32_t pos_host = 0;
+  if (opts_.profile) {
+    UAII_HIP(hipMemcpy(&pos_host, &state_->pos, 4, hipMemcpyDeviceToHost));
+  }
+  for (int64_t li = 0; li < d.n_layers; ++li) {
+    const Layer& L = *layers_[(size_t)li];
+    const LayerSpec& ls = d.layers[(size_t)li];
+    uint8_t* kbase = static_cast<uint8_t*>(kv_) + (size_t)li * 2 * layer_kv;
+    uint8_t* vbase = kbase + layer_kv;
+
+    GemvArgs a{};
+    a.nseg = 3;
+    a.epi = EPI_QKV;
+    a.K = d.dim;
+    a.x = x_;
+    a.norm_w = L.attn_norm;
+    a.eps = d.rms_eps;
+    a.y = q_;
+    a.seg[0].w = L.wq.view; a.seg[0].rows = d.q_dim; a.seg[0].kind = 0; a.seg[0].bias = L.bq;
+    a.seg[1].w = L.wk.view; a.seg[1].rows = d.kv_dim; a.seg[1].kind = 1; a.seg[1].bias = L.bk;
+    a.seg[2].w = L.wv.view; a.seg[2].rows = d.kv_dim; a.seg[2].kind = 2; a.seg[2].bias = L.bv;
+    a.kcache = kbase;
+    a.vcache = vbase;
+    a.kv_f16 = opts_.kv_f16 ? 1 : 0;
+    a.max_seq = max_ctx_;
+    a.head_dim = (int)d.head_dim;
+    a.rope_mode = d.rope_mode;
+    a.rope = rope_;
+    a.state = state_;
+    const double qkv_bytes = gemv_bytes(L.wq.view) + gemv_bytes(L.wk.view) + gemv_bytes(L.wv.view);
+    UAII_TRY(timed("gemv_qkv", qkv_bytes, [&] { return launch_gemv(a, s); }));
+
+    AttnArgs at{};
+    at.q = q_;
+    at.kcache = kbase;
+    at.vcache = vbase;
+    at.kv_f16 = opts_.kv_f16 ? 1 : 0;
+    at.max_seq = max_ctx_;
+    at.n_heads = (int)d.n_heads;
+    at.n_kv = (int)d.n_kv_heads;
+    at.hd = (int)d.head_dim;
+    at.state = state_;
+    at.fixed_len = 0;
+    at.out = attn_;
+    at.part = attn_part_;
+    at.ticket = attn_ticket_;
+    at.splits = attn_splits_;
+    const double attn_bytes = 2.0 * (double)(pos_host + 1) * (double)d.kv_dim * (double)elem +
+                              8.0 * (double)d.q_dim;
+    UAII_TRY(timed("attention", attn_bytes, [&] { return launch_attention_decode(at, s); }));
+
+    GemvArgs o{};
+    o.nseg = 1;
+    o.epi = EPI_ADD;
+    o.K = d.q_dim;
+    o.x = attn_;
+    o.y = x_;
+    o.tap = tap_r1_ + li * d.dim;
+    o.seg[0].w = L.wo.view;
+    o.seg[0].rows = d.dim;
+    o.state = state_;
+    UAII_TRY(timed("gemv_o", gemv_bytes(L.wo.view), [&] { return launch_gemv(o, s); }));
+
+    if (ls.ffn == LayerSpec::kSwiGLU) {
+      GemvArgs g{};
+      g.nseg = 1;
+      g.epi = EPI_SWIGLU;
+      g.K = d.dim;
+      g.x = x_;
+      g.norm_w = L.ffn_norm;  // null when the layer has no ffn_norm (gguf.cpp:1055-1062)
+      g.eps = d.rms_eps;
+      g.y = h_;
+      g.seg[0].w = L.gate.view;
+      g.seg[0].w2 = L.up.view;
+      g.seg[0].rows = 2 * ls.inter;
+      g.state = state_;
+      UAII_TRY(timed("gemv_gate_up", gemv_bytes(L.gate.view) + gemv_bytes(L.up.view),
+                     [&] { return launch_gemv(g, s); }));
+      GemvArgs dn{};
+      dn.nseg = 1;
+      dn.epi = EPI_ADD;
+      dn.K = ls.inter;
+      dn.x = h_;
+      dn.y = x_;
+      dn.tap = tap_r2_ + li * d.dim;
+      dn.seg[0].w = L.down.view;
+      dn.seg[0].rows = d.dim;
+      dn.state = state_;
+      UAII_TRY(timed("gemv_down", gemv_bytes(L.down.view), [&] { return launch_gemv(dn, s); }));
+    } else {
+      UAII_HIP(hipMemcpyAsync(tap_r2_ + li * d.dim, x_, 4 * (size_t)d.dim, hipMemcpyDeviceToDevice, s));
+    }
+  }
+  if (want_logits) {
+    GemvArgs lm{};
+    lm.nseg = 1;
+    lm.epi = EPI_LOGITS;
+    lm.K = d.dim;
+    lm.x = x_;
+    lm.norm_w = out_norm_;
+    lm.eps = d.rms_eps;
+    lm.y = logits_;
+    lm.xtap = tap_normed_;
+    lm.seg[0].w = d.tied ? tok_embd_.view : output_.view;
+    lm.seg[0].rows = d.vocab;
+    lm.part_val = lm_part_val_;
+    lm.part_idx = lm_part_idx_;
+    lm.ticket = lm_ticket_;
+    lm.ids = ids_;
+    lm.state = state_;
+    UAII_TRY(timed("gemv_lm_head", gemv_bytes(lm.seg[0].w), [&] { return launch_gemv(lm, s); }));
+  } else {
+    UAII_TRY(timed("advance", 0.0, [&] { return launch_advance(state_, ids_, s); }));
+  }
+  return Error::success();
+}
+
+Error DecoderProgram::step(bool want_logits) {
+  if (!kv_) return Error::make(ErrorCode::InvalidArgument, "KvCache not configured");
+  if (opts_.profile || !opts_.use_graph) return encode_step(want_logits);
+  hipGraphExec_t& ex = graph_[want_logits ? 1 : 0];
+  if (!ex) {
+    hipGraph_t g = nullptr;
+    UAII_HIP(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal));
+    Error err = encode_step(want_logits);
+    hipError_t st = hipStreamEndCapture(stream_, &g);
+    UAII_TRY(err);
+    UAII_HIP(st);
+    st = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    UAII_HIP(st);
+  }
+  UAII_HIP(hipGraphLaunch(ex, stream_));
+  return Error::success();
+}
+
+Error DecoderProgram::read_tap(const std::string& name, std::vector<float>* out) {
+  const DecoderSpec& d = spec_;
+  const float* src = nullptr;
+  size_t n = 0;
+  if (name == "hidden") { src = tap_hidden_; n = (size_t)d.dim; }
+  else if (name == "normed") { src = tap_normed_; n = (size_t)d.dim; }
+  else if (name == "logits") { src = logits_; n = (size_t)d.vocab; }
+  else if (name == "probs") {
+    UAII_HIP(launch_softmax(logits_, probs_, d.vocab, stream_));
+    src = probs_;
+    n = (size_t)d.vocab;
+  } else if (name.rfind("blk.", 0) == 0) {
+    const size_t dot = name.find('.', 4);
+    if (dot == std::string::npos) return Error::make(ErrorCode::NotFound, "tensor not found: " + name);
+    const int64_t li = std::atoll(name.substr(4, dot - 4).c_str());
+    const std::string what = name.substr(dot + 1);
+    if (li < 0 || li >= d.n_layers) return Error::make(ErrorCode::NotFound, "tensor not found: " + name);
+    if (what == "resid1") src = tap_r1_ + li * d.dim;
+    else if (what == "resid2") src = tap_r2_ + li * d.dim;
+    else return Error::make(ErrorCode::NotFound, "tensor not found: " + name);
+    n = (size_t)d.dim;
+  } else {
+    return Error::make(ErrorCode::NotFound, "tensor not found: " + name);
+  }
+  out->resize(n);
+  UAII_HIP(hipStreamSynchronize(stream_));
+  UAII_HIP(hipMemcpy(out->data(), src, n * 4, hipMemcpyDeviceToHost));
+  return Error::success();
+}
+
+std::string DecoderProgram::profile_summary() const {
+  std::ostringstream os;
+  os << "{";
+  bool first = true;
+  for (const auto& kv : timing_) {
+    const KernelTiming& t = kv.second;
+    if (!first) os << ",";
+    first = false;
+    const double avg_us = t.launches ? 1000.0 * t.total_ms / (double)t.launches : 0.0;
+    const double gbs = t.total_ms > 0 ? t.bytes / (t.total_ms * 1e-3) / 1e9 : 0.0;
+    os << "\"" << kv.first << "\":{\"launches\":" << t.launches << ",\"total_ms\":" << t.total_ms
+       << ",\"avg_us\":" << avg_us << ",\"bytes\":" << t.bytes << ",\"gbps\":" << gbs << "}";
+  }
+  os << "}";
+  return os.str();
+}
+
+}  // namespace uaii

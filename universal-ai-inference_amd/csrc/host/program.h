@@ -1,0 +1,125 @@
+// program.h — the device-resident decoder program behind Session.
+//
+// Owns every device allocation of a session: split-layout weights (HBM resident
+// for the life of the session), the KV cache ([layer][kv_head][max_seq][hd], f16
+// or f32), activations, RoPE tables, the decode state and the step graphs. One
+// token step is a fixed kernel sequence whose dynamic inputs (position, token)
+// live in device memory, so the sequence is captured once into a hipGraph and
+// replayed per token; only the generated ids come back to the host.
+#pragma once
+
+#include "error.h"
+#include "gguf_file.h"
+
+#include "hip/uaii_hip_internal.h"
+
+#include <cstdint>
+#include <map>
+#include <memory>
+#include <string>
+#include <vector>
+
+namespace uaii {
+
+// A weight in the split device layout (see csrc/hip/repack.hip).
+struct DeviceWeight {
+  uaii_hip::DevWeight view{};
+  void* base = nullptr;
+  size_t bytes = 0;
+  DeviceWeight() = default;
+  DeviceWeight(const DeviceWeight&) = delete;
+  DeviceWeight& operator=(const DeviceWeight&) = delete;
+  ~DeviceWeight();
+};
+
+// Upload `rows` GGUF rows of `cols` values and re-lay them out on the device.
+Error upload_weight(int type, const uint8_t* host, int64_t rows, int64_t cols, hipStream_t s,
+                    DeviceWeight* out);
+
+struct ProgramOptions {
+  bool kv_f16 = false;        // KV cache storage dtype
+  bool use_graph = true;      // replay the captured step graph
+  bool profile = false;       // per-kernel HIP event timing (direct launches)
+  int64_t max_context = 0;    // 0: GGUF context_length
+};
+
+struct KernelTiming {
+  double total_ms = 0.0;
+  int64_t launches = 0;
+  double bytes = 0.0;  // algorithmic bytes per launch summed
+};
+
+class DecoderProgram {
+ public:
+  DecoderProgram() = default;
+  ~DecoderProgram();
+  DecoderProgram(const DecoderProgram&) = delete;
+  DecoderProgram& operator=(const DecoderProgram&) = delete;
+
+  Error build(const DecoderSpec& spec, const ProgramOptions& opts);
+  const DecoderSpec& spec() const { return spec_; }
+  int64_t max_context() const { return max_ctx_; }
+
+  // Size KV and the token buffer for `max_seq` positions (re-captures graphs on growth).
+  Error ensure_capacity(int64_t max_seq);
+  // Reset to position 0 with the given prompt (ids copied to the device).
+  Error begin(const int64_t* prompt, int64_t n_prompt);
+  // Enqueue one token step at the current position.
+  Error step(bool want_logits);
+  Error synchronize();
+  // Copy ids[0..n) (prompt + generated) to the host.
+  Error read_ids(int64_t* out, int64_t n);
+  Error read_state(uaii_hip::StepState* st);
+  // Overwrite the token fed at the current position.
+  Error set_token(int64_t token);
+  Error read_tap(const std::string& name, std::vector<float>* out);
+  std::string profile_summary() const;
+  const std::map<std::string, KernelTiming>& timings() const { return timing_; }
+  void reset_timings() { timing_.clear(); }
+  hipStream_t stream() const { return stream_; }
+
+ private:
+  struct Layer {
+    DeviceWeight wq, wk, wv, wo, gate, up, down, gate_inp, gate_exps, up_exps, down_exps;
+    float *attn_norm = nullptr, *ffn_norm = nullptr, *bq = nullptr, *bk = nullptr, *bv = nullptr;
+  };
+
+  Error upload_f32(const GgufTensor* t, float** out);
+  Error encode_step(bool want_logits);
+  void free_dynamic();
+
+  DecoderSpec spec_;
+  ProgramOptions opts_;
+  hipStream_t stream_ = nullptr;
+  std::vector<std::unique_ptr<Layer>> layers_;
+  DeviceWeight tok_embd_, output_;
+  float* out_norm_ = nullptr;
+  std::vector<void*> allocs_;  // owned static allocations (norms, biases, activations)
+
+  // activations
+  float *x_ = nullptr, *q_ = nullptr, *attn_ = nullptr, *h_ = nullptr, *logits_ = nullptr,
+        *probs_ = nullptr, *tap_hidden_ = nullptr, *tap_r1_ = nullptr, *tap_r2_ = nullptr,
+        *tap_normed_ = nullptr, *moe_logits_ = nullptr, *moe_w_ = nullptr;
+  int32_t* moe_ids_ = nullptr;
+  float* lm_part_val_ = nullptr;
+  int32_t* lm_part_idx_ = nullptr;
+  uint32_t* lm_ticket_ = nullptr;
+  uaii_hip::StepState* state_ = nullptr;
+
+  // sized by ensure_capacity
+  int64_t max_ctx_ = 0;
+  void* kv_ = nullptr;
+  size_t kv_bytes_ = 0;
+  int32_t* ids_ = nullptr;
+  float2* rope_ = nullptr;
+  float* attn_part_ = nullptr;
+  uint32_t* attn_ticket_ = nullptr;
+  int attn_splits_ = 1;
+
+  hipGraphExec_t graph_[2] = {nullptr, nullptr};
+  std::map<std::string, KernelTiming> timing_;
+  hipEvent_t ev0_ = nullptr, ev1_ = nullptr;
+  int64_t ffn_max_ = 0;
+};
+
+}  // namespace uaii

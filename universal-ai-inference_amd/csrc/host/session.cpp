@@ -1,0 +1,138 @@
+// session.cpp — see session.h.
+#include "session.h"
+
+#include <algorithm>
+
+namespace uaii {
+namespace runtime {
+
+Error Session::create(const std::string& gguf_path, SessionOptions options) {
+  options_ = std::move(options);
+  ready_ = false;
+  if (options_.backend_name != "rocm") {
+    return Error::make(ErrorCode::NotImplemented,
+                       "backend '" + options_.backend_name +
+                           "' is not provided by this library (it implements 'rocm')");
+  }
+  if (!options_.keep_quantized_weights) {
+    return Error::make(ErrorCode::NotImplemented,
+                       "keep_quantized_weights=0 is not supported: device weights stay block-packed");
+  }
+  if (options_.enable_streaming) {
+    return Error::make(ErrorCode::NotImplemented,
+                       "weight streaming is not supported: the model is HBM resident");
+  }
+  std::string path = gguf_path;
+  if (!options_.weights_dir.empty() && !path.empty() && path[0] != '/')
+    path = options_.weights_dir + "/" + path;
+  UAII_TRY(file_.open(path));
+  UAII_TRY(derive_decoder(file_, &spec_));
+  ProgramOptions po;
+  po.kv_f16 = options_.kv_f16;
+  po.use_graph = options_.use_graph;
+  po.profile = options_.enable_profiler;
+  po.max_context = options_.max_context;
+  program_ = std::make_unique<DecoderProgram>();
+  UAII_TRY(program_->build(spec_, po));
+  ready_ = true;
+  return Error::success();
+}
+
+// max_context option, else GGUF context_length (session.cpp:936-946).
+int64_t Session::resolve_max_context() const {
+  if (options_.max_context > 0) return options_.max_context;
+  return spec_.ctx_len;
+}
+
+Error Session::generate(const std::vector<int64_t>& prompt, int64_t max_new,
+                        std::vector<int64_t>* out, const std::vector<int64_t>& stop_ids,
+                        const OnNewToken& on_new_token, const SampleParams& sample) {
+  if (!ready_) return Error::make(ErrorCode::InvalidArgument, "session not ready");
+  if (out == nullptr) return Error::make(ErrorCode::InvalidArgument, "out_tokens null");
+  if (prompt.empty()) return Error::make(ErrorCode::InvalidArgument, "prompt_tokens empty");
+  if (max_new < 0) return Error::make(ErrorCode::InvalidArgument, "max_new_tokens < 0");
+  if (!sample.greedy())
+    return Error::make(ErrorCode::NotImplemented, "only greedy sampling runs on the device");
+  const int64_t max_ctx = resolve_max_context();
+  const int64_t n_prompt = (int64_t)prompt.size();
+  const int64_t total = n_prompt + max_new;
+  if (max_ctx > 0) {
+    if (n_prompt > max_ctx)
+      return Error::make(ErrorCode::InvalidArgument,
+                         "prompt length exceeds max_context (" + std::to_string(n_prompt) + " > " +
+                             std::to_string(max_ctx) + ")");
+    if (total > max_ctx)
+      return Error::make(ErrorCode::InvalidArgument,
+                         "prompt+max_new_tokens exceeds max_context (" + std::to_string(total) +
+                             " > " + std::to_string(max_ctx) + ")");
+  }
+  const int64_t kv_max =
+      max_ctx > 0 ? max_ctx : std::max<int64_t>(total, n_prompt + std::max<int64_t>(max_new, 1));
+  DecoderProgram& p = *program_;
+  UAII_TRY(p.ensure_capacity(kv_max));
+  UAII_TRY(p.begin(prompt.data(), n_prompt));
+  run_started_ = true;
+
+  out->clear();
+  // Prefill: one step per prompt token; logits only needed after the last one.
+  for (int64_t i = 0; i < n_prompt; ++i) UAII_TRY(p.step(i == n_prompt - 1));
+  const bool per_token = (bool)on_new_token || !stop_ids.empty();
+  auto is_stop = [&](int64_t t) { return std::find(stop_ids.begin(), stop_ids.end(), t) != stop_ids.end(); };
+  if (!per_token) {
+    // Whole decode on the device: every step's argmax feeds the next step.
+    for (int64_t t = 0; t + 1 < max_new; ++t) UAII_TRY(p.step(true));
+    out->resize((size_t)total);
+    UAII_TRY(p.read_ids(out->data(), total));
+    return Error::success();
+  }
+  out->assign(prompt.begin(), prompt.end());
+  for (int64_t t = 0; t < max_new; ++t) {
+    std::vector<int64_t> ids((size_t)(n_prompt + t + 1));
+    UAII_TRY(p.read_ids(ids.data(), n_prompt + t + 1));
+    const int64_t next = ids.back();
+    out->push_back(next);
+    if (on_new_token && !on_new_token(next)) return Error::success();
+    if (is_stop(next)) return Error::success();
+    if (t + 1 >= max_new) break;
+    UAII_TRY(p.step(true));
+  }
+  return Error::success();
+}
+
+Error Session::set_tensor_f32(const std::string& name, const std::vector<float>& values) {
+  if (!ready_) return Error::make(ErrorCode::InvalidArgument, "session not ready");
+  if (name != "tokens")
+    return Error::make(ErrorCode::NotFound, "settable tensor is 'tokens' only: " + name);
+  if (values.empty()) return Error::make(ErrorCode::InvalidArgument, "tokens buffer empty");
+  // seq=1 graphs take the last id (session.cpp:858-873)
+  pending_token_ = (int64_t)values.back();
+  if (run_started_) return program_->set_token(pending_token_);
+  return Error::success();
+}
+
+Error Session::run() {
+  if (!ready_) return Error::make(ErrorCode::InvalidArgument, "session not ready");
+  DecoderProgram& p = *program_;
+  if (!run_started_) {
+    const int64_t max_ctx = resolve_max_context();
+    UAII_TRY(p.ensure_capacity(max_ctx > 0 ? max_ctx : 4096));
+    const int64_t tok = pending_token_;
+    UAII_TRY(p.begin(&tok, 1));
+    run_started_ = true;
+  }
+  uaii_hip::StepState st{};
+  UAII_TRY(p.read_state(&st));
+  if (st.pos >= p.max_context())
+    return Error::make(ErrorCode::InvalidArgument, "KvCache capacity exceeded");
+  UAII_TRY(p.step(true));
+  return p.synchronize();
+}
+
+Error Session::get_tensor_f32(const std::string& name, std::vector<float>* values) {
+  if (!ready_) return Error::make(ErrorCode::InvalidArgument, "session not ready");
+  if (values == nullptr) return Error::make(ErrorCode::InvalidArgument, "values null");
+  return program_->read_tap(name, values);
+}
+
+}  // namespace runtime
+}  // namespace uaii

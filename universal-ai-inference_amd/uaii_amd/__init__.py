@@ -1,0 +1,257 @@
+"""ctypes bindings of libuaii_amd.so (the MI355X GGUF token loop) and the
+synthetic GGUF writer.
+
+The C ABI is the product boundary (include/uaii/c_api/uaii.h and
+include/uaii_hip.h); these bindings exist for tests, the smoke check and the
+benchmark. Loading fails loudly when the built library is missing: there is no
+CPU fallback.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from pathlib import Path
+
+PKG_DIR = Path(__file__).resolve().parent.parent
+LIB_DIR = PKG_DIR / "lib"
+LIB_PATH = LIB_DIR / "libuaii_amd.so"
+SYNTH_PATH = LIB_DIR / "libuaii_synth.so"
+
+# GGUF tensor type ids (reference include/uaii/loaders/gguf.hpp:18-36)
+F32, F16, Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K = 0, 1, 2, 3, 6, 7, 8, 10, 11, 12, 13, 14
+TYPE_NAMES = {F32: "f32", F16: "f16", Q4_0: "q4_0", Q4_1: "q4_1", Q5_0: "q5_0", Q5_1: "q5_1",
+              Q8_0: "q8_0", Q2_K: "q2_k", Q3_K: "q3_k", Q4_K: "q4_k", Q5_K: "q5_k", Q6_K: "q6_k"}
+BLOCK = {F32: (1, 4), F16: (1, 2), Q4_0: (32, 18), Q4_1: (32, 20), Q5_0: (32, 22), Q5_1: (32, 24),
+         Q8_0: (32, 34), Q2_K: (256, 84), Q3_K: (256, 110), Q4_K: (256, 144), Q5_K: (256, 176),
+         Q6_K: (256, 210)}
+
+
+def row_bytes(t: int, cols: int) -> int:
+    be, bb = BLOCK[t]
+    return cols // be * bb
+
+
+class UaiiError(RuntimeError):
+    pass
+
+
+class SessionOptions(C.Structure):
+    """uaii_session_options (identical layout to the reference's C API 0.3.0)."""
+    _fields_ = [
+        ("struct_size", C.c_uint32),
+        ("backend", C.c_char_p),
+        ("weights_dir", C.c_char_p),
+        ("weight_init", C.c_int),
+        ("enable_fusion", C.c_int),
+        ("enable_memory_reuse", C.c_int),
+        ("enable_profiler", C.c_int),
+        ("profile_trace_path", C.c_char_p),
+        ("budget_bytes", C.c_uint64),
+        ("enable_streaming", C.c_int),
+        ("allow_missing_weights", C.c_int),
+        ("weights_sandbox", C.c_char_p),
+        ("compute_dtype", C.c_int),
+        ("keep_quantized_weights", C.c_int),
+        ("max_context", C.c_int64),
+    ]
+
+
+_lib = None
+
+
+def lib() -> C.CDLL:
+    """Load libuaii_amd.so (raises if it was not built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise UaiiError(f"{LIB_PATH} is missing: run __graft_entry__.build() first")
+    L = C.CDLL(str(LIB_PATH))
+    vp, i64, i32, f32p = C.c_void_p, C.c_int64, C.c_int32, C.POINTER(C.c_float)
+    sig = {
+        "uaii_session_options_init": (None, [C.POINTER(SessionOptions)]),
+        "uaii_status_name": (C.c_char_p, [C.c_int]),
+        "uaii_last_error": (C.c_char_p, []),
+        "uaii_get_c_api_version_string": (C.c_char_p, []),
+        "uaii_get_version_string": (C.c_char_p, []),
+        "uaii_session_create": (C.c_int, [C.c_char_p, C.POINTER(SessionOptions), C.POINTER(vp)]),
+        "uaii_session_destroy": (None, [vp]),
+        "uaii_session_run": (C.c_int, [vp]),
+        "uaii_session_set_f32": (C.c_int, [vp, C.c_char_p, f32p, C.c_size_t]),
+        "uaii_session_get_f32": (C.c_int, [vp, C.c_char_p, f32p, C.c_size_t, C.POINTER(C.c_size_t)]),
+        "uaii_session_generate": (C.c_int, [vp, C.POINTER(i64), C.c_size_t, i64, C.POINTER(i64),
+                                            C.c_size_t, C.POINTER(C.c_size_t)]),
+        "uaii_session_profile_summary": (C.c_int, [vp, C.c_char_p, C.c_size_t]),
+        "uaii_hip_init": (C.c_int, [C.c_int]),
+        "uaii_hip_device_count": (C.c_int, [C.POINTER(C.c_int)]),
+        "uaii_hip_error_string": (C.c_char_p, [C.c_int]),
+        "uaii_hip_malloc": (C.c_int, [C.POINTER(vp), C.c_size_t]),
+        "uaii_hip_free": (C.c_int, [vp]),
+        "uaii_hip_memcpy_h2d": (C.c_int, [vp, vp, C.c_size_t]),
+        "uaii_hip_memcpy_d2h": (C.c_int, [vp, vp, C.c_size_t]),
+        "uaii_hip_memset": (C.c_int, [vp, C.c_int, C.c_size_t]),
+        "uaii_hip_synchronize": (C.c_int, []),
+        "uaii_hip_weight_create": (C.c_int, [C.c_int, vp, i64, i64, C.POINTER(vp)]),
+        "uaii_hip_weight_destroy": (C.c_int, [vp]),
+        "uaii_hip_weight_bytes": (i64, [vp]),
+        "uaii_hip_dequant_rows": (C.c_int, [vp, i64, i64, vp, vp]),
+        "uaii_hip_gemv": (C.c_int, [vp, vp, vp, vp]),
+        "uaii_hip_gemv_rmsnorm": (C.c_int, [vp, vp, vp, C.c_float, vp, vp]),
+        "uaii_hip_gemm": (C.c_int, [vp, vp, i64, vp, vp]),
+        "uaii_hip_rmsnorm": (C.c_int, [vp, vp, vp, i64, i64, C.c_float, vp]),
+        "uaii_hip_softmax": (C.c_int, [vp, vp, i64, vp]),
+        "uaii_hip_argmax": (C.c_int, [vp, i64, vp, vp]),
+        "uaii_hip_rope_table": (C.c_int, [C.c_float, C.c_int, i64, vp]),
+        "uaii_hip_rope": (C.c_int, [vp, i64, i64, C.c_int, C.c_int, vp, vp, vp]),
+        "uaii_hip_attention_decode": (C.c_int, [vp, vp, vp, C.c_int, i64, C.c_int, C.c_int, C.c_int,
+                                                i64, vp, vp]),
+        "uaii_hip_time_gemv": (C.c_int, [vp, vp, vp, C.c_int, f32p]),
+        "uaii_hip_time_gemm": (C.c_int, [vp, vp, i64, vp, C.c_int, f32p]),
+        "uaii_hip_time_copy": (C.c_int, [vp, vp, C.c_size_t, C.c_int, f32p]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = L
+    return L
+
+
+def check_hip(rc: int, what: str = "") -> None:
+    if rc != 0:
+        msg = lib().uaii_hip_error_string(rc).decode()
+        raise UaiiError(f"{what}: HIP layer error {rc} ({msg})")
+
+
+class DeviceBuffer:
+    """A device allocation owned from Python (numpy <-> device copies)."""
+
+    def __init__(self, nbytes: int):
+        self.nbytes = int(nbytes)
+        self.ptr = C.c_void_p()
+        check_hip(lib().uaii_hip_malloc(C.byref(self.ptr), max(self.nbytes, 4)), "malloc")
+
+    @classmethod
+    def from_array(cls, arr):
+        import numpy as np
+        a = np.ascontiguousarray(arr)
+        buf = cls(a.nbytes)
+        check_hip(lib().uaii_hip_memcpy_h2d(buf.ptr, a.ctypes.data_as(C.c_void_p), a.nbytes), "h2d")
+        return buf
+
+    def to_array(self, dtype, count):
+        import numpy as np
+        out = np.empty(count, dtype=dtype)
+        check_hip(lib().uaii_hip_memcpy_d2h(out.ctypes.data_as(C.c_void_p), self.ptr, out.nbytes), "d2h")
+        return out
+
+    def zero(self):
+        check_hip(lib().uaii_hip_memset(self.ptr, 0, self.nbytes), "memset")
+
+    def free(self):
+        if self.ptr:
+            lib().uaii_hip_free(self.ptr)
+            self.ptr = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class DeviceWeight:
+    """GGUF rows uploaded to the device split layout (uaii_hip_weight_create)."""
+
+    def __init__(self, gguf_type: int, packed, rows: int, cols: int):
+        import numpy as np
+        p = np.ascontiguousarray(packed, dtype=np.uint8)
+        if p.nbytes != rows * row_bytes(gguf_type, cols):
+            raise UaiiError("packed size does not match rows x cols")
+        self.type, self.rows, self.cols = gguf_type, rows, cols
+        self.h = C.c_void_p()
+        check_hip(lib().uaii_hip_weight_create(gguf_type, p.ctypes.data_as(C.c_void_p), rows, cols,
+                                               C.byref(self.h)), "weight_create")
+
+    def free(self):
+        if self.h:
+            lib().uaii_hip_weight_destroy(self.h)
+            self.h = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class Session:
+    """uaii_session_* through the C ABI."""
+
+    def __init__(self, path: str, *, kv_f16: bool = False, max_context: int = 0,
+                 profile: bool = False, backend: str = "rocm"):
+        L = lib()
+        opts = SessionOptions()
+        L.uaii_session_options_init(C.byref(opts))
+        self._backend = backend.encode()
+        opts.backend = self._backend
+        opts.compute_dtype = 1 if kv_f16 else 0
+        opts.max_context = max_context
+        opts.enable_profiler = 1 if profile else 0
+        self.h = C.c_void_p()
+        rc = L.uaii_session_create(str(path).encode(), C.byref(opts), C.byref(self.h))
+        if rc != 0:
+            raise UaiiError(f"uaii_session_create: {L.uaii_status_name(rc).decode()}: "
+                            f"{L.uaii_last_error().decode()}")
+
+    def generate(self, prompt, max_new: int):
+        import numpy as np
+        L = lib()
+        p = np.ascontiguousarray(prompt, dtype=np.int64)
+        cap = len(p) + max(max_new, 0)
+        out = np.zeros(max(cap, 1), dtype=np.int64)
+        n = C.c_size_t()
+        rc = L.uaii_session_generate(self.h, p.ctypes.data_as(C.POINTER(C.c_int64)), len(p), max_new,
+                                     out.ctypes.data_as(C.POINTER(C.c_int64)), cap, C.byref(n))
+        if rc != 0:
+            raise UaiiError(f"uaii_session_generate: {L.uaii_status_name(rc).decode()}: "
+                            f"{L.uaii_last_error().decode()}")
+        return out[: n.value]
+
+    def get(self, name: str):
+        import numpy as np
+        L = lib()
+        n = C.c_size_t()
+        rc = L.uaii_session_get_f32(self.h, name.encode(), None, 0, C.byref(n))
+        if rc != 0:
+            raise UaiiError(f"get_f32({name}): {L.uaii_last_error().decode()}")
+        out = np.zeros(n.value, dtype=np.float32)
+        rc = L.uaii_session_get_f32(self.h, name.encode(), out.ctypes.data_as(C.POINTER(C.c_float)),
+                                    n.value, C.byref(n))
+        if rc != 0:
+            raise UaiiError(f"get_f32({name}): {L.uaii_last_error().decode()}")
+        return out
+
+    def profile_summary(self) -> str:
+        buf = C.create_string_buffer(1 << 16)
+        rc = lib().uaii_session_profile_summary(self.h, buf, len(buf))
+        if rc != 0:
+            raise UaiiError("profile_summary failed")
+        return buf.value.decode()
+
+    def close(self):
+        if self.h:
+            lib().uaii_session_destroy(self.h)
+            self.h = C.c_void_p()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
