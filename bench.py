@@ -1,0 +1,198 @@
+#!/usr/bin/env python3
+"""Decode throughput of the GGUF token loop on one MI355X.
+
+Workload: Llama-3-8B-shape decoder, Q4_0 weights, fp16 KV
+cache, bs=1. A seeded random prompt fills the context to 3840 tokens, then the
+timed region is K greedy decode steps ending at ctx 4096 (one step = one token
+through all 32 layers + LM head + argmax, replayed from the captured hipGraph).
+
+Also reported: token-by-token prefill rate, per-kernel device time from HIP
+events on the session stream (a profiled replay of the same decode window right
+after the timed region), the dominant kernel's HBM roofline fraction, a
+device-to-device copy rate, and the reference's CPU path timed on a bounded
+window (reference kernels built from the reference sources, oracle/_ref).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "universal-ai-inference_amd"))
+
+METRIC = "decode tok/s bs1 Llama-3-8B-shape Q4_0 @ctx4096; GEMV+attn HBM GB/s % peak"
+HBM_PEAK_GBS = 8000.0
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def cpu_baseline(path: str, start_pos: int, n_steps: int, threads: int):
+    """Reference CPU path on a bounded decode window (rank 0, N=1)."""
+    sys.path.insert(0, str(ROOT))
+    import oracle  # checker / baseline only
+    import ctypes as C
+    os.environ["UAII_NUM_THREADS"] = str(threads)  # reference thread_pool.cpp:13-22
+    R = oracle.ref()
+    if R is not None:
+        R.uref_time_decode_window.restype = C.c_double
+        R.uref_time_decode_window.argtypes = [C.c_char_p, C.c_int64, C.c_int64]
+        secs = R.uref_time_decode_window(path.encode(), start_pos, n_steps)
+        kind = "reference"
+    else:
+        secs = oracle.Model(path).time_decode_window(start_pos, n_steps, threads)
+        kind = "port"
+    if secs <= 0:
+        raise RuntimeError("cpu baseline failed")
+    return {"value": n_steps / secs, "unit": "tok/s", "cores": threads, "kind": kind,
+            "sample": f"{n_steps} decode steps at ctx {start_pos}..{start_pos + n_steps} "
+                      f"(KV filled with deterministic values), {secs:.1f} s wall"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=240)
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--config", default="8b")
+    ap.add_argument("--ctx", type=int, default=4096)
+    ap.add_argument("--profile-steps", type=int, default=32)
+    ap.add_argument("--cpu-steps", type=int, default=3)
+    ap.add_argument("--cpu-threads", type=int, default=16)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-profile", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); "
+              "the path has no multi-GPU mode", file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import uaii_amd
+    from uaii_amd import synth
+
+    cfg = synth.PRESETS[args.config]
+    ctx = min(args.ctx, cfg.ctx_len)
+    K, W = args.steps, args.warmup
+    n_prompt = ctx - K - W
+    if n_prompt < 1:
+        raise SystemExit("steps + warmup must be below the context length")
+
+    t = time.time()
+    path = synth.cached_model(cfg, nthreads=16)
+    log(f"model {path} ready in {time.time() - t:.1f}s")
+
+    # device copy rate (HBM read+write) for context
+    L = uaii_amd.lib()
+    uaii_amd.check_hip(L.uaii_hip_init(0), "init")
+    nb = 1 << 30
+    src, dst = uaii_amd.DeviceBuffer(nb), uaii_amd.DeviceBuffer(nb)
+    ms = __import__("ctypes").c_float()
+    uaii_amd.check_hip(L.uaii_hip_time_copy(src.ptr, dst.ptr, nb, 10, __import__("ctypes").byref(ms)))
+    copy_gbs = 2 * nb / (ms.value * 1e-3) / 1e9
+    src.free(), dst.free()
+    log(f"d2d copy {copy_gbs:.0f} GB/s (read+write)")
+
+    t = time.time()
+    sess = uaii_amd.Session(path, kv_f16=True, max_context=ctx)
+    log(f"session created in {time.time() - t:.1f}s")
+    prompt = np.random.default_rng(cfg.seed + 1).integers(0, cfg.vocab, n_prompt)
+
+    # prefill: one step per prompt token (the reference's method), untimed for `value`
+    sess.begin(prompt, ctx)
+    sess.sync()
+    t0 = time.perf_counter()
+    for i in range(n_prompt):
+        sess.step_async(i == n_prompt - 1)
+    sess.sync()
+    prefill_s = time.perf_counter() - t0
+    log(f"prefill {n_prompt} tokens in {prefill_s:.2f}s ({n_prompt / prefill_s:.0f} tok/s)")
+
+    for _ in range(W):
+        sess.step_async(True)
+    sess.sync()
+
+    # timed region: K decode steps (graph replays), synchronised on both sides
+    uaii_amd.check_hip(L.uaii_hip_synchronize())
+    t0 = time.perf_counter()
+    for _ in range(K):
+        sess.step_async(True)
+    sess.sync()
+    uaii_amd.check_hip(L.uaii_hip_synchronize())
+    dt = time.perf_counter() - t0
+    tok_s = K / dt
+    log(f"decode {K} steps in {dt:.3f}s -> {tok_s:.1f} tok/s ({1e3 * dt / K:.3f} ms/step)")
+    ids = sess.read_ids(ctx)
+    best, second = sess.last_margin()
+
+    kernels = {}
+    roofline = None
+    if not args.no_profile:
+        P = min(args.profile_steps, K)
+        sess.seek(n_prompt + W)
+        sess.set_profiling(True)
+        for _ in range(P):
+            sess.step_async(True)
+        sess.sync()
+        kernels = json.loads(sess.profile_summary())
+        sess.set_profiling(False)
+        ids2 = sess.read_ids(n_prompt + W + P + 1)
+        replay_ok = bool(np.array_equal(ids2, ids[: n_prompt + W + P + 1]))
+        log(f"profiled replay of {P} steps reproduces the ids: {replay_ok}")
+        # dominant kernel by device time
+        dom = max(kernels, key=lambda k: kernels[k]["total_ms"])
+        k = kernels[dom]
+        achieved = k["bytes"] / (k["total_ms"] * 1e-3) / 1e9
+        gemv_attn = [v for n, v in kernels.items() if n.startswith("gemv") or n == "attention"]
+        agg_b = sum(v["bytes"] for v in gemv_attn)
+        agg_ms = sum(v["total_ms"] for v in gemv_attn)
+        step_ms = sum(v["total_ms"] for v in kernels.values()) / P
+        roofline = {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1),
+                    "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                    "traffic": None,
+                    "bytes_per_launch": k["bytes"] / k["launches"],
+                    "avg_launch_us": round(k["avg_us"], 2),
+                    "gemv_attn_achieved": round(agg_b / (agg_ms * 1e-3) / 1e9, 1),
+                    "gemv_attn_frac": round(agg_b / (agg_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                    "kernel_ms_per_step": round(step_ms, 4),
+                    "profiled_steps": P, "profiled_replay_ids_match": replay_ok}
+    sess.close()
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        try:
+            cpu = cpu_baseline(path, n_prompt + W + K // 2, args.cpu_steps, args.cpu_threads)
+            log(f"cpu baseline {cpu}")
+        except Exception as e:  # the GPU figure stands on its own
+            log(f"cpu baseline unavailable: {e}")
+
+    out = {
+        "metric": METRIC, "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": K,
+        "warmup": W, "ms_per_step": round(1e3 * dt / K, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (seeded N(0,0.02) weights quantized to GGUF blocks, random prompt ids)",
+        "config": {"workload": f"{args.config} decode bs1, prompt {n_prompt} + {W} warmup, "
+                               f"timed ctx {n_prompt + W}->{n_prompt + W + K}",
+                   "weights": uaii_amd.TYPE_NAMES[cfg.type_default], "kv_cache": "f16",
+                   "n_layers": cfg.n_layers, "dim": cfg.dim, "heads": f"{cfg.n_heads}/{cfg.n_kv_heads}",
+                   "ffn": cfg.ffn, "vocab": cfg.vocab},
+        "prefill_tok_s": round(n_prompt / prefill_s, 1),
+        "copy_gbps": round(copy_gbs, 1),
+        "argmax_margin_last": round(best - second, 6),
+        "roofline": roofline,
+        "kernels": {n: {"avg_us": round(v["avg_us"], 2), "gbps": round(v["gbps"], 1),
+                        "launches_per_step": v["launches"] / max(1, args.profile_steps)}
+                    for n, v in kernels.items()},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

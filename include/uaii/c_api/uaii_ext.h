@@ -1,0 +1,52 @@
+/*
+ * uaii_ext.h — token-loop extensions of libuaii_amd.so beyond the reference ABI.
+ *
+ * No counterpart in the reference C API: these entry points expose the device
+ * token loop step by step for streaming callers and for measurement (the
+ * reference's uaii_session_run is synchronous and uaii_session_generate runs the
+ * whole loop). They operate on the same session as uaii.h.
+ */
+#ifndef UAII_C_API_UAII_EXT_H_
+#define UAII_C_API_UAII_EXT_H_
+
+#include "uaii/c_api/uaii.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/** Reset the session to position 0 with `prompt_n` prompt ids on the device
+ * (KV capacity sized for `capacity` positions, 0 = max_context). */
+UAII_CAPI_API uaii_status uaii_session_begin(uaii_session* session, const int64_t* prompt_tokens,
+                                             size_t prompt_n, int64_t capacity);
+
+/** Enqueue one token step at the current position without waiting. With
+ * want_logits the step also runs the LM head and greedy argmax; without it the
+ * next prompt token is fed (valid only inside the prompt). */
+UAII_CAPI_API uaii_status uaii_session_step_async(uaii_session* session, int want_logits);
+
+/** Wait for all enqueued steps. */
+UAII_CAPI_API uaii_status uaii_session_sync(uaii_session* session);
+
+/** Current position (tokens processed so far). */
+UAII_CAPI_API uaii_status uaii_session_position(uaii_session* session, int64_t* pos);
+
+/** Copy ids[0..n) (prompt followed by generated ids) to `out`. */
+UAII_CAPI_API uaii_status uaii_session_read_ids(uaii_session* session, int64_t* out, size_t n);
+
+/** Move back to position `pos` (0 < pos <= current): ids and KV entries below
+ * `pos` are kept, the token at `pos` is fed next. */
+UAII_CAPI_API uaii_status uaii_session_seek(uaii_session* session, int64_t pos);
+
+/** Per-kernel HIP event timing on (direct launches) or off (graph replay). */
+UAII_CAPI_API uaii_status uaii_session_set_profiling(uaii_session* session, int on);
+
+/** Greedy argmax margin of the last step: (best logit, runner-up logit). */
+UAII_CAPI_API uaii_status uaii_session_last_margin(uaii_session* session, float* best,
+                                                   float* second);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* UAII_C_API_UAII_EXT_H_ */

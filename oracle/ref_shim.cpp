@@ -22,6 +22,7 @@ extern "C" {
 #include "uaii_oracle.h"
 }
 
+#include <chrono>
 #include <cstring>
 #include <memory>
 #include <random>
@@ -250,28 +251,41 @@ Error matmul(const TensorView& x, const Weight& w, TensorView* y) {
   return kernels::matmul_f32(x, w.view, y, false, true);
 }
 
-}  // namespace
+// One GGUF decoder driven through the reference kernels: weights bound Path B
+// (Path A for MoE, whose experts only work on f32, transformer.cpp:551-554), a
+// reference KvCache, and run() = one Session::run() over the graph order of
+// gguf.cpp:935-1209.
+struct RefRunner {
+  orc_model* m = nullptr;
+  std::int64_t L = 0, D = 0, H = 0, HKV = 0, hd = 0, V = 0, E = 0, topk = 0, rope_mode = 0,
+               ctx = 0, qd = 0, kvd = 0, ff = 1;
+  float theta = 0.f, eps = 0.f;
+  bool path_a = false;
+  Weight emb, onorm, lm;
+  std::vector<Weight> W;
+  runtime::KvCache kv;
+  std::unique_ptr<Owned> tokens, x, n1, res1, q, k, v, qb, kb, vb, qr, kr, att, ao, n2, g, u, ga,
+      hid, fo, res2, normed, logits, probs, mp, mt, fi, fin;
 
-// Greedy generate through the reference kernels. taps_logits (vocab floats) and
-// taps_resid2 (n_layers*dim floats) receive the last run()'s values when non-NULL.
-int uref_generate(const char* path, int max_layers, const std::int64_t* prompt,
-                  std::int64_t n_prompt, std::int64_t max_new, std::int64_t* out,
-                  std::int64_t* out_n, float* taps_logits, float* taps_resid2) {
-  orc_model* m = orc_model_open(path, max_layers);
-  if (!m) { g_err = orc_last_error(); return -1; }
-  std::int64_t hp[12];
-  float fp[2];
-  orc_model_hparams(m, hp);
-  orc_model_fparams(m, fp);
-  const std::int64_t L = hp[0], D = hp[1], H = hp[2], HKV = hp[3], hd = hp[4], V = hp[5];
-  const std::int64_t E = hp[7], topk = hp[8], rope_mode = hp[9], ctx = hp[10];
-  const float theta = fp[0], eps = fp[1];
-  const bool path_a = E > 0;
-  const std::int64_t qd = H * hd, kvd = HKV * hd;
-  int rc = -1;
-  {
-    Weight emb, onorm, lm;
-    std::vector<Weight> W(static_cast<std::size_t>(L * 16));
+  ~RefRunner() {
+    kernels::set_active_kv_cache(nullptr);
+    if (m) orc_model_close(m);
+  }
+
+  Error open(const char* path, int max_layers, std::int64_t kv_max_override,
+             std::int64_t total_hint, std::int64_t n_prompt) {
+    m = orc_model_open(path, max_layers);
+    if (!m) return Error::make(ErrorCode::NotFound, orc_last_error());
+    std::int64_t hp[12];
+    float fp[2];
+    orc_model_hparams(m, hp);
+    orc_model_fparams(m, fp);
+    L = hp[0]; D = hp[1]; H = hp[2]; HKV = hp[3]; hd = hp[4]; V = hp[5];
+    E = hp[7]; topk = hp[8]; rope_mode = hp[9]; ctx = hp[10];
+    theta = fp[0]; eps = fp[1];
+    path_a = E > 0;
+    qd = H * hd; kvd = HKV * hd;
+    W.resize(static_cast<std::size_t>(L * 16));
     bind_weight(m, "token_embd.weight", false, path_a, &emb);
     bind_weight(m, "output_norm.weight", true, path_a, &onorm);
     if (!bind_weight(m, "output.weight", false, path_a, &lm)) {
@@ -283,147 +297,174 @@ int uref_generate(const char* path, int max_layers, const std::int64_t* prompt,
                                     "ffn_down_exps", "attn_q.bias", "attn_k.bias",
                                     "attn_v.bias"};
     for (std::int64_t li = 0; li < L; ++li) {
-      for (int k = 0; k < 16; ++k) {
-        std::string nm = "blk." + std::to_string(li) + "." + names[k];
-        if (k < 13) nm += ".weight";
-        const bool f32_always = (k == 0 || k == 5 || k >= 9);
-        bind_weight(m, nm, f32_always, path_a, &W[li * 16 + k]);
+      for (int kk = 0; kk < 16; ++kk) {
+        std::string nm = "blk." + std::to_string(li) + "." + names[kk];
+        if (kk < 13) nm += ".weight";
+        const bool f32_always = (kk == 0 || kk == 5 || kk >= 9);
+        bind_weight(m, nm, f32_always, path_a, &W[li * 16 + kk]);
       }
     }
-    std::int64_t ff = 1;
     for (std::int64_t li = 0; li < L; ++li) {
       const Weight& up = W[li * 16 + 7];
       const Weight& ge = W[li * 16 + 10];
       if (up.present) ff = std::max<std::int64_t>(ff, up.shape[0]);
       if (ge.present) ff = std::max<std::int64_t>(ff, ge.shape[1]);
     }
-
-    runtime::KvCache kv;
-    const std::int64_t total = n_prompt + max_new;
-    const std::int64_t kv_max = ctx > 0 ? ctx : std::max<std::int64_t>(total, n_prompt + 1);
+    const std::int64_t kv_max =
+        kv_max_override > 0 ? kv_max_override
+                            : (ctx > 0 ? ctx : std::max<std::int64_t>(total_hint, n_prompt + 1));
     Error e = kv.configure(L, 1, kv_max, kvd, HKV);
-    if (!e.ok()) { g_err = e.message(); orc_model_close(m); return -1; }
+    if (!e.ok()) return e;
     kernels::set_active_kv_cache(&kv);
+    tokens = f32_tensor({1, 1});
+    x = f32_tensor({1, D}); n1 = f32_tensor({1, D}); res1 = f32_tensor({1, D});
+    q = f32_tensor({1, qd}); k = f32_tensor({1, kvd}); v = f32_tensor({1, kvd});
+    qb = f32_tensor({1, qd}); kb = f32_tensor({1, kvd}); vb = f32_tensor({1, kvd});
+    qr = f32_tensor({1, qd}); kr = f32_tensor({1, kvd});
+    att = f32_tensor({1, qd}); ao = f32_tensor({1, D}); n2 = f32_tensor({1, D});
+    g = f32_tensor({1, ff}); u = f32_tensor({1, ff}); ga = f32_tensor({1, ff});
+    hid = f32_tensor({1, ff}); fo = f32_tensor({1, D}); res2 = f32_tensor({1, D});
+    normed = f32_tensor({1, D}); logits = f32_tensor({1, V}); probs = f32_tensor({1, V});
+    mp = f32_tensor({1, std::max<std::int64_t>(E, 1)}); mt = f32_tensor({1, 1});
+    fi = f32_tensor({1, D}); fin = f32_tensor({1, D});
+    return Error::success();
+  }
 
-    auto tokens = f32_tensor({1, 1});
-    auto x = f32_tensor({1, D}), n1 = f32_tensor({1, D}), res1 = f32_tensor({1, D});
-    auto q = f32_tensor({1, qd}), k = f32_tensor({1, kvd}), v = f32_tensor({1, kvd});
-    auto qb = f32_tensor({1, qd}), kb = f32_tensor({1, kvd}), vb = f32_tensor({1, kvd});
-    auto qr = f32_tensor({1, qd}), kr = f32_tensor({1, kvd});
-    auto att = f32_tensor({1, qd}), ao = f32_tensor({1, D}), n2 = f32_tensor({1, D});
-    auto g = f32_tensor({1, ff}), u = f32_tensor({1, ff}), ga = f32_tensor({1, ff});
-    auto hid = f32_tensor({1, ff}), fo = f32_tensor({1, D}), res2 = f32_tensor({1, D});
-    auto normed = f32_tensor({1, D}), logits = f32_tensor({1, V}), probs = f32_tensor({1, V});
-    auto mp = f32_tensor({1, std::max<std::int64_t>(E, 1)}), mt = f32_tensor({1, 1});
-
-    auto run = [&](std::int64_t token, bool last) -> Error {
-      tokens->f32[0] = static_cast<float>(token);
-      Error err = kernels::embedding_f32(tokens->view, emb.view, &x->view);
+  // Session::run() then KvCache::commit_step() (session.cpp:1048-1164).
+  Error run(std::int64_t token, float* taps_resid2) {
+    tokens->f32[0] = static_cast<float>(token);
+    Error err = kernels::embedding_f32(tokens->view, emb.view, &x->view);
+    if (!err.ok()) return err;
+    std::memcpy(fi->f32.data(), x->f32.data(), D * 4);
+    for (std::int64_t li = 0; li < L; ++li) {
+      Weight* w = &W[li * 16];
+      if (!(err = kernels::rmsnorm_f32(fi->view, &w[0].view, &n1->view, eps)).ok()) return err;
+      if (!(err = matmul(n1->view, w[1], &q->view)).ok()) return err;
+      if (!(err = matmul(n1->view, w[2], &k->view)).ok()) return err;
+      if (!(err = matmul(n1->view, w[3], &v->view)).ok()) return err;
+      TensorView qq = q->view, kk = k->view, vv = v->view;
+      if (w[13].present) { (void)kernels::add_f32(q->view, w[13].view, &qb->view); qq = qb->view; }
+      if (w[14].present) { (void)kernels::add_f32(k->view, w[14].view, &kb->view); kk = kb->view; }
+      if (w[15].present) { (void)kernels::add_f32(v->view, w[15].view, &vb->view); vv = vb->view; }
+      if (!(err = kernels::rope_f32(qq, nullptr, &qr->view, theta, hd,
+                                    static_cast<int>(rope_mode))).ok()) return err;
+      if (!(err = kernels::rope_f32(kk, nullptr, &kr->view, theta, hd,
+                                    static_cast<int>(rope_mode))).ok()) return err;
+      // Attention with the active KV cache (dispatch.cpp:219-231)
+      TensorView pk = kv.k_view(li), pv = kv.v_view(li);
+      err = kernels::attention_kv_f32(qr->view, kr->view, vv, &att->view, static_cast<int>(H), 0.0f,
+                                      true, pk.data ? &pk : nullptr, pv.data ? &pv : nullptr,
+                                      nullptr, nullptr);
       if (!err.ok()) return err;
-      TensorView feat = x->view;
-      std::vector<float> cur(x->f32);
-      for (std::int64_t li = 0; li < L; ++li) {
-        Weight* w = &W[li * 16];
-        auto fi = f32_tensor({1, D});
-        fi->f32 = cur;
-        fi->view.data = fi->f32.data();
-        err = kernels::rmsnorm_f32(fi->view, &w[0].view, &n1->view, eps);
-        if (!err.ok()) return err;
-        if (!(err = matmul(n1->view, w[1], &q->view)).ok()) return err;
-        if (!(err = matmul(n1->view, w[2], &k->view)).ok()) return err;
-        if (!(err = matmul(n1->view, w[3], &v->view)).ok()) return err;
-        TensorView qq = q->view, kk = k->view, vv = v->view;
-        if (w[13].present) { (void)kernels::add_f32(q->view, w[13].view, &qb->view); qq = qb->view; }
-        if (w[14].present) { (void)kernels::add_f32(k->view, w[14].view, &kb->view); kk = kb->view; }
-        if (w[15].present) { (void)kernels::add_f32(v->view, w[15].view, &vb->view); vv = vb->view; }
-        if (!(err = kernels::rope_f32(qq, nullptr, &qr->view, theta, hd,
-                                      static_cast<int>(rope_mode))).ok()) return err;
-        if (!(err = kernels::rope_f32(kk, nullptr, &kr->view, theta, hd,
-                                      static_cast<int>(rope_mode))).ok()) return err;
-        // Attention with the active KV cache (dispatch.cpp:219-231)
-        TensorView pk = kv.k_view(li), pv = kv.v_view(li);
-        err = kernels::attention_kv_f32(qr->view, kr->view, vv, &att->view,
-                                        static_cast<int>(H), 0.0f, true,
-                                        pk.data ? &pk : nullptr, pv.data ? &pv : nullptr,
-                                        nullptr, nullptr);
-        if (!err.ok()) return err;
-        if (!(err = kv.append_layer(li, kr->view, vv)).ok()) return err;
-        if (!(err = matmul(att->view, w[4], &ao->view)).ok()) return err;
-        if (!(err = kernels::add_f32(fi->view, ao->view, &res1->view)).ok()) return err;
-        TensorView min = res1->view;
-        if (w[5].present) {
-          if (!(err = kernels::rmsnorm_f32(res1->view, &w[5].view, &n2->view, eps)).ok()) return err;
-          min = n2->view;
-        }
-        if (w[9].present && w[10].present) {
-          if (!(err = kernels::moe_router_f32(min, w[9].view, &mp->view, &mt->view)).ok()) return err;
-          err = kernels::moe_experts_swiglu_f32(min, w[10].view, w[11].view, w[12].view,
-                                                mp->view, &fo->view, static_cast<int>(E),
-                                                static_cast<int>(topk));
-          if (!err.ok()) return err;
-        } else {
-          const std::int64_t I = w[7].shape[0];
-          g->shape[1] = u->shape[1] = ga->shape[1] = hid->shape[1] = I;
-          g->view.nbytes = u->view.nbytes = ga->view.nbytes = hid->view.nbytes =
-              static_cast<std::size_t>(I) * 4;
-          if (!(err = matmul(min, w[6], &g->view)).ok()) return err;
-          if (!(err = matmul(min, w[7], &u->view)).ok()) return err;
-          if (!(err = kernels::silu_f32(g->view, &ga->view)).ok()) return err;
-          if (!(err = kernels::mul_f32(ga->view, u->view, &hid->view)).ok()) return err;
-          if (!(err = matmul(hid->view, w[8], &fo->view)).ok()) return err;
-        }
-        if (!(err = kernels::add_f32(res1->view, fo->view, &res2->view)).ok()) return err;
-        cur = res2->f32;
-        if (last && taps_resid2) std::memcpy(taps_resid2 + li * D, res2->f32.data(), D * 4);
+      if (!(err = kv.append_layer(li, kr->view, vv)).ok()) return err;
+      if (!(err = matmul(att->view, w[4], &ao->view)).ok()) return err;
+      if (!(err = kernels::add_f32(fi->view, ao->view, &res1->view)).ok()) return err;
+      TensorView min = res1->view;
+      if (w[5].present) {
+        if (!(err = kernels::rmsnorm_f32(res1->view, &w[5].view, &n2->view, eps)).ok()) return err;
+        min = n2->view;
       }
-      auto fin = f32_tensor({1, D});
-      fin->f32 = cur;
-      fin->view.data = fin->f32.data();
-      TensorView fv = fin->view;
-      if (onorm.present) {
-        if (!(err = kernels::rmsnorm_f32(fin->view, &onorm.view, &normed->view, eps)).ok()) return err;
-        fv = normed->view;
+      if (w[9].present && w[10].present) {
+        if (!(err = kernels::moe_router_f32(min, w[9].view, &mp->view, &mt->view)).ok()) return err;
+        err = kernels::moe_experts_swiglu_f32(min, w[10].view, w[11].view, w[12].view, mp->view,
+                                              &fo->view, static_cast<int>(E), static_cast<int>(topk));
+        if (!err.ok()) return err;
+      } else {
+        const std::int64_t I = w[7].shape[0];
+        g->shape[1] = u->shape[1] = ga->shape[1] = hid->shape[1] = I;
+        g->view.nbytes = u->view.nbytes = ga->view.nbytes = hid->view.nbytes =
+            static_cast<std::size_t>(I) * 4;
+        if (!(err = matmul(min, w[6], &g->view)).ok()) return err;
+        if (!(err = matmul(min, w[7], &u->view)).ok()) return err;
+        if (!(err = kernels::silu_f32(g->view, &ga->view)).ok()) return err;
+        if (!(err = kernels::mul_f32(ga->view, u->view, &hid->view)).ok()) return err;
+        if (!(err = matmul(hid->view, w[8], &fo->view)).ok()) return err;
       }
-      if (!(err = matmul(fv, lm, &logits->view)).ok()) return err;
-      if (!(err = kernels::softmax_f32(logits->view, &probs->view, -1)).ok()) return err;
-      if (last && taps_logits) std::memcpy(taps_logits, logits->f32.data(), V * 4);
-      (void)feat;
-      return Error::success();
-    };
+      if (!(err = kernels::add_f32(res1->view, fo->view, &res2->view)).ok()) return err;
+      std::memcpy(fi->f32.data(), res2->f32.data(), D * 4);
+      if (taps_resid2) std::memcpy(taps_resid2 + li * D, res2->f32.data(), D * 4);
+    }
+    std::memcpy(fin->f32.data(), fi->f32.data(), D * 4);
+    TensorView fv = fin->view;
+    if (onorm.present) {
+      if (!(err = kernels::rmsnorm_f32(fin->view, &onorm.view, &normed->view, eps)).ok()) return err;
+      fv = normed->view;
+    }
+    if (!(err = matmul(fv, lm, &logits->view)).ok()) return err;
+    if (!(err = kernels::softmax_f32(logits->view, &probs->view, -1)).ok()) return err;
+    kv.commit_step();
+    return Error::success();
+  }
+};
 
-    std::vector<std::int64_t> hist;
+}  // namespace
+
+// Greedy generate through the reference kernels. taps_logits (vocab floats) and
+// taps_resid2 (n_layers*dim floats) receive the last run()'s values when non-NULL.
+int uref_generate(const char* path, int max_layers, const std::int64_t* prompt,
+                  std::int64_t n_prompt, std::int64_t max_new, std::int64_t* out,
+                  std::int64_t* out_n, float* taps_logits, float* taps_resid2) {
+  RefRunner R;
+  Error err = R.open(path, max_layers, 0, n_prompt + max_new, n_prompt);
+  if (!err.ok()) { g_err = err.message(); return -1; }
+  std::vector<std::int64_t> hist;
+  runtime::SampleParams greedy;
+  std::mt19937_64 rng{0};
+  for (std::int64_t i = 0; i < n_prompt; ++i) {
+    const bool last = max_new <= 1 && i == n_prompt - 1;
+    err = R.run(prompt[i], last ? taps_resid2 : nullptr);
+    if (!err.ok()) { g_err = err.message(); return -1; }
+    hist.push_back(prompt[i]);
+  }
+  for (std::int64_t t = 0; t < max_new; ++t) {
+    std::int64_t next = 0;
+    err = runtime::sample_token_f32(R.probs->f32.data(), static_cast<std::size_t>(R.V), greedy, hist,
+                                    &rng, &next);
+    if (!err.ok()) { g_err = err.message(); return -1; }
+    hist.push_back(next);
+    if (t + 1 >= max_new) break;
+    err = R.run(next, t + 2 >= max_new ? taps_resid2 : nullptr);
+    if (!err.ok()) { g_err = err.message(); return -1; }
+  }
+  if (taps_logits) std::memcpy(taps_logits, R.logits->f32.data(), R.V * 4);
+  for (std::size_t i = 0; i < hist.size(); ++i) out[i] = hist[i];
+  *out_n = static_cast<std::int64_t>(hist.size());
+  return 0;
+}
+
+// CPU baseline window: `n_steps` decode runs at positions start_pos.. through the
+// reference kernels, after filling the reference KvCache with start_pos
+// deterministic K/V rows (values in [-0.5, 0.5)). Returns the wall seconds of the
+// n_steps runs (the fill is not timed), or < 0 on error.
+double uref_time_decode_window(const char* path, std::int64_t start_pos, std::int64_t n_steps) {
+  RefRunner R;
+  Error err = R.open(path, 0, start_pos + n_steps + 1, 0, 1);
+  if (!err.ok()) { g_err = err.message(); return -1.0; }
+  auto kt = f32_tensor({1, R.kvd}), vt = f32_tensor({1, R.kvd});
+  for (std::int64_t p = 0; p < start_pos; ++p) {
+    for (std::int64_t li = 0; li < R.L; ++li) {
+      for (std::int64_t j = 0; j < R.kvd; ++j) {
+        const std::uint32_t h = static_cast<std::uint32_t>((p * R.kvd + j) * 2654435761u + li * 40503u);
+        kt->f32[j] = static_cast<float>(h & 0xffff) / 65536.0f - 0.5f;
+        vt->f32[j] = static_cast<float>((h >> 16) & 0xffff) / 65536.0f - 0.5f;
+      }
+      err = R.kv.append_layer(li, kt->view, vt->view);
+      if (!err.ok()) { g_err = err.message(); return -1.0; }
+    }
+    R.kv.commit_step();
+  }
+  const auto t0 = std::chrono::steady_clock::now();
+  std::int64_t tok = 1;
+  for (std::int64_t i = 0; i < n_steps; ++i) {
+    err = R.run(tok, nullptr);
+    if (!err.ok()) { g_err = err.message(); return -1.0; }
     runtime::SampleParams greedy;
     std::mt19937_64 rng{0};
-    Error err;
-    bool ok = true;
-    for (std::int64_t i = 0; i < n_prompt && ok; ++i) {
-      err = run(prompt[i], max_new <= 1 && i == n_prompt - 1);
-      if (!err.ok()) { ok = false; break; }
-      kv.commit_step();
-      hist.push_back(prompt[i]);
-    }
-    for (std::int64_t t = 0; t < max_new && ok; ++t) {
-      std::int64_t next = 0;
-      err = runtime::sample_token_f32(probs->f32.data(), static_cast<std::size_t>(V), greedy,
-                                      hist, &rng, &next);
-      if (!err.ok()) { ok = false; break; }
-      hist.push_back(next);
-      if (t + 1 >= max_new) break;
-      err = run(next, t + 2 >= max_new);
-      if (!err.ok()) { ok = false; break; }
-      kv.commit_step();
-    }
-    kernels::set_active_kv_cache(nullptr);
-    if (!ok) {
-      g_err = err.message();
-    } else {
-      for (std::size_t i = 0; i < hist.size(); ++i) out[i] = hist[i];
-      *out_n = static_cast<std::int64_t>(hist.size());
-      rc = 0;
-    }
+    (void)runtime::sample_token_f32(R.probs->f32.data(), static_cast<std::size_t>(R.V), greedy, {},
+                                    &rng, &tok);
   }
-  orc_model_close(m);
-  return rc;
+  const auto t1 = std::chrono::steady_clock::now();
+  return std::chrono::duration<double>(t1 - t0).count();
 }
 
 }  // extern "C"

@@ -9,9 +9,10 @@
 // Split-K over the sequence: block (h, s) takes a contiguous slice of keys for
 // kv head h, stages K and V tiles in LDS, and keeps an online-softmax running
 // max / sum / output for all G query heads of the group (K/V read once per
-// group). Each block writes (o, m, l) partials; the last block of head h to
-// finish (atomic ticket) merges the splits and writes the output, then re-arms
-// the ticket so the kernel can be replayed from a graph.
+// group). Each block writes (o, m, l) partials; a second small kernel merges the
+// splits of every query head. (A last-block ticket merge inside the split kernel
+// needs a device-scope release per block, i.e. an L2 write-back on CDNA4, which
+// costs more than the extra launch.)
 
 #include "common.h"
 #include "uaii_hip_internal.h"
@@ -40,7 +41,6 @@ __global__ void __launch_bounds__(NT) k_attn(AttnArgs a) {
   float* v_s = k_s + TILE * ld;         // [TILE][ld]
   float* p_s = v_s + TILE * ld;         // [G][TILE]
   __shared__ float m_run[MAXG], l_run[MAXG], alpha[MAXG];
-  __shared__ int last;
 
   const int h = blockIdx.x, s = blockIdx.y, S = gridDim.y;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = NT / 64;
@@ -126,34 +126,201 @@ __global__ void __launch_bounds__(NT) k_attn(AttnArgs a) {
     part[tid * pstride + hd] = m_run[tid];
     part[tid * pstride + hd + 1] = l_run[tid];
   }
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) {
-    const uint32_t prev = atomicAdd(&a.ticket[h], 1u);
-    last = (prev == (uint32_t)S - 1);
-  }
-  __syncthreads();
-  if (!last) return;
-  __threadfence();
-
-  // merge the S splits of kv head h
-  const volatile float* hp = a.part + (int64_t)h * S * G * pstride;
-  for (int idx = tid; idx < G * hd; idx += NT) {
-    const int g = idx / hd, d = idx % hd;
-    float M = -INFINITY;
-    for (int k = 0; k < S; ++k) M = fmaxf(M, hp[(k * G + g) * pstride + hd]);
-    float num = 0.0f, den = 0.0f;
-    for (int k = 0; k < S; ++k) {
-      const float mk = hp[(k * G + g) * pstride + hd];
-      if (mk == -INFINITY) continue;
-      const float w = expf(mk - M);
-      num += w * hp[(k * G + g) * pstride + d];
-      den += w * hp[(k * G + g) * pstride + hd + 1];
-    }
-    a.out[((int64_t)h * G + g) * hd + d] = den > 0.0f ? num / den : 0.0f;
-  }
-  if (tid == 0) a.ticket[h] = 0u;
 }
+
+// ---- fast path: head_dim 64 / 128, group size 1 / 2 / 4 / 8 ----------------------
+//
+// Block (h, s) of 4 waves owns a contiguous key range of kv head h; each wave
+// takes a quarter and walks it in tiles of 64 keys. Scores: lane = key, the
+// lane's K row is read in 16-byte chunks and dotted with the G query rows held in
+// LDS (same-address reads broadcast). P.V: lane = slice of head_dim, V rows read
+// coalesced (64 lanes x HD/64 elements per key). Online softmax per wave, the 4
+// wave states merged in LDS into one block partial; k_attn_merge combines the
+// block partials.
+
+template <bool F16>
+__device__ inline void load8(const void* base, int64_t elem, float* out) {
+  if constexpr (F16) {
+    const uint4 r = *reinterpret_cast<const uint4*>(reinterpret_cast<const __half*>(base) + elem);
+    const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      out[2 * i] = __half2float(__ushort_as_half((uint16_t)(w[i] & 0xffff)));
+      out[2 * i + 1] = __half2float(__ushort_as_half((uint16_t)(w[i] >> 16)));
+    }
+  } else {
+    const float4* p = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(base) + elem);
+    const float4 a = p[0], b = p[1];
+    out[0] = a.x; out[1] = a.y; out[2] = a.z; out[3] = a.w;
+    out[4] = b.x; out[5] = b.y; out[6] = b.z; out[7] = b.w;
+  }
+}
+
+template <bool F16, int DPL>
+__device__ inline void load_slice(const void* base, int64_t elem, float* out) {
+  if constexpr (F16) {
+    const __half* p = reinterpret_cast<const __half*>(base) + elem;
+    if constexpr (DPL == 2) {
+      const uint32_t w = *reinterpret_cast<const uint32_t*>(p);
+      out[0] = __half2float(__ushort_as_half((uint16_t)(w & 0xffff)));
+      out[1] = __half2float(__ushort_as_half((uint16_t)(w >> 16)));
+    } else {
+#pragma unroll
+      for (int e = 0; e < DPL; ++e) out[e] = __half2float(p[e]);
+    }
+  } else {
+    const float* p = reinterpret_cast<const float*>(base) + elem;
+#pragma unroll
+    for (int e = 0; e < DPL; ++e) out[e] = p[e];
+  }
+}
+
+template <bool F16, int HD, int G>
+__global__ void __launch_bounds__(256) k_attn_fast(AttnArgs a) {
+  constexpr int DPL = HD / 64;  // head-dim elements per lane in P.V
+  constexpr int NW = 4;
+  __shared__ float q_s[G * HD];
+  __shared__ float p_s[NW][G][64];
+  __shared__ float wm[NW][G], wl[NW][G];
+  __shared__ float wo[NW][G * HD];
+
+  const int h = blockIdx.x, sblk = blockIdx.y, SB = gridDim.y;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t n = a.fixed_len > 0 ? (int64_t)a.fixed_len : (int64_t)a.state->pos + 1;
+  const int64_t CB = (n + SB - 1) / SB;                  // keys per block
+  const int64_t b0 = (int64_t)sblk * CB, b1 = (b0 + CB < n) ? b0 + CB : n;
+  const int64_t CW = (CB + NW - 1) / NW;                  // keys per wave
+  const int64_t w0 = b0 + (int64_t)wave * CW;
+  const int64_t w1 = (w0 + CW < b1) ? w0 + CW : b1;
+  const float scale = 1.0f / sqrtf((float)HD);
+
+  for (int i = tid; i < G * HD; i += 256) q_s[i] = a.q[(int64_t)h * G * HD + i];
+  __syncthreads();
+
+  const size_t esz = F16 ? 2 : 4;
+  const char* kc = reinterpret_cast<const char*>(a.kcache) + (size_t)h * a.max_seq * HD * esz;
+  const char* vc = reinterpret_cast<const char*>(a.vcache) + (size_t)h * a.max_seq * HD * esz;
+
+  float m[G], l[G], o[G][DPL];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    m[g] = -INFINITY;
+    l[g] = 0.0f;
+#pragma unroll
+    for (int e = 0; e < DPL; ++e) o[g][e] = 0.0f;
+  }
+
+  for (int64_t t0 = w0; t0 < w1; t0 += 64) {
+    const int tn = (int)((w1 - t0 < 64) ? (w1 - t0) : 64);
+    // scores, lane = key
+    float sc[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) sc[g] = 0.0f;
+    if (lane < tn) {
+      const int64_t row = (t0 + lane) * HD;
+#pragma unroll 4
+      for (int c = 0; c < HD / 8; ++c) {
+        float kf[8];
+        load8<F16>(kc, row + 8 * c, kf);
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          const float4 qa = *reinterpret_cast<const float4*>(&q_s[g * HD + 8 * c]);
+          const float4 qb = *reinterpret_cast<const float4*>(&q_s[g * HD + 8 * c + 4]);
+          sc[g] += qa.x * kf[0] + qa.y * kf[1] + qa.z * kf[2] + qa.w * kf[3] +
+                   qb.x * kf[4] + qb.y * kf[5] + qb.z * kf[6] + qb.w * kf[7];
+        }
+      }
+    }
+    float alpha[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float sv = (lane < tn) ? sc[g] * scale : -INFINITY;
+      const float mnew = fmaxf(m[g], wave_max(sv));
+      const float pv = (lane < tn) ? expf(sv - mnew) : 0.0f;
+      alpha[g] = (m[g] == -INFINITY) ? 0.0f : expf(m[g] - mnew);
+      l[g] = l[g] * alpha[g] + wave_sum(pv);
+      m[g] = mnew;
+      p_s[wave][g][lane] = pv;
+    }
+    // the probabilities are read back by other lanes of this wave (in-order LDS)
+    __builtin_amdgcn_wave_barrier();
+    // P.V, lane = head-dim slice
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int e = 0; e < DPL; ++e) o[g][e] *= alpha[g];
+#pragma unroll 8
+    for (int jj = 0; jj < tn; ++jj) {
+      float vf[DPL];
+      load_slice<F16, DPL>(vc, (t0 + jj) * HD + lane * DPL, vf);
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const float pg = p_s[wave][g][jj];
+#pragma unroll
+        for (int e = 0; e < DPL; ++e) o[g][e] += pg * vf[e];
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+
+  // combine the 4 wave states of this block
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    if (lane == 0) { wm[wave][g] = m[g]; wl[wave][g] = l[g]; }
+#pragma unroll
+    for (int e = 0; e < DPL; ++e) wo[wave][g * HD + lane * DPL + e] = o[g][e];
+  }
+  __syncthreads();
+  const int64_t pstride = HD + 2;
+  float* part = a.part + ((int64_t)h * SB + sblk) * G * pstride;
+  for (int i = tid; i < G * HD; i += 256) {
+    const int g = i / HD;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) M = fmaxf(M, wm[w][g]);
+    float acc = 0.0f, den = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const float f = (wm[w][g] == -INFINITY) ? 0.0f : expf(wm[w][g] - M);
+      acc += f * wo[w][i];
+      den += f * wl[w][g];
+    }
+    part[g * pstride + (i % HD)] = acc;
+    if (i % HD == 0) {
+      part[g * pstride + HD] = M;
+      part[g * pstride + HD + 1] = den;
+    }
+  }
+}
+
+// Merge the SB block partials of every query head (one block per head):
+// out = sum_s w_s o_s / sum_s w_s l_s with w_s = exp(m_s - max_s m_s).
+__global__ void __launch_bounds__(256) k_attn_merge(AttnArgs a) {
+  __shared__ float w[64];
+  __shared__ float inv_den;
+  const int hq = blockIdx.x, hd = a.hd, G = a.n_heads / a.n_kv, SB = a.splits;
+  const int kvh = hq / G, g = hq % G;
+  const int64_t pstride = hd + 2;
+  const float* hp = a.part + ((int64_t)kvh * SB * G + g) * pstride;  // split k at + k*G*pstride
+  if (threadIdx.x < 64) {
+    const int k = threadIdx.x;
+    const float mk = (k < SB) ? hp[(int64_t)k * G * pstride + hd] : -INFINITY;
+    const float M = wave_max(mk);
+    const float wk = (k < SB && mk != -INFINITY) ? expf(mk - M) : 0.0f;
+    const float lk = (k < SB) ? hp[(int64_t)k * G * pstride + hd + 1] : 0.0f;
+    const float den = wave_sum(wk * lk);
+    w[k] = wk;
+    if (k == 0) inv_den = den > 0.0f ? 1.0f / den : 0.0f;
+  }
+  __syncthreads();
+  for (int d = threadIdx.x; d < hd; d += blockDim.x) {
+    float num = 0.0f;
+    for (int k = 0; k < SB; ++k) num += w[k] * hp[(int64_t)k * G * pstride + d];
+    a.out[(int64_t)hq * hd + d] = num * inv_den;
+  }
+}
+
 
 }  // namespace
 
@@ -168,9 +335,33 @@ hipError_t prepare_attention() {
   return hipSuccess;
 }
 
+template <bool F16, int HD>
+bool launch_fast_hd(const AttnArgs& a, int G, hipStream_t s) {
+  dim3 grid(a.n_kv, a.splits);
+  switch (G) {
+    case 1: hipLaunchKernelGGL((k_attn_fast<F16, HD, 1>), grid, dim3(256), 0, s, a); return true;
+    case 2: hipLaunchKernelGGL((k_attn_fast<F16, HD, 2>), grid, dim3(256), 0, s, a); return true;
+    case 4: hipLaunchKernelGGL((k_attn_fast<F16, HD, 4>), grid, dim3(256), 0, s, a); return true;
+    case 8: hipLaunchKernelGGL((k_attn_fast<F16, HD, 8>), grid, dim3(256), 0, s, a); return true;
+    default: return false;
+  }
+}
+
 hipError_t launch_attention_decode(const AttnArgs& a, hipStream_t s) {
   const int G = a.n_heads / a.n_kv;
   if (G < 1 || G > MAXG || a.hd > 256 || a.hd % 2 || a.n_heads % a.n_kv) return hipErrorInvalidValue;
+  if (a.splits < 1 || a.splits > 64) return hipErrorInvalidValue;
+  if ((a.hd == 64 || a.hd == 128) && (G == 1 || G == 2 || G == 4 || G == 8)) {
+    bool ok;
+    if (a.hd == 64) ok = a.kv_f16 ? launch_fast_hd<true, 64>(a, G, s) : launch_fast_hd<false, 64>(a, G, s);
+    else ok = a.kv_f16 ? launch_fast_hd<true, 128>(a, G, s) : launch_fast_hd<false, 128>(a, G, s);
+    if (ok) {
+      const hipError_t st = hipGetLastError();
+      if (st != hipSuccess) return st;
+      hipLaunchKernelGGL(k_attn_merge, dim3(a.n_heads), dim3(256), 0, s, a);
+      return hipGetLastError();
+    }
+  }
   const int tile = a.hd > 64 ? 32 : 64;
   const size_t lds = sizeof(float) * ((size_t)G * a.hd + 2 * tile * (size_t)(a.hd + 1) + (size_t)G * tile);
   if ((int)lds > lds_limit() - 1024) return hipErrorInvalidValue;
@@ -182,6 +373,9 @@ hipError_t launch_attention_decode(const AttnArgs& a, hipStream_t s) {
     if (a.kv_f16) hipLaunchKernelGGL((k_attn<true, 32>), grid, dim3(NT), lds, s, a);
     else hipLaunchKernelGGL((k_attn<false, 32>), grid, dim3(NT), lds, s, a);
   }
+  const hipError_t st = hipGetLastError();
+  if (st != hipSuccess) return st;
+  hipLaunchKernelGGL(k_attn_merge, dim3(a.n_heads), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 

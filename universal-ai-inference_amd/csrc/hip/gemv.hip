@@ -18,6 +18,8 @@
 #include "common.h"
 #include "uaii_hip_internal.h"
 
+#include <algorithm>
+
 namespace uaii_hip {
 namespace {
 
@@ -307,18 +309,29 @@ __device__ inline void load_x(const float* __restrict__ xsm, int64_t t, float* x
 }
 
 // Accumulate RPW row dots over the row payloads; lane l takes chunks l, l+64, ...
+// Two chunks per iteration so each lane has 2*RPW 16-byte loads in flight.
 template <int FMT>
 __device__ inline void rows_dot(const RowPtr* P, int64_t nch, const float* xsm, int lane,
                                 float* acc) {
-  for (int64_t t = lane; t < nch; t += 64) {
+  for (int64_t t = lane; t < nch; t += 128) {
+    const bool two = t + 64 < nch;
+    Raw r0[RPW], r1[RPW];
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) load_raw<FMT>(P[r], t, r0[r]);
+    if (two) {
+#pragma unroll
+      for (int r = 0; r < RPW; ++r) load_raw<FMT>(P[r], t + 64, r1[r]);
+    }
     float xv[xn<FMT>()];
     float xsum[4];
-    Raw raw[RPW];
-#pragma unroll
-    for (int r = 0; r < RPW; ++r) load_raw<FMT>(P[r], t, raw[r]);
     load_x<FMT>(xsm, t, xv, xsum);
 #pragma unroll
-    for (int r = 0; r < RPW; ++r) acc[r] += chunk_dot<FMT>(raw[r], t, xv, xsum);
+    for (int r = 0; r < RPW; ++r) acc[r] += chunk_dot<FMT>(r0[r], t, xv, xsum);
+    if (two) {
+      load_x<FMT>(xsm, t + 64, xv, xsum);
+#pragma unroll
+      for (int r = 0; r < RPW; ++r) acc[r] += chunk_dot<FMT>(r1[r], t + 64, xv, xsum);
+    }
   }
 }
 
@@ -374,97 +387,112 @@ __global__ void __launch_bounds__(WPB * 64) k_gemv(GemvArgs a) {
   __shared__ float red[WPB];
   __shared__ float bval[WPB];
   __shared__ int32_t bidx[WPB];
-  __shared__ int last_block;
 
   // segment lookup (uniform per block)
   int si = 0;
   for (int k = 1; k < a.nseg; ++k) if ((int)blockIdx.x >= a.seg[k].block0) si = k;
   const GemvSeg& seg = a.seg[si];
+  const int nblk = (si + 1 < a.nseg ? a.seg[si + 1].block0 : (int)gridDim.x) - seg.block0;
+  const int64_t ngroups = (seg.rows + WPB * RPW - 1) / (WPB * RPW);
 
   stage_x(a, xsm, red);
 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
-  const int64_t lrow0 = ((int64_t)(blockIdx.x - seg.block0) * WPB + wave) * RPW;
-  RowPtr P[RPW];
-#pragma unroll
-  for (int r = 0; r < RPW; ++r) {
-    int64_t l = lrow0 + r;
-    if (l >= seg.rows) l = seg.rows - 1;  // clamp: duplicate work, result dropped
-    if constexpr (EPI == EPI_SWIGLU) {
-      P[r] = row_ptr((l & 1) ? seg.w2 : seg.w, l >> 1);
-    } else if constexpr (EPI == EPI_QKV) {
-      P[r] = row_ptr(seg.w, seg.kind == 2 ? l : qkv_phys(l, a.rope_mode, a.head_dim));
-    } else {
-      P[r] = row_ptr(seg.w, l);
-    }
-  }
-  float acc[RPW];
-#pragma unroll
-  for (int r = 0; r < RPW; ++r) acc[r] = 0.0f;
-  rows_dot<FMT>(P, seg.w.a_row / 16, xsm, lane, acc);
-#pragma unroll
-  for (int r = 0; r < RPW; ++r) acc[r] = wave_sum(acc[r]);
+  float best_v = -INFINITY;
+  int32_t best_i = 0x7fffffff;
 
-  if constexpr (EPI == EPI_STORE || EPI == EPI_ADD || EPI == EPI_LOGITS) {
-    if (lane < RPW) {
-      float v = 0.0f;
+  // persistent loop: this block takes row groups blk, blk + nblk, ...
+  for (int64_t grp = blockIdx.x - seg.block0; grp < ngroups; grp += nblk) {
+    const int64_t lrow0 = (grp * WPB + wave) * RPW;
+    RowPtr P[RPW];
 #pragma unroll
-      for (int r = 0; r < RPW; ++r) if (r == lane) v = acc[r];
-      const int64_t l = lrow0 + lane;
-      if (l < seg.rows) {
-        const int64_t o = seg.row_base + l;
-        if constexpr (EPI == EPI_ADD) v = a.y[o] + v;
-        a.y[o] = v;
-        if (a.tap) a.tap[o] = v;
+    for (int r = 0; r < RPW; ++r) {
+      int64_t l = lrow0 + r;
+      if (l >= seg.rows) l = seg.rows - 1;  // clamp: duplicate work, result dropped
+      if constexpr (EPI == EPI_SWIGLU) {
+        P[r] = row_ptr((l & 1) ? seg.w2 : seg.w, l >> 1);
+      } else if constexpr (EPI == EPI_QKV) {
+        P[r] = row_ptr(seg.w, seg.kind == 2 ? l : qkv_phys(l, a.rope_mode, a.head_dim));
+      } else {
+        P[r] = row_ptr(seg.w, l);
       }
     }
-  } else if constexpr (EPI == EPI_SWIGLU) {
-    // pairs (gate, up) at logical rows (2j, 2j+1)
-    if (lane < RPW / 2) {
-      float g = 0.0f, u = 0.0f;
+    float acc[RPW];
 #pragma unroll
-      for (int r = 0; r < RPW; r += 2) if (r == 2 * lane) { g = acc[r]; u = acc[r + 1]; }
-      const int64_t l = lrow0 + 2 * lane;
-      if (l < seg.rows) {
-        const float act = g / (1.0f + expf(-g));  // silu (elementwise.cpp:73-84)
-        a.y[seg.row_base + (l >> 1)] = act * u;
-      }
-    }
-  } else if constexpr (EPI == EPI_QKV) {
-    if (lane < RPW / 2) {
-      float v0 = 0.0f, v1 = 0.0f;
+    for (int r = 0; r < RPW; ++r) acc[r] = 0.0f;
+    rows_dot<FMT>(P, seg.w.a_row / 16, xsm, lane, acc);
 #pragma unroll
-      for (int r = 0; r < RPW; r += 2) if (r == 2 * lane) { v0 = acc[r]; v1 = acc[r + 1]; }
-      const int64_t l = lrow0 + 2 * lane;
-      if (l < seg.rows) {
-        const int64_t r0 = (seg.kind == 2) ? l : qkv_phys(l, a.rope_mode, a.head_dim);
-        const int64_t r1 = (seg.kind == 2) ? l + 1 : qkv_phys(l + 1, a.rope_mode, a.head_dim);
-        if (seg.bias) { v0 = v0 + seg.bias[r0]; v1 = v1 + seg.bias[r1]; }
-        const int pos = a.state->pos;
-        if (seg.kind != 2) {
-          // rotate pair p of its head by the host-built angle table
-          const int64_t p = (a.rope_mode == 2) ? (r0 % a.head_dim) : ((r0 % a.head_dim) >> 1);
-          const float2 cs = a.rope[(int64_t)pos * (a.head_dim / 2) + p];
-          const float n0 = v0 * cs.x - v1 * cs.y;
-          const float n1 = v0 * cs.y + v1 * cs.x;
-          v0 = n0; v1 = n1;
+    for (int r = 0; r < RPW; ++r) acc[r] = wave_sum(acc[r]);
+
+    if constexpr (EPI == EPI_STORE || EPI == EPI_ADD || EPI == EPI_LOGITS) {
+      if (lane < RPW) {
+        float v = 0.0f;
+#pragma unroll
+        for (int r = 0; r < RPW; ++r) if (r == lane) v = acc[r];
+        const int64_t l = lrow0 + lane;
+        if (l < seg.rows) {
+          const int64_t o = seg.row_base + l;
+          if constexpr (EPI == EPI_ADD) v = a.y[o] + v;
+          a.y[o] = v;
+          if (a.tap) a.tap[o] = v;
         }
-        if (seg.kind == 0) {
-          a.y[r0] = v0;
-          a.y[r1] = v1;
-        } else {
-          // K after RoPE and raw V go to the cache at `pos` (gguf.cpp:1043, dispatch.cpp:218)
-          void* cache = (seg.kind == 1) ? a.kcache : a.vcache;
-          const int64_t hd = a.head_dim;
-          const int64_t o0 = ((r0 / hd) * a.max_seq + pos) * hd + (r0 % hd);
-          const int64_t o1 = ((r1 / hd) * a.max_seq + pos) * hd + (r1 % hd);
-          if (a.kv_f16) {
-            reinterpret_cast<__half*>(cache)[o0] = __float2half(v0);
-            reinterpret_cast<__half*>(cache)[o1] = __float2half(v1);
+      }
+      if constexpr (EPI == EPI_LOGITS) {
+        // running greedy argmax of this wave (rows ascend, strict '>' keeps the lowest)
+#pragma unroll
+        for (int r = 0; r < RPW; ++r) {
+          const int64_t l = lrow0 + r;
+          if (l < seg.rows && (best_i == 0x7fffffff || acc[r] > best_v)) { best_v = acc[r]; best_i = (int32_t)l; }
+        }
+      }
+    } else if constexpr (EPI == EPI_SWIGLU) {
+      // pairs (gate, up) at logical rows (2j, 2j+1)
+      if (lane < RPW / 2) {
+        float g = 0.0f, u = 0.0f;
+#pragma unroll
+        for (int r = 0; r < RPW; r += 2) if (r == 2 * lane) { g = acc[r]; u = acc[r + 1]; }
+        const int64_t l = lrow0 + 2 * lane;
+        if (l < seg.rows) {
+          const float act = g / (1.0f + expf(-g));  // silu (elementwise.cpp:73-84)
+          a.y[seg.row_base + (l >> 1)] = act * u;
+        }
+      }
+    } else if constexpr (EPI == EPI_QKV) {
+      if (lane < RPW / 2) {
+        float v0 = 0.0f, v1 = 0.0f;
+#pragma unroll
+        for (int r = 0; r < RPW; r += 2) if (r == 2 * lane) { v0 = acc[r]; v1 = acc[r + 1]; }
+        const int64_t l = lrow0 + 2 * lane;
+        if (l < seg.rows) {
+          const int64_t r0 = (seg.kind == 2) ? l : qkv_phys(l, a.rope_mode, a.head_dim);
+          const int64_t r1 = (seg.kind == 2) ? l + 1 : qkv_phys(l + 1, a.rope_mode, a.head_dim);
+          if (seg.bias) { v0 = v0 + seg.bias[r0]; v1 = v1 + seg.bias[r1]; }
+          const int pos = a.state->pos;
+          if (seg.kind != 2) {
+            // rotate pair p of its head by the host-built angle table
+            const int64_t p = (a.rope_mode == 2) ? (r0 % a.head_dim) : ((r0 % a.head_dim) >> 1);
+            const float2 cs = a.rope[(int64_t)pos * (a.head_dim / 2) + p];
+            const float n0 = v0 * cs.x - v1 * cs.y;
+            const float n1 = v0 * cs.y + v1 * cs.x;
+            v0 = n0; v1 = n1;
+          }
+          if (seg.kind == 0) {
+            a.y[r0] = v0;
+            a.y[r1] = v1;
           } else {
-            reinterpret_cast<float*>(cache)[o0] = v0;
-            reinterpret_cast<float*>(cache)[o1] = v1;
+            // K after RoPE and raw V go to the cache at `pos` (gguf.cpp:1043, dispatch.cpp:218)
+            void* cache = (seg.kind == 1) ? a.kcache : a.vcache;
+            const int64_t hd = a.head_dim;
+            const int64_t o0 = ((r0 / hd) * a.max_seq + pos) * hd + (r0 % hd);
+            const int64_t o1 = ((r1 / hd) * a.max_seq + pos) * hd + (r1 % hd);
+            if (a.kv_f16) {
+              reinterpret_cast<__half*>(cache)[o0] = __float2half(v0);
+              reinterpret_cast<__half*>(cache)[o1] = __float2half(v1);
+            } else {
+              reinterpret_cast<float*>(cache)[o0] = v0;
+              reinterpret_cast<float*>(cache)[o1] = v1;
+            }
           }
         }
       }
@@ -472,18 +500,8 @@ __global__ void __launch_bounds__(WPB * 64) k_gemv(GemvArgs a) {
   }
 
   if constexpr (EPI == EPI_LOGITS) {
-    // ---- fused greedy argmax: block partial, then the last block reduces ------
-    if (lane == 0) {
-      float bv = -INFINITY;
-      int32_t bi = 0x7fffffff;
-#pragma unroll
-      for (int r = 0; r < RPW; ++r) {
-        const int64_t l = lrow0 + r;
-        if (l < seg.rows && (bi == 0x7fffffff || acc[r] > bv)) { bv = acc[r]; bi = (int32_t)l; }
-      }
-      bval[wave] = bv;
-      bidx[wave] = bi;
-    }
+    // block partial of the greedy argmax; k_argmax_final reduces the partials
+    if (lane == 0) { bval[wave] = best_v; bidx[wave] = best_i; }
     __syncthreads();
     if (threadIdx.x == 0) {
       float bv = bval[0];
@@ -494,60 +512,58 @@ __global__ void __launch_bounds__(WPB * 64) k_gemv(GemvArgs a) {
       }
       a.part_val[blockIdx.x] = bv;
       a.part_idx[blockIdx.x] = bi;
-      __threadfence();
-      const uint32_t prev = atomicAdd(a.ticket, 1u);
-      last_block = (prev == gridDim.x - 1);
     }
-    __syncthreads();
-    if (!last_block) return;
-    __threadfence();
-    // last block: reduce all partials, lowest index wins ties (sampling.cpp:38-50)
-    float bv = -INFINITY, b2 = -INFINITY;
-    int32_t bi = 0x7fffffff;
-    for (int k = threadIdx.x; k < (int)gridDim.x; k += blockDim.x) {
-      const float v = reinterpret_cast<volatile const float*>(a.part_val)[k];
-      const int32_t ix = reinterpret_cast<volatile const int32_t*>(a.part_idx)[k];
-      if (ix == 0x7fffffff) continue;
-      if (bi == 0x7fffffff || v > bv || (v == bv && ix < bi)) { b2 = fmaxf(b2, bv); bv = v; bi = ix; }
-      else b2 = fmaxf(b2, v);
-    }
+  }
+}
+
+// Final greedy argmax over the LM-head block partials (lowest index wins ties,
+// sampling.cpp:38-50), then the token advance: inside the prompt the next token
+// is the prompt's, afterwards the argmax (session.cpp:1006-1044).
+__global__ void __launch_bounds__(1024) k_argmax_final(GemvArgs a, int nparts) {
+  __shared__ float fv[16], f2[16];
+  __shared__ int32_t fi[16];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  float bv = -INFINITY, b2 = -INFINITY;
+  int32_t bi = 0x7fffffff;
+  for (int k = threadIdx.x; k < nparts; k += blockDim.x) {
+    const float v = a.part_val[k];
+    const int32_t ix = a.part_idx[k];
+    if (ix == 0x7fffffff) continue;
+    if (bi == 0x7fffffff || v > bv || (v == bv && ix < bi)) { b2 = fmaxf(b2, bv); bv = v; bi = ix; }
+    else b2 = fmaxf(b2, v);
+  }
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      const float ov = __shfl_xor(bv, o, 64);
-      const int32_t oi = __shfl_xor(bi, o, 64);
-      const float o2 = __shfl_xor(b2, o, 64);
-      if (oi != 0x7fffffff && (bi == 0x7fffffff || ov > bv || (ov == bv && oi < bi))) {
-        b2 = fmaxf(fmaxf(b2, o2), bv); bv = ov; bi = oi;
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(bv, o, 64);
+    const int32_t oi = __shfl_xor(bi, o, 64);
+    const float o2 = __shfl_xor(b2, o, 64);
+    if (oi != 0x7fffffff && (bi == 0x7fffffff || ov > bv || (ov == bv && oi < bi))) {
+      b2 = fmaxf(fmaxf(b2, o2), bv); bv = ov; bi = oi;
+    } else {
+      b2 = fmaxf(fmaxf(b2, o2), ov);
+    }
+  }
+  if (lane == 0) { fv[wave] = bv; fi[wave] = bi; f2[wave] = b2; }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float v = fv[0], s2 = f2[0];
+    int32_t ix = fi[0];
+    for (int k = 1; k < (int)(blockDim.x >> 6); ++k) {
+      if (fi[k] != 0x7fffffff && (ix == 0x7fffffff || fv[k] > v || (fv[k] == v && fi[k] < ix))) {
+        s2 = fmaxf(fmaxf(s2, f2[k]), v); v = fv[k]; ix = fi[k];
       } else {
-        b2 = fmaxf(fmaxf(b2, o2), ov);
+        s2 = fmaxf(fmaxf(s2, f2[k]), fv[k]);
       }
     }
-    __shared__ float fv[WPB], f2[WPB];
-    __shared__ int32_t fi[WPB];
-    if (lane == 0) { fv[wave] = bv; fi[wave] = bi; f2[wave] = b2; }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      float v = fv[0], s2 = f2[0];
-      int32_t ix = fi[0];
-      for (int k = 1; k < WPB; ++k) {
-        if (fi[k] != 0x7fffffff && (ix == 0x7fffffff || fv[k] > v || (fv[k] == v && fi[k] < ix))) {
-          s2 = fmaxf(fmaxf(s2, f2[k]), v); v = fv[k]; ix = fi[k];
-        } else {
-          s2 = fmaxf(fmaxf(s2, f2[k]), fv[k]);
-        }
-      }
-      StepState* st = a.state;
-      st->argmax = ix;
-      st->max_logit = v;
-      st->second = s2;
-      // advance: inside the prompt the next token is the prompt's
-      const int p = st->pos + 1;
-      const int next = (p < st->n_prompt) ? a.ids[p] : ix;
-      a.ids[p] = next;
-      st->token = next;
-      st->pos = p;
-      *a.ticket = 0u;  // re-arm for the next step / graph replay
-    }
+    StepState* st = a.state;
+    st->argmax = ix;
+    st->max_logit = v;
+    st->second = s2;
+    const int p = st->pos + 1;
+    const int next = (p < st->n_prompt) ? a.ids[p] : ix;
+    a.ids[p] = next;
+    st->token = next;
+    st->pos = p;
   }
 }
 
@@ -602,23 +618,54 @@ hipError_t prepare_gemv() {
   return hipSuccess;
 }
 
-int gemv_grid(const GemvArgs& a) {
+int cu_count() {
+  static int n = 0;
+  if (n == 0) {
+    int dev = 0, v = 0;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
+      n = v;
+    else
+      n = 256;
+  }
+  return n;
+}
+
+// Blocks per segment: one per row group, capped so a launch holds at most
+// kBlocksPerCU blocks per CU in total (the rest loop), shared out by group count.
+constexpr int kBlocksPerCU = 4;
+
+void plan_blocks(const GemvArgs& a, int* per_seg) {
   const int rpb = WPB * RPW;
+  int64_t total = 0;
+  for (int k = 0; k < a.nseg; ++k) total += (a.seg[k].rows + rpb - 1) / rpb;
+  const int64_t cap = (int64_t)cu_count() * kBlocksPerCU;
+  for (int k = 0; k < a.nseg; ++k) {
+    const int64_t g = (a.seg[k].rows + rpb - 1) / rpb;
+    int64_t b = g;
+    if (total > cap) b = std::max<int64_t>(1, (g * cap + total - 1) / total);
+    per_seg[k] = (int)std::min<int64_t>(b, g);
+  }
+}
+
+int gemv_grid(const GemvArgs& a) {
+  int per[3] = {0, 0, 0};
+  plan_blocks(a, per);
   int blocks = 0;
-  for (int k = 0; k < a.nseg; ++k) blocks += (int)((a.seg[k].rows + rpb - 1) / rpb);
+  for (int k = 0; k < a.nseg; ++k) blocks += per[k];
   return blocks;
 }
 
 // One launch per run of segments sharing a weight type (the kernel is
 // specialised per type); QKV with mixed types therefore takes several launches.
 hipError_t launch_gemv(const GemvArgs& in, hipStream_t s) {
-  const int rpb = WPB * RPW;
   const size_t lds = (size_t)in.K * sizeof(float);
   if ((int)lds > lds_limit() - 1024 || in.K % 4) return hipErrorInvalidValue;
   if (in.epi == EPI_LOGITS && in.nseg != 1) return hipErrorInvalidValue;
   for (int k = 0; k < in.nseg; ++k) {
     if (in.epi == EPI_SWIGLU && in.seg[k].w2.type != in.seg[k].w.type) return hipErrorInvalidValue;
     if ((in.epi == EPI_SWIGLU || in.epi == EPI_QKV) && (in.seg[k].rows % 2)) return hipErrorInvalidValue;
+    if (in.seg[k].w.cols != in.K) return hipErrorInvalidValue;
   }
   int k0 = 0;
   while (k0 < in.nseg) {
@@ -626,11 +673,13 @@ hipError_t launch_gemv(const GemvArgs& in, hipStream_t s) {
     while (k1 < in.nseg && in.seg[k1].w.type == in.seg[k0].w.type) ++k1;
     GemvArgs a = in;
     a.nseg = k1 - k0;
+    for (int k = 0; k < a.nseg; ++k) a.seg[k] = in.seg[k0 + k];
+    int per[3] = {0, 0, 0};
+    plan_blocks(a, per);
     int blocks = 0;
     for (int k = 0; k < a.nseg; ++k) {
-      a.seg[k] = in.seg[k0 + k];
       a.seg[k].block0 = blocks;
-      blocks += (int)((a.seg[k].rows + rpb - 1) / rpb);
+      blocks += per[k];
     }
     if (k0 > 0) a.xtap = nullptr;
     KernelFn fn = pick(a.epi, a.seg[0].w.type);
@@ -639,6 +688,11 @@ hipError_t launch_gemv(const GemvArgs& in, hipStream_t s) {
       hipLaunchKernelGGL(fn, dim3(blocks), dim3(WPB * 64), lds, s, a);
       const hipError_t st = hipGetLastError();
       if (st != hipSuccess) return st;
+      if (a.epi == EPI_LOGITS) {
+        hipLaunchKernelGGL(k_argmax_final, dim3(1), dim3(1024), 0, s, a, blocks);
+        const hipError_t st2 = hipGetLastError();
+        if (st2 != hipSuccess) return st2;
+      }
     }
     k0 = k1;
   }

@@ -23,7 +23,7 @@ enum Epilogue : int {
   EPI_ADD = 1,     // y[row] = y[row] + dot        (residual add)
   EPI_QKV = 2,     // bias, RoPE pairs, q -> y, k/v -> KV cache at pos
   EPI_SWIGLU = 3,  // rows (gate i, up i) -> y[i] = silu(g) * u
-  EPI_LOGITS = 4,  // y[row] = dot, fused greedy argmax + token advance
+  EPI_LOGITS = 4,  // y[row] = dot, block argmax partials (+ final argmax/advance kernel)
 };
 
 // Persistent decode state shared by the step kernels (device memory).
@@ -67,9 +67,8 @@ struct GemvArgs {
   int rope_mode;
   const float2* rope;    // [max_seq][hd/2] (cos, sin)
   // EPI_LOGITS
-  float* part_val;       // [gridDim]
+  float* part_val;       // [gridDim] block partials of the argmax
   int32_t* part_idx;
-  uint32_t* ticket;
   int32_t* ids;          // token history [max_seq + 1]
   // shared
   StepState* state;
@@ -108,7 +107,6 @@ struct AttnArgs {
   int fixed_len;           // >0: use this key count instead of state->pos + 1
   float* out;            // [n_heads * hd]
   float* part;           // [n_kv][splits][group][hd + 2]
-  uint32_t* ticket;      // [n_kv]
   int splits;
 };
 

@@ -1,5 +1,6 @@
 // capi.cpp — the uaii.h C ABI over runtime::Session (libs/uaii-capi/src/capi.cpp).
 #include "uaii/c_api/uaii.h"
+#include "uaii/c_api/uaii_ext.h"
 
 #include "session.h"
 
@@ -198,6 +199,78 @@ uaii_status uaii_session_write_trace(uaii_session* session, const char* path) {
   std::fputs(s.c_str(), f);
   std::fclose(f);
   g_last_error.clear();
+  return UAII_OK;
+}
+
+// ---- uaii_ext.h ------------------------------------------------------------
+
+uaii_status uaii_session_begin(uaii_session* session, const int64_t* prompt_tokens,
+                               size_t prompt_n, int64_t capacity) {
+  if (session == nullptr || (prompt_tokens == nullptr && prompt_n > 0))
+    return fail(UAII_ERR_INVALID_ARGUMENT, "begin null args");
+  auto* h = reinterpret_cast<SessionHandle*>(session);
+  std::vector<int64_t> prompt(prompt_tokens, prompt_tokens + prompt_n);
+  return from_error(h->session.begin(prompt, capacity));
+}
+
+uaii_status uaii_session_step_async(uaii_session* session, int want_logits) {
+  if (session == nullptr) return fail(UAII_ERR_INVALID_ARGUMENT, "session null");
+  return from_error(reinterpret_cast<SessionHandle*>(session)->session.step_async(want_logits != 0));
+}
+
+uaii_status uaii_session_sync(uaii_session* session) {
+  if (session == nullptr) return fail(UAII_ERR_INVALID_ARGUMENT, "session null");
+  auto* p = reinterpret_cast<SessionHandle*>(session)->session.program();
+  if (!p) return fail(UAII_ERR_INVALID_ARGUMENT, "session not ready");
+  return from_error(p->synchronize());
+}
+
+uaii_status uaii_session_position(uaii_session* session, int64_t* pos) {
+  if (session == nullptr || pos == nullptr) return fail(UAII_ERR_INVALID_ARGUMENT, "null args");
+  auto* p = reinterpret_cast<SessionHandle*>(session)->session.program();
+  if (!p) return fail(UAII_ERR_INVALID_ARGUMENT, "session not ready");
+  uaii_hip::StepState st{};
+  uaii::Error err = p->read_state(&st);
+  if (!err.ok()) return from_error(err);
+  *pos = st.pos;
+  return UAII_OK;
+}
+
+uaii_status uaii_session_read_ids(uaii_session* session, int64_t* out, size_t n) {
+  if (session == nullptr || (out == nullptr && n > 0)) return fail(UAII_ERR_INVALID_ARGUMENT, "null args");
+  auto* p = reinterpret_cast<SessionHandle*>(session)->session.program();
+  if (!p) return fail(UAII_ERR_INVALID_ARGUMENT, "session not ready");
+  return from_error(p->read_ids(out, (int64_t)n));
+}
+
+uaii_status uaii_session_seek(uaii_session* session, int64_t pos) {
+  if (session == nullptr) return fail(UAII_ERR_INVALID_ARGUMENT, "session null");
+  auto* p = reinterpret_cast<SessionHandle*>(session)->session.program();
+  if (!p) return fail(UAII_ERR_INVALID_ARGUMENT, "session not ready");
+  return from_error(p->seek(pos));
+}
+
+uaii_status uaii_session_set_profiling(uaii_session* session, int on) {
+  if (session == nullptr) return fail(UAII_ERR_INVALID_ARGUMENT, "session null");
+  auto* p = reinterpret_cast<SessionHandle*>(session)->session.program();
+  if (!p) return fail(UAII_ERR_INVALID_ARGUMENT, "session not ready");
+  uaii::Error err = p->synchronize();
+  if (!err.ok()) return from_error(err);
+  p->set_profile(on != 0);
+  if (on) p->reset_timings();
+  return UAII_OK;
+}
+
+uaii_status uaii_session_last_margin(uaii_session* session, float* best, float* second) {
+  if (session == nullptr || best == nullptr || second == nullptr)
+    return fail(UAII_ERR_INVALID_ARGUMENT, "null args");
+  auto* p = reinterpret_cast<SessionHandle*>(session)->session.program();
+  if (!p) return fail(UAII_ERR_INVALID_ARGUMENT, "session not ready");
+  uaii_hip::StepState st{};
+  uaii::Error err = p->read_state(&st);
+  if (!err.ok()) return from_error(err);
+  *best = st.max_logit;
+  *second = st.second;
   return UAII_OK;
 }
 

@@ -19,7 +19,7 @@ constexpr int kErrArg = -1;      // invalid argument
 constexpr int kErrNotImpl = -2;  // not implemented
 
 std::mutex g_scratch_mu;
-void* g_scratch = nullptr;       // attention partials + tickets for uaii_hip_attention_decode
+void* g_scratch = nullptr;       // attention partials for uaii_hip_attention_decode
 size_t g_scratch_bytes = 0;
 
 hipStream_t S(void* s) { return static_cast<hipStream_t>(s); }
@@ -187,13 +187,10 @@ int uaii_hip_attention_decode(const float* q, const void* kcache, const void* vc
       n_heads % n_kv_heads || head_dim <= 0 || n_keys <= 0 || n_keys > max_seq)
     return kErrArg;
   std::lock_guard<std::mutex> lk(g_scratch_mu);
-  const int splits = (int)std::min<int64_t>(64, std::max<int64_t>(1, (max_seq + 63) / 64));
+  const int splits = (int)std::min<int64_t>(32, std::max<int64_t>(1, (max_seq + 127) / 128));
   const int G = n_heads / n_kv_heads;
-  // tickets first at a fixed offset (re-armed to zero by the kernel), partials after
-  if (n_kv_heads > 1024) return kErrArg;
   const size_t part = (size_t)n_kv_heads * splits * G * (size_t)(head_dim + 2) * 4;
-  const size_t part_off = 4096;
-  int rc = grow_scratch(part_off + part);
+  int rc = grow_scratch(part);
   if (rc) return rc;
   AttnArgs a{};
   a.q = q;
@@ -207,8 +204,7 @@ int uaii_hip_attention_decode(const float* q, const void* kcache, const void* vc
   a.state = nullptr;
   a.fixed_len = (int)n_keys;
   a.out = out;
-  a.part = reinterpret_cast<float*>(static_cast<char*>(g_scratch) + part_off);
-  a.ticket = static_cast<uint32_t*>(g_scratch);
+  a.part = static_cast<float*>(g_scratch);
   a.splits = splits;
   return (int)launch_attention_decode(a, S(stream));
 }

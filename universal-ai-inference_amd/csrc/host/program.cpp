@@ -106,10 +106,10 @@ void DecoderProgram::free_dynamic() {
     if (g) (void)hipGraphExecDestroy(g);
     g = nullptr;
   }
-  for (void* p : {(void*)kv_, (void*)ids_, (void*)rope_, (void*)attn_part_, (void*)attn_ticket_}) {
+  for (void* p : {(void*)kv_, (void*)ids_, (void*)rope_, (void*)attn_part_}) {
     if (p) (void)hipFree(p);
   }
-  kv_ = nullptr; ids_ = nullptr; rope_ = nullptr; attn_part_ = nullptr; attn_ticket_ = nullptr;
+  kv_ = nullptr; ids_ = nullptr; rope_ = nullptr; attn_part_ = nullptr;
   max_ctx_ = 0;
 }
 
@@ -225,7 +225,6 @@ Error DecoderProgram::build(const DecoderSpec& spec, const ProgramOptions& opts)
   const int lm_blocks = gemv_grid(lm);
   UAII_TRY(alloc(4 * (size_t)lm_blocks, (void**)&lm_part_val_));
   UAII_TRY(alloc(4 * (size_t)lm_blocks, (void**)&lm_part_idx_));
-  UAII_TRY(alloc(4, (void**)&lm_ticket_));
   UAII_HIP(hipStreamSynchronize(stream_));
   int64_t want = opts_.max_context > 0 ? opts_.max_context : d.ctx_len;
   if (want > 0) UAII_TRY(ensure_capacity(want));
@@ -247,12 +246,10 @@ Error DecoderProgram::ensure_capacity(int64_t max_seq) {
   std::vector<float2> tab = rope_table(d.rope_theta, hd, max_seq);
   UAII_HIP(hipMalloc((void**)&rope_, tab.size() * sizeof(float2)));
   UAII_HIP(hipMemcpy(rope_, tab.data(), tab.size() * sizeof(float2), hipMemcpyHostToDevice));
-  attn_splits_ = (int)std::min<int64_t>(64, std::max<int64_t>(1, (max_seq + 63) / 64));
+  attn_splits_ = (int)std::min<int64_t>(32, std::max<int64_t>(1, (max_seq + 127) / 128));
   const int G = (int)(d.n_heads / d.n_kv_heads);
   const size_t part = (size_t)d.n_kv_heads * attn_splits_ * G * (size_t)(hd + 2);
   UAII_HIP(hipMalloc((void**)&attn_part_, part * 4));
-  UAII_HIP(hipMalloc((void**)&attn_ticket_, 4 * (size_t)d.n_kv_heads));
-  UAII_HIP(hipMemsetAsync(attn_ticket_, 0, 4 * (size_t)d.n_kv_heads, stream_));
   UAII_HIP(hipStreamSynchronize(stream_));
   max_ctx_ = max_seq;
   return Error::success();
@@ -286,6 +283,19 @@ Error DecoderProgram::set_token(int64_t token) {
   const int32_t t = (int32_t)token;
   UAII_HIP(hipStreamSynchronize(stream_));
   UAII_HIP(hipMemcpy(&state_->token, &t, 4, hipMemcpyHostToDevice));
+  return Error::success();
+}
+
+Error DecoderProgram::seek(int64_t pos) {
+  StepState st{};
+  UAII_TRY(read_state(&st));
+  if (pos <= 0 || pos > st.pos || pos >= max_ctx_)
+    return Error::make(ErrorCode::InvalidArgument, "seek position out of range");
+  int32_t tok = 0;
+  UAII_HIP(hipMemcpy(&tok, ids_ + pos, 4, hipMemcpyDeviceToHost));
+  st.pos = (int32_t)pos;
+  st.token = tok;
+  UAII_HIP(hipMemcpy(state_, &st, sizeof(st), hipMemcpyHostToDevice));
   return Error::success();
 }
 
@@ -380,7 +390,6 @@ Error DecoderProgram::encode_step(bool want_logits) {
     at.fixed_len = 0;
     at.out = attn_;
     at.part = attn_part_;
-    at.ticket = attn_ticket_;
     at.splits = attn_splits_;
     const double attn_bytes = 2.0 * (double)(pos_host + 1) * (double)d.kv_dim * (double)elem +
                               8.0 * (double)d.q_dim;
@@ -442,7 +451,6 @@ Error DecoderProgram::encode_step(bool want_logits) {
     lm.seg[0].rows = d.vocab;
     lm.part_val = lm_part_val_;
     lm.part_idx = lm_part_idx_;
-    lm.ticket = lm_ticket_;
     lm.ids = ids_;
     lm.state = state_;
     UAII_TRY(timed("gemv_lm_head", gemv_bytes(lm.seg[0].w), [&] { return launch_gemv(lm, s); }));

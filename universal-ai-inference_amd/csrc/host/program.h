@@ -72,6 +72,9 @@ class DecoderProgram {
   Error read_state(uaii_hip::StepState* st);
   // Overwrite the token fed at the current position.
   Error set_token(int64_t token);
+  // Rewind to `pos` (ids and KV below it are kept; ids[pos] is fed next).
+  Error seek(int64_t pos);
+  void set_profile(bool on) { opts_.profile = on; }
   Error read_tap(const std::string& name, std::vector<float>* out);
   std::string profile_summary() const;
   const std::map<std::string, KernelTiming>& timings() const { return timing_; }
@@ -103,7 +106,6 @@ class DecoderProgram {
   int32_t* moe_ids_ = nullptr;
   float* lm_part_val_ = nullptr;
   int32_t* lm_part_idx_ = nullptr;
-  uint32_t* lm_ticket_ = nullptr;
   uaii_hip::StepState* state_ = nullptr;
 
   // sized by ensure_capacity
@@ -113,7 +115,6 @@ class DecoderProgram {
   int32_t* ids_ = nullptr;
   float2* rope_ = nullptr;
   float* attn_part_ = nullptr;
-  uint32_t* attn_ticket_ = nullptr;
   int attn_splits_ = 1;
 
   hipGraphExec_t graph_[2] = {nullptr, nullptr};

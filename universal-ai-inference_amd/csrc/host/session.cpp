@@ -2,6 +2,7 @@
 #include "session.h"
 
 #include <algorithm>
+#include <cstdlib>
 
 namespace uaii {
 namespace runtime {
@@ -29,7 +30,10 @@ Error Session::create(const std::string& gguf_path, SessionOptions options) {
   UAII_TRY(derive_decoder(file_, &spec_));
   ProgramOptions po;
   po.kv_f16 = options_.kv_f16;
-  po.use_graph = options_.use_graph;
+  // UAII_NO_GRAPH=1 launches the step kernels directly instead of replaying the
+  // captured graph (same kernels; for tools that cannot follow stream capture).
+  const char* ng = std::getenv("UAII_NO_GRAPH");
+  po.use_graph = options_.use_graph && !(ng && ng[0] == '1');
   po.profile = options_.enable_profiler;
   po.max_context = options_.max_context;
   program_ = std::make_unique<DecoderProgram>();
@@ -97,6 +101,25 @@ Error Session::generate(const std::vector<int64_t>& prompt, int64_t max_new,
     UAII_TRY(p.step(true));
   }
   return Error::success();
+}
+
+Error Session::begin(const std::vector<int64_t>& prompt, int64_t capacity) {
+  if (!ready_) return Error::make(ErrorCode::InvalidArgument, "session not ready");
+  if (prompt.empty()) return Error::make(ErrorCode::InvalidArgument, "prompt_tokens empty");
+  int64_t cap = capacity > 0 ? capacity : resolve_max_context();
+  if (cap <= 0) cap = (int64_t)prompt.size() + 1;
+  const int64_t max_ctx = resolve_max_context();
+  if (max_ctx > 0 && cap > max_ctx)
+    return Error::make(ErrorCode::InvalidArgument, "capacity exceeds max_context");
+  UAII_TRY(program_->ensure_capacity(cap));
+  UAII_TRY(program_->begin(prompt.data(), (int64_t)prompt.size()));
+  run_started_ = true;
+  return Error::success();
+}
+
+Error Session::step_async(bool want_logits) {
+  if (!ready_ || !run_started_) return Error::make(ErrorCode::InvalidArgument, "session not started");
+  return program_->step(want_logits);
 }
 
 Error Session::set_tensor_f32(const std::string& name, const std::vector<float>& values) {

@@ -76,6 +76,10 @@ class Session {
   Error set_tensor_f32(const std::string& name, const std::vector<float>& values);
   Error get_tensor_f32(const std::string& name, std::vector<float>* values);
   std::string profile_summary() const { return program_ ? program_->profile_summary() : "{}"; }
+
+  // Step-level token loop (uaii_ext.h).
+  Error begin(const std::vector<int64_t>& prompt, int64_t capacity);
+  Error step_async(bool want_logits);
   DecoderProgram* program() { return program_.get(); }
   const DecoderSpec& spec() const { return spec_; }
 

@@ -82,6 +82,14 @@ def lib() -> C.CDLL:
         "uaii_session_generate": (C.c_int, [vp, C.POINTER(i64), C.c_size_t, i64, C.POINTER(i64),
                                             C.c_size_t, C.POINTER(C.c_size_t)]),
         "uaii_session_profile_summary": (C.c_int, [vp, C.c_char_p, C.c_size_t]),
+        "uaii_session_begin": (C.c_int, [vp, C.POINTER(i64), C.c_size_t, i64]),
+        "uaii_session_step_async": (C.c_int, [vp, C.c_int]),
+        "uaii_session_sync": (C.c_int, [vp]),
+        "uaii_session_position": (C.c_int, [vp, C.POINTER(i64)]),
+        "uaii_session_read_ids": (C.c_int, [vp, C.POINTER(i64), C.c_size_t]),
+        "uaii_session_seek": (C.c_int, [vp, i64]),
+        "uaii_session_set_profiling": (C.c_int, [vp, C.c_int]),
+        "uaii_session_last_margin": (C.c_int, [vp, f32p, f32p]),
         "uaii_hip_init": (C.c_int, [C.c_int]),
         "uaii_hip_device_count": (C.c_int, [C.POINTER(C.c_int)]),
         "uaii_hip_error_string": (C.c_char_p, [C.c_int]),
@@ -231,6 +239,46 @@ class Session:
         if rc != 0:
             raise UaiiError(f"get_f32({name}): {L.uaii_last_error().decode()}")
         return out
+
+    def _ok(self, rc, what):
+        if rc != 0:
+            L = lib()
+            raise UaiiError(f"{what}: {L.uaii_status_name(rc).decode()}: {L.uaii_last_error().decode()}")
+
+    def begin(self, prompt, capacity: int = 0):
+        import numpy as np
+        p = np.ascontiguousarray(prompt, dtype=np.int64)
+        self._ok(lib().uaii_session_begin(self.h, p.ctypes.data_as(C.POINTER(C.c_int64)), len(p),
+                                          capacity), "begin")
+
+    def step_async(self, want_logits: bool = True):
+        self._ok(lib().uaii_session_step_async(self.h, int(want_logits)), "step_async")
+
+    def sync(self):
+        self._ok(lib().uaii_session_sync(self.h), "sync")
+
+    def position(self) -> int:
+        v = C.c_int64()
+        self._ok(lib().uaii_session_position(self.h, C.byref(v)), "position")
+        return v.value
+
+    def read_ids(self, n: int):
+        import numpy as np
+        out = np.zeros(max(n, 1), dtype=np.int64)
+        self._ok(lib().uaii_session_read_ids(self.h, out.ctypes.data_as(C.POINTER(C.c_int64)), n),
+                 "read_ids")
+        return out[:n]
+
+    def seek(self, pos: int):
+        self._ok(lib().uaii_session_seek(self.h, pos), "seek")
+
+    def set_profiling(self, on: bool):
+        self._ok(lib().uaii_session_set_profiling(self.h, int(on)), "set_profiling")
+
+    def last_margin(self):
+        b, s2 = C.c_float(), C.c_float()
+        self._ok(lib().uaii_session_last_margin(self.h, C.byref(b), C.byref(s2)), "last_margin")
+        return b.value, s2.value
 
     def profile_summary(self) -> str:
         buf = C.create_string_buffer(1 << 16)
