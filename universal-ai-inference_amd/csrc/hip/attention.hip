@@ -316,6 +316,7 @@ __global__ void __launch_bounds__(256) k_attn_merge(AttnArgs a) {
   __syncthreads();
   for (int d = threadIdx.x; d < hd; d += blockDim.x) {
     float num = 0.0f;
+#pragma unroll 16
     for (int k = 0; k < SB; ++k) num += w[k] * hp[(int64_t)k * G * pstride + d];
     a.out[(int64_t)hq * hd + d] = num * inv_den;
   }

@@ -87,6 +87,24 @@ __device__ inline uint16_t ld_u16(const uint8_t* p) {
   return *reinterpret_cast<const uint16_t*>(p);
 }
 
+// Invoke f.template operator()<T>() for the runtime GGUF type `type`.
+#define UAII_FOR_TYPE(type, BODY)                      \
+  switch (type) {                                      \
+    case T_F32: { constexpr int FT = T_F32; BODY; } break;   \
+    case T_F16: { constexpr int FT = T_F16; BODY; } break;   \
+    case T_Q4_0: { constexpr int FT = T_Q4_0; BODY; } break; \
+    case T_Q4_1: { constexpr int FT = T_Q4_1; BODY; } break; \
+    case T_Q5_0: { constexpr int FT = T_Q5_0; BODY; } break; \
+    case T_Q5_1: { constexpr int FT = T_Q5_1; BODY; } break; \
+    case T_Q8_0: { constexpr int FT = T_Q8_0; BODY; } break; \
+    case T_Q2_K: { constexpr int FT = T_Q2_K; BODY; } break; \
+    case T_Q3_K: { constexpr int FT = T_Q3_K; BODY; } break; \
+    case T_Q4_K: { constexpr int FT = T_Q4_K; BODY; } break; \
+    case T_Q5_K: { constexpr int FT = T_Q5_K; BODY; } break; \
+    case T_Q6_K: { constexpr int FT = T_Q6_K; BODY; } break; \
+    default: break;                                    \
+  }
+
 // Exact-rounding helpers: the reference evaluates dequant products and
 // differences as separate f32 operations; these keep the compiler from fusing
 // them into an FMA where bit-exactness is required.
@@ -128,12 +146,15 @@ struct ChunkOut {
   int n;
 };
 
+// FMT is the weight type as a template constant so every loop bound and array
+// index folds to a constant (no scratch spills).
+template <int FMT>
 __device__ inline void decode_chunk(const DevWeight& w, int64_t r, int64_t t, ChunkOut& o) {
   const uint8_t* a = w.a + r * w.a_row + t * 16;
   uint8_t q[16];
 #pragma unroll
   for (int i = 0; i < 16; ++i) q[i] = a[i];
-  switch (w.type) {
+  switch (FMT) {
     case T_F32: {
       const float* f = reinterpret_cast<const float*>(q);
       for (int i = 0; i < 4; ++i) { o.v[i] = f[i]; o.idx[i] = (int)(4 * t + i); }
@@ -174,7 +195,7 @@ __device__ inline void decode_chunk(const DevWeight& w, int64_t r, int64_t t, Ch
     case T_Q5_0:
     case T_Q5_1: {  // b: 4-byte high bits per block, c: d (Q5_0) or (d, m) (Q5_1)
       const uint32_t hb = *reinterpret_cast<const uint32_t*>(w.b + r * w.b_row + t * 4);
-      const bool one = w.type == T_Q5_1;
+      const bool one = FMT == T_Q5_1;
       const uint8_t* dm = w.c + r * w.c_row + t * (one ? 4 : 2);
       const float d = h2f(ld_u16(dm));
       const float m = one ? h2f(ld_u16(dm + 2)) : 0.0f;
@@ -215,7 +236,7 @@ __device__ inline void decode_chunk(const DevWeight& w, int64_t r, int64_t t, Ch
       const float d1 = fmul_rn(d, (float)sc), m1 = fmul_rn(dmin, (float)mn);
       kscale(2 * cc + 1, meta + 4, sc, mn);
       const float d2 = fmul_rn(d, (float)sc), m2 = fmul_rn(dmin, (float)mn);
-      const uint8_t* qh = (w.type == T_Q5_K) ? w.c + r * w.c_row + sb * 32 : nullptr;
+      const uint8_t* qh = (FMT == T_Q5_K) ? w.c + r * w.c_row + sb * 32 : nullptr;
       for (int i = 0; i < 16; ++i) {
         const int l = 16 * hh + i;
         int lo = q[i] & 15, hi = q[i] >> 4;
@@ -257,7 +278,7 @@ __device__ inline void decode_chunk(const DevWeight& w, int64_t r, int64_t t, Ch
       // Q3_K b: hmask (32 B / sb), c: meta 16 B (scales[12], d, pad).
       const int64_t sb = t / 4;
       const int h = (int)((t % 4) / 2), g = (int)(t % 2);
-      if (w.type == T_Q2_K) {
+      if (FMT == T_Q2_K) {
         const uint8_t* scl = w.b + r * w.b_row + sb * 16;
         const uint8_t* dd = w.c + r * w.c_row + sb * 4;
         const float d = h2f(ld_u16(dd)), dmin = h2f(ld_u16(dd + 2));

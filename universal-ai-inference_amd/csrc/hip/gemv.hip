@@ -340,33 +340,100 @@ __device__ inline void rows_dot(const RowPtr* P, int64_t nch, const float* xsm, 
 // Stage x (optionally RMS-normalised: x * (1/sqrt(mean(x^2)+eps)) * w, two
 // roundings per element as in norm.cpp:122-127) into LDS.
 __device__ inline void stage_x(const GemvArgs& a, float* xsm, float* red) {
+  // Loads are issued in unrolled batches of 8 float4 per thread so a block pays
+  // one memory round trip per batch (a plain strided loop serialises them).
+  constexpr int B = 8;
   const int tid = threadIdx.x, nt = blockDim.x;
-  const int64_t K = a.K;
-  if (a.norm_w == nullptr) {
-    for (int64_t i = tid; i < K / 4; i += nt) {
-      const float4 v = reinterpret_cast<const float4*>(a.x)[i];
-      reinterpret_cast<float4*>(xsm)[i] = v;
-      if (a.xtap && blockIdx.x == 0) reinterpret_cast<float4*>(a.xtap)[i] = v;
+  const int nv = (int)(a.K / 4);
+  const float4* x4 = reinterpret_cast<const float4*>(a.x);
+  const float4* w4 = reinterpret_cast<const float4*>(a.norm_w);
+  float4* s4 = reinterpret_cast<float4*>(xsm);
+  const bool tap = a.xtap && blockIdx.x == 0;
+  const bool norm = a.norm_w != nullptr;
+  const bool w_in_regs = norm && nv <= B * nt;
+  float4 wr[B];
+  float ss = 0.0f;
+  for (int base = 0; base < nv; base += B * nt) {
+    float4 xr[B];
+#pragma unroll
+    for (int j = 0; j < B; ++j) {
+      const int i = base + j * nt + tid;
+      if (i < nv) {
+        xr[j] = x4[i];
+        if (w_in_regs) wr[j] = w4[i];
+      }
     }
+#pragma unroll
+    for (int j = 0; j < B; ++j) {
+      const int i = base + j * nt + tid;
+      if (i < nv) {
+        const float4 v = xr[j];
+        ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+        if (!w_in_regs) {
+          s4[i] = v;
+          if (!norm && tap) reinterpret_cast<float4*>(a.xtap)[i] = v;
+        } else {
+          xr[j] = v;  // kept for the normalisation below
+        }
+      }
+    }
+    if (w_in_regs) {
+      // single batch: finish the norm from registers after the reduction
+      ss = wave_sum(ss);
+      if ((tid & 63) == 0) red[tid >> 6] = ss;
+      __syncthreads();
+      float tot = 0.0f;
+      for (int k = 0; k < (nt >> 6); ++k) tot += red[k];
+      const float inv = 1.0f / sqrtf(tot / (float)a.K + a.eps);
+#pragma unroll
+      for (int j = 0; j < B; ++j) {
+        const int i = base + j * nt + tid;
+        if (i < nv) {
+          float4 v = xr[j];
+          const float4 w = wr[j];
+          v.x = fmul_rn(fmul_rn(v.x, inv), w.x);
+          v.y = fmul_rn(fmul_rn(v.y, inv), w.y);
+          v.z = fmul_rn(fmul_rn(v.z, inv), w.z);
+          v.w = fmul_rn(fmul_rn(v.w, inv), w.w);
+          s4[i] = v;
+          if (tap) reinterpret_cast<float4*>(a.xtap)[i] = v;
+        }
+      }
+      __syncthreads();
+      return;
+    }
+  }
+  if (!norm) {
     __syncthreads();
     return;
   }
-  float ss = 0.0f;
-  for (int64_t i = tid; i < K / 4; i += nt) {
-    const float4 v = reinterpret_cast<const float4*>(a.x)[i];
-    reinterpret_cast<float4*>(xsm)[i] = v;
-    ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
-  }
+  // RMSNorm with K > 8 * 4 * blockDim: second pass over LDS with batched weight loads
   ss = wave_sum(ss);
   if ((tid & 63) == 0) red[tid >> 6] = ss;
   __syncthreads();
   float tot = 0.0f;
-  for (int i = 0; i < (nt >> 6); ++i) tot += red[i];
-  const float inv = 1.0f / sqrtf(tot / (float)K + a.eps);
-  for (int64_t i = tid; i < K; i += nt) {
-    const float v = fmul_rn(fmul_rn(xsm[i], inv), a.norm_w[i]);
-    xsm[i] = v;
-    if (a.xtap && blockIdx.x == 0) a.xtap[i] = v;
+  for (int k = 0; k < (nt >> 6); ++k) tot += red[k];
+  const float inv = 1.0f / sqrtf(tot / (float)a.K + a.eps);
+  for (int base = 0; base < nv; base += B * nt) {
+#pragma unroll
+    for (int j = 0; j < B; ++j) {
+      const int i = base + j * nt + tid;
+      if (i < nv) wr[j] = w4[i];
+    }
+#pragma unroll
+    for (int j = 0; j < B; ++j) {
+      const int i = base + j * nt + tid;
+      if (i < nv) {
+        float4 v = s4[i];
+        const float4 w = wr[j];
+        v.x = fmul_rn(fmul_rn(v.x, inv), w.x);
+        v.y = fmul_rn(fmul_rn(v.y, inv), w.y);
+        v.z = fmul_rn(fmul_rn(v.z, inv), w.z);
+        v.w = fmul_rn(fmul_rn(v.w, inv), w.w);
+        s4[i] = v;
+        if (tap) reinterpret_cast<float4*>(a.xtap)[i] = v;
+      }
+    }
   }
   __syncthreads();
 }
@@ -643,7 +710,11 @@ void plan_blocks(const GemvArgs& a, int* per_seg) {
   for (int k = 0; k < a.nseg; ++k) {
     const int64_t g = (a.seg[k].rows + rpb - 1) / rpb;
     int64_t b = g;
-    if (total > cap) b = std::max<int64_t>(1, (g * cap + total - 1) / total);
+    if (total > cap) {
+      b = std::max<int64_t>(1, (g * cap + total - 1) / total);
+      const int64_t per = (g + b - 1) / b;  // groups per block, then even out the blocks
+      b = (g + per - 1) / per;
+    }
     per_seg[k] = (int)std::min<int64_t>(b, g);
   }
 }

@@ -15,6 +15,7 @@ namespace {
 
 // One block per row: each thread decodes chunks of the embedding row. Bit-exact
 // with the reference's dequant of the token's row.
+template <int FMT>
 __global__ void k_embed(DevWeight w, const StepState* st, const int32_t* ids, float* x,
                         float* tap) {
   const int64_t row = blockIdx.x;
@@ -28,10 +29,13 @@ __global__ void k_embed(DevWeight w, const StepState* st, const int32_t* ids, fl
   const int64_t nch = w.a_row / 16;
   for (int64_t t = threadIdx.x; t < nch; t += blockDim.x) {
     ChunkOut o;
-    decode_chunk(w, tok, t, o);
-    for (int i = 0; i < o.n; ++i) {
-      dst[o.idx[i]] = o.v[i];
-      if (tap) tap[row * w.cols + o.idx[i]] = o.v[i];
+    decode_chunk<FMT>(w, tok, t, o);
+#pragma unroll
+    for (int i = 0; i < 64; ++i) {
+      if (i < o.n) {
+        dst[o.idx[i]] = o.v[i];
+        if (tap) tap[row * w.cols + o.idx[i]] = o.v[i];
+      }
     }
   }
 }
@@ -150,15 +154,16 @@ __global__ void k_rope(float* x, int64_t rows, int64_t dim, int hd, const int32_
 
 hipError_t launch_embed(const DevWeight& w, const StepState* st, float* x, float* tap,
                         hipStream_t s) {
-  hipLaunchKernelGGL(k_embed, dim3(1), dim3(256), 0, s, w, st, (const int32_t*)nullptr, x, tap);
+  UAII_FOR_TYPE(w.type, hipLaunchKernelGGL(k_embed<FT>, dim3(1), dim3(256), 0, s, w, st,
+                                           (const int32_t*)nullptr, x, tap));
   return hipGetLastError();
 }
 
 hipError_t launch_embed_rows(const DevWeight& w, const int32_t* ids, int64_t n, float* x,
                              hipStream_t s) {
   if (n <= 0) return hipSuccess;
-  hipLaunchKernelGGL(k_embed, dim3((unsigned)n), dim3(256), 0, s, w, (const StepState*)nullptr,
-                     ids, x, (float*)nullptr);
+  UAII_FOR_TYPE(w.type, hipLaunchKernelGGL(k_embed<FT>, dim3((unsigned)n), dim3(256), 0, s, w,
+                                           (const StepState*)nullptr, ids, x, (float*)nullptr));
   return hipGetLastError();
 }
 

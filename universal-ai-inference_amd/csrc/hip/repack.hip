@@ -84,15 +84,18 @@ __global__ void k_repack(DevWeight w, const uint8_t* __restrict__ src, int64_t n
 }
 
 // One thread per 16-byte chunk; writes the decoded values to out[r - row0][idx].
+template <int FMT>
 __global__ void k_dequant(DevWeight w, int64_t row0, int64_t nrows, float* __restrict__ out) {
   const int64_t nchunks = w.a_row / 16;
   const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (gid >= nrows * nchunks) return;
   const int64_t rr = gid / nchunks, t = gid % nchunks;
   ChunkOut o;
-  decode_chunk(w, row0 + rr, t, o);
+  decode_chunk<FMT>(w, row0 + rr, t, o);
   float* dst = out + rr * w.cols;
-  for (int i = 0; i < o.n; ++i) dst[o.idx[i]] = o.v[i];
+#pragma unroll
+  for (int i = 0; i < 64; ++i)
+    if (i < o.n) dst[o.idx[i]] = o.v[i];
 }
 
 }  // namespace
@@ -113,7 +116,8 @@ hipError_t launch_dequant(const DevWeight& w, int64_t row0, int64_t nrows, float
   if (total == 0) return hipSuccess;
   const int threads = 256;
   const int64_t grid = (total + threads - 1) / threads;
-  hipLaunchKernelGGL(k_dequant, dim3((unsigned)grid), dim3(threads), 0, s, w, row0, nrows, out);
+  UAII_FOR_TYPE(w.type, hipLaunchKernelGGL(k_dequant<FT>, dim3((unsigned)grid), dim3(threads), 0, s,
+                                           w, row0, nrows, out));
   return hipGetLastError();
 }
 
