@@ -19,7 +19,9 @@
  *   uaii_hip_argmax            greedy sample_token_f32 (libs/uaii-runtime/src/sampling.cpp:38-50)
  *   uaii_hip_rope              rope_f32 (libs/uaii-kernels/src/transformer.cpp:144-220)
  *   uaii_hip_attention_decode  attention_kv_f32, q_seq=1 (transformer.cpp:222-433)
- *   uaii_hip_add / _silu_mul   add_f32 / silu_f32 + mul_f32 (elementwise.cpp:73-110)
+ *   uaii_hip_gemv_add          quant_gemm_f32 + residual add_f32 (elementwise.cpp:86-97)
+ *   uaii_hip_gemv_swiglu       two quant_gemm_f32 + silu_f32 * mul_f32
+ *                              (elementwise.cpp:73-110), the graph's FFN gate/up
  * and the reference ROCm stub's launchers it supersedes
  * (libs/uaii-backends/src/rocm_kernels.hpp:10-14: launch_add_f32, launch_rmsnorm_f32).
  */
@@ -64,6 +66,13 @@ UAII_HIP_API int uaii_hip_gemv(const uaii_hip_weight* w, const float* x, float* 
                                void* stream);
 UAII_HIP_API int uaii_hip_gemv_rmsnorm(const uaii_hip_weight* w, const float* x,
                                        const float* norm_w, float eps, float* y, void* stream);
+/* y[i] += (W . x')[i], x' = x or RMSNorm(x) * norm_w when norm_w is non-NULL. */
+UAII_HIP_API int uaii_hip_gemv_add(const uaii_hip_weight* w, const float* x,
+                                   const float* norm_w, float eps, float* y, void* stream);
+/* y[j] = silu((Wg . x')[j]) * (Wu . x')[j]; wg and wu share type and shape. */
+UAII_HIP_API int uaii_hip_gemv_swiglu(const uaii_hip_weight* wg, const uaii_hip_weight* wu,
+                                      const float* x, const float* norm_w, float eps, float* y,
+                                      void* stream);
 UAII_HIP_API int uaii_hip_gemm(const uaii_hip_weight* w, const float* x, int64_t m, float* y,
                                void* stream);
 UAII_HIP_API int uaii_hip_rmsnorm(const float* x, const float* w, float* y, int64_t rows,
@@ -89,6 +98,7 @@ UAII_HIP_API int uaii_hip_time_gemv(const uaii_hip_weight* w, const float* x, fl
                                     int iters, float* avg_ms);
 UAII_HIP_API int uaii_hip_time_gemm(const uaii_hip_weight* w, const float* x, int64_t m,
                                     float* y, int iters, float* avg_ms);
+/* Device-to-device copy with the library's plain copy kernel (bytes % 16 == 0). */
 UAII_HIP_API int uaii_hip_time_copy(const void* src, void* dst, size_t bytes, int iters,
                                     float* avg_ms);
 

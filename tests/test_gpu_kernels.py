@@ -144,6 +144,60 @@ def test_gemv_rmsnorm_prologue(hip, t):
     assert maxrel(got, want) < 1e-4
 
 
+def oracle_rmsnorm(x, nw, eps=1e-5):
+    xn = np.zeros(x.size, np.float32)
+    oracle.oracle().orc_rmsnorm(oracle._fp(np.ascontiguousarray(x, np.float32)),
+                                oracle._fp(np.ascontiguousarray(nw, np.float32)),
+                                oracle._fp(xn), x.size, eps)
+    return xn
+
+
+@pytest.mark.parametrize("t,rows,cols", [
+    (uaii_amd.Q4_0, 4096, 14336),   # the 8B down projection (K split over 4 waves)
+    (uaii_amd.Q8_0, 1000, 14336),   # two steps per row group
+    (uaii_amd.Q4_0, 333, 11008),    # 6 chunk columns over 4 waves (one wave idle)
+    (uaii_amd.Q6_K, 512, 14336),
+    (uaii_amd.Q4_0, 70, 256),       # one partial column, fewer rows than a group
+], ids=lambda v: str(v))
+@pytest.mark.parametrize("norm", [False, True], ids=["plain", "rmsnorm"])
+def test_gemv_add_epilogue(hip, t, rows, cols, norm):
+    """y += W . x' (residual add of the graph, elementwise.cpp:86-97)."""
+    p = random_packed(t, rows, cols, seed=rows + cols)
+    x = synth.normals(95, 1, 0, cols, 1.0)
+    nw = 1.0 + synth.normals(94, 1, 0, cols, 0.1)
+    y0 = synth.normals(93, 1, 0, rows, 1.0)
+    w = DeviceWeight(t, p, rows, cols)
+    dx, dn, dy = DeviceBuffer.from_array(x), DeviceBuffer.from_array(nw), DeviceBuffer.from_array(y0)
+    check_hip(hip.uaii_hip_gemv_add(w.h, dx.ptr, dn.ptr if norm else None, 1e-5, dy.ptr, None))
+    got = dy.to_array(np.float32, rows)
+    xin = oracle_rmsnorm(x, nw) if norm else x
+    want = y0 + oracle.quant_gemm(t, xin, p, rows, nthreads=0)[0]
+    assert maxrel(got, want) < 1e-4
+
+
+@pytest.mark.parametrize("t", [uaii_amd.Q4_0, uaii_amd.Q8_0, uaii_amd.Q4_K, uaii_amd.Q6_K],
+                         ids=lambda t: uaii_amd.TYPE_NAMES[t])
+def test_gemv_swiglu_epilogue(hip, t):
+    """y = silu(Wg . x') * (Wu . x') (elementwise.cpp:73-110) with the RMSNorm prologue."""
+    rows, cols = 1536, 4096
+    pg = random_packed(t, rows, cols, seed=11)
+    pu = random_packed(t, rows, cols, seed=12)
+    x = synth.normals(92, 1, 0, cols, 2.0)
+    nw = 1.0 + synth.normals(91, 1, 0, cols, 0.1)
+    wg, wu = DeviceWeight(t, pg, rows, cols), DeviceWeight(t, pu, rows, cols)
+    dx, dn, dy = DeviceBuffer.from_array(x), DeviceBuffer.from_array(nw), DeviceBuffer(rows * 4)
+    check_hip(hip.uaii_hip_gemv_swiglu(wg.h, wu.h, dx.ptr, dn.ptr, 1e-5, dy.ptr, None))
+    got = dy.to_array(np.float32, rows)
+    xn = oracle_rmsnorm(x, nw)
+    g = oracle.quant_gemm(t, xn, pg, rows, nthreads=0)[0].astype(np.float64)
+    u = oracle.quant_gemm(t, xn, pu, rows, nthreads=0)[0].astype(np.float64)
+    want = g / (1.0 + np.exp(-g)) * u
+    assert maxrel(got, want) < 1e-4
+    # mismatched gate/up shapes are rejected before any launch
+    wsmall = DeviceWeight(t, pg[: len(pg) // 2], rows // 2, cols)
+    assert hip.uaii_hip_gemv_swiglu(wg.h, wsmall.h, dx.ptr, dn.ptr, 1e-5, dy.ptr, None) != 0
+
+
 def test_rmsnorm_softmax_argmax(hip):
     n = 5000
     x = synth.normals(1, 2, 0, 3 * n, 2.0).reshape(3, n)

@@ -19,12 +19,32 @@
 #include "uaii_hip_internal.h"
 
 #include <algorithm>
+#include <mutex>
+#include <vector>
 
 namespace uaii_hip {
 namespace {
 
+// Tuning knobs (compile-time): resident-block cap per CU for the persistent
+// grid (0 = the runtime's occupancy figure) and the number of units whose
+// weight loads are issued together (1 or 2).
+#ifndef UAII_GEMV_BLOCKS_PER_CU
+#define UAII_GEMV_BLOCKS_PER_CU 0
+#endif
+#ifndef UAII_GEMV_BATCH
+#define UAII_GEMV_BATCH 1
+#endif
+
 constexpr int WPB = 4;  // waves per block
-constexpr int RPW = 4;  // rows per wave (even: RoPE / SwiGLU pairs share a wave)
+constexpr int NB = UAII_GEMV_BATCH;
+static_assert(NB == 1 || NB == 2, "UAII_GEMV_BATCH must be 1 or 2");
+constexpr int RPW_MAX = 4;  // rows per wave (even: RoPE / SwiGLU pairs share a wave)
+
+// Rows per wave by format: the K-quants carry more side data per chunk, so they
+// take two rows per wave to stay within 128 VGPRs.
+__host__ __device__ constexpr int rpw_of(int fmt) {
+  return (fmt == T_Q2_K || fmt == T_Q3_K || fmt == T_Q4_K || fmt == T_Q5_K || fmt == T_Q6_K) ? 2 : 4;
+}
 
 // ---- per-format chunk decode-dot ------------------------------------------------
 
@@ -67,33 +87,35 @@ __device__ inline RowPtr row_ptr(const DevWeight& w, int64_t r) {
   return p;
 }
 
-// Raw per-row data of one chunk (only the fields a format uses stay live).
+// Raw per-row data of one chunk (only the fields a format uses stay live). Only
+// bits are loaded here; every conversion happens where the chunk is decoded, so
+// a unit's loads issue back to back with nothing waiting on them.
 struct Raw {
   uint4 q;     // 16 payload bytes
   uint4 aux;   // side data (format specific)
-  uint4 aux2;  // high-bit planes (Q5_K qh, Q3_K hmask)
-  float s0, s1;
+  uint4 aux2;  // Q5_K qh, Q3_K hmask; Q6_K: the 8 scale bytes of the half block
+  uint32_t s;  // f16 scale bits: d in the low half, m / dmin in the high half
 };
 
 __device__ inline float byte_f(uint32_t w, int k) { return (float)((w >> (8 * k)) & 0xffu); }
+__device__ inline float lo_h(uint32_t s) { return h2f((uint16_t)(s & 0xffffu)); }
+__device__ inline float hi_h(uint32_t s) { return h2f((uint16_t)(s >> 16)); }
 
 template <int FMT>
 __device__ inline void load_raw(const RowPtr& p, int64_t t, Raw& o) {
   o.q = *reinterpret_cast<const uint4*>(p.a + t * 16);
   if constexpr (FMT == T_Q4_0) {
-    o.s0 = h2f(ld_u16(p.b + t * 2));
+    o.s = ld_u16(p.b + t * 2);
   } else if constexpr (FMT == T_Q8_0) {
-    o.s0 = h2f(ld_u16(p.b + (t >> 1) * 2));
+    o.s = ld_u16(p.b + (t >> 1) * 2);
   } else if constexpr (FMT == T_Q4_1) {
-    const uint32_t dm = *reinterpret_cast<const uint32_t*>(p.b + t * 4);
-    o.s0 = h2f((uint16_t)(dm & 0xffff)); o.s1 = h2f((uint16_t)(dm >> 16));
+    o.s = *reinterpret_cast<const uint32_t*>(p.b + t * 4);
   } else if constexpr (FMT == T_Q5_0) {
     o.aux.x = *reinterpret_cast<const uint32_t*>(p.b + t * 4);
-    o.s0 = h2f(ld_u16(p.c + t * 2));
+    o.s = ld_u16(p.c + t * 2);
   } else if constexpr (FMT == T_Q5_1) {
     o.aux.x = *reinterpret_cast<const uint32_t*>(p.b + t * 4);
-    const uint32_t dm = *reinterpret_cast<const uint32_t*>(p.c + t * 4);
-    o.s0 = h2f((uint16_t)(dm & 0xffff)); o.s1 = h2f((uint16_t)(dm >> 16));
+    o.s = *reinterpret_cast<const uint32_t*>(p.c + t * 4);
   } else if constexpr (FMT == T_Q4_K || FMT == T_Q5_K) {
     o.aux = *reinterpret_cast<const uint4*>(p.b + (t >> 3) * 16);
     if constexpr (FMT == T_Q5_K) {
@@ -103,17 +125,34 @@ __device__ inline void load_raw(const RowPtr& p, int64_t t, Raw& o) {
   } else if constexpr (FMT == T_Q6_K) {
     const int64_t sb = t >> 3; const int h = (int)((t & 7) >> 2), u = (int)(t & 3);
     o.aux = *reinterpret_cast<const uint4*>(p.b + sb * 64 + h * 32 + 16 * (u & 1));
-    const int8_t* sc = reinterpret_cast<const int8_t*>(p.c + sb * 16 + h * 8);
-    const float d = h2f(ld_u16(p.d + sb * 2));
-    o.s0 = d * (float)sc[u];
-    o.s1 = d * (float)sc[u + 4];
+    const uint2 sc = *reinterpret_cast<const uint2*>(p.c + sb * 16 + h * 8);
+    o.aux2.x = sc.x; o.aux2.y = sc.y;
+    o.s = ld_u16(p.d + sb * 2);
   } else if constexpr (FMT == T_Q2_K) {
     o.aux = *reinterpret_cast<const uint4*>(p.b + (t >> 2) * 16);  // scales
-    const uint32_t dd = *reinterpret_cast<const uint32_t*>(p.c + (t >> 2) * 4);
-    o.s0 = h2f((uint16_t)(dd & 0xffff)); o.s1 = h2f((uint16_t)(dd >> 16));
+    o.s = *reinterpret_cast<const uint32_t*>(p.c + (t >> 2) * 4);
   } else if constexpr (FMT == T_Q3_K) {
     o.aux = *reinterpret_cast<const uint4*>(p.c + (t >> 2) * 16);  // scales12, d
     o.aux2 = *reinterpret_cast<const uint4*>(p.b + (t >> 2) * 32 + 16 * (t & 1));
+  }
+}
+
+// Per-chunk float scales from the raw bits: s0 = d (Q6_K: d * scale of the
+// chunk's low run), s1 = m / dmin (Q6_K: d * scale of the high run).
+template <int FMT>
+__device__ inline void raw_scales(const Raw& o, int64_t t, float& s0, float& s1) {
+  s0 = 0.0f;
+  s1 = 0.0f;
+  if constexpr (FMT == T_Q4_0 || FMT == T_Q8_0 || FMT == T_Q5_0) {
+    s0 = lo_h(o.s);
+  } else if constexpr (FMT == T_Q4_1 || FMT == T_Q5_1 || FMT == T_Q2_K) {
+    s0 = lo_h(o.s);
+    s1 = hi_h(o.s);
+  } else if constexpr (FMT == T_Q6_K) {
+    const int u = (int)(t & 3);
+    const float d = lo_h(o.s);
+    s0 = d * (float)(int8_t)((o.aux2.x >> (8 * u)) & 0xffu);
+    s1 = d * (float)(int8_t)((o.aux2.y >> (8 * u)) & 0xffu);
   }
 }
 
@@ -143,6 +182,8 @@ __device__ inline void kscale_reg(int j, const uint4& meta, int& sc, int& mn) {
 template <int FMT>
 __device__ inline float chunk_dot(const Raw& o, int64_t t, const float* xv,
                                   const float* xs) {
+  float s0, s1;
+  raw_scales<FMT>(o, t, s0, s1);
   if constexpr (FMT == T_Q4_0 || FMT == T_Q4_1) {
     float s = 0.0f;
 #pragma unroll
@@ -154,8 +195,8 @@ __device__ inline float chunk_dot(const Raw& o, int64_t t, const float* xv,
         s += byte_f((wq >> 4) & 0x0f0f0f0fu, k) * xv[16 + 4 * i + k];
       }
     }
-    if constexpr (FMT == T_Q4_0) return o.s0 * (s - 8.0f * (xs[0] + xs[1]));
-    else return o.s0 * s + o.s1 * (xs[0] + xs[1]);
+    if constexpr (FMT == T_Q4_0) return s0 * (s - 8.0f * (xs[0] + xs[1]));
+    else return s0 * s + s1 * (xs[0] + xs[1]);
   } else if constexpr (FMT == T_Q5_0 || FMT == T_Q5_1) {
     const uint32_t hb = o.aux.x;
     float s = 0.0f;
@@ -166,8 +207,8 @@ __device__ inline float chunk_dot(const Raw& o, int64_t t, const float* xv,
       const uint32_t hi = (b >> 4) | (((hb >> (j + 16)) & 1u) << 4);
       s += (float)lo * xv[j] + (float)hi * xv[16 + j];
     }
-    if constexpr (FMT == T_Q5_0) return o.s0 * (s - 16.0f * (xs[0] + xs[1]));
-    else return o.s0 * s + o.s1 * (xs[0] + xs[1]);
+    if constexpr (FMT == T_Q5_0) return s0 * (s - 16.0f * (xs[0] + xs[1]));
+    else return s0 * s + s1 * (xs[0] + xs[1]);
   } else if constexpr (FMT == T_Q8_0) {
     float s = 0.0f;
 #pragma unroll
@@ -176,7 +217,7 @@ __device__ inline float chunk_dot(const Raw& o, int64_t t, const float* xv,
 #pragma unroll
       for (int k = 0; k < 4; ++k) s += (float)(int8_t)((wq >> (8 * k)) & 0xffu) * xv[4 * i + k];
     }
-    return o.s0 * s;
+    return s0 * s;
   } else if constexpr (FMT == T_Q4_K || FMT == T_Q5_K) {
     const int tt = (int)(t & 7), cc = tt >> 1;
     const float d = h2f((uint16_t)(o.aux.x & 0xffff)), dmin = h2f((uint16_t)(o.aux.x >> 16));
@@ -220,7 +261,7 @@ __device__ inline float chunk_dot(const Raw& o, int64_t t, const float* xv,
       slo += (float)lo * xv[j];
       shi += (float)hi * xv[16 + j];
     }
-    return o.s0 * (slo - 32.0f * xs[0]) + o.s1 * (shi - 32.0f * xs[1]);
+    return s0 * (slo - 32.0f * xs[0]) + s1 * (shi - 32.0f * xs[1]);
   } else if constexpr (FMT == T_Q2_K) {
     const int h = (int)((t & 3) >> 1), g = (int)(t & 1);
     float tot = 0.0f;
@@ -233,7 +274,7 @@ __device__ inline float chunk_dot(const Raw& o, int64_t t, const float* xv,
         const uint32_t b = (word(o.q, l >> 2) >> (8 * (l & 3))) & 0xffu;
         sq += (float)((b >> (2 * p)) & 3u) * xv[16 * p + l];
       }
-      tot += (o.s0 * (float)(s & 15)) * sq - (o.s1 * (float)(s >> 4)) * xs[p];
+      tot += (s0 * (float)(s & 15)) * sq - (s1 * (float)(s >> 4)) * xs[p];
     }
     return tot;
   } else if constexpr (FMT == T_Q3_K) {
@@ -280,57 +321,234 @@ constexpr int xn() {
   return (FMT == T_Q2_K || FMT == T_Q3_K) ? 64 : (FMT == T_Q8_0 ? 16 : (FMT == T_F32 ? 4 : (FMT == T_F16 ? 8 : 32)));
 }
 
+// The staged input lives in LDS as planes: plane g holds the g-th float4 of
+// every chunk's x values, indexed by chunk. The 64 lanes of a wave work on 64
+// consecutive chunks, so each plane read is 64 consecutive float4 (no bank
+// conflicts), where a chunk-contiguous layout would put every lane on the same
+// banks.
 template <int FMT>
-__device__ inline void load_x(const float* __restrict__ xsm, int64_t t, float* xv, float* xsum) {
-  if constexpr (FMT == T_F32 || FMT == T_F16) {
-    constexpr int n = (FMT == T_F32) ? 4 : 8;
-#pragma unroll
-    for (int i = 0; i < n; ++i) xv[i] = xsm[n * t + i];
-    xsum[0] = 0.0f;
+constexpr int xgroups() { return xn<FMT>() / 4; }
+
+// float4 index i of the input (elements 4i..4i+3) -> (chunk t, plane g); the
+// inverse of x_runs: plane g is float4 (g % 4) of run g / 4.
+template <int FMT>
+__device__ inline void plane_of(int64_t i, int64_t& t, int& g) {
+  if constexpr (FMT == T_Q4_0 || FMT == T_Q4_1 || FMT == T_Q5_0 || FMT == T_Q5_1) {
+    t = i >> 3; g = (int)(i & 7);
+  } else if constexpr (FMT == T_Q8_0) {
+    t = i >> 2; g = (int)(i & 3);
+  } else if constexpr (FMT == T_Q4_K || FMT == T_Q5_K) {
+    // i = 64 sb + 16 cc + 8 rr + 4 hh + k
+    const int64_t sb = i >> 6; const int r = (int)(i & 63);
+    t = 8 * sb + 2 * (r >> 4) + ((r >> 2) & 1); g = 4 * ((r >> 3) & 1) + (r & 3);
+  } else if constexpr (FMT == T_Q6_K) {
+    // i = 64 sb + 32 h + 16 rr + 4 u + k
+    const int64_t sb = i >> 6; const int r = (int)(i & 63);
+    t = 8 * sb + 4 * (r >> 5) + ((r >> 2) & 3); g = 4 * ((r >> 4) & 1) + (r & 3);
+  } else if constexpr (FMT == T_Q2_K || FMT == T_Q3_K) {
+    // i = 64 sb + 32 h + 8 p + 4 g' + k
+    const int64_t sb = i >> 6; const int r = (int)(i & 63);
+    t = 4 * sb + 2 * (r >> 5) + ((r >> 2) & 1); g = 4 * ((r >> 3) & 3) + (r & 3);
+  } else if constexpr (FMT == T_F16) {
+    t = i >> 1; g = (int)(i & 1);
   } else {
-    int64_t base[4];
-    const int nr = x_runs<FMT>(t, base);
+    t = i; g = 0;
+  }
+}
+
+template <int FMT>
+__device__ inline int64_t plane_index(int64_t i, int64_t nch) {
+  int64_t t;
+  int g;
+  plane_of<FMT>(i, t, g);
+  return (int64_t)g * nch + t;
+}
+
+// x values of chunk t (runs back to back, 16 each) and the per-run sums.
+template <int FMT>
+__device__ inline void load_x(const float* __restrict__ xsm, int64_t nch, int64_t t, float* xv,
+                              float* xsum) {
+  const float4* pl = reinterpret_cast<const float4*>(xsm);
 #pragma unroll
-    for (int rr = 0; rr < xn<FMT>() / 16; ++rr) {
-      if (rr < nr) {
-        const float4* p = reinterpret_cast<const float4*>(xsm + base[rr]);
-        float s = 0.0f;
+  for (int rr = 0; rr < (xgroups<FMT>() + 3) / 4; ++rr) {
+    float s = 0.0f;
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          const float4 v = p[k];
-          xv[16 * rr + 4 * k + 0] = v.x; xv[16 * rr + 4 * k + 1] = v.y;
-          xv[16 * rr + 4 * k + 2] = v.z; xv[16 * rr + 4 * k + 3] = v.w;
-          s += (v.x + v.y) + (v.z + v.w);
-        }
-        xsum[rr] = s;
+    for (int k = 0; k < 4; ++k) {
+      const int g = 4 * rr + k;
+      if (g < xgroups<FMT>()) {
+        const float4 v = pl[(int64_t)g * nch + t];
+        xv[4 * g + 0] = v.x; xv[4 * g + 1] = v.y;
+        xv[4 * g + 2] = v.z; xv[4 * g + 3] = v.w;
+        s += (v.x + v.y) + (v.z + v.w);
       }
+    }
+    xsum[rr] = s;
+  }
+}
+
+// Logical row L of a QKV segment -> physical row (RoPE pairs adjacent in L).
+__device__ inline int64_t qkv_phys(int64_t L, int mode, int hd) {
+  if (mode != 2) return L;
+  const int64_t P = L >> 1;
+  const int64_t h = P / (hd / 2), p = P % (hd / 2);
+  return h * hd + p + (L & 1) * (hd / 2);
+}
+
+// ---- f16-pair dot for the 4-bit block formats (Q4_0, Q4_1) ------------------------
+//
+// The dot runs on v_dot2_f32_f16. A payload word q (bytes 4i..4i+3 of a block)
+// gives four f16 pairs by masking alone: q & 0x000F000F holds the low nibbles of
+// bytes 0 and 2 as the subnormal halves n * 2^-24 (exact), q & 0x00F000F0 their
+// high nibbles as n * 2^-20, and the same masks on q >> 8 give bytes 1 and 3.
+// The input is scaled per chunk by a power of two S (the chunk's largest |x| * S
+// in [2^14, 2^15); the high-nibble entries by S / 16) and split into f16 hi + lo
+// parts, so every x keeps about 22 significant bits relative to its chunk; both
+// products per element are exact and the sums are f32. A chunk's sum of n * x is
+// then (acc_hi + acc_lo) * c with c = 2^24 / S.
+//
+// LDS: 8 uint4 planes indexed by chunk (word i: plane 2i = hi pairs, 2i+1 = lo
+// pairs, in the order (x[4i], x[4i+2]), (x[16+4i], x[16+4i+2]) / 16,
+// (x[4i+1], x[4i+3]), (x[16+4i+1], x[16+4i+3]) / 16), then one float2 per chunk:
+// (sum of the block's 32 unscaled inputs, c).
+
+typedef _Float16 h2v __attribute__((ext_vector_type(2)));
+
+template <int FMT>
+__host__ __device__ constexpr bool pair_fmt() { return FMT == T_Q4_0 || FMT == T_Q4_1; }
+
+__device__ inline float dot2(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2v, a), __builtin_bit_cast(h2v, b), c, false);
+}
+
+// 2^k for -126 <= k <= 127
+__device__ inline float pow2f(int k) { return __uint_as_float((uint32_t)(k + 127) << 23); }
+
+__device__ inline uint32_t hbits(_Float16 h) { return (uint32_t)__builtin_bit_cast(uint16_t, h); }
+
+// (a, b) -> f16 pairs hi = (f16(a), f16(b)), lo = (f16(a - hi.a), f16(b - hi.b)).
+__device__ inline void split2(float a, float b, uint32_t& hi, uint32_t& lo) {
+  const _Float16 ah = (_Float16)a, bh = (_Float16)b;
+  const _Float16 al = (_Float16)(a - (float)ah), bl = (_Float16)(b - (float)bh);
+  hi = hbits(ah) | (hbits(bh) << 16);
+  lo = hbits(al) | (hbits(bl) << 16);
+}
+
+__device__ inline void load_xpairs(const float* __restrict__ xsm, int64_t nch, int64_t t, uint4* xp,
+                                   float2& xc) {
+  const uint4* pl = reinterpret_cast<const uint4*>(xsm);
+#pragma unroll
+  for (int g = 0; g < 8; ++g) xp[g] = pl[(int64_t)g * nch + t];
+  xc = reinterpret_cast<const float2*>(pl + 8 * nch)[t];
+}
+
+template <int FMT>
+__device__ inline float chunk_dot_pairs(const Raw& o, const uint4* xp, float2 xc) {
+  const float xs = xc.x, c = xc.y;
+  float sh = 0.0f, sl = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t q = word(o.q, i), q8 = q >> 8;
+    const uint32_t p0 = q & 0x000F000Fu, p1 = q & 0x00F000F0u;
+    const uint32_t p2 = q8 & 0x000F000Fu, p3 = q8 & 0x00F000F0u;
+    const uint4 H = xp[2 * i], L = xp[2 * i + 1];
+    sh = dot2(p0, H.x, sh); sl = dot2(p0, L.x, sl);
+    sh = dot2(p1, H.y, sh); sl = dot2(p1, L.y, sl);
+    sh = dot2(p2, H.z, sh); sl = dot2(p2, L.z, sl);
+    sh = dot2(p3, H.w, sh); sl = dot2(p3, L.w, sl);
+  }
+  const float s = (sh + sl) * c;  // sum of n * x
+  if constexpr (FMT == T_Q4_0) return lo_h(o.s) * (s - 8.0f * xs);
+  else return lo_h(o.s) * s + hi_h(o.s) * xs;
+}
+
+// ---- walk over row groups ------------------------------------------------------------
+//
+// A block's WPB waves form WPB/ks row sets of RPW rows; the ks waves of one row set
+// split the row's 64-chunk columns between them (ks > 1 for long rows, so a row
+// group costs one memory round trip, not several). A wave's work is a sequence of
+// units (row group, step); one step covers two chunk columns, i.e. chunks t and
+// t + 64 of each of its rows for lane l = t % 64. Units go in batches of NB: the
+// loads of a whole batch are issued before any of it is decoded (and the first
+// unit's before the input vector is staged), and no loaded data is carried from
+// one batch to the next, so the compiler never has to wait to reuse registers.
+
+struct Walk {
+  int64_t nch;     // 16-byte chunks per row
+  int cbeg, cend;  // this wave's chunk columns [cbeg, cend)
+  int steps;       // steps per row group (the same for every wave of the block)
+};
+
+template <int FMT>
+struct UnitBuf {
+  Raw r[2][rpw_of(FMT)];
+};
+
+// Wave-uniform row pointers of logical rows l0 .. l0+R-1 of a segment.
+template <int EPI, int R>
+__device__ inline void unit_rows(const GemvArgs& a, const GemvSeg& seg, int64_t l0, RowPtr* P) {
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    int64_t l = l0 + r;
+    if (l >= seg.rows) l = seg.rows - 1;  // clamp: duplicate work, result dropped
+    if constexpr (EPI == EPI_SWIGLU) {
+      P[r] = row_ptr((l & 1) ? seg.w2 : seg.w, l >> 1);
+    } else if constexpr (EPI == EPI_QKV) {
+      P[r] = row_ptr(seg.w, seg.kind == 2 ? l : qkv_phys(l, a.rope_mode, a.head_dim));
+    } else {
+      P[r] = row_ptr(seg.w, l);
     }
   }
 }
 
-// Accumulate RPW row dots over the row payloads; lane l takes chunks l, l+64, ...
-// Two chunks per iteration so each lane has 2*RPW 16-byte loads in flight.
+template <int FMT, int EPI>
+__device__ inline void load_unit(const GemvArgs& a, const GemvSeg& seg, const Walk& wk,
+                                 int64_t l0, int step, int lane, UnitBuf<FMT>& U) {
+  constexpr int R = rpw_of(FMT);
+  RowPtr P[R];
+  unit_rows<EPI, R>(a, seg, l0, P);
+  // Straight-line loads: a column past the wave's range, or a lane past the row's
+  // last chunk, loads an in-bounds chunk again and compute_unit drops it. (A
+  // branch around some of the loads would make the compiler's wait counts
+  // conservative at the join and serialise the unit's loads.)
+  const int ncol = (int)((wk.nch + 63) / 64);
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int col = min(wk.cbeg + 2 * step + j, ncol - 1);
+    const int64_t t = min((int64_t)col * 64 + lane, wk.nch - 1);
+#pragma unroll
+    for (int r = 0; r < R; ++r) load_raw<FMT>(P[r], t, U.r[j][r]);
+  }
+}
+
 template <int FMT>
-__device__ inline void rows_dot(const RowPtr* P, int64_t nch, const float* xsm, int lane,
-                                float* acc) {
-  for (int64_t t = lane; t < nch; t += 128) {
-    const bool two = t + 64 < nch;
-    Raw r0[RPW], r1[RPW];
+__device__ inline void compute_unit(const Walk& wk, int step, int lane, const float* xsm,
+                                    const UnitBuf<FMT>& U, float* acc) {
 #pragma unroll
-    for (int r = 0; r < RPW; ++r) load_raw<FMT>(P[r], t, r0[r]);
-    if (two) {
+  for (int j = 0; j < 2; ++j) {
+    const int col = wk.cbeg + 2 * step + j;  // wave-uniform
+    {
+      const int64_t t0 = (int64_t)min(col, (int)((wk.nch + 63) / 64) - 1) * 64 + lane;
+      const bool ok = col < wk.cend && t0 < wk.nch;
+      const int64_t t = t0 < wk.nch ? t0 : wk.nch - 1;
+      if constexpr (pair_fmt<FMT>()) {
+        uint4 xp[8];
+        float2 xc;
+        load_xpairs(xsm, wk.nch, t, xp, xc);
 #pragma unroll
-      for (int r = 0; r < RPW; ++r) load_raw<FMT>(P[r], t + 64, r1[r]);
-    }
-    float xv[xn<FMT>()];
-    float xsum[4];
-    load_x<FMT>(xsm, t, xv, xsum);
+        for (int r = 0; r < rpw_of(FMT); ++r) {
+          const float v = chunk_dot_pairs<FMT>(U.r[j][r], xp, xc);
+          acc[r] += ok ? v : 0.0f;
+        }
+      } else {
+        float xv[xn<FMT>()];
+        float xsum[4];
+        load_x<FMT>(xsm, wk.nch, t, xv, xsum);
 #pragma unroll
-    for (int r = 0; r < RPW; ++r) acc[r] += chunk_dot<FMT>(r0[r], t, xv, xsum);
-    if (two) {
-      load_x<FMT>(xsm, t + 64, xv, xsum);
-#pragma unroll
-      for (int r = 0; r < RPW; ++r) acc[r] += chunk_dot<FMT>(r1[r], t + 64, xv, xsum);
+        for (int r = 0; r < rpw_of(FMT); ++r) {
+          const float v = chunk_dot<FMT>(U.r[j][r], t, xv, xsum);
+          acc[r] += ok ? v : 0.0f;
+        }
+      }
     }
   }
 }
@@ -339,10 +557,11 @@ __device__ inline void rows_dot(const RowPtr* P, int64_t nch, const float* xsm, 
 
 // Stage x (optionally RMS-normalised: x * (1/sqrt(mean(x^2)+eps)) * w, two
 // roundings per element as in norm.cpp:122-127) into LDS.
-__device__ inline void stage_x(const GemvArgs& a, float* xsm, float* red) {
-  // Loads are issued in unrolled batches of 8 float4 per thread so a block pays
+template <int FMT>
+__device__ inline void stage_x(const GemvArgs& a, int64_t nch, float* xsm, float* red) {
+  // Loads are issued in unrolled batches of 4 float4 per thread so a block pays
   // one memory round trip per batch (a plain strided loop serialises them).
-  constexpr int B = 8;
+  constexpr int B = 4;
   const int tid = threadIdx.x, nt = blockDim.x;
   const int nv = (int)(a.K / 4);
   const float4* x4 = reinterpret_cast<const float4*>(a.x);
@@ -370,7 +589,7 @@ __device__ inline void stage_x(const GemvArgs& a, float* xsm, float* red) {
         const float4 v = xr[j];
         ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
         if (!w_in_regs) {
-          s4[i] = v;
+          s4[plane_index<FMT>(i, nch)] = v;
           if (!norm && tap) reinterpret_cast<float4*>(a.xtap)[i] = v;
         } else {
           xr[j] = v;  // kept for the normalisation below
@@ -395,7 +614,7 @@ __device__ inline void stage_x(const GemvArgs& a, float* xsm, float* red) {
           v.y = fmul_rn(fmul_rn(v.y, inv), w.y);
           v.z = fmul_rn(fmul_rn(v.z, inv), w.z);
           v.w = fmul_rn(fmul_rn(v.w, inv), w.w);
-          s4[i] = v;
+          s4[plane_index<FMT>(i, nch)] = v;
           if (tap) reinterpret_cast<float4*>(a.xtap)[i] = v;
         }
       }
@@ -407,7 +626,7 @@ __device__ inline void stage_x(const GemvArgs& a, float* xsm, float* red) {
     __syncthreads();
     return;
   }
-  // RMSNorm with K > 8 * 4 * blockDim: second pass over LDS with batched weight loads
+  // RMSNorm with K > 4 * 4 * blockDim: second pass over LDS with batched weight loads
   ss = wave_sum(ss);
   if ((tid & 63) == 0) red[tid >> 6] = ss;
   __syncthreads();
@@ -424,13 +643,14 @@ __device__ inline void stage_x(const GemvArgs& a, float* xsm, float* red) {
     for (int j = 0; j < B; ++j) {
       const int i = base + j * nt + tid;
       if (i < nv) {
-        float4 v = s4[i];
+        const int64_t pi = plane_index<FMT>(i, nch);
+        float4 v = s4[pi];
         const float4 w = wr[j];
         v.x = fmul_rn(fmul_rn(v.x, inv), w.x);
         v.y = fmul_rn(fmul_rn(v.y, inv), w.y);
         v.z = fmul_rn(fmul_rn(v.z, inv), w.z);
         v.w = fmul_rn(fmul_rn(v.w, inv), w.w);
-        s4[i] = v;
+        s4[pi] = v;
         if (tap) reinterpret_cast<float4*>(a.xtap)[i] = v;
       }
     }
@@ -438,20 +658,248 @@ __device__ inline void stage_x(const GemvArgs& a, float* xsm, float* red) {
   __syncthreads();
 }
 
+// Staging of a pair format. Item (t, w) is the float4s x[8t + w] and x[8t + 4 + w]
+// (elements 32t+4w.. and 32t+16+4w..); the four items of chunk t sit on four
+// consecutive lanes. The first PB items per thread are loaded into registers by
+// stage_pairs_issue, before the block's first weight loads, so waiting for them
+// never waits for the weights.
+constexpr int PB = 4;   // items per thread in the register batch
+constexpr int PBW = 2;  // items per thread whose RMSNorm weights ride along
+
+struct PairStage {
+  float4 xa[PB], xb[PB];
+  float4 wa[PBW], wb[PBW];
+};
+
+template <int FMT>
+__device__ inline void stage_pairs_issue(const GemvArgs& a, int64_t nch, PairStage& ps) {
+  const int tid = threadIdx.x, nt = blockDim.x;
+  const int64_t items = nch * 4;
+  const float4* x4 = reinterpret_cast<const float4*>(a.x);
+  const float4* w4 = reinterpret_cast<const float4*>(a.norm_w);
+#pragma unroll
+  for (int k = 0; k < PB; ++k) {
+    const int64_t it = (int64_t)k * nt + tid;
+    if (it < items) {
+      const int64_t i0 = 8 * (it >> 2) + (it & 3);
+      ps.xa[k] = x4[i0];
+      ps.xb[k] = x4[i0 + 4];
+    }
+  }
+  if (w4 && items <= (int64_t)PBW * nt) {
+#pragma unroll
+    for (int k = 0; k < PBW; ++k) {
+      const int64_t it = (int64_t)k * nt + tid;
+      if (it < items) {
+        const int64_t i0 = 8 * (it >> 2) + (it & 3);
+        ps.wa[k] = w4[i0];
+        ps.wb[k] = w4[i0 + 4];
+      }
+    }
+  }
+}
+
+// One item: RMSNorm (two roundings, norm.cpp:122-127), the optional tap, the
+// chunk's power-of-two scale (max over the chunk's four lanes), the hi/lo split
+// into the planes, and the chunk's (sum, c) from the lane holding word 0.
+__device__ inline void emit_pair_item(const GemvArgs& a, int64_t nch, int64_t it, bool valid, float4 u,
+                                      float4 v, float4 uw, float4 vw, bool norm, float inv, bool tap,
+                                      float* xsm) {
+  const int64_t t = it >> 2;
+  const int w = (int)(it & 3);
+  if (norm) {
+    u.x = fmul_rn(fmul_rn(u.x, inv), uw.x); u.y = fmul_rn(fmul_rn(u.y, inv), uw.y);
+    u.z = fmul_rn(fmul_rn(u.z, inv), uw.z); u.w = fmul_rn(fmul_rn(u.w, inv), uw.w);
+    v.x = fmul_rn(fmul_rn(v.x, inv), vw.x); v.y = fmul_rn(fmul_rn(v.y, inv), vw.y);
+    v.z = fmul_rn(fmul_rn(v.z, inv), vw.z); v.w = fmul_rn(fmul_rn(v.w, inv), vw.w);
+  }
+  float m = 0.0f, psum = 0.0f;
+  if (valid) {
+    m = fmaxf(fmaxf(fmaxf(fabsf(u.x), fabsf(u.y)), fmaxf(fabsf(u.z), fabsf(u.w))),
+              fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    psum = ((u.x + u.y) + (u.z + u.w)) + ((v.x + v.y) + (v.z + v.w));
+  }
+  m = fmaxf(m, __shfl_xor(m, 1, 64));
+  m = fmaxf(m, __shfl_xor(m, 2, 64));
+  psum += __shfl_xor(psum, 1, 64);
+  psum += __shfl_xor(psum, 2, 64);
+  if (!valid) return;
+  const int64_t i0 = 8 * t + w;
+  if (tap) {
+    reinterpret_cast<float4*>(a.xtap)[i0] = u;
+    reinterpret_cast<float4*>(a.xtap)[i0 + 4] = v;
+  }
+  // S = 2^sh with m * S in [2^14, 2^15) (m = m' * 2^e, m' in [0.5, 1), read from
+  // the bits; the small margin covers rounding); c = 2^24 / S
+  const int e = (int)((__float_as_uint(m * 1.001f) >> 23) & 0xffu) - 126;
+  const int sh = (m > 0.0f) ? max(-100, min(100, 15 - e)) : 0;
+  const float sl_ = pow2f(sh), sh_ = pow2f(sh - 4);
+  uint32_t h0, l0, h1, l1, h2, l2, h3, l3;
+  split2(u.x * sl_, u.z * sl_, h0, l0);
+  split2(v.x * sh_, v.z * sh_, h1, l1);
+  split2(u.y * sl_, u.w * sl_, h2, l2);
+  split2(v.y * sh_, v.w * sh_, h3, l3);
+  uint4* pl = reinterpret_cast<uint4*>(xsm);
+  pl[(int64_t)(2 * w) * nch + t] = make_uint4(h0, h1, h2, h3);
+  pl[(int64_t)(2 * w + 1) * nch + t] = make_uint4(l0, l1, l2, l3);
+  if (w == 0) reinterpret_cast<float2*>(pl + 8 * nch)[t] = make_float2(psum, pow2f(24 - sh));
+}
+
+template <int FMT>
+__device__ inline void stage_pairs_finish(const GemvArgs& a, int64_t nch, const PairStage& ps,
+                                          float* xsm, float* red) {
+  const int tid = threadIdx.x, nt = blockDim.x;
+  const int64_t items = nch * 4;
+  const float4* x4 = reinterpret_cast<const float4*>(a.x);
+  const float4* w4 = reinterpret_cast<const float4*>(a.norm_w);
+  const bool norm = w4 != nullptr;
+  const bool wregs = items <= (int64_t)PBW * nt;  // norm weights of every item in registers
+  const bool tap = a.xtap && blockIdx.x == 0;
+  const float4 one = make_float4(1.0f, 1.0f, 1.0f, 1.0f);
+  float inv = 1.0f;
+  if (norm) {
+    float ss = 0.0f;
+    if (wregs) {
+#pragma unroll
+      for (int k = 0; k < PBW; ++k) {
+        if ((int64_t)k * nt + tid < items) {
+          const float4 u = ps.xa[k], v = ps.xb[k];
+          ss += (u.x * u.x + u.y * u.y) + (u.z * u.z + u.w * u.w) + (v.x * v.x + v.y * v.y) +
+                (v.z * v.z + v.w * v.w);
+        }
+      }
+    } else {
+      for (int64_t it = tid; it < items; it += nt) {
+        const int64_t i0 = 8 * (it >> 2) + (it & 3);
+        const float4 u = x4[i0], v = x4[i0 + 4];
+        ss += (u.x * u.x + u.y * u.y) + (u.z * u.z + u.w * u.w) + (v.x * v.x + v.y * v.y) +
+              (v.z * v.z + v.w * v.w);
+      }
+    }
+    ss = wave_sum(ss);
+    if ((tid & 63) == 0) red[tid >> 6] = ss;
+    __syncthreads();
+    float tot = 0.0f;
+    for (int k = 0; k < (nt >> 6); ++k) tot += red[k];
+    inv = 1.0f / sqrtf(tot / (float)a.K + a.eps);
+  }
+  // register batch
+#pragma unroll
+  for (int k = 0; k < PB; ++k) {
+    const int64_t it = (int64_t)k * nt + tid;
+    if ((int64_t)k * nt < items) {  // block-uniform; the shuffles need all lanes
+      float4 uw = one, vw = one;
+      if (norm) {
+        if (k < PBW && wregs) { uw = ps.wa[k < PBW ? k : 0]; vw = ps.wb[k < PBW ? k : 0]; }
+        else if (it < items) {
+          const int64_t i0 = 8 * (it >> 2) + (it & 3);
+          uw = w4[i0]; vw = w4[i0 + 4];
+        }
+      }
+      emit_pair_item(a, nch, it, it < items, ps.xa[k], ps.xb[k], uw, vw, norm, inv, tap, xsm);
+    }
+  }
+  // the rest (rows longer than PB * 4 * 32 * nt / 4 elements)
+  for (int64_t base = (int64_t)PB * nt; base < items; base += nt) {
+    const int64_t it = base + tid;
+    const bool valid = it < items;
+    float4 u = one, v = one, uw = one, vw = one;
+    if (valid) {
+      const int64_t i0 = 8 * (it >> 2) + (it & 3);
+      u = x4[i0]; v = x4[i0 + 4];
+      if (norm) { uw = w4[i0]; vw = w4[i0 + 4]; }
+    }
+    emit_pair_item(a, nch, it, valid, u, v, uw, vw, norm, inv, tap, xsm);
+  }
+  __syncthreads();
+}
+
 // ---- epilogues ----------------------------------------------------------------------
 
-// Logical row L of a QKV segment -> physical row (RoPE pairs adjacent in L).
-__device__ inline int64_t qkv_phys(int64_t L, int mode, int hd) {
-  if (mode != 2) return L;
-  const int64_t P = L >> 1;
-  const int64_t h = P / (hd / 2), p = P % (hd / 2);
-  return h * hd + p + (L & 1) * (hd / 2);
+// Output side of one finished row group; acc[] holds the wave-uniform full dots
+// of logical rows lrow0 .. lrow0+R-1.
+template <int EPI, int R>
+__device__ inline void epilogue(const GemvArgs& a, const GemvSeg& seg, int64_t lrow0, int lane,
+                                const float* acc, float& best_v, int32_t& best_i) {
+  if constexpr (EPI == EPI_STORE || EPI == EPI_ADD || EPI == EPI_LOGITS) {
+    if (lane < R) {
+      float v = 0.0f;
+#pragma unroll
+      for (int r = 0; r < R; ++r) if (r == lane) v = acc[r];
+      const int64_t l = lrow0 + lane;
+      if (l < seg.rows) {
+        const int64_t o = seg.row_base + l;
+        if constexpr (EPI == EPI_ADD) v = a.y[o] + v;
+        a.y[o] = v;
+        if (a.tap) a.tap[o] = v;
+      }
+    }
+    if constexpr (EPI == EPI_LOGITS) {
+      // running greedy argmax of this wave (rows ascend, strict '>' keeps the lowest)
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const int64_t l = lrow0 + r;
+        if (l < seg.rows && (best_i == 0x7fffffff || acc[r] > best_v)) { best_v = acc[r]; best_i = (int32_t)l; }
+      }
+    }
+  } else if constexpr (EPI == EPI_SWIGLU) {
+    // pairs (gate, up) at logical rows (2j, 2j+1)
+    if (lane < R / 2) {
+      float g = 0.0f, u = 0.0f;
+#pragma unroll
+      for (int r = 0; r < R; r += 2) if (r == 2 * lane) { g = acc[r]; u = acc[r + 1]; }
+      const int64_t l = lrow0 + 2 * lane;
+      if (l < seg.rows) {
+        const float act = g / (1.0f + expf(-g));  // silu (elementwise.cpp:73-84)
+        a.y[seg.row_base + (l >> 1)] = act * u;
+      }
+    }
+  } else if constexpr (EPI == EPI_QKV) {
+    if (lane < R / 2) {
+      float v0 = 0.0f, v1 = 0.0f;
+#pragma unroll
+      for (int r = 0; r < R; r += 2) if (r == 2 * lane) { v0 = acc[r]; v1 = acc[r + 1]; }
+      const int64_t l = lrow0 + 2 * lane;
+      if (l < seg.rows) {
+        const int64_t r0 = (seg.kind == 2) ? l : qkv_phys(l, a.rope_mode, a.head_dim);
+        const int64_t r1 = (seg.kind == 2) ? l + 1 : qkv_phys(l + 1, a.rope_mode, a.head_dim);
+        if (seg.bias) { v0 = v0 + seg.bias[r0]; v1 = v1 + seg.bias[r1]; }
+        const int pos = a.state->pos;
+        if (seg.kind != 2) {
+          // rotate pair p of its head by the host-built angle table
+          const int64_t p = (a.rope_mode == 2) ? (r0 % a.head_dim) : ((r0 % a.head_dim) >> 1);
+          const float2 cs = a.rope[(int64_t)pos * (a.head_dim / 2) + p];
+          const float n0 = v0 * cs.x - v1 * cs.y;
+          const float n1 = v0 * cs.y + v1 * cs.x;
+          v0 = n0; v1 = n1;
+        }
+        if (seg.kind == 0) {
+          a.y[r0] = v0;
+          a.y[r1] = v1;
+        } else {
+          // K after RoPE and raw V go to the cache at `pos` (gguf.cpp:1043, dispatch.cpp:218)
+          void* cache = (seg.kind == 1) ? a.kcache : a.vcache;
+          const int64_t hd = a.head_dim;
+          const int64_t o0 = ((r0 / hd) * a.max_seq + pos) * hd + (r0 % hd);
+          const int64_t o1 = ((r1 / hd) * a.max_seq + pos) * hd + (r1 % hd);
+          if (a.kv_f16) {
+            reinterpret_cast<__half*>(cache)[o0] = __float2half(v0);
+            reinterpret_cast<__half*>(cache)[o1] = __float2half(v1);
+          } else {
+            reinterpret_cast<float*>(cache)[o0] = v0;
+            reinterpret_cast<float*>(cache)[o1] = v1;
+          }
+        }
+      }
+    }
+  }
 }
 
 template <int FMT, int EPI>
 __global__ void __launch_bounds__(WPB * 64) k_gemv(GemvArgs a) {
   extern __shared__ float xsm[];
-  __shared__ float red[WPB];
+  __shared__ float red[2 * WPB];
+  __shared__ float kred[2][WPB][RPW_MAX];
   __shared__ float bval[WPB];
   __shared__ int32_t bidx[WPB];
 
@@ -460,108 +908,108 @@ __global__ void __launch_bounds__(WPB * 64) k_gemv(GemvArgs a) {
   for (int k = 1; k < a.nseg; ++k) if ((int)blockIdx.x >= a.seg[k].block0) si = k;
   const GemvSeg& seg = a.seg[si];
   const int nblk = (si + 1 < a.nseg ? a.seg[si + 1].block0 : (int)gridDim.x) - seg.block0;
-  const int64_t ngroups = (seg.rows + WPB * RPW - 1) / (WPB * RPW);
 
-  stage_x(a, xsm, red);
-
+  constexpr int RPW = rpw_of(FMT);
+  const int ks = a.ksplit;
+  const int nrs = WPB / ks;  // row sets per block
+  const int64_t ngroups = (seg.rows + nrs * RPW - 1) / (nrs * RPW);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
+  const int rs = wave / ks, kp = wave % ks;
+
+  Walk wk;
+  wk.nch = seg.w.a_row / 16;
+  const int ncol = (int)((wk.nch + 63) / 64);
+  const int per = (ncol + ks - 1) / ks;
+  wk.cbeg = kp * per;
+  wk.cend = min(ncol, wk.cbeg + per);
+  wk.steps = (per + 1) / 2;
+
+  const int64_t g0 = (int64_t)blockIdx.x - seg.block0;
+  const int64_t mine = (g0 < ngroups) ? (ngroups - g0 + nblk - 1) / nblk : 0;
+  const int64_t nunits = mine * wk.steps;
+
+  auto unit_l0 = [&](int64_t u) { return ((g0 + (u / wk.steps) * nblk) * nrs + rs) * RPW; };
+  auto unit_step = [&](int64_t u) { return (int)(u % wk.steps); };
+
+  // input loads first, then the first unit's weight loads, then the staging
+  // arithmetic (which waits for the input only)
+  UnitBuf<FMT> U0;
+  if constexpr (pair_fmt<FMT>()) {
+    PairStage ps;
+    stage_pairs_issue<FMT>(a, wk.nch, ps);
+    if (nunits > 0) load_unit<FMT, EPI>(a, seg, wk, unit_l0(0), 0, lane, U0);
+    stage_pairs_finish<FMT>(a, wk.nch, ps, xsm, red);
+  } else {
+    if (nunits > 0) load_unit<FMT, EPI>(a, seg, wk, unit_l0(0), 0, lane, U0);
+    stage_x<FMT>(a, wk.nch, xsm, red);
+  }
+
   float best_v = -INFINITY;
   int32_t best_i = 0x7fffffff;
+  float acc[RPW];
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) acc[r] = 0.0f;
 
-  // persistent loop: this block takes row groups blk, blk + nblk, ...
-  for (int64_t grp = blockIdx.x - seg.block0; grp < ngroups; grp += nblk) {
-    const int64_t lrow0 = (grp * WPB + wave) * RPW;
-    RowPtr P[RPW];
-#pragma unroll
-    for (int r = 0; r < RPW; ++r) {
-      int64_t l = lrow0 + r;
-      if (l >= seg.rows) l = seg.rows - 1;  // clamp: duplicate work, result dropped
-      if constexpr (EPI == EPI_SWIGLU) {
-        P[r] = row_ptr((l & 1) ? seg.w2 : seg.w, l >> 1);
-      } else if constexpr (EPI == EPI_QKV) {
-        P[r] = row_ptr(seg.w, seg.kind == 2 ? l : qkv_phys(l, a.rope_mode, a.head_dim));
-      } else {
-        P[r] = row_ptr(seg.w, l);
-      }
-    }
-    float acc[RPW];
-#pragma unroll
-    for (int r = 0; r < RPW; ++r) acc[r] = 0.0f;
-    rows_dot<FMT>(P, seg.w.a_row / 16, xsm, lane, acc);
+  // unit u -> (group index i = u / steps, step = u % steps); row group g0 + i * nblk
+  auto finish = [&](int64_t u) {
+    const int64_t i = u / wk.steps;
+    if (u - i * wk.steps != wk.steps - 1) return;
 #pragma unroll
     for (int r = 0; r < RPW; ++r) acc[r] = wave_sum(acc[r]);
-
-    if constexpr (EPI == EPI_STORE || EPI == EPI_ADD || EPI == EPI_LOGITS) {
-      if (lane < RPW) {
-        float v = 0.0f;
+    if (ks > 1) {
+      const int par = (int)(i & 1);
+      if (lane == 0) {
 #pragma unroll
-        for (int r = 0; r < RPW; ++r) if (r == lane) v = acc[r];
-        const int64_t l = lrow0 + lane;
-        if (l < seg.rows) {
-          const int64_t o = seg.row_base + l;
-          if constexpr (EPI == EPI_ADD) v = a.y[o] + v;
-          a.y[o] = v;
-          if (a.tap) a.tap[o] = v;
-        }
+        for (int r = 0; r < RPW; ++r) kred[par][wave][r] = acc[r];
       }
-      if constexpr (EPI == EPI_LOGITS) {
-        // running greedy argmax of this wave (rows ascend, strict '>' keeps the lowest)
+      __syncthreads();
+      if (kp == 0) {
 #pragma unroll
         for (int r = 0; r < RPW; ++r) {
-          const int64_t l = lrow0 + r;
-          if (l < seg.rows && (best_i == 0x7fffffff || acc[r] > best_v)) { best_v = acc[r]; best_i = (int32_t)l; }
+          float s = kred[par][wave][r];
+          for (int k = 1; k < ks; ++k) s += kred[par][wave + k][r];
+          acc[r] = s;
         }
       }
-    } else if constexpr (EPI == EPI_SWIGLU) {
-      // pairs (gate, up) at logical rows (2j, 2j+1)
-      if (lane < RPW / 2) {
-        float g = 0.0f, u = 0.0f;
+    }
+    if (kp == 0) epilogue<EPI, RPW>(a, seg, ((g0 + i * nblk) * nrs + rs) * RPW, lane, acc, best_v, best_i);
 #pragma unroll
-        for (int r = 0; r < RPW; r += 2) if (r == 2 * lane) { g = acc[r]; u = acc[r + 1]; }
-        const int64_t l = lrow0 + 2 * lane;
-        if (l < seg.rows) {
-          const float act = g / (1.0f + expf(-g));  // silu (elementwise.cpp:73-84)
-          a.y[seg.row_base + (l >> 1)] = act * u;
-        }
+    for (int r = 0; r < RPW; ++r) acc[r] = 0.0f;
+  };
+  // first batch: unit 0 (already in flight) and, for NB = 2, unit 1
+  if constexpr (NB == 1) {
+    if (nunits > 0) {
+      compute_unit<FMT>(wk, 0, lane, xsm, U0, acc);
+      finish(0);
+    }
+    for (int64_t u = 1; u < nunits; ++u) {
+      UnitBuf<FMT> V;
+      load_unit<FMT, EPI>(a, seg, wk, unit_l0(u), unit_step(u), lane, V);
+      compute_unit<FMT>(wk, unit_step(u), lane, xsm, V, acc);
+      finish(u);
+    }
+  } else {
+    if (nunits > 0) {
+      UnitBuf<FMT> U1;
+      if (nunits > 1) load_unit<FMT, EPI>(a, seg, wk, unit_l0(1), unit_step(1), lane, U1);
+      compute_unit<FMT>(wk, 0, lane, xsm, U0, acc);
+      finish(0);
+      if (nunits > 1) {
+        compute_unit<FMT>(wk, unit_step(1), lane, xsm, U1, acc);
+        finish(1);
       }
-    } else if constexpr (EPI == EPI_QKV) {
-      if (lane < RPW / 2) {
-        float v0 = 0.0f, v1 = 0.0f;
-#pragma unroll
-        for (int r = 0; r < RPW; r += 2) if (r == 2 * lane) { v0 = acc[r]; v1 = acc[r + 1]; }
-        const int64_t l = lrow0 + 2 * lane;
-        if (l < seg.rows) {
-          const int64_t r0 = (seg.kind == 2) ? l : qkv_phys(l, a.rope_mode, a.head_dim);
-          const int64_t r1 = (seg.kind == 2) ? l + 1 : qkv_phys(l + 1, a.rope_mode, a.head_dim);
-          if (seg.bias) { v0 = v0 + seg.bias[r0]; v1 = v1 + seg.bias[r1]; }
-          const int pos = a.state->pos;
-          if (seg.kind != 2) {
-            // rotate pair p of its head by the host-built angle table
-            const int64_t p = (a.rope_mode == 2) ? (r0 % a.head_dim) : ((r0 % a.head_dim) >> 1);
-            const float2 cs = a.rope[(int64_t)pos * (a.head_dim / 2) + p];
-            const float n0 = v0 * cs.x - v1 * cs.y;
-            const float n1 = v0 * cs.y + v1 * cs.x;
-            v0 = n0; v1 = n1;
-          }
-          if (seg.kind == 0) {
-            a.y[r0] = v0;
-            a.y[r1] = v1;
-          } else {
-            // K after RoPE and raw V go to the cache at `pos` (gguf.cpp:1043, dispatch.cpp:218)
-            void* cache = (seg.kind == 1) ? a.kcache : a.vcache;
-            const int64_t hd = a.head_dim;
-            const int64_t o0 = ((r0 / hd) * a.max_seq + pos) * hd + (r0 % hd);
-            const int64_t o1 = ((r1 / hd) * a.max_seq + pos) * hd + (r1 % hd);
-            if (a.kv_f16) {
-              reinterpret_cast<__half*>(cache)[o0] = __float2half(v0);
-              reinterpret_cast<__half*>(cache)[o1] = __float2half(v1);
-            } else {
-              reinterpret_cast<float*>(cache)[o0] = v0;
-              reinterpret_cast<float*>(cache)[o1] = v1;
-            }
-          }
-        }
+    }
+    for (int64_t u = 2; u < nunits; u += 2) {
+      UnitBuf<FMT> V0, V1;
+      const bool two = u + 1 < nunits;  // block-uniform
+      load_unit<FMT, EPI>(a, seg, wk, unit_l0(u), unit_step(u), lane, V0);
+      if (two) load_unit<FMT, EPI>(a, seg, wk, unit_l0(u + 1), unit_step(u + 1), lane, V1);
+      compute_unit<FMT>(wk, unit_step(u), lane, xsm, V0, acc);
+      finish(u);
+      if (two) {
+        compute_unit<FMT>(wk, unit_step(u + 1), lane, xsm, V1, acc);
+        finish(u + 1);
       }
     }
   }
@@ -685,6 +1133,8 @@ hipError_t prepare_gemv() {
   return hipSuccess;
 }
 
+namespace {
+
 int cu_count() {
   static int n = 0;
   if (n == 0) {
@@ -698,46 +1148,79 @@ int cu_count() {
   return n;
 }
 
-// Blocks per segment: one per row group, capped so a launch holds at most
-// kBlocksPerCU blocks per CU in total (the rest loop), shared out by group count.
-constexpr int kBlocksPerCU = 4;
+// Blocks of `fn` that stay resident on one CU with `lds` bytes of dynamic LDS
+// (registers, LDS and wave slots all counted by the runtime); cached per pair.
+int resident_blocks(KernelFn fn, size_t lds) {
+  struct Entry { KernelFn fn; size_t lds; int n; };
+  static std::mutex mu;
+  static std::vector<Entry> cache;
+  std::lock_guard<std::mutex> lock(mu);
+  for (const Entry& e : cache)
+    if (e.fn == fn && e.lds == lds) return e.n;
+  int n = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, WPB * 64, lds) != hipSuccess || n <= 0) {
+    (void)hipGetLastError();
+    n = 2;
+  }
+  cache.push_back({fn, lds, n});
+  return n;
+}
 
-void plan_blocks(const GemvArgs& a, int* per_seg) {
-  const int rpb = WPB * RPW;
+// Waves of a block that share one row set's K: enough that a wave walks at most
+// two 64-chunk columns of a row per group.
+int pick_ksplit(const DevWeight& w) {
+  const int64_t ncol = (w.a_row / 16 + 63) / 64;
+  int ks = 1;
+  while (ks < WPB && ks < 4 && (ncol + ks - 1) / ks > 2) ks *= 2;
+  return ks;
+}
+
+// Dynamic LDS of one block: the staged input (f32 planes, or f16 hi/lo pair
+// planes plus (sum, scale) per chunk for the pair formats).
+size_t lds_bytes(int type, int64_t K) {
+  if (type == T_Q4_0 || type == T_Q4_1) return (size_t)(K / 32) * (128 + 8);
+  return (size_t)K * sizeof(float);
+}
+
+struct Plan {
+  KernelFn fn = nullptr;
+  size_t lds = 0;
+  int ks = 1;
+  int per[3] = {0, 0, 0};  // blocks per segment
+  int blocks = 0;
+};
+
+// Blocks per segment: one per row group, capped at what stays resident (the
+// rest loop), shared out by group count and evened out so blocks do equal work.
+Plan make_plan(const GemvArgs& a) {
+  Plan p;
+  p.fn = pick(a.epi, a.seg[0].w.type);
+  p.lds = lds_bytes(a.seg[0].w.type, a.K);
+  p.ks = pick_ksplit(a.seg[0].w);
+  if (!p.fn) return p;
+  const int rpg = (WPB / p.ks) * rpw_of(a.seg[0].w.type);
   int64_t total = 0;
-  for (int k = 0; k < a.nseg; ++k) total += (a.seg[k].rows + rpb - 1) / rpb;
-  const int64_t cap = (int64_t)cu_count() * kBlocksPerCU;
+  for (int k = 0; k < a.nseg; ++k) total += (a.seg[k].rows + rpg - 1) / rpg;
+  const int per_cu = UAII_GEMV_BLOCKS_PER_CU > 0 ? UAII_GEMV_BLOCKS_PER_CU : resident_blocks(p.fn, p.lds);
+  const int64_t cap = (int64_t)cu_count() * per_cu;
   for (int k = 0; k < a.nseg; ++k) {
-    const int64_t g = (a.seg[k].rows + rpb - 1) / rpb;
+    const int64_t g = (a.seg[k].rows + rpg - 1) / rpg;
     int64_t b = g;
     if (total > cap) {
       b = std::max<int64_t>(1, (g * cap + total - 1) / total);
-      const int64_t per = (g + b - 1) / b;  // groups per block, then even out the blocks
+      const int64_t per = (g + b - 1) / b;
       b = (g + per - 1) / per;
     }
-    per_seg[k] = (int)std::min<int64_t>(b, g);
+    p.per[k] = (int)std::min<int64_t>(b, g);
+    p.blocks += p.per[k];
   }
+  return p;
 }
 
-int gemv_grid(const GemvArgs& a) {
-  int per[3] = {0, 0, 0};
-  plan_blocks(a, per);
-  int blocks = 0;
-  for (int k = 0; k < a.nseg; ++k) blocks += per[k];
-  return blocks;
-}
-
-// One launch per run of segments sharing a weight type (the kernel is
-// specialised per type); QKV with mixed types therefore takes several launches.
-hipError_t launch_gemv(const GemvArgs& in, hipStream_t s) {
-  const size_t lds = (size_t)in.K * sizeof(float);
-  if ((int)lds > lds_limit() - 1024 || in.K % 4) return hipErrorInvalidValue;
-  if (in.epi == EPI_LOGITS && in.nseg != 1) return hipErrorInvalidValue;
-  for (int k = 0; k < in.nseg; ++k) {
-    if (in.epi == EPI_SWIGLU && in.seg[k].w2.type != in.seg[k].w.type) return hipErrorInvalidValue;
-    if ((in.epi == EPI_SWIGLU || in.epi == EPI_QKV) && (in.seg[k].rows % 2)) return hipErrorInvalidValue;
-    if (in.seg[k].w.cols != in.K) return hipErrorInvalidValue;
-  }
+// Runs of consecutive segments sharing a weight type: one launch each (the
+// kernel is specialised per type), so QKV with mixed types takes several.
+template <typename F>
+hipError_t for_each_run(const GemvArgs& in, F&& f) {
   int k0 = 0;
   while (k0 < in.nseg) {
     int k1 = k0 + 1;
@@ -745,29 +1228,54 @@ hipError_t launch_gemv(const GemvArgs& in, hipStream_t s) {
     GemvArgs a = in;
     a.nseg = k1 - k0;
     for (int k = 0; k < a.nseg; ++k) a.seg[k] = in.seg[k0 + k];
-    int per[3] = {0, 0, 0};
-    plan_blocks(a, per);
-    int blocks = 0;
-    for (int k = 0; k < a.nseg; ++k) {
-      a.seg[k].block0 = blocks;
-      blocks += per[k];
-    }
     if (k0 > 0) a.xtap = nullptr;
-    KernelFn fn = pick(a.epi, a.seg[0].w.type);
-    if (!fn) return hipErrorInvalidValue;
-    if (blocks > 0) {
-      hipLaunchKernelGGL(fn, dim3(blocks), dim3(WPB * 64), lds, s, a);
-      const hipError_t st = hipGetLastError();
-      if (st != hipSuccess) return st;
-      if (a.epi == EPI_LOGITS) {
-        hipLaunchKernelGGL(k_argmax_final, dim3(1), dim3(1024), 0, s, a, blocks);
-        const hipError_t st2 = hipGetLastError();
-        if (st2 != hipSuccess) return st2;
-      }
-    }
+    const hipError_t st = f(a);
+    if (st != hipSuccess) return st;
     k0 = k1;
   }
   return hipSuccess;
+}
+
+}  // namespace
+
+int gemv_grid(const GemvArgs& in) {
+  int most = 0;
+  (void)for_each_run(in, [&](const GemvArgs& a) {
+    most = std::max(most, make_plan(a).blocks);
+    return hipSuccess;
+  });
+  return most;
+}
+
+hipError_t launch_gemv(const GemvArgs& in, hipStream_t s) {
+  if (in.K % 4) return hipErrorInvalidValue;
+  if (in.epi == EPI_LOGITS && in.nseg != 1) return hipErrorInvalidValue;
+  for (int k = 0; k < in.nseg; ++k) {
+    if (in.epi == EPI_SWIGLU && in.seg[k].w2.type != in.seg[k].w.type) return hipErrorInvalidValue;
+    if ((in.epi == EPI_SWIGLU || in.epi == EPI_QKV) && (in.seg[k].rows % 2)) return hipErrorInvalidValue;
+    if (in.seg[k].w.cols != in.K) return hipErrorInvalidValue;
+  }
+  return for_each_run(in, [&](const GemvArgs& run) {
+    GemvArgs a = run;
+    const Plan p = make_plan(a);
+    if (!p.fn) return hipErrorInvalidValue;
+    a.ksplit = p.ks;
+    int blocks = 0;
+    for (int k = 0; k < a.nseg; ++k) {
+      a.seg[k].block0 = blocks;
+      blocks += p.per[k];
+    }
+    if (blocks == 0) return hipSuccess;
+    if ((int64_t)p.lds > lds_limit() - 1024) return hipErrorInvalidValue;
+    if (a.epi == EPI_LOGITS && blocks > a.part_cap) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(p.fn, dim3(blocks), dim3(WPB * 64), p.lds, s, a);
+    hipError_t st = hipGetLastError();
+    if (st == hipSuccess && a.epi == EPI_LOGITS) {
+      hipLaunchKernelGGL(k_argmax_final, dim3(1), dim3(1024), 0, s, a, blocks);
+      st = hipGetLastError();
+    }
+    return st;
+  });
 }
 
 }  // namespace uaii_hip

@@ -6,6 +6,8 @@
 //   k_softmax     probabilities over the vocab (softmax.cpp:11-77)
 //   k_argmax      greedy argmax, lowest index wins ties (sampling.cpp:38-50)
 //   k_rope        standalone RoPE rows (transformer.cpp:144-220)
+//   k_stream_copy plain 16-byte-word copy: the yardstick for HBM rates and for
+//                 scaling the memory counters of the other kernels
 
 #include "common.h"
 #include "uaii_hip_internal.h"
@@ -150,7 +152,28 @@ __global__ void k_rope(float* x, int64_t rows, int64_t dim, int hd, const int32_
   v[i1] = a * cs.y + b * cs.x;
 }
 
+// Grid-stride copy, 16 bytes per lane per iteration, four loads in flight.
+__global__ void __launch_bounds__(256) k_stream_copy(const uint4* __restrict__ src,
+                                                     uint4* __restrict__ dst, int64_t n) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  for (; i + 3 * stride < n; i += 4 * stride) {
+    const uint4 a = src[i], b = src[i + stride], c = src[i + 2 * stride], d = src[i + 3 * stride];
+    dst[i] = a; dst[i + stride] = b; dst[i + 2 * stride] = c; dst[i + 3 * stride] = d;
+  }
+  for (; i < n; i += stride) dst[i] = src[i];
+}
+
 }  // namespace
+
+hipError_t launch_copy(const void* src, void* dst, int64_t n16, hipStream_t s) {
+  if (n16 <= 0) return hipSuccess;
+  int64_t blocks = (n16 + 255) / 256;
+  if (blocks > 8192) blocks = 8192;
+  hipLaunchKernelGGL(k_stream_copy, dim3((unsigned)blocks), dim3(256), 0, s,
+                     (const uint4*)src, (uint4*)dst, n16);
+  return hipGetLastError();
+}
 
 hipError_t launch_embed(const DevWeight& w, const StepState* st, float* x, float* tap,
                         hipStream_t s) {

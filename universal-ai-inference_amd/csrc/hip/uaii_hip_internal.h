@@ -67,11 +67,14 @@ struct GemvArgs {
   int rope_mode;
   const float2* rope;    // [max_seq][hd/2] (cos, sin)
   // EPI_LOGITS
-  float* part_val;       // [gridDim] block partials of the argmax
+  float* part_val;       // [part_cap] block partials of the argmax
   int32_t* part_idx;
+  int part_cap;          // capacity of part_val/part_idx (launch fails if the grid exceeds it)
   int32_t* ids;          // token history [max_seq + 1]
   // shared
   StepState* state;
+  // set by launch_gemv: waves of a block that split one row set's K (1, 2 or 4)
+  int ksplit;
 };
 
 hipError_t launch_gemv(const GemvArgs& a, hipStream_t s);
@@ -93,6 +96,8 @@ hipError_t launch_softmax(const float* x, float* y, int64_t n, hipStream_t s);
 hipError_t launch_argmax(const float* x, int64_t n, int32_t* out_idx, hipStream_t s);
 hipError_t launch_rope(float* x, int64_t rows, int64_t dim, int head_dim, const int32_t* pos,
                        int64_t pos_stride, const float2* tab, int mode, hipStream_t s);
+// Plain device copy of n16 16-byte words (the yardstick for HBM rates and counters).
+hipError_t launch_copy(const void* src, void* dst, int64_t n16, hipStream_t s);
 
 // ---- attention -----------------------------------------------------------------
 

@@ -106,12 +106,12 @@ int uaii_hip_dequant_rows(const uaii_hip_weight* w, int64_t row0, int64_t nrows,
 }
 
 static int gemv_common(const uaii_hip_weight* w, const float* x, const float* norm_w, float eps,
-                       float* y, void* stream) {
+                       float* y, void* stream, int epi = EPI_STORE) {
   if (!w || !x || !y) return kErrArg;
   if (w->w.view.cols % 4) return kErrArg;
   GemvArgs a{};
   a.nseg = 1;
-  a.epi = EPI_STORE;
+  a.epi = epi;
   a.K = w->w.view.cols;
   a.x = x;
   a.norm_w = norm_w;
@@ -130,6 +130,31 @@ int uaii_hip_gemv_rmsnorm(const uaii_hip_weight* w, const float* x, const float*
                           float eps, float* y, void* stream) {
   if (!norm_w) return kErrArg;
   return gemv_common(w, x, norm_w, eps, y, stream);
+}
+
+int uaii_hip_gemv_add(const uaii_hip_weight* w, const float* x, const float* norm_w, float eps,
+                      float* y, void* stream) {
+  return gemv_common(w, x, norm_w, eps, y, stream, EPI_ADD);
+}
+
+int uaii_hip_gemv_swiglu(const uaii_hip_weight* wg, const uaii_hip_weight* wu, const float* x,
+                         const float* norm_w, float eps, float* y, void* stream) {
+  if (!wg || !wu || !x || !y) return kErrArg;
+  const DevWeight& g = wg->w.view;
+  const DevWeight& u = wu->w.view;
+  if (g.type != u.type || g.rows != u.rows || g.cols != u.cols || g.cols % 4) return kErrArg;
+  GemvArgs a{};
+  a.nseg = 1;
+  a.epi = EPI_SWIGLU;
+  a.K = g.cols;
+  a.x = x;
+  a.norm_w = norm_w;
+  a.eps = eps;
+  a.y = y;
+  a.seg[0].w = g;
+  a.seg[0].w2 = u;
+  a.seg[0].rows = 2 * g.rows;  // logical rows interleave (gate j, up j)
+  return (int)launch_gemv(a, S(stream));
 }
 
 int uaii_hip_gemm(const uaii_hip_weight* w, const float* x, int64_t m, float* y, void* stream) {
@@ -248,14 +273,14 @@ int uaii_hip_time_gemm(const uaii_hip_weight* w, const float* x, int64_t m, floa
 }
 
 int uaii_hip_time_copy(const void* src, void* dst, size_t bytes, int iters, float* avg_ms) {
-  if (!src || !dst || iters <= 0 || !avg_ms) return kErrArg;
+  if (!src || !dst || iters <= 0 || !avg_ms || bytes % 16) return kErrArg;
   hipEvent_t e0, e1;
   (void)hipEventCreate(&e0);
   (void)hipEventCreate(&e1);
-  int rc = (int)hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, nullptr);
+  const int64_t n16 = (int64_t)(bytes / 16);
+  int rc = (int)uaii_hip::launch_copy(src, dst, n16, nullptr);
   (void)hipEventRecord(e0, nullptr);
-  for (int i = 0; i < iters && !rc; ++i)
-    rc = (int)hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, nullptr);
+  for (int i = 0; i < iters && !rc; ++i) rc = (int)uaii_hip::launch_copy(src, dst, n16, nullptr);
   (void)hipEventRecord(e1, nullptr);
   (void)hipEventSynchronize(e1);
   float ms = 0.0f;

@@ -219,10 +219,14 @@ Error DecoderProgram::build(const DecoderSpec& spec, const ProgramOptions& opts)
   UAII_TRY(alloc(4 * D * L, (void**)&tap_r2_));
   UAII_TRY(alloc(4 * D, (void**)&tap_normed_));
   UAII_TRY(alloc(sizeof(StepState), (void**)&state_));
-  GemvArgs lm{};
+  GemvArgs lm{};  // same plan inputs as the LM-head launch in encode_step
   lm.nseg = 1;
+  lm.epi = EPI_LOGITS;
+  lm.K = d.dim;
+  lm.seg[0].w = d.tied ? tok_embd_.view : output_.view;
   lm.seg[0].rows = d.vocab;
-  const int lm_blocks = gemv_grid(lm);
+  lm_blocks_ = gemv_grid(lm);
+  const int lm_blocks = lm_blocks_;
   UAII_TRY(alloc(4 * (size_t)lm_blocks, (void**)&lm_part_val_));
   UAII_TRY(alloc(4 * (size_t)lm_blocks, (void**)&lm_part_idx_));
   UAII_HIP(hipStreamSynchronize(stream_));
@@ -451,6 +455,7 @@ Error DecoderProgram::encode_step(bool want_logits) {
     lm.seg[0].rows = d.vocab;
     lm.part_val = lm_part_val_;
     lm.part_idx = lm_part_idx_;
+    lm.part_cap = lm_blocks_;
     lm.ids = ids_;
     lm.state = state_;
     UAII_TRY(timed("gemv_lm_head", gemv_bytes(lm.seg[0].w), [&] { return launch_gemv(lm, s); }));

@@ -106,6 +106,7 @@ class DecoderProgram {
   int32_t* moe_ids_ = nullptr;
   float* lm_part_val_ = nullptr;
   int32_t* lm_part_idx_ = nullptr;
+  int lm_blocks_ = 0;  // capacity of the LM-head partial buffers
   uaii_hip::StepState* state_ = nullptr;
 
   // sized by ensure_capacity

@@ -14,7 +14,8 @@ from pathlib import Path
 
 PKG_DIR = Path(__file__).resolve().parent.parent
 LIB_DIR = PKG_DIR / "lib"
-LIB_PATH = LIB_DIR / "libuaii_amd.so"
+# UAII_AMD_LIB selects another build of the same library (A/B timing of builds).
+LIB_PATH = Path(os.environ["UAII_AMD_LIB"]) if os.environ.get("UAII_AMD_LIB") else LIB_DIR / "libuaii_amd.so"
 SYNTH_PATH = LIB_DIR / "libuaii_synth.so"
 
 # GGUF tensor type ids (reference include/uaii/loaders/gguf.hpp:18-36)
@@ -105,6 +106,8 @@ def lib() -> C.CDLL:
         "uaii_hip_dequant_rows": (C.c_int, [vp, i64, i64, vp, vp]),
         "uaii_hip_gemv": (C.c_int, [vp, vp, vp, vp]),
         "uaii_hip_gemv_rmsnorm": (C.c_int, [vp, vp, vp, C.c_float, vp, vp]),
+        "uaii_hip_gemv_add": (C.c_int, [vp, vp, vp, C.c_float, vp, vp]),
+        "uaii_hip_gemv_swiglu": (C.c_int, [vp, vp, vp, vp, C.c_float, vp, vp]),
         "uaii_hip_gemm": (C.c_int, [vp, vp, i64, vp, vp]),
         "uaii_hip_rmsnorm": (C.c_int, [vp, vp, vp, i64, i64, C.c_float, vp]),
         "uaii_hip_softmax": (C.c_int, [vp, vp, i64, vp]),
@@ -118,7 +121,14 @@ def lib() -> C.CDLL:
         "uaii_hip_time_copy": (C.c_int, [vp, vp, C.c_size_t, C.c_int, f32p]),
     }
     for name, (res, args) in sig.items():
-        fn = getattr(L, name)
+        try:
+            fn = getattr(L, name)
+        except AttributeError:
+            # an older build without this entry point: calling it raises
+            def missing(*_a, _n=name):
+                raise UaiiError(f"{LIB_PATH} does not export {_n}")
+            setattr(L, name, missing)
+            continue
         fn.restype = res
         fn.argtypes = args
     _lib = L
