@@ -127,6 +127,13 @@ UAII_CAPI_API uaii_status uaii_session_profile_summary(uaii_session* session,
 UAII_CAPI_API uaii_status uaii_session_write_trace(uaii_session* session,
                                                    const char* path);
 
+/* Model conversion (include/uaii/c_api/uaii.h:154-155 in the reference) is not
+ * part of this library: it returns UAII_ERR_NOT_IMPLEMENTED. Exported so callers
+ * that bind the whole reference header (bindings/python/uaii/_backend.py:151-181)
+ * load this library unchanged. */
+UAII_CAPI_API uaii_status uaii_convert_model(const char* input_path,
+                                             const char* output_path);
+
 #ifdef __cplusplus
 }
 #endif

@@ -45,6 +45,12 @@ UAII_CAPI_API uaii_status uaii_session_set_profiling(uaii_session* session, int 
 UAII_CAPI_API uaii_status uaii_session_last_margin(uaii_session* session, float* best,
                                                    float* second);
 
+/** Parse a GGUF file and derive the decoder the session would run, without
+ * touching the GPU: a JSON object (arch, layer count, dims, heads, vocab,
+ * context length, rope mode/theta, rms eps, tied embeddings, per-layer FFN kind
+ * and tensor types) is written to buf (NUL-terminated, truncated to capacity). */
+UAII_CAPI_API uaii_status uaii_model_describe(const char* path, char* buf, size_t capacity);
+
 #ifdef __cplusplus
 }
 #endif

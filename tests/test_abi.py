@@ -1,0 +1,159 @@
+"""C-ABI boundary and host logic, on the CPU (no GPU is touched).
+
+* libuaii_amd.so loads and exports every entry point declared in include/*.h;
+* uaii_session_options_init defaults and the struct_size ABI check
+  (libs/uaii-capi/src/capi.cpp:62-78, :132-139);
+* status names, versions, last-error text;
+* session-create failures that the reference reports before any compute
+  (unknown backend, missing file, non-GGUF file, truncated file);
+* the GGUF loader's derivation of the decoder (libs/uaii-loaders/src/gguf.cpp:
+  801-1246) through uaii_model_describe: dims and heads from the metadata keys,
+  tied embeddings, the NeoX RoPE arch list, MoE detection, UAII_MAX_LAYERS.
+"""
+import ctypes as C
+import json
+import os
+import re
+from pathlib import Path
+
+import pytest
+
+import uaii_amd
+from uaii_amd import synth
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADERS = [ROOT / "include/uaii/c_api/uaii.h", ROOT / "include/uaii/c_api/uaii_ext.h",
+           ROOT / "include/uaii_hip.h"]
+
+
+def declared_functions():
+    names = []
+    for h in HEADERS:
+        text = h.read_text()
+        for m in re.finditer(r"UAII_(?:CAPI|HIP)_API\s+[\w\s\*]+?\b(uaii_\w+)\s*\(", text):
+            names.append(m.group(1))
+    return sorted(set(names))
+
+
+def test_headers_declare_the_reference_entry_points():
+    names = declared_functions()
+    for must in ["uaii_session_options_init", "uaii_session_create", "uaii_session_generate",
+                 "uaii_session_destroy", "uaii_last_error", "uaii_status_name",
+                 "uaii_session_run", "uaii_session_set_f32", "uaii_session_get_f32",
+                 "uaii_convert_model", "uaii_hip_gemv", "uaii_hip_attention_decode"]:
+        assert must in names
+    assert len(names) > 50
+
+
+def test_library_exports_every_declared_symbol():
+    lib = C.CDLL(str(uaii_amd.LIB_PATH))
+    missing = [n for n in declared_functions() if not hasattr(lib, n)]
+    assert not missing, f"declared but not exported: {missing}"
+
+
+def test_options_defaults_and_layout():
+    L = uaii_amd.lib()
+    o = uaii_amd.SessionOptions()
+    L.uaii_session_options_init(C.byref(o))
+    assert o.struct_size == C.sizeof(uaii_amd.SessionOptions)
+    assert o.backend == b"rocm"
+    assert o.weight_init == 0 and o.enable_fusion == 1 and o.enable_memory_reuse == 1
+    assert o.keep_quantized_weights == 1 and o.max_context == 0
+
+
+def test_status_names_versions_and_errors():
+    L = uaii_amd.lib()
+    names = [L.uaii_status_name(i).decode() for i in range(9)]
+    assert names == ["ok", "invalid_argument", "not_found", "io", "config", "plugin", "abi",
+                     "not_implemented", "internal"]
+    assert L.uaii_get_c_api_version_string().decode().count(".") == 2
+    assert L.uaii_convert_model(b"in.gguf", b"out") == 7
+    assert b"not part" in L.uaii_last_error()
+    assert L.uaii_hip_error_string(-1) == b"invalid argument"
+
+
+def _create(path, **fields):
+    L = uaii_amd.lib()
+    o = uaii_amd.SessionOptions()
+    L.uaii_session_options_init(C.byref(o))
+    for k, v in fields.items():
+        setattr(o, k, v)
+    h = C.c_void_p()
+    rc = L.uaii_session_create(path, C.byref(o), C.byref(h))
+    return rc, L.uaii_last_error().decode(), h
+
+
+def test_create_fails_before_compute(tmp_path):
+    tiny = synth.cached_model(synth.PRESETS["tiny"]).encode()
+    rc, msg, h = _create(tiny, backend=b"cpu")
+    assert rc == 7 and "rocm" in msg and not h.value
+    rc, msg, _ = _create(tiny, keep_quantized_weights=0)
+    assert rc == 7
+    rc, msg, _ = _create(tiny, struct_size=0)
+    assert rc == 6
+    rc, msg, _ = _create(tiny, struct_size=C.sizeof(uaii_amd.SessionOptions) + 8)
+    assert rc == 6
+    rc, msg, _ = _create(str(tmp_path / "absent.gguf").encode())
+    assert rc == 2
+    bad = tmp_path / "bad.gguf"
+    bad.write_bytes(b"NOTGGUF" + bytes(64))
+    rc, msg, _ = _create(str(bad).encode())
+    assert rc == 1 and "GGUF" in msg
+    # a GGUF cut inside its tensor table
+    cut = tmp_path / "cut.gguf"
+    cut.write_bytes(Path(tiny.decode()).read_bytes()[:4096])
+    rc, msg, _ = _create(str(cut).encode())
+    assert rc == 1
+
+
+def describe(path):
+    L = uaii_amd.lib()
+    L.uaii_model_describe.argtypes = [C.c_char_p, C.c_char_p, C.c_size_t]
+    buf = C.create_string_buffer(1 << 16)
+    rc = L.uaii_model_describe(str(path).encode(), buf, len(buf))
+    assert rc == 0, L.uaii_last_error()
+    return json.loads(buf.value)
+
+
+def small_cfg(**kw):
+    base = dict(n_layers=3, dim=256, n_heads=8, n_kv_heads=2, ffn=512, vocab=1000, ctx_len=512,
+                rope_theta=500000.0, type_default=uaii_amd.Q4_0, seed=77)
+    base.update(kw)
+    return synth.ModelConfig(**base)
+
+
+def test_describe_dense_gqa(tmp_path):
+    cfg = small_cfg(type_attn_v=uaii_amd.Q6_K, type_ffn_down=uaii_amd.Q8_0)
+    d = describe(synth.write_model(tmp_path / "m.gguf", cfg))
+    assert (d["arch"], d["n_layers"], d["dim"], d["n_heads"], d["n_kv_heads"]) == ("llama", 3, 256, 8, 2)
+    assert d["head_dim"] == 32 and d["q_dim"] == 256 and d["kv_dim"] == 64
+    assert d["vocab"] == 1000 and d["ctx_len"] == 512
+    assert d["rope_theta"] == 500000.0 and d["rope_mode"] == 0 and not d["tied"]
+    assert abs(d["rms_eps"] - 1e-5) < 1e-12
+    for layer in d["layers"]:
+        assert layer["ffn"] == "swiglu" and layer["inter"] == 512
+        assert layer["wq"] == uaii_amd.Q4_0 and layer["wv"] == uaii_amd.Q6_K
+        assert layer["down"] == uaii_amd.Q8_0
+
+
+def test_describe_tied_and_neox(tmp_path):
+    d = describe(synth.write_model(tmp_path / "t.gguf", small_cfg(tied=True)))
+    assert d["tied"] and d["output_type"] == d["tok_embd_type"]
+    # qwen2 is on the reference's NeoX list (gguf.cpp): rope mode 2
+    d = describe(synth.write_model(tmp_path / "q.gguf", small_cfg(arch="qwen2")))
+    assert d["arch"] == "qwen2" and d["rope_mode"] == 2
+
+
+def test_describe_moe(tmp_path):
+    d = describe(synth.write_model(tmp_path / "x.gguf",
+                                   small_cfg(n_experts=4, top_k=2, router_std=1.0 / 16)))
+    assert d["n_experts"] == 4 and d["top_k"] == 2
+    assert all(layer["ffn"] == "moe" for layer in d["layers"])
+
+
+def test_describe_max_layers_env(tmp_path, monkeypatch):
+    path = synth.write_model(tmp_path / "l.gguf", small_cfg(n_layers=5))
+    monkeypatch.setenv("UAII_MAX_LAYERS", "2")
+    assert describe(path)["n_layers"] == 2
+    monkeypatch.delenv("UAII_MAX_LAYERS")
+    assert describe(path)["n_layers"] == 5

@@ -7,6 +7,8 @@ and prompt. With an f32 KV cache the oracle is the reference's f32 path; with
 the device fp16 cache the oracle also rounds K/V to fp16 (the reference has no
 fp16 cache), and the f32-oracle distance is reported too.
 """
+from pathlib import Path
+
 import numpy as np
 import pytest
 
@@ -15,6 +17,7 @@ import uaii_amd
 from uaii_amd import synth
 
 pytestmark = pytest.mark.gpu
+GOLDEN = Path(__file__).resolve().parent / "golden"
 
 
 def maxrel(a, b):
@@ -87,6 +90,13 @@ def test_generate_tiny_config_f32_kv():
     assert maxrel(taps["logits"], want["logits"]) < 2e-3
     for li in range(cfg.n_layers):
         assert maxrel(taps[f"r2_{li}"], want["resid2"][li]) < 2e-3
+    # the same run against the vectors the reference's own kernels wrote
+    g = np.load(GOLDEN / "tiny_generate.npz")
+    assert np.array_equal(prompt, g["prompt"])
+    assert np.array_equal(ids, g["ids"])
+    assert maxrel(taps["logits"], g["logits"]) < 2e-3
+    for li in range(cfg.n_layers):
+        assert maxrel(taps[f"r2_{li}"], g["resid2"][li]) < 2e-3
 
 
 def test_generate_fp16_kv():

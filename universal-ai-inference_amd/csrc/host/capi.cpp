@@ -202,6 +202,28 @@ uaii_status uaii_session_write_trace(uaii_session* session, const char* path) {
   return UAII_OK;
 }
 
+uaii_status uaii_model_describe(const char* path, char* buf, size_t capacity) {
+  if (path == nullptr || buf == nullptr || capacity == 0)
+    return fail(UAII_ERR_INVALID_ARGUMENT, "model_describe null arg");
+  uaii::GgufFile file;
+  uaii::DecoderSpec spec;
+  uaii::Error err = file.open(path);
+  if (err.ok()) err = uaii::derive_decoder(file, &spec);
+  if (!err.ok()) return from_error(err);
+  const std::string s = uaii::describe_decoder(spec);
+  const size_t n = std::min(capacity - 1, s.size());
+  std::memcpy(buf, s.data(), n);
+  buf[n] = '\0';
+  g_last_error.clear();
+  return UAII_OK;
+}
+
+uaii_status uaii_convert_model(const char* input_path, const char* output_path) {
+  (void)input_path;
+  (void)output_path;
+  return fail(UAII_ERR_NOT_IMPLEMENTED, "uaii_convert_model: model conversion is not part of the ROCm decode library");
+}
+
 // ---- uaii_ext.h ------------------------------------------------------------
 
 uaii_status uaii_session_begin(uaii_session* session, const int64_t* prompt_tokens,

@@ -7,6 +7,7 @@
 #include <unistd.h>
 
 #include <cctype>
+#include <cstdio>
 #include <cstdlib>
 #include <cstring>
 
@@ -336,6 +337,68 @@ Error derive_decoder(const GgufFile& f, DecoderSpec* o) {
   if (d.n_experts > 0 && d.top_k > d.n_experts) d.top_k = d.n_experts;
   *o = std::move(d);
   return Error::success();
+}
+
+namespace {
+
+const char* ffn_name(LayerSpec::Ffn f) {
+  switch (f) {
+    case LayerSpec::kSwiGLU: return "swiglu";
+    case LayerSpec::kGelu: return "gelu";
+    case LayerSpec::kMoE: return "moe";
+    default: return "none";
+  }
+}
+
+int tensor_type(const GgufTensor* t) { return t ? t->type : -1; }
+
+}  // namespace
+
+std::string describe_decoder(const DecoderSpec& d) {
+  std::string s = "{";
+  auto kv = [&](const char* k, const std::string& v, bool quote) {
+    if (s.size() > 1) s += ", ";
+    s += "\"";
+    s += k;
+    s += "\": ";
+    if (quote) s += "\"" + v + "\"";
+    else s += v;
+  };
+  char f[64];
+  kv("arch", d.arch, true);
+  kv("n_layers", std::to_string(d.n_layers), false);
+  kv("dim", std::to_string(d.dim), false);
+  kv("n_heads", std::to_string(d.n_heads), false);
+  kv("n_kv_heads", std::to_string(d.n_kv_heads), false);
+  kv("head_dim", std::to_string(d.head_dim), false);
+  kv("q_dim", std::to_string(d.q_dim), false);
+  kv("kv_dim", std::to_string(d.kv_dim), false);
+  kv("vocab", std::to_string(d.vocab), false);
+  kv("ctx_len", std::to_string(d.ctx_len), false);
+  kv("n_experts", std::to_string(d.n_experts), false);
+  kv("top_k", std::to_string(d.top_k), false);
+  std::snprintf(f, sizeof f, "%.9g", (double)d.rope_theta);
+  kv("rope_theta", f, false);
+  std::snprintf(f, sizeof f, "%.9g", (double)d.rms_eps);
+  kv("rms_eps", f, false);
+  kv("rope_mode", std::to_string(d.rope_mode), false);
+  kv("tied", d.tied ? "true" : "false", false);
+  kv("tok_embd_type", std::to_string(tensor_type(d.tok_embd)), false);
+  kv("output_type", std::to_string(tensor_type(d.output)), false);
+  std::string layers = "[";
+  for (size_t i = 0; i < d.layers.size(); ++i) {
+    const LayerSpec& L = d.layers[i];
+    if (i) layers += ", ";
+    layers += "{\"ffn\": \"" + std::string(ffn_name(L.ffn)) + "\", \"inter\": " + std::to_string(L.inter) +
+              ", \"wq\": " + std::to_string(tensor_type(L.wq)) + ", \"wk\": " + std::to_string(tensor_type(L.wk)) +
+              ", \"wv\": " + std::to_string(tensor_type(L.wv)) + ", \"wo\": " + std::to_string(tensor_type(L.wo)) +
+              ", \"bias\": " + ((L.bq || L.bk || L.bv) ? "true" : "false") +
+              ", \"down\": " + std::to_string(tensor_type(L.w_down ? L.w_down : L.down_exps)) + "}";
+  }
+  layers += "]";
+  kv("layers", layers, false);
+  s += "}";
+  return s;
 }
 
 }  // namespace uaii

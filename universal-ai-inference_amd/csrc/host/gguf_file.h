@@ -106,4 +106,7 @@ struct DecoderSpec {
 // Derive the decoder; `max_layers_env` mirrors UAII_MAX_LAYERS (gguf.cpp:785-799).
 Error derive_decoder(const GgufFile& f, DecoderSpec* out);
 
+// JSON summary of a derived decoder (uaii_model_describe).
+std::string describe_decoder(const DecoderSpec& d);
+
 }  // namespace uaii
