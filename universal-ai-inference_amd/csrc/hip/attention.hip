@@ -294,6 +294,245 @@ __global__ void __launch_bounds__(256) k_attn_fast(AttnArgs a) {
   }
 }
 
+// ---- f16 KV, head_dim 64 / 128: one memory round trip per 32-key tile ---------------
+//
+// A wave takes tiles of TK = 32 keys. All K and V loads of a tile are issued
+// back to back before any arithmetic (16-byte loads, each lane group reading a
+// contiguous 64-byte (K) or 16-byte (V) run of a key row), so a block's keys cost
+// one memory round trip. Scores: LK = HD/32 lanes per key, each owning 32 dims;
+// v_dot2_f32_f16 on the exact f16 keys against q * scale split into f16 hi + lo
+// pairs (about 22 significant bits of q), sums f32, reduced over the LK lanes.
+// Online softmax per query head over the tile. P.V: LV = HD/8 lanes per key, 8
+// dims each, 64/LV keys per instruction; the key groups are reduced once at the
+// end. Partials as for the other kernels.
+typedef _Float16 attn_h2 __attribute__((ext_vector_type(2)));
+
+__device__ inline float adot2(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(attn_h2, a), __builtin_bit_cast(attn_h2, b), c, false);
+}
+
+__device__ inline uint32_t ah_bits(_Float16 h) { return (uint32_t)__builtin_bit_cast(uint16_t, h); }
+
+template <int HD, int G, int TK>
+__global__ void __launch_bounds__(256) k_attn_h16(AttnArgs a) {
+  constexpr int NW = 4;
+  static_assert(TK == 16 || TK == 32, "tile of 16 or 32 keys");
+  static_assert(TK >= 64 / (HD / 32), "at least one key per lane group in the scores");
+  constexpr int LK = HD / 32;            // lanes per key (scores)
+  constexpr int KPI = 64 / LK;           // keys per K instruction
+  constexpr int KJ = TK / KPI;           // keys per lane per tile (scores)
+  constexpr int LV = HD / 8;             // lanes per key (P.V)
+  constexpr int VPI = 64 / LV;           // keys per V instruction
+  constexpr int VJ = TK / VPI;           // keys per lane per tile (P.V)
+  __shared__ uint4 qh_s[G][HD / 8], ql_s[G][HD / 8];  // (q * scale) as f16 pairs, 4 pairs per uint4
+  __shared__ float p_s[NW][G][TK];       // layout [key % VPI][key / VPI] per g
+  __shared__ float wm[NW][G], wl[NW][G];
+  __shared__ float wo[NW][G][HD];
+
+  const int h = blockIdx.x, sblk = blockIdx.y, SB = gridDim.y;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t n = a.fixed_len > 0 ? (int64_t)a.fixed_len : (int64_t)a.state->pos + 1;
+  const int64_t CB = (n + SB - 1) / SB;
+  const int64_t b0 = (int64_t)sblk * CB, b1 = (b0 + CB < n) ? b0 + CB : n;
+  const float scale = 1.0f / sqrtf((float)HD);
+
+  // q of the group first: waiting for it does not wait for the K/V loads below
+  constexpr int QPT = (G * HD + 255) / 256;
+  float qv[QPT];
+#pragma unroll
+  for (int k = 0; k < QPT; ++k) {
+    const int i = tid + 256 * k;
+    qv[k] = (i < G * HD) ? a.q[(int64_t)h * G * HD + i] : 0.0f;
+  }
+
+  const __half* kc = reinterpret_cast<const __half*>(a.kcache) + (int64_t)h * a.max_seq * HD;
+  const __half* vc = reinterpret_cast<const __half*>(a.vcache) + (int64_t)h * a.max_seq * HD;
+  const int kq = lane % LK, kk = lane / LK;   // scores: dims [32 kq, 32 kq + 32) of key kk + KPI j
+  const int vd = lane % LV, vk = lane / LV;   // P.V: dims [8 vd, 8 vd + 8) of key vk + VPI j
+
+  uint4 kr[KJ][4], vr[VJ];
+  auto load_tile = [&](int64_t t0) {
+#pragma unroll
+    for (int j = 0; j < KJ; ++j) {
+      int64_t key = t0 + kk + KPI * j;
+      key = key < b1 ? key : b1 - 1;  // in bounds; masked below
+      const uint4* src = reinterpret_cast<const uint4*>(kc + key * HD + 32 * kq);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) kr[j][c] = src[c];
+    }
+#pragma unroll
+    for (int j = 0; j < VJ; ++j) {
+      int64_t key = t0 + vk + VPI * j;
+      key = key < b1 ? key : b1 - 1;
+      vr[j] = *reinterpret_cast<const uint4*>(vc + key * HD + 8 * vd);
+    }
+  };
+
+  const int64_t first = b0 + (int64_t)wave * TK;
+  if (first < b1) load_tile(first);
+
+  // q * scale -> f16 (hi, lo) pairs in LDS
+#pragma unroll
+  for (int k = 0; k < QPT; ++k) {
+    const int i = tid + 256 * k;
+    const float v = qv[k] * scale;
+    const _Float16 hi = (_Float16)v;
+    const _Float16 lo = (_Float16)(v - (float)hi);
+    if (i < G * HD) {
+      reinterpret_cast<uint16_t*>(&qh_s[0][0])[i] = (uint16_t)ah_bits(hi);
+      reinterpret_cast<uint16_t*>(&ql_s[0][0])[i] = (uint16_t)ah_bits(lo);
+    }
+  }
+  __syncthreads();
+
+  float m[G], l[G], o[G][8];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    m[g] = -INFINITY;
+    l[g] = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[g][e] = 0.0f;
+  }
+
+  for (int64_t t0 = first; t0 < b1; t0 += NW * TK) {
+    if (t0 != first) load_tile(t0);
+    // scores
+    float sc[KJ][G];
+#pragma unroll
+    for (int j = 0; j < KJ; ++j)
+#pragma unroll
+      for (int g = 0; g < G; ++g) sc[j][g] = 0.0f;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const uint4 qh = qh_s[g][4 * kq + c], ql = ql_s[g][4 * kq + c];
+#pragma unroll
+        for (int j = 0; j < KJ; ++j) {
+          float t = sc[j][g];
+          t = adot2(kr[j][c].x, qh.x, t); t = adot2(kr[j][c].x, ql.x, t);
+          t = adot2(kr[j][c].y, qh.y, t); t = adot2(kr[j][c].y, ql.y, t);
+          t = adot2(kr[j][c].z, qh.z, t); t = adot2(kr[j][c].z, ql.z, t);
+          t = adot2(kr[j][c].w, qh.w, t); t = adot2(kr[j][c].w, ql.w, t);
+          sc[j][g] = t;
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < KJ; ++j) {
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        float t = sc[j][g];
+#pragma unroll
+        for (int o2 = 1; o2 < LK; o2 <<= 1) t += __shfl_xor(t, o2, 64);
+        sc[j][g] = (t0 + kk + KPI * j < b1) ? t : -INFINITY;
+      }
+    }
+    // online softmax over the tile, per query head
+    float alpha[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float mx = sc[0][g];
+#pragma unroll
+      for (int j = 1; j < KJ; ++j) mx = fmaxf(mx, sc[j][g]);
+      const float mnew = fmaxf(m[g], wave_max(mx));
+      float ps = 0.0f;
+#pragma unroll
+      for (int j = 0; j < KJ; ++j) {
+        const float pv = (sc[j][g] == -INFINITY) ? 0.0f : expf(sc[j][g] - mnew);
+        ps += pv;
+        const int key = kk + KPI * j;
+        if (kq == 0) p_s[wave][g][(key % VPI) * VJ + key / VPI] = pv;
+      }
+      alpha[g] = (m[g] == -INFINITY) ? 0.0f : expf(m[g] - mnew);
+      l[g] = l[g] * alpha[g] + wave_sum(kq == 0 ? ps : 0.0f);
+      m[g] = mnew;
+    }
+    __builtin_amdgcn_wave_barrier();
+    // P.V
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[g][e] *= alpha[g];
+#pragma unroll
+    for (int j = 0; j < VJ; ++j) {
+      float vf[8];
+      const uint32_t w4[4] = {vr[j].x, vr[j].y, vr[j].z, vr[j].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        vf[2 * e] = __half2float(__ushort_as_half((uint16_t)(w4[e] & 0xffffu)));
+        vf[2 * e + 1] = __half2float(__ushort_as_half((uint16_t)(w4[e] >> 16)));
+      }
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const float pg = p_s[wave][g][vk * VJ + j];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[g][e] += pg * vf[e];
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+
+  // reduce the key groups of P.V (lanes vd, vd + LV, ...)
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float t = o[g][e];
+#pragma unroll
+      for (int o2 = LV; o2 < 64; o2 <<= 1) t += __shfl_xor(t, o2, 64);
+      o[g][e] = t;
+    }
+  // combine the 4 wave states of this block
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    if (lane == 0) { wm[wave][g] = m[g]; wl[wave][g] = l[g]; }
+    if (lane < LV) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) wo[wave][g][8 * lane + e] = o[g][e];
+    }
+  }
+  __syncthreads();
+  const int64_t pstride = HD + 2;
+  float* part = a.part + ((int64_t)h * SB + sblk) * G * pstride;
+  for (int i = tid; i < G * HD; i += 256) {
+    const int g = i / HD, d = i % HD;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) M = fmaxf(M, wm[w][g]);
+    float acc = 0.0f, den = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const float f = (wm[w][g] == -INFINITY) ? 0.0f : expf(wm[w][g] - M);
+      acc += f * wo[w][g][d];
+      den += f * wl[w][g];
+    }
+    part[g * pstride + d] = acc;
+    if (d == 0) {
+      part[g * pstride + HD] = M;
+      part[g * pstride + HD + 1] = den;
+    }
+  }
+}
+
+// Tiles of 32 keys per wave: a block covers 128 keys per pass. (16-key tiles
+// with twice the splits measured slower end to end: more blocks and a wider
+// merge cost more than the shorter per-block chain saves.)
+template <int HD>
+bool launch_h16(const AttnArgs& a, int G, hipStream_t s) {
+  constexpr int TK = 32;
+  dim3 grid(a.n_kv, a.splits);
+  switch (G) {
+    case 1: hipLaunchKernelGGL((k_attn_h16<HD, 1, TK>), grid, dim3(256), 0, s, a); return true;
+    case 2: hipLaunchKernelGGL((k_attn_h16<HD, 2, TK>), grid, dim3(256), 0, s, a); return true;
+    case 4: hipLaunchKernelGGL((k_attn_h16<HD, 4, TK>), grid, dim3(256), 0, s, a); return true;
+    case 8: hipLaunchKernelGGL((k_attn_h16<HD, 8, TK>), grid, dim3(256), 0, s, a); return true;
+    default: return false;
+  }
+}
+
+
 // Merge the SB block partials of every query head (one block per head):
 // out = sum_s w_s o_s / sum_s w_s l_s with w_s = exp(m_s - max_s m_s).
 __global__ void __launch_bounds__(256) k_attn_merge(AttnArgs a) {
@@ -348,14 +587,22 @@ bool launch_fast_hd(const AttnArgs& a, int G, hipStream_t s) {
   }
 }
 
+// Key splits of the decode attention for a cache of max_seq positions: one per
+// 128 keys, at most 32 (one 32-key tile per wave at 4096 positions).
+int attention_splits(int64_t max_seq) {
+  const int64_t s = (max_seq + 127) / 128;
+  return (int)(s < 1 ? 1 : (s > 32 ? 32 : s));
+}
+
 hipError_t launch_attention_decode(const AttnArgs& a, hipStream_t s) {
   const int G = a.n_heads / a.n_kv;
   if (G < 1 || G > MAXG || a.hd > 256 || a.hd % 2 || a.n_heads % a.n_kv) return hipErrorInvalidValue;
   if (a.splits < 1 || a.splits > 64) return hipErrorInvalidValue;
   if ((a.hd == 64 || a.hd == 128) && (G == 1 || G == 2 || G == 4 || G == 8)) {
     bool ok;
-    if (a.hd == 64) ok = a.kv_f16 ? launch_fast_hd<true, 64>(a, G, s) : launch_fast_hd<false, 64>(a, G, s);
-    else ok = a.kv_f16 ? launch_fast_hd<true, 128>(a, G, s) : launch_fast_hd<false, 128>(a, G, s);
+    if (a.kv_f16) ok = (a.hd == 64) ? launch_h16<64>(a, G, s) : launch_h16<128>(a, G, s);
+    else if (a.hd == 64) ok = launch_fast_hd<false, 64>(a, G, s);
+    else ok = launch_fast_hd<false, 128>(a, G, s);
     if (ok) {
       const hipError_t st = hipGetLastError();
       if (st != hipSuccess) return st;

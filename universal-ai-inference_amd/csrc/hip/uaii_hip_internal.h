@@ -115,6 +115,7 @@ struct AttnArgs {
   int splits;
 };
 
+int attention_splits(int64_t max_seq);
 hipError_t launch_attention_decode(const AttnArgs& a, hipStream_t s);
 hipError_t prepare_attention();
 

@@ -212,7 +212,7 @@ int uaii_hip_attention_decode(const float* q, const void* kcache, const void* vc
       n_heads % n_kv_heads || head_dim <= 0 || n_keys <= 0 || n_keys > max_seq)
     return kErrArg;
   std::lock_guard<std::mutex> lk(g_scratch_mu);
-  const int splits = (int)std::min<int64_t>(32, std::max<int64_t>(1, (max_seq + 127) / 128));
+  const int splits = uaii_hip::attention_splits(max_seq);
   const int G = n_heads / n_kv_heads;
   const size_t part = (size_t)n_kv_heads * splits * G * (size_t)(head_dim + 2) * 4;
   int rc = grow_scratch(part);

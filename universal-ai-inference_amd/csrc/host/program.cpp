@@ -250,7 +250,7 @@ Error DecoderProgram::ensure_capacity(int64_t max_seq) {
   std::vector<float2> tab = rope_table(d.rope_theta, hd, max_seq);
   UAII_HIP(hipMalloc((void**)&rope_, tab.size() * sizeof(float2)));
   UAII_HIP(hipMemcpy(rope_, tab.data(), tab.size() * sizeof(float2), hipMemcpyHostToDevice));
-  attn_splits_ = (int)std::min<int64_t>(32, std::max<int64_t>(1, (max_seq + 127) / 128));
+  attn_splits_ = attention_splits(max_seq);
   const int G = (int)(d.n_heads / d.n_kv_heads);
   const size_t part = (size_t)d.n_kv_heads * attn_splits_ * G * (size_t)(hd + 2);
   UAII_HIP(hipMalloc((void**)&attn_part_, part * 4));
