@@ -255,6 +255,8 @@ Error matmul(const TensorView& x, const Weight& w, TensorView* y) {
 // (Path A for MoE, whose experts only work on f32, transformer.cpp:551-554), a
 // reference KvCache, and run() = one Session::run() over the graph order of
 // gguf.cpp:935-1209.
+constexpr int NW = 19;  // weights per layer bound by RefRunner
+
 struct RefRunner {
   orc_model* m = nullptr;
   std::int64_t L = 0, D = 0, H = 0, HKV = 0, hd = 0, V = 0, E = 0, topk = 0, rope_mode = 0,
@@ -285,30 +287,35 @@ struct RefRunner {
     theta = fp[0]; eps = fp[1];
     path_a = E > 0;
     qd = H * hd; kvd = HKV * hd;
-    W.resize(static_cast<std::size_t>(L * 16));
+    W.resize(static_cast<std::size_t>(L * NW));
     bind_weight(m, "token_embd.weight", false, path_a, &emb);
     bind_weight(m, "output_norm.weight", true, path_a, &onorm);
     if (!bind_weight(m, "output.weight", false, path_a, &lm)) {
       bind_weight(m, "token_embd.weight", false, path_a, &lm);  // tied (gguf.cpp:813-816)
     }
-    static const char* names[16] = {"attn_norm", "attn_q", "attn_k", "attn_v", "attn_output",
+    // per layer: 0 attn_norm .. 8 ffn_down, 9-12 MoE router/experts, 13-15 q/k/v
+    // biases, 16-18 shared expert gate/up/down (gguf.cpp:1107-1128)
+    static const char* names[NW] = {"attn_norm", "attn_q", "attn_k", "attn_v", "attn_output",
                                     "ffn_norm", "ffn_gate", "ffn_up", "ffn_down",
                                     "ffn_gate_inp", "ffn_gate_exps", "ffn_up_exps",
                                     "ffn_down_exps", "attn_q.bias", "attn_k.bias",
-                                    "attn_v.bias"};
+                                    "attn_v.bias", "ffn_gate_shexp", "ffn_up_shexp",
+                                    "ffn_down_shexp"};
     for (std::int64_t li = 0; li < L; ++li) {
-      for (int kk = 0; kk < 16; ++kk) {
+      for (int kk = 0; kk < NW; ++kk) {
         std::string nm = "blk." + std::to_string(li) + "." + names[kk];
-        if (kk < 13) nm += ".weight";
-        const bool f32_always = (kk == 0 || kk == 5 || kk >= 9);
-        bind_weight(m, nm, f32_always, path_a, &W[li * 16 + kk]);
+        if (kk < 13 || kk >= 16) nm += ".weight";
+        const bool f32_always = (kk == 0 || kk == 5 || (kk >= 9 && kk < 16));
+        bind_weight(m, nm, f32_always, path_a, &W[li * NW + kk]);
       }
     }
     for (std::int64_t li = 0; li < L; ++li) {
-      const Weight& up = W[li * 16 + 7];
-      const Weight& ge = W[li * 16 + 10];
+      const Weight& up = W[li * NW + 7];
+      const Weight& ge = W[li * NW + 10];
+      const Weight& ush = W[li * NW + 17];
       if (up.present) ff = std::max<std::int64_t>(ff, up.shape[0]);
       if (ge.present) ff = std::max<std::int64_t>(ff, ge.shape[1]);
+      if (ush.present) ff = std::max<std::int64_t>(ff, ush.shape[0]);
     }
     const std::int64_t kv_max =
         kv_max_override > 0 ? kv_max_override
@@ -337,7 +344,7 @@ struct RefRunner {
     if (!err.ok()) return err;
     std::memcpy(fi->f32.data(), x->f32.data(), D * 4);
     for (std::int64_t li = 0; li < L; ++li) {
-      Weight* w = &W[li * 16];
+      Weight* w = &W[li * NW];
       if (!(err = kernels::rmsnorm_f32(fi->view, &w[0].view, &n1->view, eps)).ok()) return err;
       if (!(err = matmul(n1->view, w[1], &q->view)).ok()) return err;
       if (!(err = matmul(n1->view, w[2], &k->view)).ok()) return err;
@@ -364,11 +371,33 @@ struct RefRunner {
         if (!(err = kernels::rmsnorm_f32(res1->view, &w[5].view, &n2->view, eps)).ok()) return err;
         min = n2->view;
       }
+      auto set_width = [&](std::int64_t I) {
+        g->shape[1] = u->shape[1] = ga->shape[1] = hid->shape[1] = I;
+        g->view.nbytes = u->view.nbytes = ga->view.nbytes = hid->view.nbytes =
+            static_cast<std::size_t>(I) * 4;
+      };
       if (w[9].present && w[10].present) {
         if (!(err = kernels::moe_router_f32(min, w[9].view, &mp->view, &mt->view)).ok()) return err;
         err = kernels::moe_experts_swiglu_f32(min, w[10].view, w[11].view, w[12].view, mp->view,
                                               &fo->view, static_cast<int>(E), static_cast<int>(topk));
         if (!err.ok()) return err;
+        if (w[16].present && w[17].present && w[18].present) {
+          // shared expert: silu(min@gate_sh) * (min@up_sh) @ down_sh, added to ff_out
+          set_width(w[17].shape[0]);
+          if (!(err = matmul(min, w[16], &g->view)).ok()) return err;
+          if (!(err = matmul(min, w[17], &u->view)).ok()) return err;
+          if (!(err = kernels::silu_f32(g->view, &ga->view)).ok()) return err;
+          if (!(err = kernels::mul_f32(ga->view, u->view, &hid->view)).ok()) return err;
+          if (!(err = matmul(hid->view, w[18], &ao->view)).ok()) return err;
+          if (!(err = kernels::add_f32(fo->view, ao->view, &n1->view)).ok()) return err;
+          std::memcpy(fo->f32.data(), n1->f32.data(), D * 4);
+        }
+      } else if (!w[6].present && w[7].present && w[8].present) {
+        // dense GELU MLP (gguf.cpp:1156-1170)
+        set_width(w[7].shape[0]);
+        if (!(err = matmul(min, w[7], &u->view)).ok()) return err;
+        if (!(err = kernels::gelu_f32(u->view, &ga->view)).ok()) return err;
+        if (!(err = matmul(ga->view, w[8], &fo->view)).ok()) return err;
       } else {
         const std::int64_t I = w[7].shape[0];
         g->shape[1] = u->shape[1] = ga->shape[1] = hid->shape[1] = I;

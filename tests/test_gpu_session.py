@@ -43,6 +43,19 @@ SMALL = {
                                 vocab=1024, ctx_len=256, type_default=uaii_amd.Q5_K,
                                 type_attn_v=uaii_amd.Q5_0, type_ffn_down=uaii_amd.Q3_K,
                                 type_embd=uaii_amd.Q5_1, type_output=uaii_amd.Q2_K, seed=34),
+    # MoE: 4 experts top-2 (router on the device), Q4_K experts
+    "moe_k": synth.ModelConfig(n_layers=2, dim=512, n_heads=8, n_kv_heads=2, ffn=512,
+                               vocab=1200, ctx_len=256, type_default=uaii_amd.Q4_K, n_experts=4,
+                               top_k=2, router_std=1.0 / 22, seed=35),
+    # MoE 8 experts top-2 with a shared expert, Q4_0
+    "moe_shared": synth.ModelConfig(n_layers=2, dim=256, n_heads=4, n_kv_heads=4, ffn=320,
+                                    vocab=700, ctx_len=256, type_default=uaii_amd.Q4_0,
+                                    n_experts=8, top_k=2, router_std=1.0 / 16, shared_ffn=192,
+                                    seed=36),
+    # dense GELU MLP and Q/K/V biases
+    "gelu_bias": synth.ModelConfig(n_layers=2, dim=512, n_heads=8, n_kv_heads=4, ffn=1024,
+                                   vocab=1500, ctx_len=256, type_default=uaii_amd.Q8_0, gelu=True,
+                                   qkv_bias=True, seed=37),
 }
 
 

@@ -484,28 +484,30 @@ struct UnitBuf {
 };
 
 // Wave-uniform row pointers of logical rows l0 .. l0+R-1 of a segment.
+// `ebase` is the first physical row of the segment's expert (0 without MoE).
 template <int EPI, int R>
-__device__ inline void unit_rows(const GemvArgs& a, const GemvSeg& seg, int64_t l0, RowPtr* P) {
+__device__ inline void unit_rows(const GemvArgs& a, const GemvSeg& seg, int64_t ebase, int64_t l0,
+                                 RowPtr* P) {
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     int64_t l = l0 + r;
     if (l >= seg.rows) l = seg.rows - 1;  // clamp: duplicate work, result dropped
     if constexpr (EPI == EPI_SWIGLU) {
-      P[r] = row_ptr((l & 1) ? seg.w2 : seg.w, l >> 1);
+      P[r] = row_ptr((l & 1) ? seg.w2 : seg.w, ebase + (l >> 1));
     } else if constexpr (EPI == EPI_QKV) {
       P[r] = row_ptr(seg.w, seg.kind == 2 ? l : qkv_phys(l, a.rope_mode, a.head_dim));
     } else {
-      P[r] = row_ptr(seg.w, l);
+      P[r] = row_ptr(seg.w, ebase + l);
     }
   }
 }
 
 template <int FMT, int EPI>
-__device__ inline void load_unit(const GemvArgs& a, const GemvSeg& seg, const Walk& wk,
+__device__ inline void load_unit(const GemvArgs& a, const GemvSeg& seg, int64_t ebase, const Walk& wk,
                                  int64_t l0, int step, int lane, UnitBuf<FMT>& U) {
   constexpr int R = rpw_of(FMT);
   RowPtr P[R];
-  unit_rows<EPI, R>(a, seg, l0, P);
+  unit_rows<EPI, R>(a, seg, ebase, l0, P);
   // Straight-line loads: a column past the wave's range, or a lane past the row's
   // last chunk, loads an in-bounds chunk again and compute_unit drops it. (A
   // branch around some of the loads would make the compiler's wait counts
@@ -558,13 +560,13 @@ __device__ inline void compute_unit(const Walk& wk, int step, int lane, const fl
 // Stage x (optionally RMS-normalised: x * (1/sqrt(mean(x^2)+eps)) * w, two
 // roundings per element as in norm.cpp:122-127) into LDS.
 template <int FMT>
-__device__ inline void stage_x(const GemvArgs& a, int64_t nch, float* xsm, float* red) {
+__device__ inline void stage_x(const GemvArgs& a, const float* xin, int64_t nch, float* xsm, float* red) {
   // Loads are issued in unrolled batches of 4 float4 per thread so a block pays
   // one memory round trip per batch (a plain strided loop serialises them).
   constexpr int B = 4;
   const int tid = threadIdx.x, nt = blockDim.x;
   const int nv = (int)(a.K / 4);
-  const float4* x4 = reinterpret_cast<const float4*>(a.x);
+  const float4* x4 = reinterpret_cast<const float4*>(xin);
   const float4* w4 = reinterpret_cast<const float4*>(a.norm_w);
   float4* s4 = reinterpret_cast<float4*>(xsm);
   const bool tap = a.xtap && blockIdx.x == 0;
@@ -672,10 +674,10 @@ struct PairStage {
 };
 
 template <int FMT>
-__device__ inline void stage_pairs_issue(const GemvArgs& a, int64_t nch, PairStage& ps) {
+__device__ inline void stage_pairs_issue(const GemvArgs& a, const float* xin, int64_t nch, PairStage& ps) {
   const int tid = threadIdx.x, nt = blockDim.x;
   const int64_t items = nch * 4;
-  const float4* x4 = reinterpret_cast<const float4*>(a.x);
+  const float4* x4 = reinterpret_cast<const float4*>(xin);
   const float4* w4 = reinterpret_cast<const float4*>(a.norm_w);
 #pragma unroll
   for (int k = 0; k < PB; ++k) {
@@ -746,11 +748,11 @@ __device__ inline void emit_pair_item(const GemvArgs& a, int64_t nch, int64_t it
 }
 
 template <int FMT>
-__device__ inline void stage_pairs_finish(const GemvArgs& a, int64_t nch, const PairStage& ps,
+__device__ inline void stage_pairs_finish(const GemvArgs& a, const float* xin, int64_t nch, const PairStage& ps,
                                           float* xsm, float* red) {
   const int tid = threadIdx.x, nt = blockDim.x;
   const int64_t items = nch * 4;
-  const float4* x4 = reinterpret_cast<const float4*>(a.x);
+  const float4* x4 = reinterpret_cast<const float4*>(xin);
   const float4* w4 = reinterpret_cast<const float4*>(a.norm_w);
   const bool norm = w4 != nullptr;
   const bool wregs = items <= (int64_t)PBW * nt;  // norm weights of every item in registers
@@ -821,7 +823,7 @@ __device__ inline void stage_pairs_finish(const GemvArgs& a, int64_t nch, const 
 template <int EPI, int R>
 __device__ inline void epilogue(const GemvArgs& a, const GemvSeg& seg, int64_t lrow0, int lane,
                                 const float* acc, float& best_v, int32_t& best_i) {
-  if constexpr (EPI == EPI_STORE || EPI == EPI_ADD || EPI == EPI_LOGITS) {
+  if constexpr (EPI == EPI_STORE || EPI == EPI_ADD || EPI == EPI_LOGITS || EPI == EPI_GELU) {
     if (lane < R) {
       float v = 0.0f;
 #pragma unroll
@@ -829,7 +831,15 @@ __device__ inline void epilogue(const GemvArgs& a, const GemvSeg& seg, int64_t l
       const int64_t l = lrow0 + lane;
       if (l < seg.rows) {
         const int64_t o = seg.row_base + l;
-        if constexpr (EPI == EPI_ADD) v = a.y[o] + v;
+        if constexpr (EPI == EPI_ADD) {
+          if (seg.scale) v = seg.scale[0] * v;  // MoE expert weight (transformer.cpp:600-608)
+          v = a.y[o] + v;
+        }
+        if constexpr (EPI == EPI_GELU) {
+          // tanh-form GELU (elementwise.cpp:57-71)
+          const float inner = 0.7978845608f * (v + 0.044715f * v * v * v);
+          v = 0.5f * v * (1.0f + tanhf(inner));
+        }
         a.y[o] = v;
         if (a.tap) a.tap[o] = v;
       }
@@ -925,6 +935,8 @@ __global__ void __launch_bounds__(WPB * 64) k_gemv(GemvArgs a) {
   wk.cend = min(ncol, wk.cbeg + per);
   wk.steps = (per + 1) / 2;
 
+  const float* xin = seg.x ? seg.x : a.x;
+  const int64_t ebase = seg.expert ? (int64_t)seg.expert[0] * seg.expert_rows : 0;
   const int64_t g0 = (int64_t)blockIdx.x - seg.block0;
   const int64_t mine = (g0 < ngroups) ? (ngroups - g0 + nblk - 1) / nblk : 0;
   const int64_t nunits = mine * wk.steps;
@@ -937,12 +949,12 @@ __global__ void __launch_bounds__(WPB * 64) k_gemv(GemvArgs a) {
   UnitBuf<FMT> U0;
   if constexpr (pair_fmt<FMT>()) {
     PairStage ps;
-    stage_pairs_issue<FMT>(a, wk.nch, ps);
-    if (nunits > 0) load_unit<FMT, EPI>(a, seg, wk, unit_l0(0), 0, lane, U0);
-    stage_pairs_finish<FMT>(a, wk.nch, ps, xsm, red);
+    stage_pairs_issue<FMT>(a, xin, wk.nch, ps);
+    if (nunits > 0) load_unit<FMT, EPI>(a, seg, ebase, wk, unit_l0(0), 0, lane, U0);
+    stage_pairs_finish<FMT>(a, xin, wk.nch, ps, xsm, red);
   } else {
-    if (nunits > 0) load_unit<FMT, EPI>(a, seg, wk, unit_l0(0), 0, lane, U0);
-    stage_x<FMT>(a, wk.nch, xsm, red);
+    if (nunits > 0) load_unit<FMT, EPI>(a, seg, ebase, wk, unit_l0(0), 0, lane, U0);
+    stage_x<FMT>(a, xin, wk.nch, xsm, red);
   }
 
   float best_v = -INFINITY;
@@ -985,14 +997,14 @@ __global__ void __launch_bounds__(WPB * 64) k_gemv(GemvArgs a) {
     }
     for (int64_t u = 1; u < nunits; ++u) {
       UnitBuf<FMT> V;
-      load_unit<FMT, EPI>(a, seg, wk, unit_l0(u), unit_step(u), lane, V);
+      load_unit<FMT, EPI>(a, seg, ebase, wk, unit_l0(u), unit_step(u), lane, V);
       compute_unit<FMT>(wk, unit_step(u), lane, xsm, V, acc);
       finish(u);
     }
   } else {
     if (nunits > 0) {
       UnitBuf<FMT> U1;
-      if (nunits > 1) load_unit<FMT, EPI>(a, seg, wk, unit_l0(1), unit_step(1), lane, U1);
+      if (nunits > 1) load_unit<FMT, EPI>(a, seg, ebase, wk, unit_l0(1), unit_step(1), lane, U1);
       compute_unit<FMT>(wk, 0, lane, xsm, U0, acc);
       finish(0);
       if (nunits > 1) {
@@ -1003,8 +1015,8 @@ __global__ void __launch_bounds__(WPB * 64) k_gemv(GemvArgs a) {
     for (int64_t u = 2; u < nunits; u += 2) {
       UnitBuf<FMT> V0, V1;
       const bool two = u + 1 < nunits;  // block-uniform
-      load_unit<FMT, EPI>(a, seg, wk, unit_l0(u), unit_step(u), lane, V0);
-      if (two) load_unit<FMT, EPI>(a, seg, wk, unit_l0(u + 1), unit_step(u + 1), lane, V1);
+      load_unit<FMT, EPI>(a, seg, ebase, wk, unit_l0(u), unit_step(u), lane, V0);
+      if (two) load_unit<FMT, EPI>(a, seg, ebase, wk, unit_l0(u + 1), unit_step(u + 1), lane, V1);
       compute_unit<FMT>(wk, unit_step(u), lane, xsm, V0, acc);
       finish(u);
       if (two) {
@@ -1110,6 +1122,7 @@ KernelFn pick(int epi, int type) {
     case EPI_QKV: return pick_fmt<EPI_QKV>(type);
     case EPI_SWIGLU: return pick_fmt<EPI_SWIGLU>(type);
     case EPI_LOGITS: return pick_fmt<EPI_LOGITS>(type);
+    case EPI_GELU: return pick_fmt<EPI_GELU>(type);
     default: return nullptr;
   }
 }
@@ -1119,7 +1132,7 @@ KernelFn pick(int epi, int type) {
 // Raise each instantiation's dynamic-LDS limit to what the device allows per
 // block (where the runtime accepts the attribute; otherwise its default holds).
 hipError_t prepare_gemv() {
-  const int epis[] = {EPI_STORE, EPI_ADD, EPI_QKV, EPI_SWIGLU, EPI_LOGITS};
+  const int epis[] = {EPI_STORE, EPI_ADD, EPI_QKV, EPI_SWIGLU, EPI_LOGITS, EPI_GELU};
   const int types[] = {T_Q4_0, T_Q8_0, T_Q4_K, T_Q6_K, T_Q4_1, T_Q5_0,
                        T_Q5_1, T_Q5_K, T_Q2_K, T_Q3_K, T_F32,  T_F16};
   const int lim = lds_limit();
@@ -1254,6 +1267,16 @@ hipError_t launch_gemv(const GemvArgs& in, hipStream_t s) {
     if (in.epi == EPI_SWIGLU && in.seg[k].w2.type != in.seg[k].w.type) return hipErrorInvalidValue;
     if ((in.epi == EPI_SWIGLU || in.epi == EPI_QKV) && (in.seg[k].rows % 2)) return hipErrorInvalidValue;
     if (in.seg[k].w.cols != in.K) return hipErrorInvalidValue;
+    // every row a segment can touch lies inside its weight (and up-weight)
+    const GemvSeg& g = in.seg[k];
+    const int64_t need = (in.epi == EPI_SWIGLU) ? g.rows / 2 : g.rows;
+    if (g.expert) {
+      if (g.expert_rows <= 0 || need > g.expert_rows || g.w.rows % g.expert_rows) return hipErrorInvalidValue;
+      if (in.epi == EPI_SWIGLU && g.w2.rows != g.w.rows) return hipErrorInvalidValue;
+    } else if (in.epi != EPI_QKV) {
+      if (need > g.w.rows) return hipErrorInvalidValue;
+      if (in.epi == EPI_SWIGLU && need > g.w2.rows) return hipErrorInvalidValue;
+    }
   }
   return for_each_run(in, [&](const GemvArgs& run) {
     GemvArgs a = run;

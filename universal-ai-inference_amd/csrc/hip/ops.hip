@@ -8,6 +8,8 @@
 //   k_rope        standalone RoPE rows (transformer.cpp:144-220)
 //   k_stream_copy plain 16-byte-word copy: the yardstick for HBM rates and for
 //                 scaling the memory counters of the other kernels
+//   k_moe_route   router softmax, top-k, renormalised weights (transformer.cpp:446-481,
+//                 :565-580)
 
 #include "common.h"
 #include "uaii_hip_internal.h"
@@ -164,7 +166,69 @@ __global__ void __launch_bounds__(256) k_stream_copy(const uint4* __restrict__ s
   for (; i < n; i += stride) dst[i] = src[i];
 }
 
+// One wave, E <= 256 router logits: probs = softmax (exp(l - max), times 1/sum,
+// softmax.cpp:11-77), then k rounds of the largest remaining prob (ties: the
+// lower expert), weights = p / (sum of the k chosen probs). Writes ids[k], w[k].
+__global__ void __launch_bounds__(64) k_moe_route(const float* __restrict__ logits, int E, int k,
+                                                  int32_t* __restrict__ ids, float* __restrict__ w) {
+  const int lane = threadIdx.x;
+  float p[4];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int e = lane + 64 * j;
+    p[j] = e < E ? logits[e] : -INFINITY;
+    mx = fmaxf(mx, p[j]);
+  }
+  mx = wave_max(mx);
+  float sum = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int e = lane + 64 * j;
+    p[j] = e < E ? expf(p[j] - mx) : 0.0f;
+    sum += p[j];
+  }
+  sum = wave_sum(sum);
+  const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) p[j] = (lane + 64 * j < E) ? p[j] * inv : -1.0f;
+  float mass = 0.0f;
+  for (int t = 0; t < k; ++t) {
+    // lane-local best (lowest index on ties), then across the wave
+    float bv = -1.0f;
+    int be = 0x7fffffff;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (p[j] > bv) { bv = p[j]; be = lane + 64 * j; }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const float ov = __shfl_xor(bv, o, 64);
+      const int oe = __shfl_xor(be, o, 64);
+      if (ov > bv || (ov == bv && oe < be)) { bv = ov; be = oe; }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (lane + 64 * j == be) p[j] = -1.0f;  // taken
+    if (lane == 0) {
+      ids[t] = (be >= 0 && be < E) ? be : 0;
+      w[t] = bv;
+    }
+    mass += bv;
+  }
+  if (!(mass > 0.0f)) mass = 1.0f;
+  if (lane == 0) {
+    for (int t = 0; t < k; ++t) w[t] = w[t] / mass;
+  }
+}
+
 }  // namespace
+
+hipError_t launch_moe_route(const float* logits, int n_experts, int k, int32_t* ids, float* w,
+                            hipStream_t s) {
+  if (n_experts < 1 || n_experts > 256 || k < 1 || k > 8 || k > n_experts) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_moe_route, dim3(1), dim3(64), 0, s, logits, n_experts, k, ids, w);
+  return hipGetLastError();
+}
 
 hipError_t launch_copy(const void* src, void* dst, int64_t n16, hipStream_t s) {
   if (n16 <= 0) return hipSuccess;

@@ -24,6 +24,7 @@ enum Epilogue : int {
   EPI_QKV = 2,     // bias, RoPE pairs, q -> y, k/v -> KV cache at pos
   EPI_SWIGLU = 3,  // rows (gate i, up i) -> y[i] = silu(g) * u
   EPI_LOGITS = 4,  // y[row] = dot, block argmax partials (+ final argmax/advance kernel)
+  EPI_GELU = 5,    // y[row] = gelu(dot) (tanh form, elementwise.cpp:57-71)
 };
 
 // Persistent decode state shared by the step kernels (device memory).
@@ -45,6 +46,12 @@ struct GemvSeg {
   int64_t row_base;    // first logical row in the epilogue's output space
   int kind;            // EPI_QKV: 0 = q, 1 = k, 2 = v
   int block0;          // first block of this segment
+  // MoE: the weight rows of expert *expert (device memory) of a [E * expert_rows]
+  // stack: physical row = *expert * expert_rows + row (w and w2 alike)
+  const int32_t* expert;
+  int64_t expert_rows;
+  const float* scale;  // EPI_ADD: y += *scale * dot (device memory), or null
+  const float* x;      // this segment's input vector, or null for GemvArgs::x
 };
 
 struct GemvArgs {
@@ -82,6 +89,11 @@ hipError_t launch_gemv(const GemvArgs& a, hipStream_t s);
 hipError_t prepare_gemv();
 // Number of blocks launch_gemv will use for the given args (for partial buffers).
 int gemv_grid(const GemvArgs& a);
+
+// MoE routing (transformer.cpp:446-481, :565-580): probs = softmax(logits[E]),
+// the k largest (ties: lower expert first), weights renormalised over them.
+hipError_t launch_moe_route(const float* logits, int n_experts, int k, int32_t* ids, float* w,
+                            hipStream_t s);
 
 // ---- small ops -------------------------------------------------------------------
 

@@ -189,13 +189,42 @@ Error DecoderProgram::build(const DecoderSpec& spec, const ProgramOptions& opts)
       UAII_TRY(up(s.w_gate, &L->gate));
       UAII_TRY(up(s.w_up, &L->up));
       UAII_TRY(up(s.w_down, &L->down));
-      ffn_max_ = std::max(ffn_max_, s.inter);
-    } else if (s.ffn == LayerSpec::kNone) {
-      // resid2 = resid1 (gguf.cpp:1171-1173)
+      hid_max_ = std::max(hid_max_, 2 * s.inter);
+    } else if (s.ffn == LayerSpec::kGelu) {
+      // dense GELU MLP (gguf.cpp:1156-1170)
+      UAII_TRY(up(s.w_up, &L->up));
+      UAII_TRY(up(s.w_down, &L->down));
+      hid_max_ = std::max(hid_max_, s.inter);
+    } else if (s.ffn == LayerSpec::kMoE) {
+      // router + expert stacks [E, I, D] / [E, D, I] as 2-D weights of E*I (E*D) rows
+      // (gguf.cpp:1076-1106), optional shared expert (:1107-1128)
+      const int64_t E = d.n_experts, I = s.inter;
+      if (E < 1 || E > 256 || d.top_k < 1 || d.top_k > 8)
+        return Error::make(ErrorCode::NotImplemented, "MoE with more than 256 experts or top_k > 8");
+      if (s.gate_exps->type != s.up_exps->type)
+        return Error::make(ErrorCode::NotImplemented, "ffn_gate_exps and ffn_up_exps must share a quant type");
+      if (s.gate_inp->rows() != E || s.gate_inp->cols() != d.dim || s.gate_exps->rows() != E * I ||
+          s.up_exps->rows() != E * I || s.down_exps->rows() != E * d.dim || s.down_exps->cols() != I)
+        return Error::make(ErrorCode::InvalidArgument, "MoE tensor shapes do not match expert_count");
+      UAII_TRY(up(s.gate_inp, &L->gate_inp));
+      UAII_TRY(up(s.gate_exps, &L->gate_exps));
+      UAII_TRY(up(s.up_exps, &L->up_exps));
+      UAII_TRY(up(s.down_exps, &L->down_exps));
+      int64_t width = std::min<int64_t>(d.top_k, E) * I;
+      if (s.gate_sh && s.up_sh && s.down_sh) {
+        if (s.gate_sh->type != s.up_sh->type)
+          return Error::make(ErrorCode::NotImplemented, "ffn_gate_shexp and ffn_up_shexp must share a quant type");
+        UAII_TRY(up(s.gate_sh, &L->gate_sh));
+        UAII_TRY(up(s.up_sh, &L->up_sh));
+        UAII_TRY(up(s.down_sh, &L->down_sh));
+        L->shared = true;
+        L->inter_sh = s.up_sh->rows();
+        width += L->inter_sh;
+      }
+      hid_max_ = std::max(hid_max_, width);
+      moe_ = true;
     } else {
-      return Error::make(ErrorCode::NotImplemented,
-                         s.ffn == LayerSpec::kMoE ? "MoE FFN not supported by this build yet"
-                                                  : "GELU FFN not supported by this build yet");
+      // kNone: resid2 = resid1 (gguf.cpp:1171-1173)
     }
     layers_.push_back(std::move(L));
   }
@@ -211,7 +240,12 @@ Error DecoderProgram::build(const DecoderSpec& spec, const ProgramOptions& opts)
   UAII_TRY(alloc(4 * D, (void**)&x_));
   UAII_TRY(alloc(4 * Q, (void**)&q_));
   UAII_TRY(alloc(4 * Q, (void**)&attn_));
-  UAII_TRY(alloc(4 * (size_t)std::max<int64_t>(ffn_max_, 1) * 2, (void**)&h_));
+  UAII_TRY(alloc(4 * (size_t)std::max<int64_t>(hid_max_, 1), (void**)&h_));
+  if (moe_) {
+    UAII_TRY(alloc(4 * (size_t)d.n_experts, (void**)&moe_logits_));
+    UAII_TRY(alloc(4 * 8, (void**)&moe_ids_));
+    UAII_TRY(alloc(4 * 8, (void**)&moe_w_));
+  }
   UAII_TRY(alloc(4 * V, (void**)&logits_));
   UAII_TRY(alloc(4 * V, (void**)&probs_));
   UAII_TRY(alloc(4 * D, (void**)&tap_hidden_));
@@ -437,6 +471,109 @@ Error DecoderProgram::encode_step(bool want_logits) {
       dn.seg[0].rows = d.dim;
       dn.state = state_;
       UAII_TRY(timed("gemv_down", gemv_bytes(L.down.view), [&] { return launch_gemv(dn, s); }));
+    } else if (ls.ffn == LayerSpec::kGelu) {
+      GemvArgs g{};
+      g.nseg = 1;
+      g.epi = EPI_GELU;
+      g.K = d.dim;
+      g.x = x_;
+      g.norm_w = L.ffn_norm;
+      g.eps = d.rms_eps;
+      g.y = h_;
+      g.seg[0].w = L.up.view;
+      g.seg[0].rows = ls.inter;
+      g.state = state_;
+      UAII_TRY(timed("gemv_up_gelu", gemv_bytes(L.up.view), [&] { return launch_gemv(g, s); }));
+      GemvArgs dn{};
+      dn.nseg = 1;
+      dn.epi = EPI_ADD;
+      dn.K = ls.inter;
+      dn.x = h_;
+      dn.y = x_;
+      dn.tap = tap_r2_ + li * d.dim;
+      dn.seg[0].w = L.down.view;
+      dn.seg[0].rows = d.dim;
+      dn.state = state_;
+      UAII_TRY(timed("gemv_down", gemv_bytes(L.down.view), [&] { return launch_gemv(dn, s); }));
+    } else if (ls.ffn == LayerSpec::kMoE) {
+      // router logits on the ffn_norm'd input, then softmax / top-k / weights on
+      // the device (transformer.cpp:446-481)
+      const int64_t E = d.n_experts, I = ls.inter;
+      const int k = (int)std::min<int64_t>(d.top_k, E);
+      GemvArgs r{};
+      r.nseg = 1;
+      r.epi = EPI_STORE;
+      r.K = d.dim;
+      r.x = x_;
+      r.norm_w = L.ffn_norm;
+      r.eps = d.rms_eps;
+      r.y = moe_logits_;
+      r.seg[0].w = L.gate_inp.view;
+      r.seg[0].rows = E;
+      r.state = state_;
+      UAII_TRY(timed("moe_router", gemv_bytes(L.gate_inp.view), [&] { return launch_gemv(r, s); }));
+      UAII_TRY(timed("moe_route", 0.0, [&] { return launch_moe_route(moe_logits_, (int)E, k, moe_ids_, moe_w_, s); }));
+      // gate/up of the k chosen experts (+ the shared expert): one segment each,
+      // rows of expert moe_ids_[t], outputs at h_[t * I]
+      const int nsegs = k + (L.shared ? 1 : 0);
+      for (int t0 = 0; t0 < nsegs; t0 += 3) {
+        GemvArgs g{};
+        g.epi = EPI_SWIGLU;
+        g.K = d.dim;
+        g.x = x_;
+        g.norm_w = L.ffn_norm;
+        g.eps = d.rms_eps;
+        g.y = h_;
+        g.state = state_;
+        double bytes = 0.0;
+        for (int t = t0; t < std::min(nsegs, t0 + 3); ++t) {
+          GemvSeg& sg = g.seg[g.nseg++];
+          if (t < k) {
+            sg.w = L.gate_exps.view;
+            sg.w2 = L.up_exps.view;
+            sg.rows = 2 * I;
+            sg.row_base = (int64_t)t * I;
+            sg.expert = moe_ids_ + t;
+            sg.expert_rows = I;
+            bytes += 2.0 * gemv_bytes(L.gate_exps.view) / (double)E;
+          } else {
+            sg.w = L.gate_sh.view;
+            sg.w2 = L.up_sh.view;
+            sg.rows = 2 * L.inter_sh;
+            sg.row_base = (int64_t)k * I;
+            bytes += gemv_bytes(L.gate_sh.view) + gemv_bytes(L.up_sh.view);
+          }
+        }
+        UAII_TRY(timed("moe_gate_up", bytes, [&] { return launch_gemv(g, s); }));
+      }
+      // x += w_t * down_{e_t}(h_t) per chosen expert (then + shared down), the
+      // residual tap after the last one
+      for (int t = 0; t < nsegs; ++t) {
+        GemvArgs dn{};
+        dn.nseg = 1;
+        dn.epi = EPI_ADD;
+        dn.y = x_;
+        dn.state = state_;
+        if (t + 1 == nsegs) dn.tap = tap_r2_ + li * d.dim;
+        double bytes;
+        if (t < k) {
+          dn.K = I;
+          dn.x = h_ + (int64_t)t * I;
+          dn.seg[0].w = L.down_exps.view;
+          dn.seg[0].rows = d.dim;
+          dn.seg[0].expert = moe_ids_ + t;
+          dn.seg[0].expert_rows = d.dim;
+          dn.seg[0].scale = moe_w_ + t;
+          bytes = gemv_bytes(L.down_exps.view) / (double)E;
+        } else {
+          dn.K = L.inter_sh;
+          dn.x = h_ + (int64_t)k * I;
+          dn.seg[0].w = L.down_sh.view;
+          dn.seg[0].rows = d.dim;
+          bytes = gemv_bytes(L.down_sh.view);
+        }
+        UAII_TRY(timed("moe_down", bytes, [&] { return launch_gemv(dn, s); }));
+      }
     } else {
       UAII_HIP(hipMemcpyAsync(tap_r2_ + li * d.dim, x_, 4 * (size_t)d.dim, hipMemcpyDeviceToDevice, s));
     }

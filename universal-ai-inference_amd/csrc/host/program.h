@@ -84,7 +84,10 @@ class DecoderProgram {
  private:
   struct Layer {
     DeviceWeight wq, wk, wv, wo, gate, up, down, gate_inp, gate_exps, up_exps, down_exps;
+    DeviceWeight gate_sh, up_sh, down_sh;  // MoE shared expert (ffn_*_shexp)
     float *attn_norm = nullptr, *ffn_norm = nullptr, *bq = nullptr, *bk = nullptr, *bv = nullptr;
+    bool shared = false;
+    int64_t inter_sh = 0;
   };
 
   Error upload_f32(const GgufTensor* t, float** out);
@@ -121,7 +124,8 @@ class DecoderProgram {
   hipGraphExec_t graph_[2] = {nullptr, nullptr};
   std::map<std::string, KernelTiming> timing_;
   hipEvent_t ev0_ = nullptr, ev1_ = nullptr;
-  int64_t ffn_max_ = 0;
+  int64_t hid_max_ = 0;  // floats of the FFN hidden buffer (gate/up output)
+  bool moe_ = false;
 };
 
 }  // namespace uaii

@@ -439,6 +439,11 @@ int uaii_synth_write_gguf(const char* path, const uaii_synth_config* c, int nthr
     ts.push_back({p + "attn_q.weight", c->type_default, {D, Q}, 0});
     ts.push_back({p + "attn_k.weight", c->type_default, {D, KV}, 0});
     ts.push_back({p + "attn_v.weight", pick(c->type_attn_v), {D, KV}, 0});
+    if (c->qkv_bias) {
+      ts.push_back({p + "attn_q.bias", 0, {Q}, 0});
+      ts.push_back({p + "attn_k.bias", 0, {KV}, 0});
+      ts.push_back({p + "attn_v.bias", 0, {KV}, 0});
+    }
     ts.push_back({p + "attn_output.weight", c->type_default, {Q, D}, 0});
     ts.push_back({p + "ffn_norm.weight", 0, {D}, 1});
     if (c->n_experts > 0) {
@@ -446,6 +451,15 @@ int uaii_synth_write_gguf(const char* path, const uaii_synth_config* c, int nthr
       ts.push_back({p + "ffn_gate_exps.weight", c->type_default, {D, F, E}, 0});
       ts.push_back({p + "ffn_up_exps.weight", c->type_default, {D, F, E}, 0});
       ts.push_back({p + "ffn_down_exps.weight", pick(c->type_ffn_down), {F, D, E}, 0});
+      if (c->shared_ffn > 0) {
+        const auto S = static_cast<std::uint64_t>(c->shared_ffn);
+        ts.push_back({p + "ffn_gate_shexp.weight", c->type_default, {D, S}, 0});
+        ts.push_back({p + "ffn_up_shexp.weight", c->type_default, {D, S}, 0});
+        ts.push_back({p + "ffn_down_shexp.weight", pick(c->type_ffn_down), {S, D}, 0});
+      }
+    } else if (c->gelu) {
+      ts.push_back({p + "ffn_up.weight", c->type_default, {D, F}, 0});
+      ts.push_back({p + "ffn_down.weight", pick(c->type_ffn_down), {F, D}, 0});
     } else {
       ts.push_back({p + "ffn_gate.weight", c->type_default, {D, F}, 0});
       ts.push_back({p + "ffn_up.weight", c->type_default, {D, F}, 0});

@@ -49,6 +49,9 @@ typedef struct uaii_synth_config {
   float std;             /* weight std, e.g. 0.02 */
   float router_std;      /* ffn_gate_inp std */
   const char* arch;      /* general.architecture, NULL -> "llama" */
+  int gelu;              /* 1: dense FFN without gate (ffn_up, ffn_down; GELU) */
+  int qkv_bias;          /* 1: attn_q/k/v.bias f32 tensors */
+  int64_t shared_ffn;    /* MoE: shared expert width (ffn_*_shexp), 0 = none */
 } uaii_synth_config;
 
 /* Write the model. nthreads <= 0 uses all cores. Returns 0 or -1 (see

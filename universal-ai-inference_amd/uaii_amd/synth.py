@@ -22,6 +22,7 @@ class _Cfg(C.Structure):
         ("type_default", C.c_int), ("type_embd", C.c_int), ("type_output", C.c_int),
         ("type_attn_v", C.c_int), ("type_ffn_down", C.c_int), ("seed", C.c_uint64),
         ("std", C.c_float), ("router_std", C.c_float), ("arch", C.c_char_p),
+        ("gelu", C.c_int), ("qkv_bias", C.c_int), ("shared_ffn", C.c_int64),
     ]
 
 
@@ -49,9 +50,17 @@ class ModelConfig:
     std: float = 0.02
     router_std: float = 0.0
     arch: str = "llama"
+    gelu: bool = False
+    qkv_bias: bool = False
+    shared_ffn: int = 0
 
     def key(self) -> str:
         d = asdict(self)
+        # the three newest fields join the key only when set, so the files of
+        # configs without them keep their cache names
+        for k in ("gelu", "qkv_bias", "shared_ffn"):
+            if not d[k]:
+                d.pop(k)
         return "_".join(f"{k}{v}" for k, v in d.items())
 
 
@@ -107,7 +116,7 @@ def write_model(path: str, cfg: ModelConfig, nthreads: int = 0) -> str:
         v = getattr(cfg, name)
         if name == "arch":
             v = v.encode()
-        elif name == "tied":
+        elif name in ("tied", "gelu", "qkv_bias"):
             v = int(v)
         setattr(c, name, v)
     rc = _synth().uaii_synth_write_gguf(str(path).encode(), C.byref(c), nthreads)
