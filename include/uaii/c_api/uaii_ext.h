@@ -45,6 +45,38 @@ UAII_CAPI_API uaii_status uaii_session_set_profiling(uaii_session* session, int 
 UAII_CAPI_API uaii_status uaii_session_last_margin(uaii_session* session, float* best,
                                                    float* second);
 
+/** Sampling parameters (include/uaii/runtime/sampling.hpp:15-27 in the
+ * reference). Greedy when temperature <= 0, top_k <= 0, top_p >= 1 and
+ * repetition_penalty <= 1. */
+typedef struct uaii_sample_params {
+  uint32_t struct_size;
+  float temperature;
+  float top_p;
+  int32_t top_k;
+  float repetition_penalty;
+  uint64_t seed;
+  int has_seed; /* 0: seed from std::random_device, as the reference */
+} uaii_sample_params;
+
+UAII_CAPI_API void uaii_sample_params_init(uaii_sample_params* params);
+
+/** uaii_session_generate with the reference's sampler (Session::generate's
+ * SampleParams argument, session.cpp:910-1046): non-greedy draws are made on
+ * the host from each step's probs row with a seeded mt19937_64. */
+UAII_CAPI_API uaii_status uaii_session_generate_sampled(uaii_session* session,
+                                                        const int64_t* prompt_tokens,
+                                                        size_t prompt_n, int64_t max_new_tokens,
+                                                        const uaii_sample_params* params,
+                                                        int64_t* out_tokens, size_t capacity,
+                                                        size_t* out_n);
+
+/** One draw of the sampler (sampling.cpp:22-125) over row[0..vocab) with a fresh
+ * mt19937_64(params->seed); penalty ids as the reference's history. Host only. */
+UAII_CAPI_API uaii_status uaii_sample_token(const float* row, size_t vocab,
+                                            const uaii_sample_params* params,
+                                            const int64_t* penalty_tokens, size_t n_penalty,
+                                            int64_t* out_token);
+
 /** Parse a GGUF file and derive the decoder the session would run, without
  * touching the GPU: a JSON object (arch, layer count, dims, heads, vocab,
  * context length, rope mode/theta, rms eps, tied embeddings, per-layer FFN kind

@@ -121,6 +121,13 @@ def ref():
         L.uref_silu.argtypes = [f, f, i64]
         L.uref_argmax.restype = i64
         L.uref_argmax.argtypes = [f, i64]
+        L.uref_sample_token.restype = C.c_int
+        L.uref_sample_token.argtypes = [f, i64, C.c_float, C.c_float, C.c_int, C.c_float, C.c_uint64,
+                                        C.POINTER(i64), i64, C.POINTER(i64)]
+        L.uref_generate_sampled.restype = C.c_int
+        L.uref_generate_sampled.argtypes = [C.c_char_p, C.POINTER(i64), i64, i64, C.c_float,
+                                            C.c_float, C.c_int, C.c_float, C.c_uint64,
+                                            C.POINTER(i64), C.POINTER(i64)]
         L.uref_generate.restype = C.c_int
         L.uref_generate.argtypes = [C.c_char_p, C.c_int, C.POINTER(i64), i64, i64, C.POINTER(i64),
                                     C.POINTER(i64), f, f]
@@ -233,3 +240,30 @@ def ref_generate(path: str, prompt, max_new: int, max_layers: int = 0, n_layers:
     if rc != 0:
         raise OracleError(R.uref_last_error().decode())
     return out[: n.value], logits, resid2.reshape(max(n_layers, 1), -1) if n_layers else None
+
+
+def ref_sample_token(row, temperature, top_p, top_k, rep, seed, penalty=()):
+    """One draw of the reference's sample_token_f32 with mt19937_64(seed) (needs _ref)."""
+    import numpy as np
+    r = np.ascontiguousarray(row, dtype=np.float32)
+    pen = np.ascontiguousarray(list(penalty) or [0], dtype=np.int64)
+    out = C.c_int64()
+    rc = ref().uref_sample_token(_fp(r), r.size, temperature, top_p, top_k, rep, seed,
+                                 pen.ctypes.data_as(C.POINTER(C.c_int64)), len(penalty), C.byref(out))
+    if rc != 0:
+        raise OracleError(ref().uref_last_error().decode())
+    return out.value
+
+
+def ref_generate_sampled(path: str, prompt, max_new: int, temperature, top_p, top_k, rep, seed):
+    """Generate through the reference kernels with the reference's sampler (needs _ref)."""
+    import numpy as np
+    p = np.ascontiguousarray(prompt, dtype=np.int64)
+    out = np.zeros(len(p) + max_new + 1, dtype=np.int64)
+    n = C.c_int64()
+    rc = ref().uref_generate_sampled(str(path).encode(), p.ctypes.data_as(C.POINTER(C.c_int64)), len(p),
+                                     max_new, temperature, top_p, top_k, rep, seed,
+                                     out.ctypes.data_as(C.POINTER(C.c_int64)), C.byref(n))
+    if rc != 0:
+        raise OracleError(ref().uref_last_error().decode())
+    return out[: n.value]

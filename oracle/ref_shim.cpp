@@ -428,17 +428,20 @@ struct RefRunner {
 
 }  // namespace
 
-// Greedy generate through the reference kernels. taps_logits (vocab floats) and
-// taps_resid2 (n_layers*dim floats) receive the last run()'s values when non-NULL.
-int uref_generate(const char* path, int max_layers, const std::int64_t* prompt,
-                  std::int64_t n_prompt, std::int64_t max_new, std::int64_t* out,
-                  std::int64_t* out_n, float* taps_logits, float* taps_resid2) {
+namespace {
+
+// Generate through the reference kernels with the reference's sampler
+// (session.cpp:989-1044): greedy when `sp` is greedy, else a seeded
+// mt19937_64 over the probs row.
+int generate_with(const char* path, int max_layers, const std::int64_t* prompt,
+                  std::int64_t n_prompt, std::int64_t max_new, const runtime::SampleParams& sp,
+                  std::int64_t* out, std::int64_t* out_n, float* taps_logits, float* taps_resid2) {
   RefRunner R;
   Error err = R.open(path, max_layers, 0, n_prompt + max_new, n_prompt);
   if (!err.ok()) { g_err = err.message(); return -1; }
   std::vector<std::int64_t> hist;
-  runtime::SampleParams greedy;
   std::mt19937_64 rng{0};
+  if (sp.has_seed) rng.seed(sp.seed);
   for (std::int64_t i = 0; i < n_prompt; ++i) {
     const bool last = max_new <= 1 && i == n_prompt - 1;
     err = R.run(prompt[i], last ? taps_resid2 : nullptr);
@@ -447,7 +450,7 @@ int uref_generate(const char* path, int max_layers, const std::int64_t* prompt,
   }
   for (std::int64_t t = 0; t < max_new; ++t) {
     std::int64_t next = 0;
-    err = runtime::sample_token_f32(R.probs->f32.data(), static_cast<std::size_t>(R.V), greedy, hist,
+    err = runtime::sample_token_f32(R.probs->f32.data(), static_cast<std::size_t>(R.V), sp, hist,
                                     &rng, &next);
     if (!err.ok()) { g_err = err.message(); return -1; }
     hist.push_back(next);
@@ -458,6 +461,52 @@ int uref_generate(const char* path, int max_layers, const std::int64_t* prompt,
   if (taps_logits) std::memcpy(taps_logits, R.logits->f32.data(), R.V * 4);
   for (std::size_t i = 0; i < hist.size(); ++i) out[i] = hist[i];
   *out_n = static_cast<std::int64_t>(hist.size());
+  return 0;
+}
+
+runtime::SampleParams make_params(float temperature, float top_p, int top_k, float rep,
+                                  std::uint64_t seed) {
+  runtime::SampleParams sp;
+  sp.temperature = temperature;
+  sp.top_p = top_p;
+  sp.top_k = top_k;
+  sp.repetition_penalty = rep;
+  sp.seed = seed;
+  sp.has_seed = true;
+  return sp;
+}
+
+}  // namespace
+
+// Greedy generate through the reference kernels. taps_logits (vocab floats) and
+// taps_resid2 (n_layers*dim floats) receive the last run()'s values when non-NULL.
+int uref_generate(const char* path, int max_layers, const std::int64_t* prompt,
+                  std::int64_t n_prompt, std::int64_t max_new, std::int64_t* out,
+                  std::int64_t* out_n, float* taps_logits, float* taps_resid2) {
+  return generate_with(path, max_layers, prompt, n_prompt, max_new, runtime::SampleParams{}, out,
+                       out_n, taps_logits, taps_resid2);
+}
+
+// The same with the reference sampler: temperature / top_p / top_k / repetition
+// penalty and a seeded mt19937_64.
+int uref_generate_sampled(const char* path, const std::int64_t* prompt, std::int64_t n_prompt,
+                          std::int64_t max_new, float temperature, float top_p, int top_k,
+                          float rep, std::uint64_t seed, std::int64_t* out, std::int64_t* out_n) {
+  return generate_with(path, 0, prompt, n_prompt, max_new,
+                       make_params(temperature, top_p, top_k, rep, seed), out, out_n, nullptr,
+                       nullptr);
+}
+
+// One reference draw (sampling.cpp:22-125) from a fresh mt19937_64(seed).
+int uref_sample_token(const float* row, std::int64_t vocab, float temperature, float top_p,
+                      int top_k, float rep, std::uint64_t seed, const std::int64_t* penalty,
+                      std::int64_t n_penalty, std::int64_t* out) {
+  std::vector<std::int64_t> pen(penalty, penalty + n_penalty);
+  std::mt19937_64 rng(seed);
+  const Error err = runtime::sample_token_f32(row, static_cast<std::size_t>(vocab),
+                                              make_params(temperature, top_p, top_k, rep, seed),
+                                              pen, &rng, out);
+  if (!err.ok()) { g_err = err.message(); return -1; }
   return 0;
 }
 

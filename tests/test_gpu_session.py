@@ -166,3 +166,25 @@ def test_generate_edge_cases():
         a = s.generate(np.array([11, 12, 13]), 5)
         b = s.generate(np.array([11, 12, 13]), 5)
         assert a.tolist() == b.tolist()
+
+
+@pytest.mark.parametrize("prm", [(0.8, 0.9, 40, 1.1), (1.0, 1.0, 0, 1.0), (0.6, 0.95, 8, 1.0)],
+                         ids=lambda p: f"T{p[0]}_p{p[1]}_k{p[2]}_r{p[3]}")
+def test_generate_sampled_matches_reference(prm):
+    """Seeded temperature / top-k / top-p / repetition-penalty sampling: the device
+    probs row through the host sampler gives the ids the reference's kernels and
+    sampler give (session.cpp:989-1044). Top-k without top-p is left out here: it
+    draws in std::nth_element's arrangement of the kept ids, which depends on the
+    exact bits of the whole row (ulp-level differences in tiny probabilities
+    reorder it), so that case is pinned on identical rows in test_sampling.py."""
+    if oracle.ref() is None:
+        pytest.skip("reference kernels not built")
+    cfg = SMALL["gqa_q4_0"]
+    path = synth.cached_model(cfg)
+    prompt = prompt_for(cfg, 12, 99)
+    t, tp, tk, rp = prm
+    with uaii_amd.Session(path) as s:
+        ids = s.generate_sampled(prompt, 24, uaii_amd.sample_params(t, tp, tk, rp, seed=7))
+    want = oracle.ref_generate_sampled(path, prompt, 24, t, tp, tk, rp, 7)
+    assert np.array_equal(ids, want)
+    assert len(set(ids[12:].tolist())) > 1

@@ -1,0 +1,58 @@
+"""The host sampler (uaii_sample_token) against the reference's own
+sample_token_f32 (libs/uaii-runtime/src/sampling.cpp:22-125, compiled into
+oracle/_ref): temperature, top-k, top-p, repetition penalty and a seeded
+mt19937_64 must pick the same id from the same row. CPU only."""
+import numpy as np
+import pytest
+
+import oracle
+import uaii_amd
+
+PARAMS = [
+    # temperature, top_p, top_k, repetition penalty
+    (0.0, 1.0, 0, 1.0),     # greedy
+    (0.0, 1.0, 0, 1.3),     # greedy order but not greedy(): penalty path
+    (0.7, 1.0, 0, 1.0),     # temperature only
+    (1.0, 1.0, 40, 1.0),    # top-k (the nth_element arrangement decides the pick)
+    (0.8, 0.9, 0, 1.0),     # nucleus
+    (0.9, 0.95, 50, 1.2),   # everything
+    (1.5, 0.5, 5, 1.0),
+]
+
+
+def rows(vocab, n, seed):
+    rng = np.random.default_rng(seed)
+    for i in range(n):
+        if i % 2:
+            x = rng.normal(0, 3, vocab).astype(np.float32)
+            e = np.exp(x - x.max())
+            yield (e / e.sum()).astype(np.float32)  # a probs row, as the session samples from
+        else:
+            yield rng.normal(0, 2, vocab).astype(np.float32)
+
+
+@pytest.mark.parametrize("vocab", [50, 3000, 32000])
+@pytest.mark.parametrize("prm", PARAMS, ids=lambda p: f"T{p[0]}_p{p[1]}_k{p[2]}_r{p[3]}")
+def test_sampler_matches_reference(vocab, prm):
+    if oracle.ref() is None:
+        pytest.skip("reference kernels not built (make -C oracle ref needs /root/reference)")
+    t, tp, tk, rp = prm
+    for i, row in enumerate(rows(vocab, 6, vocab)):
+        pen = list(range(0, vocab, 7))[:20]
+        for seed in (1, 12345, 2 ** 63 + 5):
+            p = uaii_amd.sample_params(t, tp, tk, rp, seed=seed)
+            got = uaii_amd.sample_token(row, p, pen)
+            want = oracle.ref_sample_token(row, t, tp, tk, rp, seed, pen)
+            assert got == want, (i, seed)
+
+
+def test_sampler_distribution_follows_probs():
+    """With temperature 1 and no truncation, a probs row is re-softmaxed once
+    (the reference samples from `probs`); the empirical frequencies over many
+    seeds follow softmax(probs)."""
+    probs = np.array([0.5, 0.3, 0.2], np.float32)
+    want = np.exp(probs) / np.exp(probs).sum()
+    counts = np.zeros(3)
+    for seed in range(3000):
+        counts[uaii_amd.sample_token(probs, uaii_amd.sample_params(1.0, 1.0, 0, 1.0, seed=seed))] += 1
+    assert np.abs(counts / counts.sum() - want).max() < 0.03

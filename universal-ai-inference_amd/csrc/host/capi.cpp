@@ -7,6 +7,7 @@
 #include <algorithm>
 #include <cstring>
 #include <memory>
+#include <random>
 #include <string>
 #include <vector>
 
@@ -198,6 +199,68 @@ uaii_status uaii_session_write_trace(uaii_session* session, const char* path) {
   if (!f) return fail(UAII_ERR_IO, "cannot open trace path");
   std::fputs(s.c_str(), f);
   std::fclose(f);
+  g_last_error.clear();
+  return UAII_OK;
+}
+
+void uaii_sample_params_init(uaii_sample_params* params) {
+  if (params == nullptr) return;
+  std::memset(params, 0, sizeof(*params));
+  params->struct_size = static_cast<uint32_t>(sizeof(uaii_sample_params));
+  params->temperature = 0.0f;
+  params->top_p = 1.0f;
+  params->top_k = 0;
+  params->repetition_penalty = 1.0f;
+}
+
+namespace {
+bool to_params(const uaii_sample_params* in, uaii::runtime::SampleParams* out) {
+  if (in == nullptr) return true;  // greedy
+  if (in->struct_size == 0 || in->struct_size > sizeof(uaii_sample_params)) return false;
+  uaii_sample_params p;
+  uaii_sample_params_init(&p);
+  std::memcpy(&p, in, in->struct_size);
+  out->temperature = p.temperature;
+  out->top_p = p.top_p;
+  out->top_k = p.top_k;
+  out->repetition_penalty = p.repetition_penalty;
+  out->seed = p.seed;
+  out->has_seed = p.has_seed != 0;
+  return true;
+}
+}  // namespace
+
+uaii_status uaii_session_generate_sampled(uaii_session* session, const int64_t* prompt_tokens,
+                                          size_t prompt_n, int64_t max_new_tokens,
+                                          const uaii_sample_params* params, int64_t* out_tokens,
+                                          size_t capacity, size_t* out_n) {
+  if (session == nullptr || out_tokens == nullptr || out_n == nullptr)
+    return fail(UAII_ERR_INVALID_ARGUMENT, "generate_sampled null arg");
+  if (prompt_n > 0 && prompt_tokens == nullptr) return fail(UAII_ERR_INVALID_ARGUMENT, "prompt null");
+  uaii::runtime::SampleParams sp;
+  if (!to_params(params, &sp)) return fail(UAII_ERR_ABI, "uaii_sample_params.struct_size invalid");
+  std::vector<int64_t> prompt(prompt_tokens, prompt_tokens + prompt_n);
+  std::vector<int64_t> out;
+  uaii::Error err = reinterpret_cast<SessionHandle*>(session)->session.generate(
+      prompt, max_new_tokens, &out, {}, {}, sp);
+  if (!err.ok()) return from_error(err);
+  const size_t n = std::min(capacity, out.size());
+  std::copy(out.begin(), out.begin() + (std::ptrdiff_t)n, out_tokens);
+  *out_n = n;
+  g_last_error.clear();
+  return UAII_OK;
+}
+
+uaii_status uaii_sample_token(const float* row, size_t vocab, const uaii_sample_params* params,
+                              const int64_t* penalty_tokens, size_t n_penalty, int64_t* out_token) {
+  if (row == nullptr || out_token == nullptr || (n_penalty > 0 && penalty_tokens == nullptr))
+    return fail(UAII_ERR_INVALID_ARGUMENT, "sample_token null arg");
+  uaii::runtime::SampleParams sp;
+  if (!to_params(params, &sp)) return fail(UAII_ERR_ABI, "uaii_sample_params.struct_size invalid");
+  std::vector<int64_t> pen(penalty_tokens, penalty_tokens + n_penalty);
+  std::mt19937_64 rng(sp.seed);
+  uaii::Error err = uaii::runtime::sample_token_f32(row, vocab, sp, pen, &rng, out_token);
+  if (!err.ok()) return from_error(err);
   g_last_error.clear();
   return UAII_OK;
 }

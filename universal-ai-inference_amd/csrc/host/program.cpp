@@ -321,6 +321,10 @@ Error DecoderProgram::set_token(int64_t token) {
   const int32_t t = (int32_t)token;
   UAII_HIP(hipStreamSynchronize(stream_));
   UAII_HIP(hipMemcpy(&state_->token, &t, 4, hipMemcpyHostToDevice));
+  // the id history holds the token fed at each position
+  int32_t pos = 0;
+  UAII_HIP(hipMemcpy(&pos, &state_->pos, 4, hipMemcpyDeviceToHost));
+  if (pos >= 0 && pos <= max_ctx_) UAII_HIP(hipMemcpy(ids_ + pos, &t, 4, hipMemcpyHostToDevice));
   return Error::success();
 }
 

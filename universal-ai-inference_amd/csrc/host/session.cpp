@@ -2,6 +2,7 @@
 #include "session.h"
 
 #include <algorithm>
+#include <random>
 #include <cstdlib>
 
 namespace uaii {
@@ -55,8 +56,6 @@ Error Session::generate(const std::vector<int64_t>& prompt, int64_t max_new,
   if (out == nullptr) return Error::make(ErrorCode::InvalidArgument, "out_tokens null");
   if (prompt.empty()) return Error::make(ErrorCode::InvalidArgument, "prompt_tokens empty");
   if (max_new < 0) return Error::make(ErrorCode::InvalidArgument, "max_new_tokens < 0");
-  if (!sample.greedy())
-    return Error::make(ErrorCode::NotImplemented, "only greedy sampling runs on the device");
   const int64_t max_ctx = resolve_max_context();
   const int64_t n_prompt = (int64_t)prompt.size();
   const int64_t total = n_prompt + max_new;
@@ -82,6 +81,32 @@ Error Session::generate(const std::vector<int64_t>& prompt, int64_t max_new,
   for (int64_t i = 0; i < n_prompt; ++i) UAII_TRY(p.step(i == n_prompt - 1));
   const bool per_token = (bool)on_new_token || !stop_ids.empty();
   auto is_stop = [&](int64_t t) { return std::find(stop_ids.begin(), stop_ids.end(), t) != stop_ids.end(); };
+  if (!sample.greedy()) {
+    // Non-greedy: the reference samples from the `probs` row on the host with a
+    // seeded mt19937_64 (session.cpp:989-995, :1018-1026); each step's probs come
+    // back from the device and the chosen id is fed to the next step.
+    std::mt19937_64 rng;
+    if (sample.has_seed) {
+      rng.seed(sample.seed);
+    } else {
+      std::random_device rd;
+      rng.seed((static_cast<uint64_t>(rd()) << 32) ^ static_cast<uint64_t>(rd()));
+    }
+    out->assign(prompt.begin(), prompt.end());
+    std::vector<float> probs;
+    for (int64_t t = 0; t < max_new; ++t) {
+      UAII_TRY(p.read_tap("probs", &probs));
+      int64_t next = 0;
+      UAII_TRY(sample_token_f32(probs.data(), probs.size(), sample, *out, &rng, &next));
+      out->push_back(next);
+      if (on_new_token && !on_new_token(next)) return Error::success();
+      if (is_stop(next)) return Error::success();
+      if (t + 1 >= max_new) break;
+      UAII_TRY(p.set_token(next));
+      UAII_TRY(p.step(true));
+    }
+    return Error::success();
+  }
   if (!per_token) {
     // Whole decode on the device: every step's argmax feeds the next step.
     for (int64_t t = 0; t + 1 < max_new; ++t) UAII_TRY(p.step(true));

@@ -12,6 +12,7 @@
 #include "error.h"
 #include "gguf_file.h"
 #include "program.h"
+#include "sampling.h"
 
 #include <cstdint>
 #include <functional>
@@ -42,19 +43,6 @@ struct SessionOptions {
   bool use_graph = true;             // replay captured step graphs
 };
 
-// sampling.hpp:15-31; only the greedy path is implemented on the device.
-struct SampleParams {
-  float temperature = 0.0f;
-  float top_p = 1.0f;
-  int32_t top_k = 0;
-  float repetition_penalty = 1.0f;
-  uint64_t seed = 0;
-  bool has_seed = false;
-  bool greedy() const noexcept {
-    return temperature <= 0.0f && top_k <= 0 && top_p >= 1.0f - 1e-6f &&
-           repetition_penalty <= 1.0f + 1e-6f;
-  }
-};
 
 class Session {
  public:

@@ -60,6 +60,36 @@ class SessionOptions(C.Structure):
 _lib = None
 
 
+class SampleParams(C.Structure):
+    """uaii_sample_params (include/uaii/c_api/uaii_ext.h)."""
+    _fields_ = [("struct_size", C.c_uint32), ("temperature", C.c_float), ("top_p", C.c_float),
+                ("top_k", C.c_int32), ("repetition_penalty", C.c_float), ("seed", C.c_uint64),
+                ("has_seed", C.c_int)]
+
+
+def sample_params(temperature=0.0, top_p=1.0, top_k=0, repetition_penalty=1.0, seed=None):
+    p = SampleParams()
+    lib().uaii_sample_params_init(C.byref(p))
+    p.temperature, p.top_p, p.top_k, p.repetition_penalty = temperature, top_p, top_k, repetition_penalty
+    if seed is not None:
+        p.seed, p.has_seed = seed, 1
+    return p
+
+
+def sample_token(row, params: "SampleParams", penalty=()):
+    """One host draw of the sampler (fresh mt19937_64(params.seed))."""
+    import numpy as np
+    r = np.ascontiguousarray(row, dtype=np.float32)
+    pen = np.ascontiguousarray(list(penalty) or [0], dtype=np.int64)
+    out = C.c_int64()
+    L = lib()
+    rc = L.uaii_sample_token(r.ctypes.data_as(C.POINTER(C.c_float)), r.size, C.byref(params),
+                             pen.ctypes.data_as(C.POINTER(C.c_int64)), len(penalty), C.byref(out))
+    if rc != 0:
+        raise UaiiError(f"uaii_sample_token: {L.uaii_last_error().decode()}")
+    return out.value
+
+
 def lib() -> C.CDLL:
     """Load libuaii_amd.so (raises if it was not built)."""
     global _lib
@@ -91,6 +121,13 @@ def lib() -> C.CDLL:
         "uaii_session_seek": (C.c_int, [vp, i64]),
         "uaii_session_set_profiling": (C.c_int, [vp, C.c_int]),
         "uaii_session_last_margin": (C.c_int, [vp, f32p, f32p]),
+        "uaii_sample_params_init": (None, [C.POINTER(SampleParams)]),
+        "uaii_session_generate_sampled": (C.c_int, [vp, C.POINTER(i64), C.c_size_t, i64,
+                                                    C.POINTER(SampleParams), C.POINTER(i64),
+                                                    C.c_size_t, C.POINTER(C.c_size_t)]),
+        "uaii_sample_token": (C.c_int, [f32p, C.c_size_t, C.POINTER(SampleParams), C.POINTER(i64),
+                                        C.c_size_t, C.POINTER(i64)]),
+        "uaii_model_describe": (C.c_int, [C.c_char_p, C.c_char_p, C.c_size_t]),
         "uaii_hip_init": (C.c_int, [C.c_int]),
         "uaii_hip_device_count": (C.c_int, [C.POINTER(C.c_int)]),
         "uaii_hip_error_string": (C.c_char_p, [C.c_int]),
@@ -233,6 +270,21 @@ class Session:
                                      out.ctypes.data_as(C.POINTER(C.c_int64)), cap, C.byref(n))
         if rc != 0:
             raise UaiiError(f"uaii_session_generate: {L.uaii_status_name(rc).decode()}: "
+                            f"{L.uaii_last_error().decode()}")
+        return out[: n.value]
+
+    def generate_sampled(self, prompt, max_new: int, params: "SampleParams"):
+        import numpy as np
+        L = lib()
+        p = np.ascontiguousarray(prompt, dtype=np.int64)
+        cap = len(p) + max(max_new, 0)
+        out = np.zeros(max(cap, 1), dtype=np.int64)
+        n = C.c_size_t()
+        rc = L.uaii_session_generate_sampled(self.h, p.ctypes.data_as(C.POINTER(C.c_int64)), len(p),
+                                             max_new, C.byref(params),
+                                             out.ctypes.data_as(C.POINTER(C.c_int64)), cap, C.byref(n))
+        if rc != 0:
+            raise UaiiError(f"uaii_session_generate_sampled: {L.uaii_status_name(rc).decode()}: "
                             f"{L.uaii_last_error().decode()}")
         return out[: n.value]
 
