@@ -32,6 +32,20 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+def measured_traffic(kernel: str, algo_bytes: float):
+    """HBM bytes per launch of `kernel` from the committed counter runs
+    (profiles/traffic_*.json: FETCH_SIZE + WRITE_SIZE, scaled by the copy
+    kernel), when they were taken on the same kernel and shape; else None."""
+    for f in sorted((ROOT / "profiles").glob("traffic_*.json")):
+        try:
+            t = json.loads(f.read_text())
+        except (OSError, ValueError):
+            continue
+        if t.get("bench_kernel") == kernel and abs(t["algorithmic_bytes"] - algo_bytes) <= 1e-3 * algo_bytes:
+            return round(t["traffic_bytes"])
+    return None
+
+
 def cpu_baseline(path: str, start_pos: int, n_steps: int, threads: int):
     """Reference CPU path on a bounded decode window (rank 0, N=1)."""
     sys.path.insert(0, str(ROOT))
@@ -154,7 +168,7 @@ def main() -> int:
         step_ms = sum(v["total_ms"] for v in kernels.values()) / P
         roofline = {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1),
                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                    "traffic": None,
+                    "traffic": measured_traffic(dom, k["bytes"] / k["launches"]),
                     "bytes_per_launch": k["bytes"] / k["launches"],
                     "avg_launch_us": round(k["avg_us"], 2),
                     "gemv_attn_achieved": round(agg_b / (agg_ms * 1e-3) / 1e9, 1),

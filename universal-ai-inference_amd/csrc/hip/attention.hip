@@ -524,10 +524,10 @@ bool launch_h16(const AttnArgs& a, int G, hipStream_t s) {
   constexpr int TK = 32;
   dim3 grid(a.n_kv, a.splits);
   switch (G) {
-    case 1: hipLaunchKernelGGL((k_attn_h16<HD, 1, TK>), grid, dim3(256), 0, s, a); return true;
-    case 2: hipLaunchKernelGGL((k_attn_h16<HD, 2, TK>), grid, dim3(256), 0, s, a); return true;
-    case 4: hipLaunchKernelGGL((k_attn_h16<HD, 4, TK>), grid, dim3(256), 0, s, a); return true;
-    case 8: hipLaunchKernelGGL((k_attn_h16<HD, 8, TK>), grid, dim3(256), 0, s, a); return true;
+    case 1: UAII_LAUNCH((k_attn_h16<HD, 1, TK>), grid, dim3(256), 0, s, a); return true;
+    case 2: UAII_LAUNCH((k_attn_h16<HD, 2, TK>), grid, dim3(256), 0, s, a); return true;
+    case 4: UAII_LAUNCH((k_attn_h16<HD, 4, TK>), grid, dim3(256), 0, s, a); return true;
+    case 8: UAII_LAUNCH((k_attn_h16<HD, 8, TK>), grid, dim3(256), 0, s, a); return true;
     default: return false;
   }
 }
@@ -579,10 +579,10 @@ template <bool F16, int HD>
 bool launch_fast_hd(const AttnArgs& a, int G, hipStream_t s) {
   dim3 grid(a.n_kv, a.splits);
   switch (G) {
-    case 1: hipLaunchKernelGGL((k_attn_fast<F16, HD, 1>), grid, dim3(256), 0, s, a); return true;
-    case 2: hipLaunchKernelGGL((k_attn_fast<F16, HD, 2>), grid, dim3(256), 0, s, a); return true;
-    case 4: hipLaunchKernelGGL((k_attn_fast<F16, HD, 4>), grid, dim3(256), 0, s, a); return true;
-    case 8: hipLaunchKernelGGL((k_attn_fast<F16, HD, 8>), grid, dim3(256), 0, s, a); return true;
+    case 1: UAII_LAUNCH((k_attn_fast<F16, HD, 1>), grid, dim3(256), 0, s, a); return true;
+    case 2: UAII_LAUNCH((k_attn_fast<F16, HD, 2>), grid, dim3(256), 0, s, a); return true;
+    case 4: UAII_LAUNCH((k_attn_fast<F16, HD, 4>), grid, dim3(256), 0, s, a); return true;
+    case 8: UAII_LAUNCH((k_attn_fast<F16, HD, 8>), grid, dim3(256), 0, s, a); return true;
     default: return false;
   }
 }
@@ -606,7 +606,7 @@ hipError_t launch_attention_decode(const AttnArgs& a, hipStream_t s) {
     if (ok) {
       const hipError_t st = hipGetLastError();
       if (st != hipSuccess) return st;
-      hipLaunchKernelGGL(k_attn_merge, dim3(a.n_heads), dim3(256), 0, s, a);
+      UAII_LAUNCH(k_attn_merge, dim3(a.n_heads), dim3(256), 0, s, a);
       return hipGetLastError();
     }
   }
@@ -615,15 +615,15 @@ hipError_t launch_attention_decode(const AttnArgs& a, hipStream_t s) {
   if ((int)lds > lds_limit() - 1024) return hipErrorInvalidValue;
   dim3 grid(a.n_kv, a.splits);
   if (tile == 64) {
-    if (a.kv_f16) hipLaunchKernelGGL((k_attn<true, 64>), grid, dim3(NT), lds, s, a);
-    else hipLaunchKernelGGL((k_attn<false, 64>), grid, dim3(NT), lds, s, a);
+    if (a.kv_f16) UAII_LAUNCH((k_attn<true, 64>), grid, dim3(NT), lds, s, a);
+    else UAII_LAUNCH((k_attn<false, 64>), grid, dim3(NT), lds, s, a);
   } else {
-    if (a.kv_f16) hipLaunchKernelGGL((k_attn<true, 32>), grid, dim3(NT), lds, s, a);
-    else hipLaunchKernelGGL((k_attn<false, 32>), grid, dim3(NT), lds, s, a);
+    if (a.kv_f16) UAII_LAUNCH((k_attn<true, 32>), grid, dim3(NT), lds, s, a);
+    else UAII_LAUNCH((k_attn<false, 32>), grid, dim3(NT), lds, s, a);
   }
   const hipError_t st = hipGetLastError();
   if (st != hipSuccess) return st;
-  hipLaunchKernelGGL(k_attn_merge, dim3(a.n_heads), dim3(256), 0, s, a);
+  UAII_LAUNCH(k_attn_merge, dim3(a.n_heads), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 

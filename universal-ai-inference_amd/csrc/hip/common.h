@@ -12,6 +12,30 @@
 #include <hip/hip_runtime.h>
 #include <hip/hip_fp16.h>
 #include <stdint.h>
+#include <hip/hip_ext.h>
+
+namespace uaii_hip {
+// Per-thread event pair for kernel timing: while `stop` is set, UAII_LAUNCH
+// launches through hipExtLaunchKernelGGL so the events are recorded on the
+// kernel's own dispatch (start on the first kernel after it is set, stop on
+// every one, so a group of launches is timed as a whole). Unset: plain launches.
+struct LaunchEvents {
+  hipEvent_t start = nullptr;
+  hipEvent_t stop = nullptr;
+};
+extern thread_local LaunchEvents g_launch_events;
+}  // namespace uaii_hip
+
+#define UAII_LAUNCH(K, G, B, LDS, S, ...)                                                      \
+  do {                                                                                     \
+    if (::uaii_hip::g_launch_events.stop) {                                                \
+      hipExtLaunchKernelGGL(K, G, B, LDS, S, ::uaii_hip::g_launch_events.start,            \
+                            ::uaii_hip::g_launch_events.stop, 0, __VA_ARGS__);             \
+      ::uaii_hip::g_launch_events.start = nullptr;                                         \
+    } else {                                                                               \
+      hipLaunchKernelGGL(K, G, B, LDS, S, __VA_ARGS__);                                    \
+    }                                                                                      \
+  } while (0)
 
 namespace uaii_hip {
 

@@ -1291,10 +1291,10 @@ hipError_t launch_gemv(const GemvArgs& in, hipStream_t s) {
     if (blocks == 0) return hipSuccess;
     if ((int64_t)p.lds > lds_limit() - 1024) return hipErrorInvalidValue;
     if (a.epi == EPI_LOGITS && blocks > a.part_cap) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(p.fn, dim3(blocks), dim3(WPB * 64), p.lds, s, a);
+    UAII_LAUNCH(p.fn, dim3(blocks), dim3(WPB * 64), p.lds, s, a);
     hipError_t st = hipGetLastError();
     if (st == hipSuccess && a.epi == EPI_LOGITS) {
-      hipLaunchKernelGGL(k_argmax_final, dim3(1), dim3(1024), 0, s, a, blocks);
+      UAII_LAUNCH(k_argmax_final, dim3(1), dim3(1024), 0, s, a, blocks);
       st = hipGetLastError();
     }
     return st;

@@ -223,10 +223,12 @@ __global__ void __launch_bounds__(64) k_moe_route(const float* __restrict__ logi
 
 }  // namespace
 
+thread_local LaunchEvents g_launch_events;
+
 hipError_t launch_moe_route(const float* logits, int n_experts, int k, int32_t* ids, float* w,
                             hipStream_t s) {
   if (n_experts < 1 || n_experts > 256 || k < 1 || k > 8 || k > n_experts) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_moe_route, dim3(1), dim3(64), 0, s, logits, n_experts, k, ids, w);
+  UAII_LAUNCH(k_moe_route, dim3(1), dim3(64), 0, s, logits, n_experts, k, ids, w);
   return hipGetLastError();
 }
 
@@ -234,14 +236,14 @@ hipError_t launch_copy(const void* src, void* dst, int64_t n16, hipStream_t s) {
   if (n16 <= 0) return hipSuccess;
   int64_t blocks = (n16 + 255) / 256;
   if (blocks > 8192) blocks = 8192;
-  hipLaunchKernelGGL(k_stream_copy, dim3((unsigned)blocks), dim3(256), 0, s,
+  UAII_LAUNCH(k_stream_copy, dim3((unsigned)blocks), dim3(256), 0, s,
                      (const uint4*)src, (uint4*)dst, n16);
   return hipGetLastError();
 }
 
 hipError_t launch_embed(const DevWeight& w, const StepState* st, float* x, float* tap,
                         hipStream_t s) {
-  UAII_FOR_TYPE(w.type, hipLaunchKernelGGL(k_embed<FT>, dim3(1), dim3(256), 0, s, w, st,
+  UAII_FOR_TYPE(w.type, UAII_LAUNCH(k_embed<FT>, dim3(1), dim3(256), 0, s, w, st,
                                            (const int32_t*)nullptr, x, tap));
   return hipGetLastError();
 }
@@ -249,30 +251,30 @@ hipError_t launch_embed(const DevWeight& w, const StepState* st, float* x, float
 hipError_t launch_embed_rows(const DevWeight& w, const int32_t* ids, int64_t n, float* x,
                              hipStream_t s) {
   if (n <= 0) return hipSuccess;
-  UAII_FOR_TYPE(w.type, hipLaunchKernelGGL(k_embed<FT>, dim3((unsigned)n), dim3(256), 0, s, w,
+  UAII_FOR_TYPE(w.type, UAII_LAUNCH(k_embed<FT>, dim3((unsigned)n), dim3(256), 0, s, w,
                                            (const StepState*)nullptr, ids, x, (float*)nullptr));
   return hipGetLastError();
 }
 
 hipError_t launch_advance(StepState* st, int32_t* ids, hipStream_t s) {
-  hipLaunchKernelGGL(k_advance, dim3(1), dim3(64), 0, s, st, ids);
+  UAII_LAUNCH(k_advance, dim3(1), dim3(64), 0, s, st, ids);
   return hipGetLastError();
 }
 
 hipError_t launch_rmsnorm(const float* x, const float* w, float* y, int64_t rows, int64_t n,
                           float eps, hipStream_t s) {
   if (rows <= 0) return hipSuccess;
-  hipLaunchKernelGGL(k_rmsnorm, dim3((unsigned)rows), dim3(256), 0, s, x, w, y, n, eps);
+  UAII_LAUNCH(k_rmsnorm, dim3((unsigned)rows), dim3(256), 0, s, x, w, y, n, eps);
   return hipGetLastError();
 }
 
 hipError_t launch_softmax(const float* x, float* y, int64_t n, hipStream_t s) {
-  hipLaunchKernelGGL(k_softmax, dim3(1), dim3(1024), 0, s, x, y, n);
+  UAII_LAUNCH(k_softmax, dim3(1), dim3(1024), 0, s, x, y, n);
   return hipGetLastError();
 }
 
 hipError_t launch_argmax(const float* x, int64_t n, int32_t* out, hipStream_t s) {
-  hipLaunchKernelGGL(k_argmax, dim3(1), dim3(1024), 0, s, x, n, out);
+  UAII_LAUNCH(k_argmax, dim3(1), dim3(1024), 0, s, x, n, out);
   return hipGetLastError();
 }
 
@@ -280,7 +282,7 @@ hipError_t launch_rope(float* x, int64_t rows, int64_t dim, int head_dim, const 
                        int64_t pos_stride, const float2* tab, int mode, hipStream_t s) {
   const int64_t total = rows * (dim / 2);
   if (total <= 0) return hipSuccess;
-  hipLaunchKernelGGL(k_rope, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, x, rows,
+  UAII_LAUNCH(k_rope, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, x, rows,
                      dim, head_dim, pos, pos_stride, tab, mode);
   return hipGetLastError();
 }

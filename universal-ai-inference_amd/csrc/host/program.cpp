@@ -367,22 +367,45 @@ Error DecoderProgram::encode_step(bool want_logits) {
   const size_t elem = opts_.kv_f16 ? 2 : 4;
   const size_t layer_kv = (size_t)d.kv_dim * (size_t)max_ctx_ * elem;
 
-  // Each launch optionally bracketed by events (profiling mode only).
+  // Profiling mode: each launch group records a start/stop event pair on its own
+  // kernel dispatches (hipExtLaunchKernelGGL through UAII_LAUNCH), with no
+  // synchronisation between kernels; the pairs are read after the step.
+  size_t prof_used = 0;
   auto timed = [&](const char* name, double bytes, auto&& launch) -> Error {
     if (!opts_.profile) {
       UAII_HIP(launch());
       return Error::success();
     }
-    UAII_HIP(hipEventRecord(ev0_, s));
-    UAII_HIP(launch());
-    UAII_HIP(hipEventRecord(ev1_, s));
-    UAII_HIP(hipEventSynchronize(ev1_));
-    float ms = 0.0f;
-    UAII_HIP(hipEventElapsedTime(&ms, ev0_, ev1_));
-    KernelTiming& t = timing_[name];
-    t.total_ms += ms;
-    t.launches += 1;
-    t.bytes += bytes;
+    if (prof_used == prof_events_.size()) {
+      hipEvent_t a = nullptr, b = nullptr;
+      UAII_HIP(hipEventCreate(&a));
+      UAII_HIP(hipEventCreate(&b));
+      prof_events_.push_back({a, b});
+      prof_tags_.push_back({std::string(), 0.0});
+    }
+    g_launch_events.start = prof_events_[prof_used].first;
+    g_launch_events.stop = prof_events_[prof_used].second;
+    const hipError_t st = launch();
+    g_launch_events = LaunchEvents{};
+    UAII_HIP(st);
+    prof_tags_[prof_used] = {name, bytes};
+    ++prof_used;
+    return Error::success();
+  };
+  auto collect = [&]() -> Error {
+    if (!opts_.profile) return Error::success();
+    UAII_HIP(hipStreamSynchronize(s));
+    for (size_t i = 0; i < prof_used; ++i) {
+      float ms = 0.0f;
+      if (hipEventElapsedTime(&ms, prof_events_[i].first, prof_events_[i].second) != hipSuccess) {
+        (void)hipGetLastError();  // a group that launched nothing records no time
+        continue;
+      }
+      KernelTiming& t = timing_[prof_tags_[i].first];
+      t.total_ms += ms;
+      t.launches += 1;
+      t.bytes += prof_tags_[i].second;
+    }
     return Error::success();
   };
 
@@ -603,7 +626,7 @@ Error DecoderProgram::encode_step(bool want_logits) {
   } else {
     UAII_TRY(timed("advance", 0.0, [&] { return launch_advance(state_, ids_, s); }));
   }
-  return Error::success();
+  return collect();
 }
 
 Error DecoderProgram::step(bool want_logits) {

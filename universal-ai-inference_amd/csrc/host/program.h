@@ -110,6 +110,9 @@ class DecoderProgram {
   float* lm_part_val_ = nullptr;
   int32_t* lm_part_idx_ = nullptr;
   int lm_blocks_ = 0;  // capacity of the LM-head partial buffers
+  // profiling mode: start/stop event pairs and their (kernel name, bytes) per launch group
+  std::vector<std::pair<hipEvent_t, hipEvent_t>> prof_events_;
+  std::vector<std::pair<std::string, double>> prof_tags_;
   uaii_hip::StepState* state_ = nullptr;
 
   // sized by ensure_capacity

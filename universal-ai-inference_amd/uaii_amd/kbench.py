@@ -1,0 +1,86 @@
+"""Kernel microbenchmark through the uaii_hip C ABI.
+
+Times one fused GEMV (plain, RMSNorm, residual add or gate/up SwiGLU) of a given
+GGUF type and shape on random block bytes, rotating over enough weight copies
+(> 256 MiB in total, the MI355X last-level cache) that each launch reads its
+weights from HBM, plus the plain 1 GiB copy kernel. Meant to run alone or under
+``rocprofv3 --kernel-trace --stats`` / ``--pmc`` to pin a kernel's time and
+memory traffic.
+
+    python3 -m uaii_amd.kbench --epi swiglu --type q4_0 --rows 14336 --cols 4096
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import sys
+import time
+
+import numpy as np
+
+from . import (BLOCK, DeviceBuffer, DeviceWeight, TYPE_NAMES, check_hip, lib, row_bytes)
+
+BPW = {k: BLOCK[k][1] / BLOCK[k][0] for k in BLOCK}
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--epi", choices=["plain", "rmsnorm", "add", "swiglu"], default="swiglu")
+    ap.add_argument("--type", default="q4_0")
+    ap.add_argument("--rows", type=int, default=14336, help="output rows (per weight for swiglu)")
+    ap.add_argument("--cols", type=int, default=4096)
+    ap.add_argument("--iters", type=int, default=40)
+    ap.add_argument("--copy-mib", type=int, default=1024)
+    a = ap.parse_args(argv)
+    names = {v.lower(): k for k, v in TYPE_NAMES.items()}
+    t = names[a.type.lower()]
+    L = lib()
+    check_hip(L.uaii_hip_init(0), "init")
+    rng = np.random.default_rng(0)
+    nw = 2 if a.epi == "swiglu" else 1
+    wbytes = nw * a.rows * row_bytes(t, a.cols)
+    copies = max(2, int(np.ceil(320 * 2 ** 20 / wbytes)))
+    ws = []
+    for c in range(copies):
+        group = []
+        for _ in range(nw):
+            p = rng.integers(0, 256, size=a.rows * row_bytes(t, a.cols), dtype=np.uint8)
+            blk = p.reshape(-1, BLOCK[t][1])
+            blk[:, 1] &= 0x3b  # small finite f16 scales at byte 0..1 for the 32-blocks
+            group.append(DeviceWeight(t, p, a.rows, a.cols))
+        ws.append(group)
+    x = DeviceBuffer.from_array(rng.normal(0, 1, a.cols).astype(np.float32))
+    nrm = DeviceBuffer.from_array(np.ones(a.cols, np.float32))
+    y = DeviceBuffer.from_array(np.zeros(a.rows, np.float32))
+
+    def launch(g):
+        if a.epi == "plain":
+            return L.uaii_hip_gemv(g[0].h, x.ptr, y.ptr, None)
+        if a.epi == "rmsnorm":
+            return L.uaii_hip_gemv_rmsnorm(g[0].h, x.ptr, nrm.ptr, 1e-5, y.ptr, None)
+        if a.epi == "add":
+            return L.uaii_hip_gemv_add(g[0].h, x.ptr, None, 1e-5, y.ptr, None)
+        return L.uaii_hip_gemv_swiglu(g[0].h, g[1].h, x.ptr, nrm.ptr, 1e-5, y.ptr, None)
+
+    for g in ws:  # warm
+        check_hip(launch(g), "gemv")
+    check_hip(L.uaii_hip_synchronize())
+    t0 = time.perf_counter()
+    for i in range(a.iters):
+        check_hip(launch(ws[i % copies]), "gemv")
+    check_hip(L.uaii_hip_synchronize())
+    dt = (time.perf_counter() - t0) / a.iters
+    algo = nw * (a.rows * a.cols * BPW[t] + 4 * a.cols + 4 * a.rows)
+    print(f"gemv {a.epi} {TYPE_NAMES[t]} {nw}x{a.rows}x{a.cols}: {dt * 1e6:.2f} us/launch wall, "
+          f"{algo / dt / 1e9:.0f} GB/s algorithmic ({algo:.0f} B), {copies} weight copies", flush=True)
+    nb = a.copy_mib * 2 ** 20
+    src, dst = DeviceBuffer(nb), DeviceBuffer(nb)
+    ms = C.c_float()
+    check_hip(L.uaii_hip_time_copy(src.ptr, dst.ptr, nb, 10, C.byref(ms)), "copy")
+    print(f"copy {a.copy_mib} MiB: {ms.value * 1e3:.1f} us, {2 * nb / (ms.value * 1e-3) / 1e9:.0f} GB/s (r+w)",
+          flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
