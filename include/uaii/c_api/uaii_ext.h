@@ -25,6 +25,20 @@ UAII_CAPI_API uaii_status uaii_session_begin(uaii_session* session, const int64_
  * next prompt token is fed (valid only inside the prompt). */
 UAII_CAPI_API uaii_status uaii_session_step_async(uaii_session* session, int want_logits);
 
+/** Run the next n prompt tokens (positions pos .. pos + n - 1, taken from the
+ * prompt given to uaii_session_begin) through every layer at once on the matrix
+ * cores: K/V are appended for each position and no logits are computed; the
+ * following step feeds prompt token pos + n. The reference prefills token by
+ * token (session.cpp:1005-1015); the results agree within float tolerance.
+ * Returns UAII_ERR_NOT_IMPLEMENTED when the model is outside this path (see
+ * uaii_session_prefill_supported). Synchronises with the device. */
+UAII_CAPI_API uaii_status uaii_session_prefill(uaii_session* session, int64_t n);
+
+/** *supported = 1 when uaii_session_prefill covers the model: weights in Q4_0,
+ * Q8_0, Q4_K or Q6_K, dense SwiGLU/GELU FFNs, an f16 KV cache, head_dim 64 or
+ * 128. uaii_session_generate uses it for the prompt whenever it is 1. */
+UAII_CAPI_API uaii_status uaii_session_prefill_supported(uaii_session* session, int* supported);
+
 /** Wait for all enqueued steps. */
 UAII_CAPI_API uaii_status uaii_session_sync(uaii_session* session);
 

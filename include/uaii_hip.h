@@ -22,6 +22,9 @@
  *   uaii_hip_gemv_add          quant_gemm_f32 + residual add_f32 (elementwise.cpp:86-97)
  *   uaii_hip_gemv_swiglu       two quant_gemm_f32 + silu_f32 * mul_f32
  *                              (elementwise.cpp:73-110), the graph's FFN gate/up
+ *   uaii_hip_gemm_rmsnorm/_add/_swiglu  the same three at M>1 (prefill)
+ *   uaii_hip_attention_prefill attention_kv_f32 for a run of prompt positions
+ *                              (the reference feeds them one per step)
  * and the reference ROCm stub's launchers it supersedes
  * (libs/uaii-backends/src/rocm_kernels.hpp:10-14: launch_add_f32, launch_rmsnorm_f32).
  */
@@ -73,8 +76,21 @@ UAII_HIP_API int uaii_hip_gemv_add(const uaii_hip_weight* w, const float* x,
 UAII_HIP_API int uaii_hip_gemv_swiglu(const uaii_hip_weight* wg, const uaii_hip_weight* wu,
                                       const float* x, const float* norm_w, float eps, float* y,
                                       void* stream);
+/* M > 1: y[i][:] = W . x[i][:] for i < m (x [m][cols], y [m][rows]). Q4_0, Q8_0,
+ * Q4_K and Q6_K run on the matrix cores (weights decoded to their exact small
+ * integers, x split into f16 hi + lo, block scales applied to the f32 partials);
+ * other formats run one GEMV per row. */
 UAII_HIP_API int uaii_hip_gemm(const uaii_hip_weight* w, const float* x, int64_t m, float* y,
                                void* stream);
+UAII_HIP_API int uaii_hip_gemm_rmsnorm(const uaii_hip_weight* w, const float* x, int64_t m,
+                                       const float* norm_w, float eps, float* y, void* stream);
+/* y[i][:] += W . x'[i][:], x' = x or RMSNorm(x) * norm_w when norm_w is non-NULL. */
+UAII_HIP_API int uaii_hip_gemm_add(const uaii_hip_weight* w, const float* x, int64_t m,
+                                   const float* norm_w, float eps, float* y, void* stream);
+/* y[i][j] = silu((Wg . x'[i])[j]) * (Wu . x'[i])[j], y [m][rows]. */
+UAII_HIP_API int uaii_hip_gemm_swiglu(const uaii_hip_weight* wg, const uaii_hip_weight* wu,
+                                      const float* x, int64_t m, const float* norm_w, float eps,
+                                      float* y, void* stream);
 UAII_HIP_API int uaii_hip_rmsnorm(const float* x, const float* w, float* y, int64_t rows,
                                   int64_t n, float eps, void* stream);
 UAII_HIP_API int uaii_hip_softmax(const float* x, float* y, int64_t n, void* stream);
@@ -91,6 +107,15 @@ UAII_HIP_API int uaii_hip_attention_decode(const float* q, const void* kcache,
                                            const void* vcache, int kv_f16, int64_t max_seq,
                                            int n_heads, int n_kv_heads, int head_dim,
                                            int64_t n_keys, float* out, void* stream);
+
+/* Causal attention of m queries at positions p0 .. p0 + m - 1 (q, out:
+ * [m][n_heads * head_dim]) over an f16 cache holding keys 0 .. p0 + m - 1;
+ * head_dim 64 or 128 (attention_kv_f32 applied to each query in turn,
+ * libs/uaii-kernels/src/transformer.cpp:222-433). */
+UAII_HIP_API int uaii_hip_attention_prefill(const float* q, const void* kcache,
+                                            const void* vcache, int64_t max_seq, int n_heads,
+                                            int n_kv_heads, int head_dim, int64_t p0, int64_t m,
+                                            float* out, void* stream);
 
 /* ---- timing (HIP events on `stream`) ---------------------------------------- */
 /* Average device time of `iters` back-to-back uaii_hip_gemv launches, in ms. */

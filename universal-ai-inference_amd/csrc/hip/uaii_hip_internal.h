@@ -131,4 +131,73 @@ int attention_splits(int64_t max_seq);
 hipError_t launch_attention_decode(const AttnArgs& a, hipStream_t s);
 hipError_t prepare_attention();
 
+// ---- prefill (M > 1 prompt tokens, matrix cores) ---------------------------------------
+
+// Activation rows prepared for the MFMA GEMM: x * 2^e = hi + lo in f16 (each
+// aligned group of 4 stored as k0, k2, k1, k3), per-32 sums of x * 2^e, and 2^-e.
+struct PfAct {
+  __half* hi;     // [mpad][K]
+  __half* lo;     // [mpad][K]
+  float* sx;      // [K / 32][mpad]
+  float* rs;      // [mpad]
+  int64_t mpad;   // rows allocated (multiple of 64); rows >= M are zero
+  int64_t K;
+};
+
+struct PfSeg {
+  DevWeight w;      // weight rows (EPI_SWIGLU: gate)
+  DevWeight w2;     // EPI_SWIGLU: up rows
+  int64_t rows;     // output columns of this segment
+  int64_t col0;     // first output column in y
+  int tile0;        // set by launch_pf_gemm
+};
+
+struct PfGemmArgs {
+  PfSeg seg[3];
+  int nseg;
+  int epi;              // EPI_STORE, EPI_ADD, EPI_SWIGLU, EPI_GELU
+  int64_t M, K, mpad;
+  const __half* ahi;
+  const __half* alo;
+  const float* sx;
+  const float* rs;
+  float* y;             // [M][ldy]
+  int64_t ldy;
+};
+
+struct PfQkvArgs {
+  const float* qkv;     // [M][ldq]: q | k | v before bias and RoPE
+  int64_t ldq, M;
+  int p0;               // position of row 0
+  int q_dim, kv_dim, head_dim, rope_mode;
+  const float2* rope;   // [max_seq][head_dim / 2]
+  const float *bq, *bk, *bv;
+  float* qout;          // [M][q_dim]
+  void* kcache;         // layer base [n_kv][max_seq][hd]
+  void* vcache;
+  int kv_f16;
+  int64_t max_seq;
+};
+
+struct PfAttnArgs {
+  const float* q;       // [M][ldq] post-RoPE
+  int64_t ldq;
+  const void* kcache;   // f16 layer base [n_kv][max_seq][hd]
+  const void* vcache;
+  int64_t max_seq;
+  int n_heads, n_kv, hd;
+  int64_t p0, M;        // queries at positions p0 .. p0 + M - 1 (keys 0 .. p0 + M - 1)
+  float* out;           // [M][ldo]
+  int64_t ldo;
+};
+
+bool pf_supported(int type);
+bool pf_attn_supported(int head_dim, int n_heads, int n_kv);
+int64_t pf_mpad(int64_t m);
+hipError_t launch_pf_prep(const float* x, int64_t ldx, int64_t M, const float* norm_w, float eps,
+                          const PfAct& act, hipStream_t s);
+hipError_t launch_pf_gemm(PfGemmArgs a, hipStream_t s);
+hipError_t launch_pf_qkv(const PfQkvArgs& a, hipStream_t s);
+hipError_t launch_pf_attn(const PfAttnArgs& a, hipStream_t s);
+
 }  // namespace uaii_hip

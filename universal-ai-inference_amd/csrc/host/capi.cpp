@@ -303,6 +303,19 @@ uaii_status uaii_session_step_async(uaii_session* session, int want_logits) {
   return from_error(reinterpret_cast<SessionHandle*>(session)->session.step_async(want_logits != 0));
 }
 
+uaii_status uaii_session_prefill(uaii_session* session, int64_t n) {
+  if (session == nullptr || n < 0) return fail(UAII_ERR_INVALID_ARGUMENT, "prefill args");
+  return from_error(reinterpret_cast<SessionHandle*>(session)->session.prefill(n));
+}
+
+uaii_status uaii_session_prefill_supported(uaii_session* session, int* supported) {
+  if (session == nullptr || supported == nullptr) return fail(UAII_ERR_INVALID_ARGUMENT, "null args");
+  auto* p = reinterpret_cast<SessionHandle*>(session)->session.program();
+  if (!p) return fail(UAII_ERR_INVALID_ARGUMENT, "session not ready");
+  *supported = p->prefill_supported() ? 1 : 0;
+  return UAII_OK;
+}
+
 uaii_status uaii_session_sync(uaii_session* session) {
   if (session == nullptr) return fail(UAII_ERR_INVALID_ARGUMENT, "session null");
   auto* p = reinterpret_cast<SessionHandle*>(session)->session.program();

@@ -157,14 +157,110 @@ int uaii_hip_gemv_swiglu(const uaii_hip_weight* wg, const uaii_hip_weight* wu, c
   return (int)launch_gemv(a, S(stream));
 }
 
-int uaii_hip_gemm(const uaii_hip_weight* w, const float* x, int64_t m, float* y, void* stream) {
+}  // extern "C"
+
+namespace {
+
+// M-row products: the MFMA kernel for the block formats it decodes, else one
+// GEMV launch per row (same epilogue). Prepared activations live in g_scratch.
+int gemm_common(const uaii_hip_weight* w, const uaii_hip_weight* w2, const float* x, int64_t m,
+                const float* norm_w, float eps, float* y, int epi, void* stream) {
   if (!w || !x || !y || m <= 0) return kErrArg;
-  // M rows through the GEMV kernel (prefill MFMA path not in this build yet)
-  for (int64_t i = 0; i < m; ++i) {
-    const int rc = gemv_common(w, x + i * w->w.view.cols, nullptr, 0.0f, y + i * w->w.view.rows, stream);
-    if (rc) return rc;
+  const DevWeight& v = w->w.view;
+  if (epi == EPI_SWIGLU) {
+    if (!w2) return kErrArg;
+    const DevWeight& u = w2->w.view;
+    if (u.type != v.type || u.rows != v.rows || u.cols != v.cols) return kErrArg;
   }
-  return 0;
+  const int64_t K = v.cols, N = v.rows;
+  if (!pf_supported(v.type) || K % 32) {
+    for (int64_t i = 0; i < m; ++i) {
+      const float* xi = x + i * K;
+      float* yi = y + i * N;
+      int rc = 0;
+      if (epi == EPI_SWIGLU) rc = uaii_hip_gemv_swiglu(w, w2, xi, norm_w, eps, yi, stream);
+      else rc = gemv_common(w, xi, norm_w, eps, yi, stream, epi);
+      if (rc) return rc;
+    }
+    return 0;
+  }
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  const int64_t mpad = pf_mpad(m);
+  const size_t hb = (size_t)mpad * (size_t)K * 2, sxb = (size_t)(K / 32) * (size_t)mpad * 4;
+  int rc = grow_scratch(2 * hb + sxb + (size_t)mpad * 4);
+  if (rc) return rc;
+  char* base = static_cast<char*>(g_scratch);
+  PfAct act{};
+  act.hi = reinterpret_cast<__half*>(base);
+  act.lo = reinterpret_cast<__half*>(base + hb);
+  act.sx = reinterpret_cast<float*>(base + 2 * hb);
+  act.rs = reinterpret_cast<float*>(base + 2 * hb + sxb);
+  act.mpad = mpad;
+  act.K = K;
+  hipError_t e = launch_pf_prep(x, K, m, norm_w, eps, act, S(stream));
+  if (e != hipSuccess) return (int)e;
+  PfGemmArgs a{};
+  a.nseg = 1;
+  a.epi = epi;
+  a.M = m;
+  a.K = K;
+  a.mpad = mpad;
+  a.ahi = act.hi;
+  a.alo = act.lo;
+  a.sx = act.sx;
+  a.rs = act.rs;
+  a.y = y;
+  a.ldy = N;
+  a.seg[0].w = v;
+  if (w2) a.seg[0].w2 = w2->w.view;
+  a.seg[0].rows = N;
+  a.seg[0].col0 = 0;
+  return (int)launch_pf_gemm(a, S(stream));
+}
+
+}  // namespace
+
+extern "C" {
+
+int uaii_hip_gemm(const uaii_hip_weight* w, const float* x, int64_t m, float* y, void* stream) {
+  return gemm_common(w, nullptr, x, m, nullptr, 0.0f, y, EPI_STORE, stream);
+}
+
+int uaii_hip_gemm_rmsnorm(const uaii_hip_weight* w, const float* x, int64_t m, const float* norm_w,
+                          float eps, float* y, void* stream) {
+  if (!norm_w) return kErrArg;
+  return gemm_common(w, nullptr, x, m, norm_w, eps, y, EPI_STORE, stream);
+}
+
+int uaii_hip_gemm_add(const uaii_hip_weight* w, const float* x, int64_t m, const float* norm_w,
+                      float eps, float* y, void* stream) {
+  return gemm_common(w, nullptr, x, m, norm_w, eps, y, EPI_ADD, stream);
+}
+
+int uaii_hip_gemm_swiglu(const uaii_hip_weight* wg, const uaii_hip_weight* wu, const float* x,
+                         int64_t m, const float* norm_w, float eps, float* y, void* stream) {
+  return gemm_common(wg, wu, x, m, norm_w, eps, y, EPI_SWIGLU, stream);
+}
+
+int uaii_hip_attention_prefill(const float* q, const void* kcache, const void* vcache,
+                               int64_t max_seq, int n_heads, int n_kv_heads, int head_dim,
+                               int64_t p0, int64_t m, float* out, void* stream) {
+  if (!q || !kcache || !vcache || !out || m <= 0 || p0 < 0 || p0 + m > max_seq) return kErrArg;
+  if (!pf_attn_supported(head_dim, n_heads, n_kv_heads)) return kErrNotImpl;
+  PfAttnArgs a{};
+  a.q = q;
+  a.ldq = (int64_t)n_heads * head_dim;
+  a.kcache = kcache;
+  a.vcache = vcache;
+  a.max_seq = max_seq;
+  a.n_heads = n_heads;
+  a.n_kv = n_kv_heads;
+  a.hd = head_dim;
+  a.p0 = p0;
+  a.M = m;
+  a.out = out;
+  a.ldo = a.ldq;
+  return (int)launch_pf_attn(a, S(stream));
 }
 
 int uaii_hip_rmsnorm(const float* x, const float* w, float* y, int64_t rows, int64_t n, float eps,

@@ -4,6 +4,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <sstream>
 
@@ -95,6 +96,7 @@ Error upload_weight(int type, const uint8_t* host, int64_t rows, int64_t cols, h
 
 DecoderProgram::~DecoderProgram() {
   free_dynamic();
+  for (void* p : pf_allocs_) (void)hipFree(p);
   for (void* p : allocs_) (void)hipFree(p);
   if (ev0_) (void)hipEventDestroy(ev0_);
   if (ev1_) (void)hipEventDestroy(ev1_);
@@ -266,6 +268,184 @@ Error DecoderProgram::build(const DecoderSpec& spec, const ProgramOptions& opts)
   UAII_HIP(hipStreamSynchronize(stream_));
   int64_t want = opts_.max_context > 0 ? opts_.max_context : d.ctx_len;
   if (want > 0) UAII_TRY(ensure_capacity(want));
+
+  // the matrix-core prompt path: block formats it decodes, dense FFNs, f16 cache
+  pf_ok_ = opts_.kv_f16 && !moe_ &&
+           pf_attn_supported((int)d.head_dim, (int)d.n_heads, (int)d.n_kv_heads) &&
+           d.dim % 32 == 0 && d.q_dim % 32 == 0;
+  for (int64_t li = 0; pf_ok_ && li < d.n_layers; ++li) {
+    const Layer& L = *layers_[(size_t)li];
+    const LayerSpec& ls = d.layers[(size_t)li];
+    std::vector<const DeviceWeight*> ws = {&L.wq, &L.wk, &L.wv, &L.wo};
+    if (ls.ffn == LayerSpec::kSwiGLU) ws.insert(ws.end(), {&L.gate, &L.up, &L.down});
+    if (ls.ffn == LayerSpec::kGelu) ws.insert(ws.end(), {&L.up, &L.down});
+    if ((ls.ffn == LayerSpec::kSwiGLU || ls.ffn == LayerSpec::kGelu) && ls.inter % 32) pf_ok_ = false;
+    for (const DeviceWeight* w : ws) pf_ok_ = pf_ok_ && pf_supported(w->view.type);
+  }
+  if (const char* env = std::getenv("UAII_PREFILL")) {
+    if (std::string(env) == "0") pf_ok_ = false;
+  }
+  return Error::success();
+}
+
+Error DecoderProgram::ensure_prefill_buffers(int64_t chunk) {
+  if (chunk <= pf_chunk_) return Error::success();
+  UAII_HIP(hipStreamSynchronize(stream_));
+  for (void* p : pf_allocs_) (void)hipFree(p);
+  pf_allocs_.clear();
+  const DecoderSpec& d = spec_;
+  int64_t inter = 1;
+  for (const LayerSpec& ls : d.layers) inter = std::max(inter, ls.inter);
+  const int64_t mpad = pf_mpad(chunk);
+  const int64_t kmax = std::max({d.dim, d.q_dim, inter});
+  auto alloc = [&](size_t bytes, void** p) -> Error {
+    UAII_HIP(hipMalloc(p, std::max<size_t>(bytes, 256)));
+    pf_allocs_.push_back(*p);
+    return Error::success();
+  };
+  const size_t C = (size_t)chunk;
+  UAII_TRY(alloc(4 * C * (size_t)d.dim, (void**)&pf_x_));
+  UAII_TRY(alloc(4 * C * (size_t)(d.q_dim + 2 * d.kv_dim), (void**)&pf_qkv_));
+  UAII_TRY(alloc(4 * C * (size_t)d.q_dim, (void**)&pf_q_));
+  UAII_TRY(alloc(4 * C * (size_t)d.q_dim, (void**)&pf_attn_));
+  UAII_TRY(alloc(4 * C * (size_t)inter, (void**)&pf_h_));
+  UAII_TRY(alloc(2 * (size_t)mpad * (size_t)kmax, (void**)&pf_act_.hi));
+  UAII_TRY(alloc(2 * (size_t)mpad * (size_t)kmax, (void**)&pf_act_.lo));
+  UAII_TRY(alloc(4 * (size_t)(kmax / 32) * (size_t)mpad, (void**)&pf_act_.sx));
+  UAII_TRY(alloc(4 * (size_t)mpad, (void**)&pf_act_.rs));
+  pf_act_.mpad = mpad;
+  pf_chunk_ = chunk;
+  pf_kmax_ = kmax;
+  return Error::success();
+}
+
+// One MFMA GEMM launch per run of consecutive weights of the same block format
+// (q, k and v may differ, e.g. Q6_K attn_v beside Q4_K attn_q).
+Error DecoderProgram::pf_gemm(const DeviceWeight* w[3], const int64_t cols0[3], int nw,
+                              const DeviceWeight* w2, int epi, int64_t m, float* y, int64_t ldy) {
+  for (int i = 0; i < nw;) {
+    PfGemmArgs a{};
+    a.epi = epi;
+    a.M = m;
+    a.K = w[i]->view.cols;
+    a.mpad = pf_act_.mpad;
+    a.ahi = pf_act_.hi;
+    a.alo = pf_act_.lo;
+    a.sx = pf_act_.sx;
+    a.rs = pf_act_.rs;
+    a.y = y;
+    a.ldy = ldy;
+    int j = i;
+    while (j < nw && w[j]->view.type == w[i]->view.type) {
+      PfSeg& sg = a.seg[a.nseg++];
+      sg.w = w[j]->view;
+      if (w2) sg.w2 = w2->view;
+      sg.rows = w[j]->view.rows;
+      sg.col0 = cols0[j];
+      ++j;
+    }
+    UAII_HIP(launch_pf_gemm(a, stream_));
+    i = j;
+  }
+  return Error::success();
+}
+
+Error DecoderProgram::prefill(int64_t n) {
+  if (n <= 0) return Error::success();
+  if (!pf_ok_) return Error::make(ErrorCode::NotImplemented, "prefill: model not covered by the matrix-core path");
+  if (!kv_) return Error::make(ErrorCode::InvalidArgument, "KvCache not configured");
+  const DecoderSpec& d = spec_;
+  StepState st{};
+  UAII_TRY(read_state(&st));
+  const int64_t p0 = st.pos;
+  if (p0 + n >= max_ctx_) return Error::make(ErrorCode::InvalidArgument, "prefill exceeds KV capacity");
+  int64_t target = 512;
+  if (const char* env = std::getenv("UAII_PREFILL_CHUNK")) target = std::max<int64_t>(16, std::atoll(env));
+  const int64_t chunk = std::min(n, target);
+  UAII_TRY(ensure_prefill_buffers(chunk));
+  hipStream_t s = stream_;
+  const size_t layer_kv = (size_t)d.kv_dim * (size_t)max_ctx_ * 2;
+  const int64_t ldqkv = d.q_dim + 2 * d.kv_dim;
+  auto prep = [&](const float* x, int64_t K, int64_t m, const float* norm_w) -> Error {
+    PfAct act = pf_act_;
+    act.K = K;
+    UAII_HIP(launch_pf_prep(x, K, m, norm_w, d.rms_eps, act, s));
+    return Error::success();
+  };
+  for (int64_t c0 = 0; c0 < n; c0 += chunk) {
+    const int64_t m = std::min(chunk, n - c0);
+    const int64_t p = p0 + c0;
+    UAII_HIP(launch_embed_rows(tok_embd_.view, ids_ + p, m, pf_x_, s));
+    for (int64_t li = 0; li < d.n_layers; ++li) {
+      const Layer& L = *layers_[(size_t)li];
+      const LayerSpec& ls = d.layers[(size_t)li];
+      uint8_t* kbase = static_cast<uint8_t*>(kv_) + (size_t)li * 2 * layer_kv;
+      uint8_t* vbase = kbase + layer_kv;
+      // attention block (gguf.cpp:1000-1060)
+      UAII_TRY(prep(pf_x_, d.dim, m, L.attn_norm));
+      const DeviceWeight* qkv[3] = {&L.wq, &L.wk, &L.wv};
+      const int64_t qkv_cols[3] = {0, d.q_dim, d.q_dim + d.kv_dim};
+      UAII_TRY(pf_gemm(qkv, qkv_cols, 3, nullptr, EPI_STORE, m, pf_qkv_, ldqkv));
+      PfQkvArgs qa{};
+      qa.qkv = pf_qkv_;
+      qa.ldq = ldqkv;
+      qa.M = m;
+      qa.p0 = (int)p;
+      qa.q_dim = (int)d.q_dim;
+      qa.kv_dim = (int)d.kv_dim;
+      qa.head_dim = (int)d.head_dim;
+      qa.rope_mode = d.rope_mode;
+      qa.rope = rope_;
+      qa.bq = L.bq;
+      qa.bk = L.bk;
+      qa.bv = L.bv;
+      qa.qout = pf_q_;
+      qa.kcache = kbase;
+      qa.vcache = vbase;
+      qa.kv_f16 = 1;
+      qa.max_seq = max_ctx_;
+      UAII_HIP(launch_pf_qkv(qa, s));
+      PfAttnArgs at{};
+      at.q = pf_q_;
+      at.ldq = d.q_dim;
+      at.kcache = kbase;
+      at.vcache = vbase;
+      at.max_seq = max_ctx_;
+      at.n_heads = (int)d.n_heads;
+      at.n_kv = (int)d.n_kv_heads;
+      at.hd = (int)d.head_dim;
+      at.p0 = p;
+      at.M = m;
+      at.out = pf_attn_;
+      at.ldo = d.q_dim;
+      UAII_HIP(launch_pf_attn(at, s));
+      UAII_TRY(prep(pf_attn_, d.q_dim, m, nullptr));
+      const DeviceWeight* wo[3] = {&L.wo, nullptr, nullptr};
+      const int64_t c00[3] = {0, 0, 0};
+      UAII_TRY(pf_gemm(wo, c00, 1, nullptr, EPI_ADD, m, pf_x_, d.dim));
+      // FFN block (gguf.cpp:1130-1173)
+      if (ls.ffn == LayerSpec::kSwiGLU || ls.ffn == LayerSpec::kGelu) {
+        UAII_TRY(prep(pf_x_, d.dim, m, L.ffn_norm));
+        if (ls.ffn == LayerSpec::kSwiGLU) {
+          const DeviceWeight* wg[3] = {&L.gate, nullptr, nullptr};
+          UAII_TRY(pf_gemm(wg, c00, 1, &L.up, EPI_SWIGLU, m, pf_h_, ls.inter));
+        } else {
+          const DeviceWeight* wu[3] = {&L.up, nullptr, nullptr};
+          UAII_TRY(pf_gemm(wu, c00, 1, nullptr, EPI_GELU, m, pf_h_, ls.inter));
+        }
+        UAII_TRY(prep(pf_h_, ls.inter, m, nullptr));
+        const DeviceWeight* wd[3] = {&L.down, nullptr, nullptr};
+        UAII_TRY(pf_gemm(wd, c00, 1, nullptr, EPI_ADD, m, pf_x_, d.dim));
+      }
+    }
+  }
+  // the next step feeds ids[p0 + n] at position p0 + n
+  UAII_HIP(hipStreamSynchronize(s));
+  int32_t tok = 0;
+  UAII_HIP(hipMemcpy(&tok, ids_ + p0 + n, 4, hipMemcpyDeviceToHost));
+  st.pos = (int32_t)(p0 + n);
+  st.token = tok;
+  UAII_HIP(hipMemcpy(state_, &st, sizeof(st), hipMemcpyHostToDevice));
   return Error::success();
 }
 

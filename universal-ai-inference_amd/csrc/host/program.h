@@ -70,6 +70,12 @@ class DecoderProgram {
   // Copy ids[0..n) (prompt + generated) to the host.
   Error read_ids(int64_t* out, int64_t n);
   Error read_state(uaii_hip::StepState* st);
+  // Run the n tokens ids[pos .. pos + n) through every layer as M-row matrix
+  // products on the matrix cores (K/V appended for each position, no logits),
+  // then leave ids[pos + n] as the token the next step() feeds.
+  Error prefill(int64_t n);
+  // Whether prefill() covers this model (weight formats, FFN kind, f16 KV cache).
+  bool prefill_supported() const { return pf_ok_; }
   // Overwrite the token fed at the current position.
   Error set_token(int64_t token);
   // Rewind to `pos` (ids and KV below it are kept; ids[pos] is fed next).
@@ -91,6 +97,9 @@ class DecoderProgram {
   };
 
   Error upload_f32(const GgufTensor* t, float** out);
+  Error ensure_prefill_buffers(int64_t chunk);
+  Error pf_gemm(const DeviceWeight* w[3], const int64_t cols0[3], int nw, const DeviceWeight* w2,
+                int epi, int64_t m, float* y, int64_t ldy);
   Error encode_step(bool want_logits);
   void free_dynamic();
 
@@ -129,6 +138,14 @@ class DecoderProgram {
   hipEvent_t ev0_ = nullptr, ev1_ = nullptr;
   int64_t hid_max_ = 0;  // floats of the FFN hidden buffer (gate/up output)
   bool moe_ = false;
+
+  // prefill: chunk buffers ([chunk][...] rows) and the prepared-activation scratch
+  bool pf_ok_ = false;
+  int64_t pf_chunk_ = 0, pf_kmax_ = 0;
+  float *pf_x_ = nullptr, *pf_qkv_ = nullptr, *pf_q_ = nullptr, *pf_attn_ = nullptr,
+        *pf_h_ = nullptr;
+  uaii_hip::PfAct pf_act_{};
+  std::vector<void*> pf_allocs_;
 };
 
 }  // namespace uaii

@@ -77,8 +77,16 @@ Error Session::generate(const std::vector<int64_t>& prompt, int64_t max_new,
   run_started_ = true;
 
   out->clear();
-  // Prefill: one step per prompt token; logits only needed after the last one.
-  for (int64_t i = 0; i < n_prompt; ++i) UAII_TRY(p.step(i == n_prompt - 1));
+  // Prefill. The reference runs one step per prompt token; here all prompt
+  // tokens but the last go through the matrix-core path as M-row products when
+  // the model's formats allow it, and the last one runs the ordinary step with
+  // the LM head. Otherwise one step per prompt token, logits only at the end.
+  if (n_prompt > 1 && p.prefill_supported()) {
+    UAII_TRY(p.prefill(n_prompt - 1));
+    UAII_TRY(p.step(true));
+  } else {
+    for (int64_t i = 0; i < n_prompt; ++i) UAII_TRY(p.step(i == n_prompt - 1));
+  }
   const bool per_token = (bool)on_new_token || !stop_ids.empty();
   auto is_stop = [&](int64_t t) { return std::find(stop_ids.begin(), stop_ids.end(), t) != stop_ids.end(); };
   if (!sample.greedy()) {
@@ -145,6 +153,11 @@ Error Session::begin(const std::vector<int64_t>& prompt, int64_t capacity) {
 Error Session::step_async(bool want_logits) {
   if (!ready_ || !run_started_) return Error::make(ErrorCode::InvalidArgument, "session not started");
   return program_->step(want_logits);
+}
+
+Error Session::prefill(int64_t n) {
+  if (!ready_ || !run_started_) return Error::make(ErrorCode::InvalidArgument, "session not started");
+  return program_->prefill(n);
 }
 
 Error Session::set_tensor_f32(const std::string& name, const std::vector<float>& values) {

@@ -68,6 +68,8 @@ class Session {
   // Step-level token loop (uaii_ext.h).
   Error begin(const std::vector<int64_t>& prompt, int64_t capacity);
   Error step_async(bool want_logits);
+  // Prompt tokens [pos, pos + n) through the matrix-core path (no logits).
+  Error prefill(int64_t n);
   DecoderProgram* program() { return program_.get(); }
   const DecoderSpec& spec() const { return spec_; }
 

@@ -116,6 +116,8 @@ def lib() -> C.CDLL:
         "uaii_session_begin": (C.c_int, [vp, C.POINTER(i64), C.c_size_t, i64]),
         "uaii_session_step_async": (C.c_int, [vp, C.c_int]),
         "uaii_session_sync": (C.c_int, [vp]),
+        "uaii_session_prefill": (C.c_int, [vp, i64]),
+        "uaii_session_prefill_supported": (C.c_int, [vp, C.POINTER(C.c_int)]),
         "uaii_session_position": (C.c_int, [vp, C.POINTER(i64)]),
         "uaii_session_read_ids": (C.c_int, [vp, C.POINTER(i64), C.c_size_t]),
         "uaii_session_seek": (C.c_int, [vp, i64]),
@@ -146,6 +148,11 @@ def lib() -> C.CDLL:
         "uaii_hip_gemv_add": (C.c_int, [vp, vp, vp, C.c_float, vp, vp]),
         "uaii_hip_gemv_swiglu": (C.c_int, [vp, vp, vp, vp, C.c_float, vp, vp]),
         "uaii_hip_gemm": (C.c_int, [vp, vp, i64, vp, vp]),
+        "uaii_hip_gemm_rmsnorm": (C.c_int, [vp, vp, i64, vp, C.c_float, vp, vp]),
+        "uaii_hip_gemm_add": (C.c_int, [vp, vp, i64, vp, C.c_float, vp, vp]),
+        "uaii_hip_gemm_swiglu": (C.c_int, [vp, vp, vp, i64, vp, C.c_float, vp, vp]),
+        "uaii_hip_attention_prefill": (C.c_int, [vp, vp, vp, i64, C.c_int, C.c_int, C.c_int, i64,
+                                                 i64, vp, vp]),
         "uaii_hip_rmsnorm": (C.c_int, [vp, vp, vp, i64, i64, C.c_float, vp]),
         "uaii_hip_softmax": (C.c_int, [vp, vp, i64, vp]),
         "uaii_hip_argmax": (C.c_int, [vp, i64, vp, vp]),
@@ -315,6 +322,15 @@ class Session:
 
     def step_async(self, want_logits: bool = True):
         self._ok(lib().uaii_session_step_async(self.h, int(want_logits)), "step_async")
+
+    def prefill(self, n: int):
+        """Next n prompt tokens through the matrix-core path (synchronises)."""
+        self._ok(lib().uaii_session_prefill(self.h, int(n)), "prefill")
+
+    def prefill_supported(self) -> bool:
+        v = C.c_int()
+        self._ok(lib().uaii_session_prefill_supported(self.h, C.byref(v)), "prefill_supported")
+        return bool(v.value)
 
     def sync(self):
         self._ok(lib().uaii_session_sync(self.h), "sync")
