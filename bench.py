@@ -6,7 +6,8 @@ cache, bs=1. A seeded random prompt fills the context to 3840 tokens, then the
 timed region is K greedy decode steps ending at ctx 4096 (one step = one token
 through all 32 layers + LM head + argmax, replayed from the captured hipGraph).
 
-Also reported: token-by-token prefill rate, per-kernel device time from HIP
+Also reported: the prompt prefill rate (matrix-core path, with its dominant
+GEMM's fp16 MFMA roofline fraction), per-kernel device time from HIP
 events on the session stream (a profiled replay of the same decode window right
 after the timed region), the dominant kernel's HBM roofline fraction, a
 device-to-device copy rate, and the reference's CPU path timed on a bounded
@@ -26,6 +27,7 @@ sys.path.insert(0, str(ROOT / "universal-ai-inference_amd"))
 
 METRIC = "decode tok/s bs1 Llama-3-8B-shape Q4_0 @ctx4096; GEMV+attn HBM GB/s % peak"
 HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFS = 2500.0  # dense fp16 matrix-core peak of one MI355X
 
 
 def log(*a):
@@ -117,15 +119,57 @@ def main() -> int:
     log(f"session created in {time.time() - t:.1f}s")
     prompt = np.random.default_rng(cfg.seed + 1).integers(0, cfg.vocab, n_prompt)
 
-    # prefill: one step per prompt token (the reference's method), untimed for `value`
-    sess.begin(prompt, ctx)
-    sess.sync()
-    t0 = time.perf_counter()
-    for i in range(n_prompt):
-        sess.step_async(i == n_prompt - 1)
-    sess.sync()
-    prefill_s = time.perf_counter() - t0
-    log(f"prefill {n_prompt} tokens in {prefill_s:.2f}s ({n_prompt / prefill_s:.0f} tok/s)")
+    # prefill (untimed for `value`): prompt tokens 0..n-2 as M-row products on the
+    # matrix cores, the last prompt token as an ordinary step with the LM head
+    prefill = {}
+    if sess.prefill_supported():
+        sess.begin(prompt, ctx)
+        sess.prefill(n_prompt - 1)  # first pass allocates the chunk buffers
+        sess.begin(prompt, ctx)
+        sess.sync()
+        t0 = time.perf_counter()
+        sess.prefill(n_prompt - 1)
+        sess.step_async(True)
+        sess.sync()
+        prefill_s = time.perf_counter() - t0
+        prefill["method"] = "matrix cores (MFMA), 512-token chunks"
+        if not args.no_profile:
+            # the same prefill profiled per kernel; it rebuilds the same KV state
+            sess.begin(prompt, ctx)
+            sess.set_profiling(True)
+            sess.prefill(n_prompt - 1)
+            pk = json.loads(sess.profile_summary())
+            sess.set_profiling(False)
+            sess.step_async(True)
+            sess.sync()
+            flops = sum(v["flops"] for v in pk.values())
+            gemms = {n: v for n, v in pk.items() if n.startswith("pf_gemm")}
+            dom = max(gemms, key=lambda n: gemms[n]["total_ms"])
+            d = gemms[dom]
+            prefill["kernel_ms"] = round(sum(v["total_ms"] for v in pk.values()), 2)
+            prefill["algorithmic_tflops"] = round(flops / (prefill_s * 1e12), 1)
+            prefill["roofline"] = {"bound": "mfma", "kernel": dom, "achieved": round(d["tflops"], 1),
+                                   "peak": MFMA_F16_PEAK_TFS, "unit": "TFLOP/s",
+                                   "frac": round(d["tflops"] / MFMA_F16_PEAK_TFS, 4),
+                                   "flops_per_launch": d["flops"] / d["launches"],
+                                   "avg_launch_us": round(d["avg_us"], 2)}
+            prefill["kernels"] = {n: {"total_ms": round(v["total_ms"], 2), "avg_us": round(v["avg_us"], 2),
+                                      "tflops": round(v["tflops"], 1), "gbps": round(v["gbps"], 1)}
+                                  for n, v in pk.items()}
+    else:
+        # one step per prompt token (the reference's method)
+        sess.begin(prompt, ctx)
+        sess.sync()
+        t0 = time.perf_counter()
+        for i in range(n_prompt):
+            sess.step_async(i == n_prompt - 1)
+        sess.sync()
+        prefill_s = time.perf_counter() - t0
+        prefill["method"] = "token steps"
+    prefill["tok_s"] = round(n_prompt / prefill_s, 1)
+    prefill["seconds"] = round(prefill_s, 4)
+    log(f"prefill {n_prompt} tokens in {prefill_s:.3f}s ({n_prompt / prefill_s:.0f} tok/s, "
+        f"{prefill['method']}) {json.dumps({k: v for k, v in prefill.items() if k != 'kernels'})}")
 
     for _ in range(W):
         sess.step_async(True)
@@ -196,6 +240,7 @@ def main() -> int:
                    "n_layers": cfg.n_layers, "dim": cfg.dim, "heads": f"{cfg.n_heads}/{cfg.n_kv_heads}",
                    "ffn": cfg.ffn, "vocab": cfg.vocab},
         "prefill_tok_s": round(n_prompt / prefill_s, 1),
+        "prefill": prefill,
         "copy_gbps": round(copy_gbs, 1),
         "argmax_margin_last": round(best - second, 6),
         "roofline": roofline,

@@ -366,16 +366,45 @@ Error DecoderProgram::prefill(int64_t n) {
   hipStream_t s = stream_;
   const size_t layer_kv = (size_t)d.kv_dim * (size_t)max_ctx_ * 2;
   const int64_t ldqkv = d.q_dim + 2 * d.kv_dim;
+  prof_used_ = 0;
   auto prep = [&](const float* x, int64_t K, int64_t m, const float* norm_w) -> Error {
     PfAct act = pf_act_;
     act.K = K;
-    UAII_HIP(launch_pf_prep(x, K, m, norm_w, d.rms_eps, act, s));
-    return Error::success();
+    return timed("pf_prep", 12.0 * (double)m * (double)K, 0.0,
+                 [&] { return launch_pf_prep(x, K, m, norm_w, d.rms_eps, act, s); });
+  };
+  // algorithmic work of one GEMM launch group: weights once, A (hi + lo), C
+  auto gemm_cost = [&](const DeviceWeight* const* w, int nw, int64_t m, int64_t outs, double* bytes,
+                       double* flops) {
+    *bytes = 0.0;
+    *flops = 0.0;
+    for (int i = 0; i < nw; ++i) {
+      *bytes += (double)w[i]->bytes;
+      *flops += 2.0 * (double)m * (double)w[i]->view.rows * (double)w[i]->view.cols;
+    }
+    *bytes += 4.0 * (double)m * (double)w[0]->view.cols + 4.0 * (double)m * (double)outs;
+  };
+  auto gemm = [&](const char* name, const DeviceWeight** w, const int64_t* cols0, int nw,
+                  const DeviceWeight* w2, int epi, int64_t m, float* y, int64_t ldy) -> Error {
+    double bytes = 0.0, flops = 0.0;
+    gemm_cost(w, nw, m, ldy, &bytes, &flops);
+    if (w2) {
+      bytes += (double)w2->bytes;
+      flops *= 2.0;
+    }
+    Error err = Error::success();
+    Error launched = timed(name, bytes, flops, [&]() -> hipError_t {
+      err = pf_gemm(w, cols0, nw, w2, epi, m, y, ldy);
+      return err.ok() ? hipSuccess : hipErrorInvalidValue;
+    });
+    if (!err.ok()) return err;
+    return launched;
   };
   for (int64_t c0 = 0; c0 < n; c0 += chunk) {
     const int64_t m = std::min(chunk, n - c0);
     const int64_t p = p0 + c0;
-    UAII_HIP(launch_embed_rows(tok_embd_.view, ids_ + p, m, pf_x_, s));
+    UAII_TRY(timed("pf_embed", 4.0 * (double)m * (double)d.dim, 0.0,
+                   [&] { return launch_embed_rows(tok_embd_.view, ids_ + p, m, pf_x_, s); }));
     for (int64_t li = 0; li < d.n_layers; ++li) {
       const Layer& L = *layers_[(size_t)li];
       const LayerSpec& ls = d.layers[(size_t)li];
@@ -385,7 +414,7 @@ Error DecoderProgram::prefill(int64_t n) {
       UAII_TRY(prep(pf_x_, d.dim, m, L.attn_norm));
       const DeviceWeight* qkv[3] = {&L.wq, &L.wk, &L.wv};
       const int64_t qkv_cols[3] = {0, d.q_dim, d.q_dim + d.kv_dim};
-      UAII_TRY(pf_gemm(qkv, qkv_cols, 3, nullptr, EPI_STORE, m, pf_qkv_, ldqkv));
+      UAII_TRY(gemm("pf_gemm_qkv", qkv, qkv_cols, 3, nullptr, EPI_STORE, m, pf_qkv_, ldqkv));
       PfQkvArgs qa{};
       qa.qkv = pf_qkv_;
       qa.ldq = ldqkv;
@@ -404,7 +433,8 @@ Error DecoderProgram::prefill(int64_t n) {
       qa.vcache = vbase;
       qa.kv_f16 = 1;
       qa.max_seq = max_ctx_;
-      UAII_HIP(launch_pf_qkv(qa, s));
+      UAII_TRY(timed("pf_qkv_rope", 4.0 * (double)m * (double)(ldqkv + d.q_dim + d.kv_dim), 0.0,
+                     [&] { return launch_pf_qkv(qa, s); }));
       PfAttnArgs at{};
       at.q = pf_q_;
       at.ldq = d.q_dim;
@@ -418,27 +448,32 @@ Error DecoderProgram::prefill(int64_t n) {
       at.M = m;
       at.out = pf_attn_;
       at.ldo = d.q_dim;
-      UAII_HIP(launch_pf_attn(at, s));
+      // causal (query, key) pairs x heads x (QK + PV) multiply-adds
+      const double pairs = (double)m * (double)p + 0.5 * (double)m * (double)(m + 1);
+      UAII_TRY(timed("pf_attention", 4.0 * pairs * (double)d.kv_dim, 4.0 * pairs * (double)d.q_dim, [&] {
+        return launch_pf_attn(at, s);
+      }));
       UAII_TRY(prep(pf_attn_, d.q_dim, m, nullptr));
       const DeviceWeight* wo[3] = {&L.wo, nullptr, nullptr};
       const int64_t c00[3] = {0, 0, 0};
-      UAII_TRY(pf_gemm(wo, c00, 1, nullptr, EPI_ADD, m, pf_x_, d.dim));
+      UAII_TRY(gemm("pf_gemm_o", wo, c00, 1, nullptr, EPI_ADD, m, pf_x_, d.dim));
       // FFN block (gguf.cpp:1130-1173)
       if (ls.ffn == LayerSpec::kSwiGLU || ls.ffn == LayerSpec::kGelu) {
         UAII_TRY(prep(pf_x_, d.dim, m, L.ffn_norm));
         if (ls.ffn == LayerSpec::kSwiGLU) {
           const DeviceWeight* wg[3] = {&L.gate, nullptr, nullptr};
-          UAII_TRY(pf_gemm(wg, c00, 1, &L.up, EPI_SWIGLU, m, pf_h_, ls.inter));
+          UAII_TRY(gemm("pf_gemm_gate_up", wg, c00, 1, &L.up, EPI_SWIGLU, m, pf_h_, ls.inter));
         } else {
           const DeviceWeight* wu[3] = {&L.up, nullptr, nullptr};
-          UAII_TRY(pf_gemm(wu, c00, 1, nullptr, EPI_GELU, m, pf_h_, ls.inter));
+          UAII_TRY(gemm("pf_gemm_up", wu, c00, 1, nullptr, EPI_GELU, m, pf_h_, ls.inter));
         }
         UAII_TRY(prep(pf_h_, ls.inter, m, nullptr));
         const DeviceWeight* wd[3] = {&L.down, nullptr, nullptr};
-        UAII_TRY(pf_gemm(wd, c00, 1, nullptr, EPI_ADD, m, pf_x_, d.dim));
+        UAII_TRY(gemm("pf_gemm_down", wd, c00, 1, nullptr, EPI_ADD, m, pf_x_, d.dim));
       }
     }
   }
+  UAII_TRY(collect_timings());
   // the next step feeds ids[p0 + n] at position p0 + n
   UAII_HIP(hipStreamSynchronize(s));
   int32_t tok = 0;
@@ -541,53 +576,36 @@ Error DecoderProgram::read_ids(int64_t* out, int64_t n) {
   return Error::success();
 }
 
+Error DecoderProgram::collect_timings() {
+  if (!opts_.profile) return Error::success();
+  UAII_HIP(hipStreamSynchronize(stream_));
+  for (size_t i = 0; i < prof_used_; ++i) {
+    float ms = 0.0f;
+    if (hipEventElapsedTime(&ms, prof_events_[i].first, prof_events_[i].second) != hipSuccess) {
+      (void)hipGetLastError();  // a group that launched nothing records no time
+      continue;
+    }
+    KernelTiming& t = timing_[prof_tags_[i].name];
+    t.total_ms += ms;
+    t.launches += 1;
+    t.bytes += prof_tags_[i].bytes;
+    t.flops += prof_tags_[i].flops;
+  }
+  prof_used_ = 0;
+  return Error::success();
+}
+
 Error DecoderProgram::encode_step(bool want_logits) {
   const DecoderSpec& d = spec_;
   hipStream_t s = stream_;
   const size_t elem = opts_.kv_f16 ? 2 : 4;
   const size_t layer_kv = (size_t)d.kv_dim * (size_t)max_ctx_ * elem;
 
-  // Profiling mode: each launch group records a start/stop event pair on its own
-  // kernel dispatches (hipExtLaunchKernelGGL through UAII_LAUNCH), with no
-  // synchronisation between kernels; the pairs are read after the step.
-  size_t prof_used = 0;
+  prof_used_ = 0;
   auto timed = [&](const char* name, double bytes, auto&& launch) -> Error {
-    if (!opts_.profile) {
-      UAII_HIP(launch());
-      return Error::success();
-    }
-    if (prof_used == prof_events_.size()) {
-      hipEvent_t a = nullptr, b = nullptr;
-      UAII_HIP(hipEventCreate(&a));
-      UAII_HIP(hipEventCreate(&b));
-      prof_events_.push_back({a, b});
-      prof_tags_.push_back({std::string(), 0.0});
-    }
-    g_launch_events.start = prof_events_[prof_used].first;
-    g_launch_events.stop = prof_events_[prof_used].second;
-    const hipError_t st = launch();
-    g_launch_events = LaunchEvents{};
-    UAII_HIP(st);
-    prof_tags_[prof_used] = {name, bytes};
-    ++prof_used;
-    return Error::success();
+    return this->timed(name, bytes, 0.0, launch);
   };
-  auto collect = [&]() -> Error {
-    if (!opts_.profile) return Error::success();
-    UAII_HIP(hipStreamSynchronize(s));
-    for (size_t i = 0; i < prof_used; ++i) {
-      float ms = 0.0f;
-      if (hipEventElapsedTime(&ms, prof_events_[i].first, prof_events_[i].second) != hipSuccess) {
-        (void)hipGetLastError();  // a group that launched nothing records no time
-        continue;
-      }
-      KernelTiming& t = timing_[prof_tags_[i].first];
-      t.total_ms += ms;
-      t.launches += 1;
-      t.bytes += prof_tags_[i].second;
-    }
-    return Error::success();
-  };
+  auto collect = [&]() -> Error { return collect_timings(); };
 
   UAII_TRY(timed("embed", 0.0, [&] { return launch_embed(tok_embd_.view, state_, x_, tap_hidden_, s); }));
   int32_t pos_host = 0;
@@ -868,8 +886,10 @@ std::string DecoderProgram::profile_summary() const {
     first = false;
     const double avg_us = t.launches ? 1000.0 * t.total_ms / (double)t.launches : 0.0;
     const double gbs = t.total_ms > 0 ? t.bytes / (t.total_ms * 1e-3) / 1e9 : 0.0;
+    const double tfs = t.total_ms > 0 ? t.flops / (t.total_ms * 1e-3) / 1e12 : 0.0;
     os << "\"" << kv.first << "\":{\"launches\":" << t.launches << ",\"total_ms\":" << t.total_ms
-       << ",\"avg_us\":" << avg_us << ",\"bytes\":" << t.bytes << ",\"gbps\":" << gbs << "}";
+       << ",\"avg_us\":" << avg_us << ",\"bytes\":" << t.bytes << ",\"gbps\":" << gbs
+       << ",\"flops\":" << t.flops << ",\"tflops\":" << tfs << "}";
   }
   os << "}";
   return os.str();

@@ -47,6 +47,7 @@ struct KernelTiming {
   double total_ms = 0.0;
   int64_t launches = 0;
   double bytes = 0.0;  // algorithmic bytes per launch summed
+  double flops = 0.0;  // algorithmic flops per launch summed (matrix-core kernels)
 };
 
 class DecoderProgram {
@@ -97,6 +98,12 @@ class DecoderProgram {
   };
 
   Error upload_f32(const GgufTensor* t, float** out);
+  // Profiling mode: each launch group records a start/stop event pair on its own
+  // kernel dispatches (hipExtLaunchKernelGGL through UAII_LAUNCH), with no
+  // synchronisation between kernels; collect_timings() reads the pairs.
+  template <class F>
+  Error timed(const char* name, double bytes, double flops, F&& launch);
+  Error collect_timings();
   Error ensure_prefill_buffers(int64_t chunk);
   Error pf_gemm(const DeviceWeight* w[3], const int64_t cols0[3], int nw, const DeviceWeight* w2,
                 int epi, int64_t m, float* y, int64_t ldy);
@@ -120,8 +127,13 @@ class DecoderProgram {
   int32_t* lm_part_idx_ = nullptr;
   int lm_blocks_ = 0;  // capacity of the LM-head partial buffers
   // profiling mode: start/stop event pairs and their (kernel name, bytes) per launch group
+  struct ProfTag {
+    std::string name;
+    double bytes = 0.0, flops = 0.0;
+  };
   std::vector<std::pair<hipEvent_t, hipEvent_t>> prof_events_;
-  std::vector<std::pair<std::string, double>> prof_tags_;
+  std::vector<ProfTag> prof_tags_;
+  size_t prof_used_ = 0;
   uaii_hip::StepState* state_ = nullptr;
 
   // sized by ensure_capacity
@@ -147,5 +159,28 @@ class DecoderProgram {
   uaii_hip::PfAct pf_act_{};
   std::vector<void*> pf_allocs_;
 };
+
+template <class F>
+Error DecoderProgram::timed(const char* name, double bytes, double flops, F&& launch) {
+  if (!opts_.profile) {
+    UAII_HIP(launch());
+    return Error::success();
+  }
+  if (prof_used_ == prof_events_.size()) {
+    hipEvent_t a = nullptr, b = nullptr;
+    UAII_HIP(hipEventCreate(&a));
+    UAII_HIP(hipEventCreate(&b));
+    prof_events_.push_back({a, b});
+    prof_tags_.push_back(ProfTag{});
+  }
+  uaii_hip::g_launch_events.start = prof_events_[prof_used_].first;
+  uaii_hip::g_launch_events.stop = prof_events_[prof_used_].second;
+  const hipError_t st = launch();
+  uaii_hip::g_launch_events = uaii_hip::LaunchEvents{};
+  UAII_HIP(st);
+  prof_tags_[prof_used_] = ProfTag{name, bytes, flops};
+  ++prof_used_;
+  return Error::success();
+}
 
 }  // namespace uaii
