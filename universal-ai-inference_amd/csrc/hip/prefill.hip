@@ -30,6 +30,8 @@
 // activation rows are stored with each aligned group of 4 values as
 // (k0, k2, k1, k3), the order in which the weight decode below produces them
 // from bytes 0 and 2, then 1 and 3, of a 32-bit word.
+#include <type_traits>
+
 #include "common.h"
 #include "uaii_hip_internal.h"
 
@@ -149,14 +151,33 @@ __global__ void __launch_bounds__(256) k_pf_prep(const float* __restrict__ x, in
 
 // ---- weight fragments -----------------------------------------------------------------
 
-// Raw bytes of one 32-weight block of one row for lane group g, loaded one stage
-// ahead of their use; decode() turns them into MFMA B operands and scales.
+// A stage is two consecutive 32-blocks of k (kb = 2 st, 2 st + 1). PfRaw holds
+// the bytes of one weight row's stage that lane group g needs, loaded one stage
+// ahead of use; pf_decode() turns one block of it into the MFMA B operand (the
+// block's small integers) and its scale (and offset).
 template <int FMT>
-struct PfRaw {
-  uint2 q;        // Q4_0/Q8_0/Q4_K payload bytes; Q6_K: (ql word s=0, ql word s=1)
-  uint2 h;        // Q6_K: (qh word s=0, qh word s=1)
-  uint4 meta;     // Q4_K: d, dmin, scales[12]
-  uint32_t d;     // Q4_0/Q8_0: f16 d; Q6_K: f16 d | (two int8 scales << 16)
+struct PfRaw;
+template <>
+struct PfRaw<T_Q4_0> {
+  uint2 q[2];   // qs bytes 8 (g & 1) .. +7 of each block
+  uint32_t d;   // the two f16 scales
+};
+template <>
+struct PfRaw<T_Q8_0> {
+  uint2 q[2];   // qs bytes 8 g .. +7 of each block
+  uint32_t d;
+};
+template <>
+struct PfRaw<T_Q4_K> {
+  uint2 q;      // qs bytes 8 g .. +7 of the pair: low nibbles block 0, high block 1
+  uint4 meta;   // d, dmin, scales[12] of the super-block
+};
+template <>
+struct PfRaw<T_Q6_K> {
+  uint32_t ql[4];  // ql words of (block 0, sub 0), (0, 1), (1, 0), (1, 1)
+  uint32_t qh[2];  // qh words of sub-blocks 0 and 1 (shared by both blocks)
+  uint32_t sc;     // the four int8 sub-block scales
+  uint32_t d;
 };
 
 template <int FMT>
@@ -176,53 +197,79 @@ __device__ constexpr bool pf_offset() {
   return FMT == T_Q4_K;
 }
 
-// Row `row`, 32-block `kb`, lane group g (k = 8g..8g+7 of the block, or for
-// 16-element sub-blocks k = 16s + 4g..4g+3).
+// The lane's row pointers into the split arrays, lane-group offsets folded in.
+struct PfRow {
+  const uint8_t* a;
+  const uint8_t* b;
+  const uint8_t* c;
+  const uint8_t* d;
+};
+
 template <int FMT>
-__device__ inline void pf_load(const DevWeight& w, int64_t row, int64_t kb, int g, PfRaw<FMT>& r) {
+__device__ inline PfRow pf_row(const DevWeight& w, int64_t row, int g) {
+  PfRow p{};
+  p.a = w.a + row * w.a_row;
+  p.b = w.b + row * w.b_row;
   if constexpr (FMT == T_Q4_0) {
-    r.q = *reinterpret_cast<const uint2*>(w.a + row * w.a_row + kb * 16 + 8 * (g & 1));
-    r.d = ld_u16(w.b + row * w.b_row + kb * 2);
-  } else if constexpr (FMT == T_Q8_0) {
-    r.q = *reinterpret_cast<const uint2*>(w.a + row * w.a_row + kb * 32 + 8 * g);
-    r.d = ld_u16(w.b + row * w.b_row + kb * 2);
-  } else if constexpr (FMT == T_Q4_K) {
-    const int64_t sb = kb >> 3;
-    const int j = (int)(kb & 7);
-    r.q = *reinterpret_cast<const uint2*>(w.a + row * w.a_row + sb * 128 + 32 * (j >> 1) + 8 * g);
-    r.meta = *reinterpret_cast<const uint4*>(w.b + row * w.b_row + sb * 16);
+    p.a += 8 * (g & 1);
+  } else if constexpr (FMT == T_Q8_0 || FMT == T_Q4_K) {
+    p.a += 8 * g;
   } else if constexpr (FMT == T_Q6_K) {
-    const int64_t sb = kb >> 3;
-    const int e0 = 32 * (int)(kb & 7);
-    const int hh = e0 >> 7, e = e0 & 127;
-    const uint8_t* ql = w.a + row * w.a_row + sb * 128 + 64 * hh + (e & 63) + 4 * g;
-    const uint8_t* qh = w.b + row * w.b_row + sb * 64 + 32 * hh + 4 * g;
-    r.q = make_uint2(*reinterpret_cast<const uint32_t*>(ql), *reinterpret_cast<const uint32_t*>(ql + 16));
-    r.h = make_uint2(*reinterpret_cast<const uint32_t*>(qh), *reinterpret_cast<const uint32_t*>(qh + 16));
-    const uint32_t sc2 = ld_u16(w.c + row * w.c_row + sb * 16 + 8 * hh + (e >> 4));
-    r.d = ld_u16(w.d + row * w.d_row + sb * 2) | (sc2 << 16);
+    p.a += 4 * g;
+    p.b += 4 * g;
+    p.c = w.c + row * w.c_row;
+    p.d = w.d + row * w.d_row;
   }
+  return p;
 }
 
 template <int FMT>
-__device__ inline void pf_decode(const PfRaw<FMT>& r, int64_t kb, int g, PfFrag<FMT>& f) {
+__device__ inline void pf_load(const PfRow& p, int64_t st, PfRaw<FMT>& r) {
+  if constexpr (FMT == T_Q4_0) {
+    const uint8_t* q = p.a + st * 32;
+    r.q[0] = *reinterpret_cast<const uint2*>(q);
+    r.q[1] = *reinterpret_cast<const uint2*>(q + 16);
+    r.d = *reinterpret_cast<const uint32_t*>(p.b + st * 4);
+  } else if constexpr (FMT == T_Q8_0) {
+    const uint8_t* q = p.a + st * 64;
+    r.q[0] = *reinterpret_cast<const uint2*>(q);
+    r.q[1] = *reinterpret_cast<const uint2*>(q + 32);
+    r.d = *reinterpret_cast<const uint32_t*>(p.b + st * 4);
+  } else if constexpr (FMT == T_Q4_K) {
+    r.q = *reinterpret_cast<const uint2*>(p.a + st * 32);
+    r.meta = *reinterpret_cast<const uint4*>(p.b + (st >> 2) * 16);
+  } else if constexpr (FMT == T_Q6_K) {
+    // super-block st / 4, half (st % 4) / 2, elements 64 (st % 2) .. +63 of the half
+    const uint8_t* ql = p.a + (st >> 1) * 64;
+    const uint8_t* qh = p.b + (st >> 1) * 32;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) r.ql[u] = *reinterpret_cast<const uint32_t*>(ql + 16 * u);
+    r.qh[0] = *reinterpret_cast<const uint32_t*>(qh);
+    r.qh[1] = *reinterpret_cast<const uint32_t*>(qh + 16);
+    r.sc = *reinterpret_cast<const uint32_t*>(p.c + st * 4);
+    r.d = ld_u16(p.d + (st >> 2) * 2);
+  }
+}
+
+// Block s (0 or 1) of stage st for lane group g.
+template <int FMT>
+__device__ inline void pf_decode(const PfRaw<FMT>& r, int64_t st, int s, int g, PfFrag<FMT>& f) {
   if constexpr (FMT == T_Q4_0) {
     const int sh = (g >> 1) * 4;
-    const uint32_t v0 = r.q.x >> sh, v1 = r.q.y >> sh;
+    const uint32_t v0 = r.q[s].x >> sh, v1 = r.q[s].y >> sh;
     const h2_t bias = {(_Float16)1032.0f, (_Float16)1032.0f};
     f.b = cat8(as_h2(nib_pair(v0)) - bias, as_h2(nib_pair(v0 >> 8)) - bias,
                as_h2(nib_pair(v1)) - bias, as_h2(nib_pair(v1 >> 8)) - bias);
-    f.sc[0] = h2f((uint16_t)r.d);
+    f.sc[0] = h2f((uint16_t)(r.d >> (16 * s)));
   } else if constexpr (FMT == T_Q8_0) {
-    const uint32_t v0 = r.q.x ^ 0x80808080u, v1 = r.q.y ^ 0x80808080u;
+    const uint32_t v0 = r.q[s].x ^ 0x80808080u, v1 = r.q[s].y ^ 0x80808080u;
     const h2_t bias = {(_Float16)1152.0f, (_Float16)1152.0f};
     f.b = cat8(as_h2(byte_pair(v0)) - bias, as_h2(byte_pair(v0 >> 8)) - bias,
                as_h2(byte_pair(v1)) - bias, as_h2(byte_pair(v1 >> 8)) - bias);
-    f.sc[0] = h2f((uint16_t)r.d);
+    f.sc[0] = h2f((uint16_t)(r.d >> (16 * s)));
   } else if constexpr (FMT == T_Q4_K) {
-    const int j = (int)(kb & 7);
-    const int sh = (j & 1) * 4;
-    const uint32_t v0 = r.q.x >> sh, v1 = r.q.y >> sh;
+    const int j = 2 * (int)(st & 3) + s;  // sub-block of the super-block
+    const uint32_t v0 = r.q.x >> (4 * s), v1 = r.q.y >> (4 * s);
     const h2_t bias = {(_Float16)1024.0f, (_Float16)1024.0f};
     f.b = cat8(as_h2(nib_pair(v0)) - bias, as_h2(nib_pair(v0 >> 8)) - bias,
                as_h2(nib_pair(v1)) - bias, as_h2(nib_pair(v1 >> 8)) - bias);
@@ -243,41 +290,50 @@ __device__ inline void pf_decode(const PfRaw<FMT>& r, int64_t kb, int g, PfFrag<
     f.sc[0] = fmul_rn(d, (float)sc);
     f.off = fmul_rn(dmin, (float)mn);
   } else if constexpr (FMT == T_Q6_K) {
-    const int e = (32 * (int)(kb & 7)) & 127;
-    const int nib = (e >= 64) ? 4 : 0, qsh = 2 * (e >> 5);
+    // element e = 64 (st % 2) + 32 s + 16 t + 4 g + i of the half: ql byte e % 64
+    // (high nibble when e >= 64), qh byte e % 32 at bit 2 (e / 32), scale e / 16
+    const int nib = (int)(st & 1) * 4;
+    const int qsh = 4 * (int)(st & 1) + 2 * s;
     const h2_t bias = {(_Float16)1056.0f, (_Float16)1056.0f};
-    const float d = h2f((uint16_t)(r.d & 0xffff));
+    const float d = h2f((uint16_t)r.d);
 #pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      const uint32_t ql = s ? r.q.y : r.q.x, qh = s ? r.h.y : r.h.x;
-      const uint32_t q6 = ((ql >> nib) & 0x0F0F0F0Fu) | (((qh >> qsh) & 0x03030303u) << 4);
+    for (int t = 0; t < 2; ++t) {
+      const uint32_t q6 = ((r.ql[2 * s + t] >> nib) & 0x0F0F0F0Fu) | (((r.qh[t] >> qsh) & 0x03030303u) << 4);
       const h2_t p0 = as_h2(byte_pair(q6)) - bias, p1 = as_h2(byte_pair(q6 >> 8)) - bias;
-      f.b16[s] = h4_t{p0.x, p0.y, p1.x, p1.y};
-      f.sc[s] = fmul_rn(d, (float)(int8_t)((r.d >> (16 + 8 * s)) & 0xff));
+      f.b16[t] = h4_t{p0.x, p0.y, p1.x, p1.y};
+      f.sc[t] = fmul_rn(d, (float)(int8_t)((r.sc >> (8 * (2 * s + t))) & 0xff));
     }
   }
 }
 
 // ---- GEMM -------------------------------------------------------------------------------
 
+#ifndef UAII_PF_DMA
+#define UAII_PF_DMA 1  // Q4_0 / Q8_0 through the direct-to-LDS kernel
+#endif
+#ifndef UAII_PF_TILE
+#define UAII_PF_TILE 0  // wave tile: 0 chosen per launch, 2 64x32, 3 32x32
+#endif
 constexpr int PF_WAVES = 4;   // waves per block, side by side along N
-constexpr int PF_NT = 4;      // 16-column subtiles per wave
-constexpr int PF_KB = 2;      // 32-blocks of k per LDS stage
-constexpr int PF_ROW = 40;    // halfs per staged 32-k row (32 + 8 pad: conflict-free reads)
+#ifndef UAII_PF_ROW
+#define UAII_PF_ROW 40
+#endif
+constexpr int PF_ROW = UAII_PF_ROW;  // halfs per staged 32-k row (32 + 8 pad)
 
+// LDS: [buffer 2][block 2][hi/lo 2][BM rows][PF_ROW halfs]
 template <int MT>
-constexpr int pf_bm() { return 16 * MT; }
+constexpr int pf_lds_halfs() { return 2 * 2 * 2 * 16 * MT * PF_ROW; }
 
-// LDS: [stage 2][kb PF_KB][hi/lo 2][BM rows][PF_ROW halfs]
-template <int MT>
-constexpr int pf_lds_halfs() { return 2 * PF_KB * 2 * pf_bm<MT>() * PF_ROW; }
-
-template <int FMT, int EPI, int MT>
-__global__ void __launch_bounds__(PF_WAVES * 64) k_pf_gemm(PfGemmArgs a) {
-  constexpr int BM = pf_bm<MT>();
+// Block tile: 16 MT activation rows x PF_WAVES * 16 NT weight rows (for SwiGLU
+// each wave's NT subtiles are NT / 2 gate and NT / 2 up subtiles of the same
+// rows). K advances one stage (64) at a time; activations are staged in LDS
+// (double-buffered), each lane loads its weight bytes one stage ahead.
+template <int FMT, int EPI, int MT, int NT>
+__global__ void __launch_bounds__(PF_WAVES * 64, 2) k_pf_gemm(PfGemmArgs a) {
+  constexpr int BM = 16 * MT;
   constexpr int KS = pf_ksub<FMT>();
   constexpr bool OFF = pf_offset<FMT>();
-  constexpr int NQ = (EPI == EPI_SWIGLU) ? PF_NT / 2 : PF_NT;  // distinct row subtiles
+  constexpr int NQ = (EPI == EPI_SWIGLU) ? NT / 2 : NT;  // distinct row subtiles
   __shared__ _Float16 lds[pf_lds_halfs<MT>()];
 
   // segment of this column tile
@@ -290,129 +346,335 @@ __global__ void __launch_bounds__(PF_WAVES * 64) k_pf_gemm(PfGemmArgs a) {
   const int col = lane & 15, g = lane >> 4;
   const int64_t n0 = ((int64_t)(tile - seg.tile0) * PF_WAVES + wave) * (16 * NQ);
   const int64_t m0 = (int64_t)blockIdx.y * BM;
-  const int64_t K = a.K, nkb = K / 32;
+  const int64_t K = a.K, nst = K / 64;
 
-  // weight rows of this lane per subtile (clamped: rows past the end are loaded but not stored)
-  int64_t wrow[PF_NT];
+  // weight rows of this lane per subtile (clamped: rows past the end are loaded, not stored)
+  PfRow prow[NT];
 #pragma unroll
-  for (int j = 0; j < PF_NT; ++j) {
+  for (int j = 0; j < NT; ++j) {
     const int64_t r = n0 + 16 * (j % NQ) + col;
-    wrow[j] = r < seg.rows ? r : seg.rows - 1;
+    const DevWeight& w = (EPI == EPI_SWIGLU && j >= NQ) ? seg.w2 : seg.w;
+    prow[j] = pf_row<FMT>(w, r < seg.rows ? r : seg.rows - 1, g);
   }
-  auto wt = [&](int j) -> const DevWeight& { return (EPI == EPI_SWIGLU && j >= NQ) ? seg.w2 : seg.w; };
 
-  f4_t acc[MT][PF_NT];
+  f4_t acc[MT][NT];
 #pragma unroll
   for (int i = 0; i < MT; ++i)
 #pragma unroll
-    for (int j = 0; j < PF_NT; ++j) acc[i][j] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int j = 0; j < NT; ++j) acc[i][j] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
-  // activation stage copy: BM rows x PF_KB blocks x (hi, lo) x 4 pieces of 16 B
-  constexpr int PIECES = BM * PF_KB * 2 * 4;
-  constexpr int PPT = (PIECES + PF_WAVES * 64 - 1) / (PF_WAVES * 64);
+  // activation stage: BM rows x 2 blocks x (hi, lo) x 4 pieces of 16 B
+  constexpr int PIECES = BM * 2 * 2 * 4;
+  constexpr int PPT = PIECES / (PF_WAVES * 64);
+  static_assert(PIECES % (PF_WAVES * 64) == 0, "stage pieces per thread");
+  // activation pieces one stage ahead (stored to the other LDS buffer after the
+  // compute), weight bytes two stages ahead in a ring of 3; ring indices are
+  // compile-time constants
   uint4 stg[PPT];
-  auto load_stage = [&](int64_t kb0) {
+  PfRaw<FMT> raw[3][NT];
+  auto load_stage = [&](uint4 (&dst)[PPT], int64_t st) __attribute__((always_inline)) {
 #pragma unroll
     for (int u = 0; u < PPT; ++u) {
       const int c = threadIdx.x + u * PF_WAVES * 64;
-      stg[u] = make_uint4(0, 0, 0, 0);
-      if (c < PIECES) {
-        const int q = c & 3, r = (c >> 2) % BM, kbh = (c >> 2) / BM;  // kbh = kb * 2 + h
-        const int kb = kbh >> 1, h = kbh & 1;
-        if (kb0 + kb < nkb) {
-          const __half* src = (h ? a.alo : a.ahi) + (m0 + r) * K + (kb0 + kb) * 32 + q * 8;
-          stg[u] = *reinterpret_cast<const uint4*>(src);
+      const int q = c & 3, r = (c >> 2) % BM, kbh = (c >> 2) / BM;  // kbh = block * 2 + hi/lo
+      const __half* src = ((kbh & 1) ? a.alo : a.ahi) + (m0 + r) * K + (2 * st + (kbh >> 1)) * 32 + q * 8;
+      // element-wise: a whole-struct copy here is turned into a memcpy into a
+      // stack array (scratch memory)
+      const uint4 v = *reinterpret_cast<const uint4*>(src);
+      dst[u].x = v.x;
+      dst[u].y = v.y;
+      dst[u].z = v.z;
+      dst[u].w = v.w;
+    }
+  };
+  auto store_stage = [&](const uint4 (&src)[PPT], int buf) __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < PPT; ++u) {
+      const int c = threadIdx.x + u * PF_WAVES * 64;
+      const int q = c & 3, r = (c >> 2) % BM, kbh = (c >> 2) / BM;
+      _Float16* dst = lds + (((buf * 4) + kbh) * BM + r) * PF_ROW + q * 8;
+      *reinterpret_cast<uint4*>(dst) = src[u];
+    }
+  };
+  auto load_w = [&](PfRaw<FMT>(&dst)[NT], int64_t st) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < NT; ++j) pf_load<FMT>(prow[j], st, dst[j]);
+  };
+  // LDS writes done, then the block barrier. No memory fence: a fence would also
+  // wait for the weight and activation loads in flight for later stages.
+  auto lds_barrier = []() __attribute__((always_inline)) {
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0); vmcnt, expcnt untouched
+    __builtin_amdgcn_s_barrier();
+  };
+  auto compute = [&](const PfRaw<FMT>(&rw)[NT], int64_t st, int buf) __attribute__((always_inline)) {
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      PfFrag<FMT> fr[NT];
+#pragma unroll
+      for (int j = 0; j < NT; ++j) pf_decode<FMT>(rw[j], st, s, g, fr[j]);
+      const _Float16* base = lds + ((buf * 2 + s) * 2) * BM * PF_ROW;
+#pragma unroll
+      for (int i = 0; i < MT; ++i) {
+        const _Float16* ph = base + (16 * i + col) * PF_ROW;
+        const _Float16* pl = ph + BM * PF_ROW;
+        f4_t sxv = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        if constexpr (OFF) {
+          const float4 s4 = *reinterpret_cast<const float4*>(a.sx + (2 * st + s) * a.mpad + m0 + 16 * i + 4 * g);
+          sxv = f4_t{s4.x, s4.y, s4.z, s4.w};
         }
-      }
-    }
-  };
-  auto store_stage = [&](int buf) {
+        if constexpr (KS == 32) {
+          const h8_t ahi = *reinterpret_cast<const h8_t*>(ph + 8 * g);
+          const h8_t alo = *reinterpret_cast<const h8_t*>(pl + 8 * g);
 #pragma unroll
-    for (int u = 0; u < PPT; ++u) {
-      const int c = threadIdx.x + u * PF_WAVES * 64;
-      if (c < PIECES) {
-        const int q = c & 3, r = (c >> 2) % BM, kbh = (c >> 2) / BM;
-        _Float16* dst = lds + (((buf * PF_KB * 2) + kbh) * BM + r) * PF_ROW + q * 8;
-        *reinterpret_cast<uint4*>(dst) = stg[u];
-      }
-    }
-  };
-
-  // weight bytes: rc for the stage being computed, rn for the next one (register
-  // arrays are only ever indexed by compile-time constants)
-  PfRaw<FMT> rc[PF_KB][PF_NT], rn[PF_KB][PF_NT];
-  auto load_w = [&](PfRaw<FMT> (&dst)[PF_KB][PF_NT], int64_t kb0) {
-#pragma unroll
-    for (int kb = 0; kb < PF_KB; ++kb) {
-      const int64_t b = (kb0 + kb < nkb) ? kb0 + kb : nkb - 1;
-#pragma unroll
-      for (int j = 0; j < PF_NT; ++j) pf_load<FMT>(wt(j), wrow[j], b, g, dst[kb][j]);
-    }
-  };
-
-  const int64_t nst = (nkb + PF_KB - 1) / PF_KB;
-  load_stage(0);
-  load_w(rc, 0);
-  store_stage(0);
-  __syncthreads();
-
-  for (int64_t st = 0; st < nst; ++st) {
-    const int cur = (int)(st & 1);
-    if (st + 1 < nst) {
-      load_stage((st + 1) * PF_KB);
-      load_w(rn, (st + 1) * PF_KB);
-    }
-#pragma unroll
-    for (int kb = 0; kb < PF_KB; ++kb) {
-      const int64_t kbg = st * PF_KB + kb;
-      if (kbg < nkb) {
-        PfFrag<FMT> fr[PF_NT];
-#pragma unroll
-        for (int j = 0; j < PF_NT; ++j) pf_decode<FMT>(rc[kb][j], kbg, g, fr[j]);
-        const _Float16* base = lds + ((cur * PF_KB + kb) * 2) * BM * PF_ROW;
-#pragma unroll
-        for (int i = 0; i < MT; ++i) {
-          const _Float16* ph = base + (16 * i + col) * PF_ROW;
-          const _Float16* pl = ph + BM * PF_ROW;
-          f4_t sxv = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
-          if constexpr (OFF) {
-            const float4 s4 = *reinterpret_cast<const float4*>(a.sx + kbg * a.mpad + m0 + 16 * i + 4 * g);
-            sxv = f4_t{s4.x, s4.y, s4.z, s4.w};
+          for (int j = 0; j < NT; ++j) {
+            f4_t p = mfma32(ahi, fr[j].b, f4_t{0.0f, 0.0f, 0.0f, 0.0f});
+            p = mfma32(alo, fr[j].b, p);
+            acc[i][j] += fr[j].sc[0] * p;
+            if constexpr (OFF) acc[i][j] -= fr[j].off * sxv;
           }
-          if constexpr (KS == 32) {
-            const h8_t ahi = *reinterpret_cast<const h8_t*>(ph + 8 * g);
-            const h8_t alo = *reinterpret_cast<const h8_t*>(pl + 8 * g);
+        } else {
 #pragma unroll
-            for (int j = 0; j < PF_NT; ++j) {
-              f4_t p = mfma32(ahi, fr[j].b, f4_t{0.0f, 0.0f, 0.0f, 0.0f});
-              p = mfma32(alo, fr[j].b, p);
-              acc[i][j] += fr[j].sc[0] * p;
-              if constexpr (OFF) acc[i][j] -= fr[j].off * sxv;
-            }
-          } else {
+          for (int t = 0; t < 2; ++t) {
+            const h4_t ahi = *reinterpret_cast<const h4_t*>(ph + 16 * t + 4 * g);
+            const h4_t alo = *reinterpret_cast<const h4_t*>(pl + 16 * t + 4 * g);
 #pragma unroll
-            for (int s = 0; s < 2; ++s) {
-              const h4_t ahi = *reinterpret_cast<const h4_t*>(ph + 16 * s + 4 * g);
-              const h4_t alo = *reinterpret_cast<const h4_t*>(pl + 16 * s + 4 * g);
-#pragma unroll
-              for (int j = 0; j < PF_NT; ++j) {
-                f4_t p = mfma16(ahi, fr[j].b16[s], f4_t{0.0f, 0.0f, 0.0f, 0.0f});
-                p = mfma16(alo, fr[j].b16[s], p);
-                acc[i][j] += fr[j].sc[s] * p;
-              }
+            for (int j = 0; j < NT; ++j) {
+              f4_t p = mfma16(ahi, fr[j].b16[t], f4_t{0.0f, 0.0f, 0.0f, 0.0f});
+              p = mfma16(alo, fr[j].b16[t], p);
+              acc[i][j] += fr[j].sc[t] * p;
             }
           }
         }
       }
     }
-    if (st + 1 < nst) {
-      store_stage(cur ^ 1);
+  };
+  // one stage: prefetch activations of st + 1 and weights of st + 2, compute
+  // stage st, move stage st + 1 into the other LDS buffer
+  auto step = [&](auto ws, int64_t st) __attribute__((always_inline)) {
+    constexpr int W = decltype(ws)::value;
+    if (st + 1 < nst) load_stage(stg, st + 1);
+    if (st + 2 < nst) load_w(raw[(W + 2) % 3], st + 2);
+    compute(raw[W], st, (int)(st & 1));
+    if (st + 1 < nst) store_stage(stg, (int)((st + 1) & 1));
+    lds_barrier();
+  };
+
+  load_w(raw[0], 0);
+  if (nst > 1) load_w(raw[1], 1);
+  load_stage(stg, 0);
+  store_stage(stg, 0);
+  lds_barrier();
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  for (int64_t st = 0; st < nst; st += 3) {
+    step(I0{}, st);
+    if (st + 1 >= nst) break;
+    step(I1{}, st + 1);
+    if (st + 2 >= nst) break;
+    step(I2{}, st + 2);
+  }
+
+  // epilogue: lane holds rows m0 + 16i + 4g + r of column n0 + 16j + col
 #pragma unroll
-      for (int kb = 0; kb < PF_KB; ++kb)
+  for (int i = 0; i < MT; ++i) {
 #pragma unroll
-        for (int j = 0; j < PF_NT; ++j) rc[kb][j] = rn[kb][j];
-      __syncthreads();
+    for (int r = 0; r < 4; ++r) {
+      const int64_t t = m0 + 16 * i + 4 * g + r;
+      if (t >= a.M) continue;
+      const float rs = a.rs[t];
+      float* yrow = a.y + t * a.ldy + seg.col0;
+#pragma unroll
+      for (int j = 0; j < NQ; ++j) {
+        const int64_t n = n0 + 16 * j + col;
+        if (n >= seg.rows) continue;
+        const float v = acc[i][j][r] * rs;
+        if constexpr (EPI == EPI_STORE) {
+          yrow[n] = v;
+        } else if constexpr (EPI == EPI_ADD) {
+          yrow[n] = yrow[n] + v;
+        } else if constexpr (EPI == EPI_SWIGLU) {
+          const float u = acc[i][j + NQ][r] * rs;
+          const float act = v / (1.0f + expf(-v));  // silu (elementwise.cpp:73-84)
+          yrow[n] = act * u;
+        } else if constexpr (EPI == EPI_GELU) {
+          const float inner = 0.7978845608f * (v + 0.044715f * v * v * v);
+          yrow[n] = 0.5f * v * (1.0f + tanhf(inner));
+        }
+      }
     }
+  }
+}
+
+// ---- GEMM with direct-to-LDS loads (Q4_0, Q8_0) -----------------------------------------
+//
+// Same tile math as k_pf_gemm, but activations and weight bytes travel global ->
+// LDS with global_load_lds_dwordx4 / _dword (lane i of an instruction writes the
+// 16 (4) bytes at M0 + 16 i (4 i)), so no registers hold data in flight and a
+// ring of three LDS stages keeps two stages of loads outstanding. The loads are
+// issued from inline assembly and their completion is waited for with explicit
+// vmcnt counts: the compiler would otherwise wait for every outstanding LDS
+// load before each LDS read. Each activation row's four 16-byte pieces are
+// stored XOR-swizzled (piece p of row r in slot p ^ swz(r)) so the fragment
+// reads of 16 consecutive rows hit distinct banks.
+
+__device__ inline void dma16(const void* g, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(g) : "memory", "m0");
+}
+__device__ inline void dma4(const void* g, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, off" ::"s"(lds), "v"(g) : "memory", "m0");
+}
+__device__ inline uint32_t lds_addr(const void* p) {
+  return __builtin_amdgcn_readfirstlane(
+      (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p);
+}
+__device__ inline int pf_swz(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
+
+template <int FMT>
+constexpr int dma_qbytes() { return FMT == T_Q8_0 ? 64 : 32; }  // payload bytes per row per stage
+template <int MT>
+constexpr int dma_a_bytes() { return 2 * 2 * 16 * MT * 64; }      // [block][hi/lo][row][64 B]
+template <int FMT>
+constexpr int dma_w_bytes() { return PF_WAVES * 32 * (dma_qbytes<FMT>() + 8); }  // per wave: 32 rows
+template <int FMT, int MT>
+constexpr int dma_stage_bytes() { return dma_a_bytes<MT>() + dma_w_bytes<FMT>(); }
+// DMA instructions each wave issues per stage (the vmcnt unit)
+template <int FMT, int MT>
+constexpr int dma_per_stage() { return MT + dma_qbytes<FMT>() / 32 + 1; }
+
+template <int FMT, int EPI, int MT>
+__global__ void __launch_bounds__(PF_WAVES * 64, 2) k_pf_gemm_dma(PfGemmArgs a) {
+  constexpr int NT = 2;
+  constexpr int BM = 16 * MT;
+  constexpr int NQ = (EPI == EPI_SWIGLU) ? 1 : NT;
+  constexpr int QB = dma_qbytes<FMT>();
+  constexpr int SB = dma_stage_bytes<FMT, MT>();
+  constexpr int ND = dma_per_stage<FMT, MT>();
+  static_assert(ND <= 15, "vmcnt immediate");
+  __shared__ __attribute__((aligned(16))) uint8_t lds[3 * SB];
+
+  const int tile = blockIdx.x;
+  int si = 0;
+  for (int k = 1; k < a.nseg; ++k) if (tile >= a.seg[k].tile0) si = k;
+  const PfSeg& seg = a.seg[si];
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int col = lane & 15, g = lane >> 4;
+  const int64_t n0 = ((int64_t)(tile - seg.tile0) * PF_WAVES + wave) * (16 * NQ);
+  const int64_t m0 = (int64_t)blockIdx.y * BM;
+  const int64_t K = a.K, nst = K / 64;
+
+  // this lane's DMA sources. Activations: wave w copies (block w >> 1, hi/lo
+  // w & 1); instruction u covers rows 16u .. 16u + 15, lane -> (row, slot).
+  const int arow = lane >> 2, aslot = lane & 3;
+  const __half* asrc = (wave & 1) ? a.alo : a.ahi;
+  const int ablk = wave >> 1;
+  // Weights: the wave's 32 rows (subtile j = row / 16; SwiGLU: j = 1 is the up
+  // tensor), QB / 16 lanes per row for the payload, one dword per row of scales.
+  const int wl_per_row = QB / 16;
+  const int wrow_q = lane / wl_per_row, wpart = lane % wl_per_row;  // payload: 2 passes for Q8_0
+  const uint8_t* wsrc_q[QB / 32];
+#pragma unroll
+  for (int u = 0; u < QB / 32; ++u) {
+    const int rl = (lane + 64 * u) / wl_per_row;
+    const int j = rl >> 4;
+    const DevWeight& w = (EPI == EPI_SWIGLU && j >= NQ) ? seg.w2 : seg.w;
+    int64_t r = n0 + 16 * (j % NQ) + (rl & 15);
+    r = r < seg.rows ? r : seg.rows - 1;
+    wsrc_q[u] = w.a + r * w.a_row + 16 * ((lane + 64 * u) % wl_per_row);
+  }
+  const uint8_t* wsrc_s;
+  {
+    const int rl = lane & 31;
+    const int j = rl >> 4;
+    const DevWeight& w = (EPI == EPI_SWIGLU && j >= NQ) ? seg.w2 : seg.w;
+    int64_t r = n0 + 16 * (j % NQ) + (rl & 15);
+    r = r < seg.rows ? r : seg.rows - 1;
+    wsrc_s = w.b + r * w.b_row;
+  }
+  (void)wrow_q;
+  (void)wpart;
+
+  auto issue = [&](int64_t st, int slot) __attribute__((always_inline)) {
+    uint8_t* base = lds + slot * SB;
+    // activations
+#pragma unroll
+    for (int u = 0; u < MT; ++u) {
+      const int r = 16 * u + arow;
+      const int piece = aslot ^ pf_swz(r);
+      const __half* src = asrc + (m0 + r) * K + (2 * st + ablk) * 32 + piece * 8;
+      dma16(src, lds_addr(base + ((ablk * 2 + (wave & 1)) * BM + 16 * u) * 64));
+    }
+    // weight payload and scales of this wave's rows
+    uint8_t* wb = base + dma_a_bytes<MT>() + wave * (32 * (QB + 8));
+#pragma unroll
+    for (int u = 0; u < QB / 32; ++u) dma16(wsrc_q[u] + st * QB, lds_addr(wb + u * 1024));
+    dma4(wsrc_s + st * 4, lds_addr(wb + 32 * QB));
+  };
+  auto wait_stage = [&](int64_t st) __attribute__((always_inline)) {
+    // stage st is complete when at most the next stage's loads are outstanding
+    if (st + 1 < nst) __builtin_amdgcn_s_waitcnt(0x0f70 | ND);  // vmcnt(ND), lgkm/exp untouched
+    else __builtin_amdgcn_s_waitcnt(0x0f70);                    // vmcnt(0)
+    __builtin_amdgcn_s_barrier();
+  };
+
+  f4_t acc[MT][NT];
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int j = 0; j < NT; ++j) acc[i][j] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+  auto compute = [&](int64_t st, int slot) __attribute__((always_inline)) {
+    const uint8_t* base = lds + slot * SB;
+    const uint8_t* wb = base + dma_a_bytes<MT>() + wave * (32 * (QB + 8));
+    PfRaw<FMT> rw[NT];
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+      const uint8_t* rowp = wb + (16 * j + col) * QB;
+      if constexpr (FMT == T_Q4_0) {
+        rw[j].q[0] = *reinterpret_cast<const uint2*>(rowp + 8 * (g & 1));
+        rw[j].q[1] = *reinterpret_cast<const uint2*>(rowp + 16 + 8 * (g & 1));
+      } else {
+        rw[j].q[0] = *reinterpret_cast<const uint2*>(rowp + 8 * g);
+        rw[j].q[1] = *reinterpret_cast<const uint2*>(rowp + 32 + 8 * g);
+      }
+      rw[j].d = *reinterpret_cast<const uint32_t*>(wb + 32 * QB + 4 * (16 * j + col));
+    }
+#pragma unroll
+    for (int sb = 0; sb < 2; ++sb) {
+      PfFrag<FMT> fr[NT];
+#pragma unroll
+      for (int j = 0; j < NT; ++j) pf_decode<FMT>(rw[j], st, sb, g, fr[j]);
+#pragma unroll
+      for (int i = 0; i < MT; ++i) {
+        const int r = 16 * i + col;
+        const int off = r * 64 + 16 * (g ^ pf_swz(r));
+        const h8_t ahi = *reinterpret_cast<const h8_t*>(base + ((sb * 2 + 0) * BM) * 64 + off);
+        const h8_t alo = *reinterpret_cast<const h8_t*>(base + ((sb * 2 + 1) * BM) * 64 + off);
+#pragma unroll
+        for (int j = 0; j < NT; ++j) {
+          f4_t p = mfma32(ahi, fr[j].b, f4_t{0.0f, 0.0f, 0.0f, 0.0f});
+          p = mfma32(alo, fr[j].b, p);
+          acc[i][j] += fr[j].sc[0] * p;
+        }
+      }
+    }
+  };
+
+  issue(0, 0);
+  if (nst > 1) issue(1, 1);
+  for (int64_t st = 0; st < nst; st += 3) {
+    wait_stage(st);
+    if (st + 2 < nst) issue(st + 2, 2);
+    compute(st, 0);
+    if (st + 1 >= nst) break;
+    wait_stage(st + 1);
+    if (st + 3 < nst) issue(st + 3, 0);
+    compute(st + 1, 1);
+    if (st + 2 >= nst) break;
+    wait_stage(st + 2);
+    if (st + 4 < nst) issue(st + 4, 1);
+    compute(st + 2, 2);
   }
 
   // epilogue: lane holds rows m0 + 16i + 4g + r of column n0 + 16j + col
@@ -692,35 +954,72 @@ hipError_t launch_pf_prep(const float* x, int64_t ldx, int64_t M, const float* n
 }
 
 namespace {
-template <int FMT, int EPI, int MT>
-hipError_t pf_gemm_go(const PfGemmArgs& a, int ntiles, hipStream_t s) {
-  dim3 grid((unsigned)ntiles, (unsigned)(a.mpad / pf_bm<MT>()));
-  UAII_LAUNCH((k_pf_gemm<FMT, EPI, MT>), grid, dim3(PF_WAVES * 64), 0, s, a);
+template <int FMT, int EPI, int MT, int NT>
+hipError_t pf_gemm_go(PfGemmArgs a, hipStream_t s) {
+  const int per_tile = PF_WAVES * 16 * (EPI == EPI_SWIGLU ? NT / 2 : NT);
+  int ntiles = 0;
+  for (int k = 0; k < a.nseg; ++k) {
+    a.seg[k].tile0 = ntiles;
+    ntiles += (int)((a.seg[k].rows + per_tile - 1) / per_tile);
+  }
+  dim3 grid((unsigned)ntiles, (unsigned)(a.mpad / (16 * MT)));
+  UAII_LAUNCH((k_pf_gemm<FMT, EPI, MT, NT>), grid, dim3(PF_WAVES * 64), 0, s, a);
   return hipGetLastError();
 }
 
-template <int FMT, int MT>
-hipError_t pf_gemm_epi(const PfGemmArgs& a, int ntiles, hipStream_t s) {
+template <int FMT, int EPI, int MT>
+hipError_t pf_gemm_dma_go(PfGemmArgs a, hipStream_t s) {
+  const int per_tile = PF_WAVES * 16 * (EPI == EPI_SWIGLU ? 1 : 2);
+  int ntiles = 0;
+  for (int k = 0; k < a.nseg; ++k) {
+    a.seg[k].tile0 = ntiles;
+    ntiles += (int)((a.seg[k].rows + per_tile - 1) / per_tile);
+  }
+  dim3 grid((unsigned)ntiles, (unsigned)(a.mpad / (16 * MT)));
+  UAII_LAUNCH((k_pf_gemm_dma<FMT, EPI, MT>), grid, dim3(PF_WAVES * 64), 0, s, a);
+  return hipGetLastError();
+}
+
+// Wave tile per launch: 64 x 32 (measured best at M = 512 for the 8B shapes,
+// ahead of 64 x 64 and 32 x 32) unless that leaves the grid under one block per
+// CU, or the format's weight ring does not fit the registers of two waves per
+// SIMD at that tile (Q4_K, Q6_K); then 32 x 32.
+template <int FMT, int EPI>
+hipError_t pf_gemm_tile(const PfGemmArgs& a, hipStream_t s) {
+  int64_t rows = 0;
+  for (int k = 0; k < a.nseg; ++k) rows += a.seg[k].rows;
+  if (EPI == EPI_SWIGLU) rows *= 2;
+  const int64_t mid = (rows / 128) * (a.mpad / 64);
+  constexpr bool wide = FMT == T_Q4_0 || FMT == T_Q8_0;
+  const int want = UAII_PF_TILE;
+  if constexpr (wide) {
+    if (UAII_PF_DMA) {
+      if (want == 2 || (want == 0 && mid >= 256)) return pf_gemm_dma_go<FMT, EPI, 4>(a, s);
+      return pf_gemm_dma_go<FMT, EPI, 2>(a, s);
+    }
+    if (want == 2 || (want == 0 && mid >= 256)) return pf_gemm_go<FMT, EPI, 4, 2>(a, s);
+  }
+  return pf_gemm_go<FMT, EPI, 2, 2>(a, s);
+}
+
+template <int FMT>
+hipError_t pf_gemm_epi(const PfGemmArgs& a, hipStream_t s) {
   switch (a.epi) {
-    case EPI_STORE: return pf_gemm_go<FMT, EPI_STORE, MT>(a, ntiles, s);
-    case EPI_ADD: return pf_gemm_go<FMT, EPI_ADD, MT>(a, ntiles, s);
-    case EPI_SWIGLU: return pf_gemm_go<FMT, EPI_SWIGLU, MT>(a, ntiles, s);
-    case EPI_GELU: return pf_gemm_go<FMT, EPI_GELU, MT>(a, ntiles, s);
+    case EPI_STORE: return pf_gemm_tile<FMT, EPI_STORE>(a, s);
+    case EPI_ADD: return pf_gemm_tile<FMT, EPI_ADD>(a, s);
+    case EPI_SWIGLU: return pf_gemm_tile<FMT, EPI_SWIGLU>(a, s);
+    case EPI_GELU: return pf_gemm_tile<FMT, EPI_GELU>(a, s);
     default: return hipErrorInvalidValue;
   }
 }
 }  // namespace
 
 hipError_t launch_pf_gemm(PfGemmArgs a, hipStream_t s) {
-  if (a.nseg < 1 || a.nseg > 3 || a.M <= 0 || a.M > a.mpad || a.mpad % 64 || a.K % 32)
+  if (a.nseg < 1 || a.nseg > 3 || a.M <= 0 || a.M > a.mpad || a.mpad % 64 || a.K % 64)
     return hipErrorInvalidValue;
   const int type = a.seg[0].w.type;
   if (!pf_supported(type)) return hipErrorInvalidValue;
-  if (type == T_Q4_K || type == T_Q6_K) {
-    if (a.K % 256) return hipErrorInvalidValue;
-  }
-  const int per_tile = PF_WAVES * 16 * (a.epi == EPI_SWIGLU ? PF_NT / 2 : PF_NT);
-  int ntiles = 0;
+  if ((type == T_Q4_K || type == T_Q6_K) && a.K % 256) return hipErrorInvalidValue;
   for (int k = 0; k < a.nseg; ++k) {
     const PfSeg& sg = a.seg[k];
     if (sg.w.type != type || sg.w.cols != a.K || sg.rows <= 0 || sg.rows > sg.w.rows)
@@ -728,16 +1027,12 @@ hipError_t launch_pf_gemm(PfGemmArgs a, hipStream_t s) {
     if (a.epi == EPI_SWIGLU &&
         (sg.w2.type != type || sg.w2.cols != a.K || sg.rows > sg.w2.rows))
       return hipErrorInvalidValue;
-    a.seg[k].tile0 = ntiles;
-    ntiles += (int)((sg.rows + per_tile - 1) / per_tile);
   }
-  // 32-row tiles when 64-row tiles leave most of the chip idle
-  const bool small = (int64_t)ntiles * (a.mpad / 64) < 512;
   switch (type) {
-    case T_Q4_0: return small ? pf_gemm_epi<T_Q4_0, 2>(a, ntiles, s) : pf_gemm_epi<T_Q4_0, 4>(a, ntiles, s);
-    case T_Q8_0: return small ? pf_gemm_epi<T_Q8_0, 2>(a, ntiles, s) : pf_gemm_epi<T_Q8_0, 4>(a, ntiles, s);
-    case T_Q4_K: return small ? pf_gemm_epi<T_Q4_K, 2>(a, ntiles, s) : pf_gemm_epi<T_Q4_K, 4>(a, ntiles, s);
-    case T_Q6_K: return small ? pf_gemm_epi<T_Q6_K, 2>(a, ntiles, s) : pf_gemm_epi<T_Q6_K, 4>(a, ntiles, s);
+    case T_Q4_0: return pf_gemm_epi<T_Q4_0>(a, s);
+    case T_Q8_0: return pf_gemm_epi<T_Q8_0>(a, s);
+    case T_Q4_K: return pf_gemm_epi<T_Q4_K>(a, s);
+    case T_Q6_K: return pf_gemm_epi<T_Q6_K>(a, s);
     default: return hipErrorInvalidValue;
   }
 }

@@ -173,7 +173,7 @@ int gemm_common(const uaii_hip_weight* w, const uaii_hip_weight* w2, const float
     if (u.type != v.type || u.rows != v.rows || u.cols != v.cols) return kErrArg;
   }
   const int64_t K = v.cols, N = v.rows;
-  if (!pf_supported(v.type) || K % 32) {
+  if (!pf_supported(v.type) || K % 64) {
     for (int64_t i = 0; i < m; ++i) {
       const float* xi = x + i * K;
       float* yi = y + i * N;

@@ -272,14 +272,14 @@ Error DecoderProgram::build(const DecoderSpec& spec, const ProgramOptions& opts)
   // the matrix-core prompt path: block formats it decodes, dense FFNs, f16 cache
   pf_ok_ = opts_.kv_f16 && !moe_ &&
            pf_attn_supported((int)d.head_dim, (int)d.n_heads, (int)d.n_kv_heads) &&
-           d.dim % 32 == 0 && d.q_dim % 32 == 0;
+           d.dim % 64 == 0 && d.q_dim % 64 == 0;
   for (int64_t li = 0; pf_ok_ && li < d.n_layers; ++li) {
     const Layer& L = *layers_[(size_t)li];
     const LayerSpec& ls = d.layers[(size_t)li];
     std::vector<const DeviceWeight*> ws = {&L.wq, &L.wk, &L.wv, &L.wo};
     if (ls.ffn == LayerSpec::kSwiGLU) ws.insert(ws.end(), {&L.gate, &L.up, &L.down});
     if (ls.ffn == LayerSpec::kGelu) ws.insert(ws.end(), {&L.up, &L.down});
-    if ((ls.ffn == LayerSpec::kSwiGLU || ls.ffn == LayerSpec::kGelu) && ls.inter % 32) pf_ok_ = false;
+    if ((ls.ffn == LayerSpec::kSwiGLU || ls.ffn == LayerSpec::kGelu) && ls.inter % 64) pf_ok_ = false;
     for (const DeviceWeight* w : ws) pf_ok_ = pf_ok_ && pf_supported(w->view.type);
   }
   if (const char* env = std::getenv("UAII_PREFILL")) {

@@ -1,7 +1,8 @@
 """Kernel microbenchmark through the uaii_hip C ABI.
 
 Times one fused GEMV (plain, RMSNorm, residual add or gate/up SwiGLU) of a given
-GGUF type and shape on random block bytes, rotating over enough weight copies
+GGUF type and shape on random block bytes (or, with --m > 1, the prefill MFMA
+GEMM with the same epilogues), rotating over enough weight copies
 (> 256 MiB in total, the MI355X last-level cache) that each launch reads its
 weights from HBM, plus the plain 1 GiB copy kernel. Meant to run alone or under
 ``rocprofv3 --kernel-trace --stats`` / ``--pmc`` to pin a kernel's time and
@@ -31,6 +32,8 @@ def main(argv=None) -> int:
     ap.add_argument("--cols", type=int, default=4096)
     ap.add_argument("--iters", type=int, default=40)
     ap.add_argument("--copy-mib", type=int, default=1024)
+    ap.add_argument("--m", type=int, default=1,
+                    help="activation rows: 1 = decode GEMV, > 1 = prefill MFMA GEMM (TFLOP/s)")
     a = ap.parse_args(argv)
     names = {v.lower(): k for k, v in TYPE_NAMES.items()}
     t = names[a.type.lower()]
@@ -49,11 +52,19 @@ def main(argv=None) -> int:
             blk[:, 1] &= 0x3b  # small finite f16 scales at byte 0..1 for the 32-blocks
             group.append(DeviceWeight(t, p, a.rows, a.cols))
         ws.append(group)
-    x = DeviceBuffer.from_array(rng.normal(0, 1, a.cols).astype(np.float32))
+    x = DeviceBuffer.from_array(rng.normal(0, 1, a.m * a.cols).astype(np.float32))
     nrm = DeviceBuffer.from_array(np.ones(a.cols, np.float32))
-    y = DeviceBuffer.from_array(np.zeros(a.rows, np.float32))
+    y = DeviceBuffer.from_array(np.zeros(a.m * a.rows, np.float32))
 
     def launch(g):
+        if a.m > 1:
+            if a.epi == "plain":
+                return L.uaii_hip_gemm(g[0].h, x.ptr, a.m, y.ptr, None)
+            if a.epi == "rmsnorm":
+                return L.uaii_hip_gemm_rmsnorm(g[0].h, x.ptr, a.m, nrm.ptr, 1e-5, y.ptr, None)
+            if a.epi == "add":
+                return L.uaii_hip_gemm_add(g[0].h, x.ptr, a.m, None, 1e-5, y.ptr, None)
+            return L.uaii_hip_gemm_swiglu(g[0].h, g[1].h, x.ptr, a.m, nrm.ptr, 1e-5, y.ptr, None)
         if a.epi == "plain":
             return L.uaii_hip_gemv(g[0].h, x.ptr, y.ptr, None)
         if a.epi == "rmsnorm":
@@ -70,6 +81,11 @@ def main(argv=None) -> int:
         check_hip(launch(ws[i % copies]), "gemv")
     check_hip(L.uaii_hip_synchronize())
     dt = (time.perf_counter() - t0) / a.iters
+    if a.m > 1:
+        flops = 2.0 * nw * a.m * a.rows * a.cols
+        print(f"gemm {a.epi} {TYPE_NAMES[t]} M={a.m} {nw}x{a.rows}x{a.cols}: {dt * 1e6:.1f} us/launch "
+              f"wall (activation prep included), {flops / dt / 1e12:.1f} TFLOP/s algorithmic", flush=True)
+        return 0
     algo = nw * (a.rows * a.cols * BPW[t] + 4 * a.cols + 4 * a.rows)
     print(f"gemv {a.epi} {TYPE_NAMES[t]} {nw}x{a.rows}x{a.cols}: {dt * 1e6:.2f} us/launch wall, "
           f"{algo / dt / 1e9:.0f} GB/s algorithmic ({algo:.0f} B), {copies} weight copies", flush=True)
