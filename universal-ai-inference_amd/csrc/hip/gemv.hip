@@ -35,7 +35,13 @@ namespace {
 #define UAII_GEMV_BATCH 1
 #endif
 
-constexpr int WPB = 4;  // waves per block
+// Waves per block (measured per role on the 8B decode step): 4 in general; 8 for
+// the QKV epilogue (6144 rows of K = 4096: more row sets share one staged
+// input); 16 for the K-split long rows of the residual-add GEMV (the down
+// projection, whose staged input is as large as a 4-wave block's weight bytes).
+constexpr int WPB = 4;
+constexpr int WPB_QKV = 8;
+constexpr int WPB_LONG = 16;
 constexpr int NB = UAII_GEMV_BATCH;
 static_assert(NB == 1 || NB == 2, "UAII_GEMV_BATCH must be 1 or 2");
 constexpr int RPW_MAX = 4;  // rows per wave (even: RoPE / SwiGLU pairs share a wave)
@@ -905,13 +911,13 @@ __device__ inline void epilogue(const GemvArgs& a, const GemvSeg& seg, int64_t l
   }
 }
 
-template <int FMT, int EPI>
-__global__ void __launch_bounds__(WPB * 64) k_gemv(GemvArgs a) {
+template <int FMT, int EPI, int W>
+__global__ void __launch_bounds__(W * 64) k_gemv(GemvArgs a) {
   extern __shared__ float xsm[];
-  __shared__ float red[2 * WPB];
-  __shared__ float kred[2][WPB][RPW_MAX];
-  __shared__ float bval[WPB];
-  __shared__ int32_t bidx[WPB];
+  __shared__ float red[2 * W];
+  __shared__ float kred[2][W][RPW_MAX];
+  __shared__ float bval[W];
+  __shared__ int32_t bidx[W];
 
   // segment lookup (uniform per block)
   int si = 0;
@@ -921,7 +927,7 @@ __global__ void __launch_bounds__(WPB * 64) k_gemv(GemvArgs a) {
 
   constexpr int RPW = rpw_of(FMT);
   const int ks = a.ksplit;
-  const int nrs = WPB / ks;  // row sets per block
+  const int nrs = W / ks;  // row sets per block
   const int64_t ngroups = (seg.rows + nrs * RPW - 1) / (nrs * RPW);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
@@ -1033,7 +1039,7 @@ __global__ void __launch_bounds__(WPB * 64) k_gemv(GemvArgs a) {
     if (threadIdx.x == 0) {
       float bv = bval[0];
       int32_t bi = bidx[0];
-      for (int k = 1; k < WPB; ++k) {
+      for (int k = 1; k < W; ++k) {
         if (bidx[k] == 0x7fffffff) continue;
         if (bi == 0x7fffffff || bval[k] > bv || (bval[k] == bv && bidx[k] < bi)) { bv = bval[k]; bi = bidx[k]; }
       }
@@ -1096,35 +1102,47 @@ __global__ void __launch_bounds__(1024) k_argmax_final(GemvArgs a, int nparts) {
 
 using KernelFn = void (*)(GemvArgs);
 
-template <int EPI>
+template <int EPI, int W>
 KernelFn pick_fmt(int type) {
   switch (type) {
-    case T_Q4_0: return k_gemv<T_Q4_0, EPI>;
-    case T_Q8_0: return k_gemv<T_Q8_0, EPI>;
-    case T_Q4_K: return k_gemv<T_Q4_K, EPI>;
-    case T_Q6_K: return k_gemv<T_Q6_K, EPI>;
-    case T_Q4_1: return k_gemv<T_Q4_1, EPI>;
-    case T_Q5_0: return k_gemv<T_Q5_0, EPI>;
-    case T_Q5_1: return k_gemv<T_Q5_1, EPI>;
-    case T_Q5_K: return k_gemv<T_Q5_K, EPI>;
-    case T_Q2_K: return k_gemv<T_Q2_K, EPI>;
-    case T_Q3_K: return k_gemv<T_Q3_K, EPI>;
-    case T_F32: return k_gemv<T_F32, EPI>;
-    case T_F16: return k_gemv<T_F16, EPI>;
+    case T_Q4_0: return k_gemv<T_Q4_0, EPI, W>;
+    case T_Q8_0: return k_gemv<T_Q8_0, EPI, W>;
+    case T_Q4_K: return k_gemv<T_Q4_K, EPI, W>;
+    case T_Q6_K: return k_gemv<T_Q6_K, EPI, W>;
+    case T_Q4_1: return k_gemv<T_Q4_1, EPI, W>;
+    case T_Q5_0: return k_gemv<T_Q5_0, EPI, W>;
+    case T_Q5_1: return k_gemv<T_Q5_1, EPI, W>;
+    case T_Q5_K: return k_gemv<T_Q5_K, EPI, W>;
+    case T_Q2_K: return k_gemv<T_Q2_K, EPI, W>;
+    case T_Q3_K: return k_gemv<T_Q3_K, EPI, W>;
+    case T_F32: return k_gemv<T_F32, EPI, W>;
+    case T_F16: return k_gemv<T_F16, EPI, W>;
     default: return nullptr;
   }
 }
 
-KernelFn pick(int epi, int type) {
+// Kernel for (epilogue, format, waves per block): WPB for every epilogue,
+// WPB_QKV for the QKV epilogue, WPB_LONG for the residual add.
+KernelFn pick(int epi, int type, int w) {
+  if (w == WPB_QKV) return epi == EPI_QKV ? pick_fmt<EPI_QKV, WPB_QKV>(type) : nullptr;
+  if (w == WPB_LONG) return epi == EPI_ADD ? pick_fmt<EPI_ADD, WPB_LONG>(type) : nullptr;
+  if (w != WPB) return nullptr;
   switch (epi) {
-    case EPI_STORE: return pick_fmt<EPI_STORE>(type);
-    case EPI_ADD: return pick_fmt<EPI_ADD>(type);
-    case EPI_QKV: return pick_fmt<EPI_QKV>(type);
-    case EPI_SWIGLU: return pick_fmt<EPI_SWIGLU>(type);
-    case EPI_LOGITS: return pick_fmt<EPI_LOGITS>(type);
-    case EPI_GELU: return pick_fmt<EPI_GELU>(type);
+    case EPI_STORE: return pick_fmt<EPI_STORE, WPB>(type);
+    case EPI_ADD: return pick_fmt<EPI_ADD, WPB>(type);
+    case EPI_QKV: return pick_fmt<EPI_QKV, WPB>(type);
+    case EPI_SWIGLU: return pick_fmt<EPI_SWIGLU, WPB>(type);
+    case EPI_LOGITS: return pick_fmt<EPI_LOGITS, WPB>(type);
+    case EPI_GELU: return pick_fmt<EPI_GELU, WPB>(type);
     default: return nullptr;
   }
+}
+
+// Waves per block for a launch of epilogue `epi` whose rows split K over `ks` waves.
+int pick_waves(int epi, int ks) {
+  if (epi == EPI_ADD && ks == 4) return WPB_LONG;
+  if (epi == EPI_QKV) return WPB_QKV;
+  return WPB;
 }
 
 }  // namespace
@@ -1138,9 +1156,12 @@ hipError_t prepare_gemv() {
   const int lim = lds_limit();
   for (int e : epis) {
     for (int t : types) {
-      (void)hipFuncSetAttribute((const void*)pick(e, t), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                lim - 1024);
-      (void)hipGetLastError();
+      for (int w : {WPB, WPB_QKV, WPB_LONG}) {
+        const KernelFn fn = pick(e, t, w);
+        if (!fn) continue;
+        (void)hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, lim - 1024);
+        (void)hipGetLastError();
+      }
     }
   }
   return hipSuccess;
@@ -1163,7 +1184,7 @@ int cu_count() {
 
 // Blocks of `fn` that stay resident on one CU with `lds` bytes of dynamic LDS
 // (registers, LDS and wave slots all counted by the runtime); cached per pair.
-int resident_blocks(KernelFn fn, size_t lds) {
+int resident_blocks(KernelFn fn, size_t lds, int waves) {
   struct Entry { KernelFn fn; size_t lds; int n; };
   static std::mutex mu;
   static std::vector<Entry> cache;
@@ -1171,7 +1192,7 @@ int resident_blocks(KernelFn fn, size_t lds) {
   for (const Entry& e : cache)
     if (e.fn == fn && e.lds == lds) return e.n;
   int n = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, WPB * 64, lds) != hipSuccess || n <= 0) {
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, waves * 64, lds) != hipSuccess || n <= 0) {
     (void)hipGetLastError();
     n = 2;
   }
@@ -1184,7 +1205,7 @@ int resident_blocks(KernelFn fn, size_t lds) {
 int pick_ksplit(const DevWeight& w) {
   const int64_t ncol = (w.a_row / 16 + 63) / 64;
   int ks = 1;
-  while (ks < WPB && ks < 4 && (ncol + ks - 1) / ks > 2) ks *= 2;
+  while (ks < 4 && (ncol + ks - 1) / ks > 2) ks *= 2;
   return ks;
 }
 
@@ -1199,6 +1220,7 @@ struct Plan {
   KernelFn fn = nullptr;
   size_t lds = 0;
   int ks = 1;
+  int waves = WPB;
   int per[3] = {0, 0, 0};  // blocks per segment
   int blocks = 0;
 };
@@ -1207,14 +1229,15 @@ struct Plan {
 // rest loop), shared out by group count and evened out so blocks do equal work.
 Plan make_plan(const GemvArgs& a) {
   Plan p;
-  p.fn = pick(a.epi, a.seg[0].w.type);
   p.lds = lds_bytes(a.seg[0].w.type, a.K);
   p.ks = pick_ksplit(a.seg[0].w);
+  p.waves = pick_waves(a.epi, p.ks);
+  p.fn = pick(a.epi, a.seg[0].w.type, p.waves);
   if (!p.fn) return p;
-  const int rpg = (WPB / p.ks) * rpw_of(a.seg[0].w.type);
+  const int rpg = (p.waves / p.ks) * rpw_of(a.seg[0].w.type);
   int64_t total = 0;
   for (int k = 0; k < a.nseg; ++k) total += (a.seg[k].rows + rpg - 1) / rpg;
-  const int per_cu = UAII_GEMV_BLOCKS_PER_CU > 0 ? UAII_GEMV_BLOCKS_PER_CU : resident_blocks(p.fn, p.lds);
+  const int per_cu = UAII_GEMV_BLOCKS_PER_CU > 0 ? UAII_GEMV_BLOCKS_PER_CU : resident_blocks(p.fn, p.lds, p.waves);
   const int64_t cap = (int64_t)cu_count() * per_cu;
   for (int k = 0; k < a.nseg; ++k) {
     const int64_t g = (a.seg[k].rows + rpg - 1) / rpg;
@@ -1291,7 +1314,7 @@ hipError_t launch_gemv(const GemvArgs& in, hipStream_t s) {
     if (blocks == 0) return hipSuccess;
     if ((int64_t)p.lds > lds_limit() - 1024) return hipErrorInvalidValue;
     if (a.epi == EPI_LOGITS && blocks > a.part_cap) return hipErrorInvalidValue;
-    UAII_LAUNCH(p.fn, dim3(blocks), dim3(WPB * 64), p.lds, s, a);
+    UAII_LAUNCH(p.fn, dim3(blocks), dim3(p.waves * 64), p.lds, s, a);
     hipError_t st = hipGetLastError();
     if (st == hipSuccess && a.epi == EPI_LOGITS) {
       UAII_LAUNCH(k_argmax_final, dim3(1), dim3(1024), 0, s, a, blocks);
