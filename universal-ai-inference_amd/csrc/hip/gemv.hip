@@ -981,7 +981,10 @@ __global__ void __launch_bounds__(W * 64) k_gemv(GemvArgs a) {
 #pragma unroll
         for (int r = 0; r < RPW; ++r) kred[par][wave][r] = acc[r];
       }
-      __syncthreads();
+      // LDS only: a full __syncthreads() would also wait for the weight loads
+      // already in flight for the next unit
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+      __builtin_amdgcn_s_barrier();
       if (kp == 0) {
 #pragma unroll
         for (int r = 0; r < RPW; ++r) {
