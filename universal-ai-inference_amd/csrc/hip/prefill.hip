@@ -65,9 +65,10 @@ __device__ inline float pow2f_i(int e) { return __uint_as_float((uint32_t)(e + 1
 // ---- activation prep ----------------------------------------------------------------
 
 // One block per row; rows >= M (tile padding) are written as zeros.
-__global__ void __launch_bounds__(256) k_pf_prep(const float* __restrict__ x, int64_t ldx,
+__global__ void __launch_bounds__(256) k_pf_prep(float* __restrict__ x, int64_t ldx,
                                                  int64_t M, const float* __restrict__ norm_w,
-                                                 float eps, PfAct act) {
+                                                 float eps, PfAct act, const float* __restrict__ part,
+                                                 int nsplit) {
   extern __shared__ float row[];
   __shared__ float red[4];
   const int64_t t = blockIdx.x;
@@ -83,10 +84,20 @@ __global__ void __launch_bounds__(256) k_pf_prep(const float* __restrict__ x, in
     return;
   }
   float4* r4 = reinterpret_cast<float4*>(row);
-  const float4* x4 = reinterpret_cast<const float4*>(x + t * ldx);
+  float4* x4 = reinterpret_cast<float4*>(x + t * ldx);
   float ss = 0.0f, amax = 0.0f;
   for (int i = tid; i < nv; i += 256) {
-    const float4 v = x4[i];
+    float4 v = x4[i];
+    if (nsplit > 0) {
+      // residual add of a K-split GEMM's partials, in split order
+      float4 p = reinterpret_cast<const float4*>(part + t * ldx)[i];
+      for (int z = 1; z < nsplit; ++z) {
+        const float4 q = reinterpret_cast<const float4*>(part + ((int64_t)z * M + t) * ldx)[i];
+        p.x += q.x; p.y += q.y; p.z += q.z; p.w += q.w;
+      }
+      v.x += p.x; v.y += p.y; v.z += p.z; v.w += p.w;
+      x4[i] = v;
+    }
     r4[i] = v;
     ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
     amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
@@ -346,7 +357,8 @@ __global__ void __launch_bounds__(PF_WAVES * 64, 2) k_pf_gemm(PfGemmArgs a) {
   const int col = lane & 15, g = lane >> 4;
   const int64_t n0 = ((int64_t)(tile - seg.tile0) * PF_WAVES + wave) * (16 * NQ);
   const int64_t m0 = (int64_t)blockIdx.y * BM;
-  const int64_t K = a.K, nst = K / 64;
+  const int64_t K = a.K, nst = K / 64 / a.ksplit;  // stages of this block's K range
+  const int64_t sbase = (int64_t)blockIdx.z * nst;  // its first stage
 
   // weight rows of this lane per subtile (clamped: rows past the end are loaded, not stored)
   PfRow prow[NT];
@@ -377,7 +389,7 @@ __global__ void __launch_bounds__(PF_WAVES * 64, 2) k_pf_gemm(PfGemmArgs a) {
     for (int u = 0; u < PPT; ++u) {
       const int c = threadIdx.x + u * PF_WAVES * 64;
       const int q = c & 3, r = (c >> 2) % BM, kbh = (c >> 2) / BM;  // kbh = block * 2 + hi/lo
-      const __half* src = ((kbh & 1) ? a.alo : a.ahi) + (m0 + r) * K + (2 * st + (kbh >> 1)) * 32 + q * 8;
+      const __half* src = ((kbh & 1) ? a.alo : a.ahi) + (m0 + r) * K + (2 * (sbase + st) + (kbh >> 1)) * 32 + q * 8;
       // element-wise: a whole-struct copy here is turned into a memcpy into a
       // stack array (scratch memory)
       const uint4 v = *reinterpret_cast<const uint4*>(src);
@@ -398,7 +410,7 @@ __global__ void __launch_bounds__(PF_WAVES * 64, 2) k_pf_gemm(PfGemmArgs a) {
   };
   auto load_w = [&](PfRaw<FMT>(&dst)[NT], int64_t st) __attribute__((always_inline)) {
 #pragma unroll
-    for (int j = 0; j < NT; ++j) pf_load<FMT>(prow[j], st, dst[j]);
+    for (int j = 0; j < NT; ++j) pf_load<FMT>(prow[j], sbase + st, dst[j]);
   };
   // LDS writes done, then the block barrier. No memory fence: a fence would also
   // wait for the weight and activation loads in flight for later stages.
@@ -406,7 +418,8 @@ __global__ void __launch_bounds__(PF_WAVES * 64, 2) k_pf_gemm(PfGemmArgs a) {
     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0); vmcnt, expcnt untouched
     __builtin_amdgcn_s_barrier();
   };
-  auto compute = [&](const PfRaw<FMT>(&rw)[NT], int64_t st, int buf) __attribute__((always_inline)) {
+  auto compute = [&](const PfRaw<FMT>(&rw)[NT], int64_t stl, int buf) __attribute__((always_inline)) {
+    const int64_t st = sbase + stl;
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
       PfFrag<FMT> fr[NT];
@@ -492,7 +505,8 @@ __global__ void __launch_bounds__(PF_WAVES * 64, 2) k_pf_gemm(PfGemmArgs a) {
         if constexpr (EPI == EPI_STORE) {
           yrow[n] = v;
         } else if constexpr (EPI == EPI_ADD) {
-          yrow[n] = yrow[n] + v;
+          if (a.ksplit > 1) a.part[((int64_t)blockIdx.z * a.M + t) * a.ldy + seg.col0 + n] = v;
+          else yrow[n] = yrow[n] + v;
         } else if constexpr (EPI == EPI_SWIGLU) {
           const float u = acc[i][j + NQ][r] * rs;
           const float act = v / (1.0f + expf(-v));  // silu (elementwise.cpp:73-84)
@@ -562,7 +576,8 @@ __global__ void __launch_bounds__(PF_WAVES * 64, 2) k_pf_gemm_dma(PfGemmArgs a) 
   const int col = lane & 15, g = lane >> 4;
   const int64_t n0 = ((int64_t)(tile - seg.tile0) * PF_WAVES + wave) * (16 * NQ);
   const int64_t m0 = (int64_t)blockIdx.y * BM;
-  const int64_t K = a.K, nst = K / 64;
+  const int64_t K = a.K, nst = K / 64 / a.ksplit;  // stages of this block's K range
+  const int64_t sbase = (int64_t)blockIdx.z * nst;  // its first stage
 
   // this lane's DMA sources. Activations: wave w copies (block w >> 1, hi/lo
   // w & 1); instruction u covers rows 16u .. 16u + 15, lane -> (row, slot).
@@ -595,7 +610,8 @@ __global__ void __launch_bounds__(PF_WAVES * 64, 2) k_pf_gemm_dma(PfGemmArgs a) 
   (void)wrow_q;
   (void)wpart;
 
-  auto issue = [&](int64_t st, int slot) __attribute__((always_inline)) {
+  auto issue = [&](int64_t stl, int slot) __attribute__((always_inline)) {
+    const int64_t st = sbase + stl;
     uint8_t* base = lds + slot * SB;
     // activations
 #pragma unroll
@@ -624,7 +640,8 @@ __global__ void __launch_bounds__(PF_WAVES * 64, 2) k_pf_gemm_dma(PfGemmArgs a) 
 #pragma unroll
     for (int j = 0; j < NT; ++j) acc[i][j] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
-  auto compute = [&](int64_t st, int slot) __attribute__((always_inline)) {
+  auto compute = [&](int64_t stl, int slot) __attribute__((always_inline)) {
+    const int64_t st = sbase + stl;
     const uint8_t* base = lds + slot * SB;
     const uint8_t* wb = base + dma_a_bytes<MT>() + wave * (32 * (QB + 8));
     PfRaw<FMT> rw[NT];
@@ -694,7 +711,8 @@ __global__ void __launch_bounds__(PF_WAVES * 64, 2) k_pf_gemm_dma(PfGemmArgs a) 
         if constexpr (EPI == EPI_STORE) {
           yrow[n] = v;
         } else if constexpr (EPI == EPI_ADD) {
-          yrow[n] = yrow[n] + v;
+          if (a.ksplit > 1) a.part[((int64_t)blockIdx.z * a.M + t) * a.ldy + seg.col0 + n] = v;
+          else yrow[n] = yrow[n] + v;
         } else if constexpr (EPI == EPI_SWIGLU) {
           const float u = acc[i][j + NQ][r] * rs;
           const float act = v / (1.0f + expf(-v));  // silu (elementwise.cpp:73-84)
@@ -939,8 +957,9 @@ bool pf_supported(int type) {
 
 int64_t pf_mpad(int64_t m) { return (m + 63) / 64 * 64; }
 
-hipError_t launch_pf_prep(const float* x, int64_t ldx, int64_t M, const float* norm_w, float eps,
-                          const PfAct& act, hipStream_t s) {
+hipError_t launch_pf_prep(float* x, int64_t ldx, int64_t M, const float* norm_w, float eps,
+                          const PfAct& act, hipStream_t s, const float* part, int nsplit) {
+  if (nsplit < 0 || (nsplit > 0 && !part)) return hipErrorInvalidValue;
   if (M <= 0 || M > act.mpad || act.K % 32 || act.mpad % 64 || ldx % 4) return hipErrorInvalidValue;
   const size_t lds = (size_t)act.K * 4;
   if ((int64_t)lds > lds_limit()) return hipErrorInvalidValue;
@@ -949,7 +968,8 @@ hipError_t launch_pf_prep(const float* x, int64_t ldx, int64_t M, const float* n
                                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
   }
-  UAII_LAUNCH(k_pf_prep, dim3((unsigned)act.mpad), dim3(256), lds, s, x, ldx, M, norm_w, eps, act);
+  UAII_LAUNCH(k_pf_prep, dim3((unsigned)act.mpad), dim3(256), lds, s, x, ldx, M, norm_w, eps, act,
+              part, nsplit);
   return hipGetLastError();
 }
 
@@ -962,7 +982,7 @@ hipError_t pf_gemm_go(PfGemmArgs a, hipStream_t s) {
     a.seg[k].tile0 = ntiles;
     ntiles += (int)((a.seg[k].rows + per_tile - 1) / per_tile);
   }
-  dim3 grid((unsigned)ntiles, (unsigned)(a.mpad / (16 * MT)));
+  dim3 grid((unsigned)ntiles, (unsigned)(a.mpad / (16 * MT)), (unsigned)a.ksplit);
   UAII_LAUNCH((k_pf_gemm<FMT, EPI, MT, NT>), grid, dim3(PF_WAVES * 64), 0, s, a);
   return hipGetLastError();
 }
@@ -975,7 +995,7 @@ hipError_t pf_gemm_dma_go(PfGemmArgs a, hipStream_t s) {
     a.seg[k].tile0 = ntiles;
     ntiles += (int)((a.seg[k].rows + per_tile - 1) / per_tile);
   }
-  dim3 grid((unsigned)ntiles, (unsigned)(a.mpad / (16 * MT)));
+  dim3 grid((unsigned)ntiles, (unsigned)(a.mpad / (16 * MT)), (unsigned)a.ksplit);
   UAII_LAUNCH((k_pf_gemm_dma<FMT, EPI, MT>), grid, dim3(PF_WAVES * 64), 0, s, a);
   return hipGetLastError();
 }
@@ -1014,12 +1034,34 @@ hipError_t pf_gemm_epi(const PfGemmArgs& a, hipStream_t s) {
 }
 }  // namespace
 
+// K split for a residual-add launch: enough blocks for two per CU (each block's
+// K range a whole number of stages and, for the K-quants, super-blocks).
+int pf_gemm_ksplit(const PfGemmArgs& a, int cus) {
+  if (a.epi != EPI_ADD || a.nseg < 1) return 1;
+  const int type = a.seg[0].w.type;
+  if (!pf_supported(type)) return 1;
+  int64_t rows = 0;
+  for (int k = 0; k < a.nseg; ++k) rows += a.seg[k].rows;
+  const bool wide = type == T_Q4_0 || type == T_Q8_0;
+  const int64_t mid = (rows / 128) * (a.mpad / 64);
+  const bool big_tile = wide && (UAII_PF_TILE == 2 || (UAII_PF_TILE == 0 && mid >= 256));
+  const int64_t tiles = (rows + PF_WAVES * 32 - 1) / (PF_WAVES * 32);
+  const int64_t blocks = tiles * (a.mpad / (big_tile ? 64 : 32));
+  const int64_t kq = wide ? 64 : 256;
+  int ks = 1;
+  while (ks < 4 && blocks * ks < 2 * (int64_t)cus && a.K % (kq * ks * 2) == 0) ks *= 2;
+  return ks;
+}
+
 hipError_t launch_pf_gemm(PfGemmArgs a, hipStream_t s) {
+  if (a.ksplit < 1) a.ksplit = 1;
   if (a.nseg < 1 || a.nseg > 3 || a.M <= 0 || a.M > a.mpad || a.mpad % 64 || a.K % 64)
     return hipErrorInvalidValue;
   const int type = a.seg[0].w.type;
   if (!pf_supported(type)) return hipErrorInvalidValue;
-  if ((type == T_Q4_K || type == T_Q6_K) && a.K % 256) return hipErrorInvalidValue;
+  const int64_t kq = (type == T_Q4_K || type == T_Q6_K) ? 256 : 64;  // K granule of a block's range
+  if (a.K % (kq * a.ksplit)) return hipErrorInvalidValue;
+  if (a.ksplit > 1 && (a.epi != EPI_ADD || !a.part)) return hipErrorInvalidValue;
   for (int k = 0; k < a.nseg; ++k) {
     const PfSeg& sg = a.seg[k];
     if (sg.w.type != type || sg.w.cols != a.K || sg.rows <= 0 || sg.rows > sg.w.rows)

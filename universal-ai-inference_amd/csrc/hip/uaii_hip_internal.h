@@ -163,6 +163,11 @@ struct PfGemmArgs {
   const float* rs;
   float* y;             // [M][ldy]
   int64_t ldy;
+  // EPI_ADD split over K: ksplit > 1 blocks along grid z each take K / ksplit
+  // and store their partial to part[z][M][ldy] instead of adding into y; the
+  // next launch_pf_prep of y adds the partials (z in order) into y
+  int ksplit;
+  float* part;
 };
 
 struct PfQkvArgs {
@@ -194,9 +199,14 @@ struct PfAttnArgs {
 bool pf_supported(int type);
 bool pf_attn_supported(int head_dim, int n_heads, int n_kv);
 int64_t pf_mpad(int64_t m);
-hipError_t launch_pf_prep(const float* x, int64_t ldx, int64_t M, const float* norm_w, float eps,
-                          const PfAct& act, hipStream_t s);
+// x [M][ldx] -> act. With nsplit > 0, x first becomes x + sum_z part[z][M][ldx]
+// (written back: x is the residual stream).
+hipError_t launch_pf_prep(float* x, int64_t ldx, int64_t M, const float* norm_w, float eps,
+                          const PfAct& act, hipStream_t s, const float* part = nullptr,
+                          int nsplit = 0);
 hipError_t launch_pf_gemm(PfGemmArgs a, hipStream_t s);
+// K split launch_pf_gemm can take for `a` (EPI_ADD only; 1 = none) on `cus` CUs.
+int pf_gemm_ksplit(const PfGemmArgs& a, int cus);
 hipError_t launch_pf_qkv(const PfQkvArgs& a, hipStream_t s);
 hipError_t launch_pf_attn(const PfAttnArgs& a, hipStream_t s);
 

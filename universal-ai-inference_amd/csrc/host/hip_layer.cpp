@@ -197,7 +197,7 @@ int gemm_common(const uaii_hip_weight* w, const uaii_hip_weight* w2, const float
   act.rs = reinterpret_cast<float*>(base + 2 * hb + sxb);
   act.mpad = mpad;
   act.K = K;
-  hipError_t e = launch_pf_prep(x, K, m, norm_w, eps, act, S(stream));
+  hipError_t e = launch_pf_prep(const_cast<float*>(x), K, m, norm_w, eps, act, S(stream));
   if (e != hipSuccess) return (int)e;
   PfGemmArgs a{};
   a.nseg = 1;

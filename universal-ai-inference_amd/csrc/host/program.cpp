@@ -309,6 +309,7 @@ Error DecoderProgram::ensure_prefill_buffers(int64_t chunk) {
   UAII_TRY(alloc(4 * C * (size_t)d.q_dim, (void**)&pf_q_));
   UAII_TRY(alloc(4 * C * (size_t)d.q_dim, (void**)&pf_attn_));
   UAII_TRY(alloc(4 * C * (size_t)inter, (void**)&pf_h_));
+  UAII_TRY(alloc(4 * 4 * C * (size_t)d.dim, (void**)&pf_part_));
   UAII_TRY(alloc(2 * (size_t)mpad * (size_t)kmax, (void**)&pf_act_.hi));
   UAII_TRY(alloc(2 * (size_t)mpad * (size_t)kmax, (void**)&pf_act_.lo));
   UAII_TRY(alloc(4 * (size_t)(kmax / 32) * (size_t)mpad, (void**)&pf_act_.sx));
@@ -344,9 +345,31 @@ Error DecoderProgram::pf_gemm(const DeviceWeight* w[3], const int64_t cols0[3], 
       sg.col0 = cols0[j];
       ++j;
     }
+    // a residual add into the stream of a single-format launch may split K; its
+    // partials are added by the next prep of the stream (pf_prep)
+    a.ksplit = 1;
+    if (epi == EPI_ADD && y == pf_x_ && i == 0 && j == nw && pf_pending_ == 0) {
+      if (cus_ == 0) {
+        int dev = 0;
+        UAII_HIP(hipGetDevice(&dev));
+        UAII_HIP(hipDeviceGetAttribute(&cus_, hipDeviceAttributeMultiprocessorCount, dev));
+      }
+      a.ksplit = pf_gemm_ksplit(a, cus_);
+      a.part = pf_part_;
+    }
     UAII_HIP(launch_pf_gemm(a, stream_));
+    if (a.ksplit > 1) pf_pending_ = a.ksplit;
     i = j;
   }
+  return Error::success();
+}
+
+Error DecoderProgram::pf_prep(float* x, int64_t K, int64_t m, const float* norm_w) {
+  PfAct act = pf_act_;
+  act.K = K;
+  const int pend = (x == pf_x_) ? pf_pending_ : 0;
+  UAII_HIP(launch_pf_prep(x, K, m, norm_w, spec_.rms_eps, act, stream_, pend ? pf_part_ : nullptr, pend));
+  if (pend) pf_pending_ = 0;
   return Error::success();
 }
 
@@ -367,11 +390,14 @@ Error DecoderProgram::prefill(int64_t n) {
   const size_t layer_kv = (size_t)d.kv_dim * (size_t)max_ctx_ * 2;
   const int64_t ldqkv = d.q_dim + 2 * d.kv_dim;
   prof_used_ = 0;
-  auto prep = [&](const float* x, int64_t K, int64_t m, const float* norm_w) -> Error {
-    PfAct act = pf_act_;
-    act.K = K;
-    return timed("pf_prep", 12.0 * (double)m * (double)K, 0.0,
-                 [&] { return launch_pf_prep(x, K, m, norm_w, d.rms_eps, act, s); });
+  auto prep = [&](float* x, int64_t K, int64_t m, const float* norm_w) -> Error {
+    Error err = Error::success();
+    Error launched = timed("pf_prep", 12.0 * (double)m * (double)K, 0.0, [&]() -> hipError_t {
+      err = pf_prep(x, K, m, norm_w);
+      return err.ok() ? hipSuccess : hipErrorInvalidValue;
+    });
+    if (!err.ok()) return err;
+    return launched;
   };
   // algorithmic work of one GEMM launch group: weights once, A (hi + lo), C
   auto gemm_cost = [&](const DeviceWeight* const* w, int nw, int64_t m, int64_t outs, double* bytes,
@@ -405,6 +431,7 @@ Error DecoderProgram::prefill(int64_t n) {
     const int64_t p = p0 + c0;
     UAII_TRY(timed("pf_embed", 4.0 * (double)m * (double)d.dim, 0.0,
                    [&] { return launch_embed_rows(tok_embd_.view, ids_ + p, m, pf_x_, s); }));
+    pf_pending_ = 0;  // a new chunk's stream: the last chunk's final partials are moot
     for (int64_t li = 0; li < d.n_layers; ++li) {
       const Layer& L = *layers_[(size_t)li];
       const LayerSpec& ls = d.layers[(size_t)li];

@@ -107,6 +107,7 @@ class DecoderProgram {
   Error ensure_prefill_buffers(int64_t chunk);
   Error pf_gemm(const DeviceWeight* w[3], const int64_t cols0[3], int nw, const DeviceWeight* w2,
                 int epi, int64_t m, float* y, int64_t ldy);
+  Error pf_prep(float* x, int64_t K, int64_t m, const float* norm_w);
   Error encode_step(bool want_logits);
   void free_dynamic();
 
@@ -156,6 +157,9 @@ class DecoderProgram {
   int64_t pf_chunk_ = 0, pf_kmax_ = 0;
   float *pf_x_ = nullptr, *pf_qkv_ = nullptr, *pf_q_ = nullptr, *pf_attn_ = nullptr,
         *pf_h_ = nullptr;
+  float* pf_part_ = nullptr;  // [4][chunk][dim]: K-split partials of a residual-add GEMM
+  int pf_pending_ = 0;        // splits in pf_part_ still to be added into pf_x_
+  int cus_ = 0;
   uaii_hip::PfAct pf_act_{};
   std::vector<void*> pf_allocs_;
 };
