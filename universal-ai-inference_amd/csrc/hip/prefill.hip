@@ -776,174 +776,257 @@ __global__ void __launch_bounds__(256) k_pf_qkv(PfQkvArgs a) {
 // ---- causal attention over the f16 cache ---------------------------------------------------
 
 constexpr int PA_TK = 64;  // keys per LDS tile
+// 16-query subtiles per wave. 2 halves the K/V staging per matrix-core op but
+// needs 430 registers at head_dim 128 (one wave per SIMD): measured 1.6x slower
+// than 1 on the 8B prefill.
+#ifndef UAII_PA_QW
+#define UAII_PA_QW 1
+#endif
+constexpr int PA_QW = UAII_PA_QW;
 
 // Block: 4 waves on kv head blockIdx.y / (G / GW); wave w takes q head
-// (w % GW) of the block's GW heads and query subtile w / GW (16 queries each).
+// (w % GW) of the block's GW heads and query subtiles PA_QW (w / GW) ..
+// PA_QW (w / GW) + PA_QW - 1 (16 queries each). K tiles and transposed V tiles
+// of 64 keys are double-buffered in LDS; each thread loads the next tile's K/V
+// pieces into registers while the current tile is computed.
 template <int HD>
-__global__ void __launch_bounds__(256) k_pf_attn(PfAttnArgs a) {
+__global__ void __launch_bounds__(256, 2) k_pf_attn(PfAttnArgs a) {
   constexpr int KP = HD + 8;        // K tile row (halfs)
   constexpr int VP = PA_TK + 8;     // V^T tile row (halfs)
   constexpr int NC = HD / 32;       // 32-wide hd chunks (S)
   constexpr int ND = HD / 16;       // 16-row hd subtiles (O)
-  __shared__ _Float16 ks[PA_TK * KP];
-  __shared__ _Float16 vt[HD * VP];
+  constexpr int KPIECES = PA_TK * (HD / 8) / 256;       // 16-byte K pieces per thread
+  constexpr int VPAIRS = PA_TK / 2 * (HD / 8) / 256;    // (2 keys x 8 dims) V pieces per thread
+  __shared__ _Float16 ks[2][PA_TK * KP];
+  __shared__ _Float16 vt[2][HD * VP];
 
   const int G = a.n_heads / a.n_kv;
   const int GW = G < 4 ? G : 4;
   const int QS = 4 / GW;
-  const int hb = blockIdx.y;                 // head block
+  const int hb = blockIdx.y;
   const int kvh = hb / (G / GW);
   const int hbase = kvh * G + (hb % (G / GW)) * GW;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63, col = lane & 15, g = lane >> 4;
   const bool active = wave < GW * QS;
   const int head = hbase + (wave % GW);
-  const int64_t q0 = (int64_t)blockIdx.x * (16 * QS);
-  const int64_t qrow = q0 + 16 * (wave / GW) + col;  // this lane's query (column)
-  const bool qvalid = active && qrow < a.M;
-  const int64_t qpos = a.p0 + qrow;
-  const int64_t qend = min((int64_t)a.M, q0 + 16 * QS);
+  const int64_t q0 = (int64_t)blockIdx.x * (16 * PA_QW * QS);
+  const int64_t qw0 = q0 + 16 * PA_QW * (wave / GW);   // this wave's first query
+  const int64_t qend = min((int64_t)a.M, q0 + 16 * PA_QW * QS);
   const int64_t nkeys = a.p0 + qend;  // keys the block needs (causal)
 
-  // q * scale * 2^e as f16 hi + lo, natural hd order: lane (query col, group g)
-  // holds hd 32c + 8g .. +7 of chunk c. The matrix cores flush f16 subnormals,
+  // q * scale * 2^e as f16 hi + lo per query subtile u: lane (query col, group g)
+  // holds hd 32c + 8g .. +7 of chunk c; the matrix cores flush f16 subnormals,
   // so each query row is scaled to put its largest element in [2^14, 2^15)
-  // (lo stays normal) and the scores are scaled back by 2^-e.
   const float scale = 1.0f / sqrtf((float)HD);
-  float qv[NC][8];
-  float qmax = 0.0f;
+  h8_t qhi[PA_QW][NC], qlo[PA_QW][NC];
+  float qrs[PA_QW];
+  bool qvalid[PA_QW];
+  int64_t qpos[PA_QW];
 #pragma unroll
-  for (int c = 0; c < NC; ++c) {
-    if (qvalid) {
-      const float4* qp = reinterpret_cast<const float4*>(a.q + qrow * a.ldq + (int64_t)head * HD + 32 * c + 8 * g);
-      const float4 x0 = qp[0], x1 = qp[1];
-      qv[c][0] = x0.x; qv[c][1] = x0.y; qv[c][2] = x0.z; qv[c][3] = x0.w;
-      qv[c][4] = x1.x; qv[c][5] = x1.y; qv[c][6] = x1.z; qv[c][7] = x1.w;
-    } else {
+  for (int u = 0; u < PA_QW; ++u) {
+    const int64_t qrow = qw0 + 16 * u + col;
+    qvalid[u] = active && qrow < a.M;
+    qpos[u] = a.p0 + qrow;
+    float qv[NC][8];
+    float qmax = 0.0f;
 #pragma unroll
-      for (int k = 0; k < 8; ++k) qv[c][k] = 0.0f;
+    for (int c = 0; c < NC; ++c) {
+      if (qvalid[u]) {
+        const float4* qp = reinterpret_cast<const float4*>(a.q + qrow * a.ldq + (int64_t)head * HD + 32 * c + 8 * g);
+        const float4 x0 = qp[0], x1 = qp[1];
+        qv[c][0] = x0.x; qv[c][1] = x0.y; qv[c][2] = x0.z; qv[c][3] = x0.w;
+        qv[c][4] = x1.x; qv[c][5] = x1.y; qv[c][6] = x1.z; qv[c][7] = x1.w;
+      } else {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) qv[c][k] = 0.0f;
+      }
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        qv[c][k] = qv[c][k] * scale;
+        qmax = fmaxf(qmax, fabsf(qv[c][k]));
+      }
     }
+    qmax = fmaxf(qmax, __shfl_xor(qmax, 16, 64));
+    qmax = fmaxf(qmax, __shfl_xor(qmax, 32, 64));
+    int qe = 0;
+    if (qmax > 0.0f) qe = min(100, max(-100, 15 - ((int)((__float_as_uint(qmax) >> 23) & 0xff) - 126)));
+    const float qs = pow2f_i(qe);
+    qrs[u] = pow2f_i(-qe);
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      qv[c][k] = qv[c][k] * scale;
-      qmax = fmaxf(qmax, fabsf(qv[c][k]));
-    }
-  }
-  qmax = fmaxf(qmax, __shfl_xor(qmax, 16, 64));
-  qmax = fmaxf(qmax, __shfl_xor(qmax, 32, 64));
-  int qe = 0;
-  if (qmax > 0.0f) qe = min(100, max(-100, 15 - ((int)((__float_as_uint(qmax) >> 23) & 0xff) - 126)));
-  const float qs = pow2f_i(qe), qrs = pow2f_i(-qe);
-  h8_t qhi[NC], qlo[NC];
+    for (int c = 0; c < NC; ++c) {
 #pragma unroll
-  for (int c = 0; c < NC; ++c) {
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const float s = qv[c][k] * qs;
-      const _Float16 h = (_Float16)s;
-      qhi[c][k] = h;
-      qlo[c][k] = (_Float16)(s - (float)h);
+      for (int k = 0; k < 8; ++k) {
+        const float v = qv[c][k] * qs;
+        const _Float16 h = (_Float16)v;
+        qhi[u][c][k] = h;
+        qlo[u][c][k] = (_Float16)(v - (float)h);
+      }
     }
   }
 
-  f4_t o[ND];
+  f4_t o[PA_QW][ND];
+  float mrun[PA_QW], lrun[PA_QW];
 #pragma unroll
-  for (int d = 0; d < ND; ++d) o[d] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
-  float mrun = -INFINITY, lrun = 0.0f;
+  for (int u = 0; u < PA_QW; ++u) {
+    mrun[u] = -INFINITY;
+    lrun[u] = 0.0f;
+#pragma unroll
+    for (int d = 0; d < ND; ++d) o[u][d] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  }
 
   const __half* kbase = reinterpret_cast<const __half*>(a.kcache) + (int64_t)kvh * a.max_seq * HD;
   const __half* vbase = reinterpret_cast<const __half*>(a.vcache) + (int64_t)kvh * a.max_seq * HD;
 
-  for (int64_t kt = 0; kt < nkeys; kt += PA_TK) {
-    // stage K rows and V transposed (keys past nkeys read as zeros)
-    __syncthreads();
-    for (int c = threadIdx.x; c < PA_TK * (HD / 8); c += 256) {
+  // tile staging: K pieces (key, 8 dims) and V pairs (keys 2k, 2k + 1, 8 dims);
+  // keys past nkeys read as zeros
+  uint4 kreg[KPIECES], vreg[VPAIRS][2];
+  auto load_tile = [&](int64_t kt) __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < KPIECES; ++u) {
+      const int c = threadIdx.x + 256 * u;
       const int key = c / (HD / 8), p = c % (HD / 8);
-      uint4 kv = make_uint4(0, 0, 0, 0), vv = make_uint4(0, 0, 0, 0);
+      kreg[u] = make_uint4(0, 0, 0, 0);
       if (kt + key < nkeys) {
-        kv = *reinterpret_cast<const uint4*>(kbase + (kt + key) * HD + 8 * p);
-        vv = *reinterpret_cast<const uint4*>(vbase + (kt + key) * HD + 8 * p);
+        const uint4 v = *reinterpret_cast<const uint4*>(kbase + (kt + key) * HD + 8 * p);
+        kreg[u].x = v.x; kreg[u].y = v.y; kreg[u].z = v.z; kreg[u].w = v.w;
       }
-      *reinterpret_cast<uint4*>(ks + key * KP + 8 * p) = kv;
-      const _Float16* ve = reinterpret_cast<const _Float16*>(&vv);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) vt[(8 * p + e) * VP + key] = ve[e];
     }
-    __syncthreads();
-    if (!active) continue;
+#pragma unroll
+    for (int u = 0; u < VPAIRS; ++u) {
+      const int c = threadIdx.x + 256 * u;
+      const int kp = c / (HD / 8), p = c % (HD / 8);
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        vreg[u][e] = make_uint4(0, 0, 0, 0);
+        if (kt + 2 * kp + e < nkeys) {
+          const uint4 v = *reinterpret_cast<const uint4*>(vbase + (kt + 2 * kp + e) * HD + 8 * p);
+          vreg[u][e].x = v.x; vreg[u][e].y = v.y; vreg[u][e].z = v.z; vreg[u][e].w = v.w;
+        }
+      }
+    }
+  };
+  auto store_tile = [&](int buf) __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < KPIECES; ++u) {
+      const int c = threadIdx.x + 256 * u;
+      const int key = c / (HD / 8), p = c % (HD / 8);
+      *reinterpret_cast<uint4*>(&ks[buf][key * KP + 8 * p]) = kreg[u];
+    }
+#pragma unroll
+    for (int u = 0; u < VPAIRS; ++u) {
+      const int c = threadIdx.x + 256 * u;
+      const int kp = c / (HD / 8), p = c % (HD / 8);
+      const uint32_t w0[4] = {vreg[u][0].x, vreg[u][0].y, vreg[u][0].z, vreg[u][0].w};
+      const uint32_t w1[4] = {vreg[u][1].x, vreg[u][1].y, vreg[u][1].z, vreg[u][1].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        // dims 8p + 2e and 8p + 2e + 1 of keys 2kp and 2kp + 1, as key pairs
+        const uint32_t lo = (w0[e] & 0xffffu) | (w1[e] << 16);
+        const uint32_t hi = (w0[e] >> 16) | (w1[e] & 0xffff0000u);
+        *reinterpret_cast<uint32_t*>(&vt[buf][(8 * p + 2 * e) * VP + 2 * kp]) = lo;
+        *reinterpret_cast<uint32_t*>(&vt[buf][(8 * p + 2 * e + 1) * VP + 2 * kp]) = hi;
+      }
+    }
+  };
+  auto lds_barrier = []() __attribute__((always_inline)) {
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+  };
 
-    // S^T for 4 key subtiles: lane holds keys kt + 16s + 4g + r of query col
-    f4_t sc[4];
+  auto compute = [&](int64_t kt, int buf) __attribute__((always_inline)) {
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      f4_t acc = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int u = 0; u < PA_QW; ++u) {
+      // S^T for 4 key subtiles: lane holds keys kt + 16s + 4g + r of query col
+      f4_t sc[4];
 #pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        const h8_t kf = *reinterpret_cast<const h8_t*>(ks + (16 * s + col) * KP + 32 * c + 8 * g);
-        acc = mfma32(kf, qhi[c], acc);
-        acc = mfma32(kf, qlo[c], acc);
+      for (int s4 = 0; s4 < 4; ++s4) {
+        f4_t acc = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          const h8_t kf = *reinterpret_cast<const h8_t*>(&ks[buf][(16 * s4 + col) * KP + 32 * c + 8 * g]);
+          acc = mfma32(kf, qhi[u][c], acc);
+          acc = mfma32(kf, qlo[u][c], acc);
+        }
+        sc[s4] = acc * qrs[u];
       }
-      sc[s] = acc * qrs;
+      float tmax = -INFINITY;
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int64_t key = kt + 16 * s4 + 4 * g + r;
+          if (!qvalid[u] || key > qpos[u]) sc[s4][r] = -INFINITY;
+          tmax = fmaxf(tmax, sc[s4][r]);
+        }
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+      const float mnew = fmaxf(mrun[u], tmax);
+      const float alpha = (mrun[u] == -INFINITY) ? 0.0f : expf(mrun[u] - mnew);
+      float psum = 0.0f;
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float p = (sc[s4][r] == -INFINITY) ? 0.0f : expf(sc[s4][r] - mnew);
+          sc[s4][r] = p;
+          psum += p;
+        }
+      psum += __shfl_xor(psum, 16, 64);
+      psum += __shfl_xor(psum, 32, 64);
+      lrun[u] = lrun[u] * alpha + psum;
+      mrun[u] = mnew;
+#pragma unroll
+      for (int d = 0; d < ND; ++d) o[u][d] *= alpha;
+      // O^T += V^T . (2^14 P)^T over two 32-key chunks (p <= 1, so 2^14 p keeps
+      // hi and lo normal); lane's keys: 32c + 4g + r (r < 4), 32c + 16 + 4g + (r - 4)
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        h8_t phi, plo;
+#pragma unroll
+        for (int r = 0; r < 8; ++r) {
+          const float p = sc[2 * c + (r >> 2)][r & 3] * 16384.0f;
+          const _Float16 h = (_Float16)p;
+          phi[r] = h;
+          plo[r] = (_Float16)(p - (float)h);
+        }
+#pragma unroll
+        for (int d = 0; d < ND; ++d) {
+          const _Float16* vr = &vt[buf][(16 * d + col) * VP + 32 * c + 4 * g];
+          const h4_t v0 = *reinterpret_cast<const h4_t*>(vr);
+          const h4_t v1 = *reinterpret_cast<const h4_t*>(vr + 16);
+          const h8_t vf = h8_t{v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+          o[u][d] = mfma32(vf, phi, o[u][d]);
+          o[u][d] = mfma32(vf, plo, o[u][d]);
+        }
+      }
     }
-    float tmax = -INFINITY;
-#pragma unroll
-    for (int s = 0; s < 4; ++s)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int64_t key = kt + 16 * s + 4 * g + r;
-        if (!qvalid || key > qpos) sc[s][r] = -INFINITY;
-        tmax = fmaxf(tmax, sc[s][r]);
-      }
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-    const float mnew = fmaxf(mrun, tmax);
-    const float alpha = (mrun == -INFINITY) ? 0.0f : expf(mrun - mnew);
-    float psum = 0.0f;
-#pragma unroll
-    for (int s = 0; s < 4; ++s)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float p = (sc[s][r] == -INFINITY) ? 0.0f : expf(sc[s][r] - mnew);
-        sc[s][r] = p;
-        psum += p;
-      }
-    psum += __shfl_xor(psum, 16, 64);
-    psum += __shfl_xor(psum, 32, 64);
-    lrun = lrun * alpha + psum;
-    mrun = mnew;
-#pragma unroll
-    for (int d = 0; d < ND; ++d) o[d] *= alpha;
+  };
 
-    // O^T += V^T . (2^14 P)^T over two 32-key chunks (p <= 1, so 2^14 p keeps
-    // hi and lo normal); lane's keys: 32c + 4g + r (r < 4) and 32c + 16 + 4g + (r - 4)
-#pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      h8_t phi, plo;
-#pragma unroll
-      for (int r = 0; r < 8; ++r) {
-        const float p = sc[2 * c + (r >> 2)][r & 3] * 16384.0f;
-        const _Float16 h = (_Float16)p;
-        phi[r] = h;
-        plo[r] = (_Float16)(p - (float)h);
-      }
-#pragma unroll
-      for (int d = 0; d < ND; ++d) {
-        const _Float16* vr = vt + (16 * d + col) * VP + 32 * c + 4 * g;
-        const h4_t v0 = *reinterpret_cast<const h4_t*>(vr);
-        const h4_t v1 = *reinterpret_cast<const h4_t*>(vr + 16);
-        const h8_t vf = h8_t{v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
-        o[d] = mfma32(vf, phi, o[d]);
-        o[d] = mfma32(vf, plo, o[d]);
-      }
-    }
+  load_tile(0);
+  store_tile(0);
+  lds_barrier();
+  int buf = 0;
+  for (int64_t kt = 0; kt < nkeys; kt += PA_TK) {
+    const bool more = kt + PA_TK < nkeys;  // block-uniform
+    if (more) load_tile(kt + PA_TK);
+    if (active) compute(kt, buf);
+    if (more) store_tile(buf ^ 1);
+    lds_barrier();
+    buf ^= 1;
   }
-  if (!qvalid) return;
-  const float inv = (1.0f / 16384.0f) / lrun;
-  float* out = a.out + qrow * a.ldo + (int64_t)head * HD;
+
 #pragma unroll
-  for (int d = 0; d < ND; ++d) {
-    float4 v = make_float4(o[d][0] * inv, o[d][1] * inv, o[d][2] * inv, o[d][3] * inv);
-    *reinterpret_cast<float4*>(out + 16 * d + 4 * g) = v;
+  for (int u = 0; u < PA_QW; ++u) {
+    if (!qvalid[u]) continue;
+    const int64_t qrow = qw0 + 16 * u + col;
+    const float inv = (1.0f / 16384.0f) / lrun[u];
+    float* out = a.out + qrow * a.ldo + (int64_t)head * HD;
+#pragma unroll
+    for (int d = 0; d < ND; ++d) {
+      const float4 v = make_float4(o[u][d][0] * inv, o[u][d][1] * inv, o[u][d][2] * inv, o[u][d][3] * inv);
+      *reinterpret_cast<float4*>(out + 16 * d + 4 * g) = v;
+    }
   }
 }
 
@@ -1102,7 +1185,8 @@ hipError_t launch_pf_attn(const PfAttnArgs& a, hipStream_t s) {
   const int G = a.n_heads / a.n_kv;
   const int GW = G < 4 ? G : 4;
   const int QS = 4 / GW;
-  dim3 grid((unsigned)((a.M + 16 * QS - 1) / (16 * QS)), (unsigned)(a.n_kv * (G / GW)));
+  const int QT = 16 * PA_QW * QS;  // queries per block
+  dim3 grid((unsigned)((a.M + QT - 1) / QT), (unsigned)(a.n_kv * (G / GW)));
   if (a.hd == 64) UAII_LAUNCH(k_pf_attn<64>, grid, dim3(256), 0, s, a);
   else UAII_LAUNCH(k_pf_attn<128>, grid, dim3(256), 0, s, a);
   return hipGetLastError();
