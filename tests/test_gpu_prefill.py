@@ -197,6 +197,15 @@ PREFILL_CFGS = {
     "gelu_bias": synth.ModelConfig(n_layers=2, dim=512, n_heads=8, n_kv_heads=4, ffn=1024,
                                    vocab=1500, ctx_len=512, type_default=uaii_amd.Q8_0, gelu=True,
                                    qkv_bias=True, seed=44),
+    # MoE: 4 experts top-2 over Q4_K experts; every expert's token list a gather
+    "moe_k": synth.ModelConfig(n_layers=2, dim=512, n_heads=8, n_kv_heads=2, ffn=512,
+                               vocab=1200, ctx_len=512, type_default=uaii_amd.Q4_K, n_experts=4,
+                               top_k=2, router_std=1.0 / 22, seed=45),
+    # MoE 8 experts top-2 beside a shared expert, Q4_0
+    "moe_shared": synth.ModelConfig(n_layers=2, dim=256, n_heads=4, n_kv_heads=4, ffn=320,
+                                    vocab=700, ctx_len=512, type_default=uaii_amd.Q4_0,
+                                    n_experts=8, top_k=2, router_std=1.0 / 16, shared_ffn=192,
+                                    seed=46),
 }
 
 
@@ -220,11 +229,32 @@ def test_generate_with_prefill(name):
         assert maxrel(r2[li], want["resid2"][li]) < 2e-3
 
 
-def test_prefill_chunks_and_offsets(monkeypatch):
+@pytest.mark.parametrize("name", ["moe_k", "moe_shared"])
+def test_moe_prefill_long_prompt(name):
+    """A 400-token prompt: each expert's gathered rows span several row tiles
+    of the grouped expert GEMMs, the last one partial."""
+    cfg = PREFILL_CFGS[name]
+    path = synth.cached_model(cfg)
+    prompt = np.random.default_rng(cfg.seed + 7).integers(0, cfg.vocab, 400).astype(np.int64)
+    with uaii_amd.Session(path, kv_f16=True) as s:
+        assert s.prefill_supported()
+        ids = s.generate(prompt, 8)
+        taps = {k: s.get(k) for k in ("logits", "normed")}
+        r2 = [s.get(f"blk.{li}.resid2") for li in range(cfg.n_layers)]
+    want_ids, want = oracle.Model(path).generate(prompt, 8, kv_f16=True)
+    assert np.array_equal(ids, want_ids)
+    assert maxrel(taps["logits"], want["logits"]) < 2e-3
+    assert maxrel(taps["normed"], want["normed"]) < 2e-3
+    for li in range(cfg.n_layers):
+        assert maxrel(r2[li], want["resid2"][li]) < 2e-3
+
+
+@pytest.mark.parametrize("name", ["gqa_q4_0", "moe_shared"])
+def test_prefill_chunks_and_offsets(monkeypatch, name):
     """A 150-token prompt in 32-token chunks (queries at p0 > 0 over earlier
-    chunks' keys), after 5 tokens stepped one at a time, equals the token-by-token
-    run: same ids, logits within 2e-3."""
-    cfg = PREFILL_CFGS["gqa_q4_0"]
+    chunks' keys; MoE token lists rebuilt per chunk), after 5 tokens stepped one
+    at a time, equals the token-by-token run: same ids, logits within 2e-3."""
+    cfg = PREFILL_CFGS[name]
     path = synth.cached_model(cfg)
     prompt = np.random.default_rng(3).integers(0, cfg.vocab, 150).astype(np.int64)
     monkeypatch.setenv("UAII_PREFILL", "0")

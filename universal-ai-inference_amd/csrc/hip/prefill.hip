@@ -335,6 +335,36 @@ constexpr int PF_ROW = UAII_PF_ROW;  // halfs per staged 32-k row (32 + 8 pad)
 template <int MT>
 constexpr int pf_lds_halfs() { return 2 * 2 * 2 * 16 * MT * PF_ROW; }
 
+// Output rows [m0, mend) of this grid row and the first weight row of its
+// expert (0 without grouping).
+struct PfRange {
+  int64_t m0, mend, mfirst, wrow0;
+};
+__device__ inline PfRange pf_range(const PfGemmArgs& a, int bm, int64_t seg_rows) {
+  PfRange r;
+  if (a.gtab) {
+    const int32_t* e = a.gtab + 3 * blockIdx.y;
+    r.wrow0 = (int64_t)e[0] * seg_rows;
+    r.m0 = e[1];
+    r.mend = e[2];
+    r.mfirst = r.m0;
+  } else {
+    r.wrow0 = 0;
+    r.m0 = (int64_t)blockIdx.y * bm;
+    r.mend = a.M;
+    r.mfirst = 0;
+  }
+  return r;
+}
+// Activation row of output row t. Rows past the range read its first row (the
+// map's first entry without grouping); their results are dropped. Unmapped,
+// ungrouped rows below mpad are read as they are.
+__device__ inline int64_t pf_arow(const PfGemmArgs& a, const PfRange& r, int64_t t) {
+  if (!a.arow && !a.gtab) return t;
+  const int64_t tc = t < r.mend ? t : r.mfirst;
+  return a.arow ? (int64_t)a.arow[tc] : tc;
+}
+
 // Block tile: 16 MT activation rows x PF_WAVES * 16 NT weight rows (for SwiGLU
 // each wave's NT subtiles are NT / 2 gate and NT / 2 up subtiles of the same
 // rows). K advances one stage (64) at a time; activations are staged in LDS
@@ -356,7 +386,8 @@ __global__ void __launch_bounds__(PF_WAVES * 64, 2) k_pf_gemm(PfGemmArgs a) {
   const int lane = threadIdx.x & 63;
   const int col = lane & 15, g = lane >> 4;
   const int64_t n0 = ((int64_t)(tile - seg.tile0) * PF_WAVES + wave) * (16 * NQ);
-  const int64_t m0 = (int64_t)blockIdx.y * BM;
+  const PfRange mr = pf_range(a, BM, seg.rows);
+  const int64_t m0 = mr.m0;
   const int64_t K = a.K, nst = K / 64 / a.ksplit;  // stages of this block's K range
   const int64_t sbase = (int64_t)blockIdx.z * nst;  // its first stage
 
@@ -366,7 +397,7 @@ __global__ void __launch_bounds__(PF_WAVES * 64, 2) k_pf_gemm(PfGemmArgs a) {
   for (int j = 0; j < NT; ++j) {
     const int64_t r = n0 + 16 * (j % NQ) + col;
     const DevWeight& w = (EPI == EPI_SWIGLU && j >= NQ) ? seg.w2 : seg.w;
-    prow[j] = pf_row<FMT>(w, r < seg.rows ? r : seg.rows - 1, g);
+    prow[j] = pf_row<FMT>(w, mr.wrow0 + (r < seg.rows ? r : seg.rows - 1), g);
   }
 
   f4_t acc[MT][NT];
@@ -375,6 +406,7 @@ __global__ void __launch_bounds__(PF_WAVES * 64, 2) k_pf_gemm(PfGemmArgs a) {
 #pragma unroll
     for (int j = 0; j < NT; ++j) acc[i][j] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
+  auto arow_of = [&](int64_t t) __attribute__((always_inline)) -> int64_t { return pf_arow(a, mr, t); };
   // activation stage: BM rows x 2 blocks x (hi, lo) x 4 pieces of 16 B
   constexpr int PIECES = BM * 2 * 2 * 4;
   constexpr int PPT = PIECES / (PF_WAVES * 64);
@@ -389,7 +421,7 @@ __global__ void __launch_bounds__(PF_WAVES * 64, 2) k_pf_gemm(PfGemmArgs a) {
     for (int u = 0; u < PPT; ++u) {
       const int c = threadIdx.x + u * PF_WAVES * 64;
       const int q = c & 3, r = (c >> 2) % BM, kbh = (c >> 2) / BM;  // kbh = block * 2 + hi/lo
-      const __half* src = ((kbh & 1) ? a.alo : a.ahi) + (m0 + r) * K + (2 * (sbase + st) + (kbh >> 1)) * 32 + q * 8;
+      const __half* src = ((kbh & 1) ? a.alo : a.ahi) + arow_of(m0 + r) * K + (2 * (sbase + st) + (kbh >> 1)) * 32 + q * 8;
       // element-wise: a whole-struct copy here is turned into a memcpy into a
       // stack array (scratch memory)
       const uint4 v = *reinterpret_cast<const uint4*>(src);
@@ -432,8 +464,14 @@ __global__ void __launch_bounds__(PF_WAVES * 64, 2) k_pf_gemm(PfGemmArgs a) {
         const _Float16* pl = ph + BM * PF_ROW;
         f4_t sxv = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
         if constexpr (OFF) {
-          const float4 s4 = *reinterpret_cast<const float4*>(a.sx + (2 * st + s) * a.mpad + m0 + 16 * i + 4 * g);
-          sxv = f4_t{s4.x, s4.y, s4.z, s4.w};
+          if (a.arow || a.gtab) {
+            const float* sxr = a.sx + (2 * st + s) * a.sx_ld;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) sxv[r] = sxr[arow_of(m0 + 16 * i + 4 * g + r)];
+          } else {
+            const float4 s4 = *reinterpret_cast<const float4*>(a.sx + (2 * st + s) * a.mpad + m0 + 16 * i + 4 * g);
+            sxv = f4_t{s4.x, s4.y, s4.z, s4.w};
+          }
         }
         if constexpr (KS == 32) {
           const h8_t ahi = *reinterpret_cast<const h8_t*>(ph + 8 * g);
@@ -494,8 +532,8 @@ __global__ void __launch_bounds__(PF_WAVES * 64, 2) k_pf_gemm(PfGemmArgs a) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int64_t t = m0 + 16 * i + 4 * g + r;
-      if (t >= a.M) continue;
-      const float rs = a.rs[t];
+      if (t >= mr.mend) continue;
+      const float rs = a.rs[pf_arow(a, mr, t)];
       float* yrow = a.y + t * a.ldy + seg.col0;
 #pragma unroll
       for (int j = 0; j < NQ; ++j) {
@@ -575,13 +613,14 @@ __global__ void __launch_bounds__(PF_WAVES * 64, 2) k_pf_gemm_dma(PfGemmArgs a) 
   const int lane = threadIdx.x & 63;
   const int col = lane & 15, g = lane >> 4;
   const int64_t n0 = ((int64_t)(tile - seg.tile0) * PF_WAVES + wave) * (16 * NQ);
-  const int64_t m0 = (int64_t)blockIdx.y * BM;
+  const PfRange mr = pf_range(a, BM, seg.rows);
+  const int64_t m0 = mr.m0;
   const int64_t K = a.K, nst = K / 64 / a.ksplit;  // stages of this block's K range
   const int64_t sbase = (int64_t)blockIdx.z * nst;  // its first stage
 
   // this lane's DMA sources. Activations: wave w copies (block w >> 1, hi/lo
   // w & 1); instruction u covers rows 16u .. 16u + 15, lane -> (row, slot).
-  const int arow = lane >> 2, aslot = lane & 3;
+  const int arow_l = lane >> 2, aslot = lane & 3;
   const __half* asrc = (wave & 1) ? a.alo : a.ahi;
   const int ablk = wave >> 1;
   // Weights: the wave's 32 rows (subtile j = row / 16; SwiGLU: j = 1 is the up
@@ -595,7 +634,7 @@ __global__ void __launch_bounds__(PF_WAVES * 64, 2) k_pf_gemm_dma(PfGemmArgs a) 
     const int j = rl >> 4;
     const DevWeight& w = (EPI == EPI_SWIGLU && j >= NQ) ? seg.w2 : seg.w;
     int64_t r = n0 + 16 * (j % NQ) + (rl & 15);
-    r = r < seg.rows ? r : seg.rows - 1;
+    r = mr.wrow0 + (r < seg.rows ? r : seg.rows - 1);
     wsrc_q[u] = w.a + r * w.a_row + 16 * ((lane + 64 * u) % wl_per_row);
   }
   const uint8_t* wsrc_s;
@@ -604,7 +643,7 @@ __global__ void __launch_bounds__(PF_WAVES * 64, 2) k_pf_gemm_dma(PfGemmArgs a) 
     const int j = rl >> 4;
     const DevWeight& w = (EPI == EPI_SWIGLU && j >= NQ) ? seg.w2 : seg.w;
     int64_t r = n0 + 16 * (j % NQ) + (rl & 15);
-    r = r < seg.rows ? r : seg.rows - 1;
+    r = mr.wrow0 + (r < seg.rows ? r : seg.rows - 1);
     wsrc_s = w.b + r * w.b_row;
   }
   (void)wrow_q;
@@ -616,9 +655,10 @@ __global__ void __launch_bounds__(PF_WAVES * 64, 2) k_pf_gemm_dma(PfGemmArgs a) 
     // activations
 #pragma unroll
     for (int u = 0; u < MT; ++u) {
-      const int r = 16 * u + arow;
+      const int r = 16 * u + arow_l;
       const int piece = aslot ^ pf_swz(r);
-      const __half* src = asrc + (m0 + r) * K + (2 * st + ablk) * 32 + piece * 8;
+      const int64_t ar = pf_arow(a, mr, m0 + r);
+      const __half* src = asrc + ar * K + (2 * st + ablk) * 32 + piece * 8;
       dma16(src, lds_addr(base + ((ablk * 2 + (wave & 1)) * BM + 16 * u) * 64));
     }
     // weight payload and scales of this wave's rows
@@ -700,8 +740,8 @@ __global__ void __launch_bounds__(PF_WAVES * 64, 2) k_pf_gemm_dma(PfGemmArgs a) 
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int64_t t = m0 + 16 * i + 4 * g + r;
-      if (t >= a.M) continue;
-      const float rs = a.rs[t];
+      if (t >= mr.mend) continue;
+      const float rs = a.rs[pf_arow(a, mr, t)];
       float* yrow = a.y + t * a.ldy + seg.col0;
 #pragma unroll
       for (int j = 0; j < NQ; ++j) {
@@ -1030,6 +1070,168 @@ __global__ void __launch_bounds__(256, 2) k_pf_attn(PfAttnArgs a) {
   }
 }
 
+// ---- MoE over prompt rows ----------------------------------------------------------------
+
+// One block per token: RMSNorm of x[t] (the k_pf_prep arithmetic), router
+// logits against F32 / F16 rows, then the routing of k_moe_route on wave 0:
+// softmax (exp(l - max) * 1/sum), k rounds of the largest remaining probability
+// (ties: the lower expert), weights renormalised over the chosen k
+// (transformer.cpp:446-481, :565-580).
+template <int RT>
+__global__ void __launch_bounds__(256) k_pf_moe_route(const float* __restrict__ x, int64_t K,
+                                                      const float* __restrict__ norm_w, float eps,
+                                                      DevWeight router, int E, int k,
+                                                      int32_t* __restrict__ ids, float* __restrict__ wout) {
+  extern __shared__ float row[];
+  __shared__ float red[4];
+  __shared__ float logit[256];
+  const int64_t t = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nv = (int)(K / 4);
+  float4* r4 = reinterpret_cast<float4*>(row);
+  const float4* x4 = reinterpret_cast<const float4*>(x + t * K);
+  float ss = 0.0f;
+  for (int i = tid; i < nv; i += 256) {
+    const float4 v = x4[i];
+    r4[i] = v;
+    ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+  }
+  ss = wave_sum(ss);
+  if (lane == 0) red[wave] = ss;
+  __syncthreads();
+  const float tot = red[0] + red[1] + red[2] + red[3];
+  const float inv = 1.0f / sqrtf(tot / (float)K + eps);
+  const float4* w4 = reinterpret_cast<const float4*>(norm_w);
+  for (int i = tid; i < nv; i += 256) {
+    float4 v = r4[i];
+    const float4 w = w4[i];
+    v.x = fmul_rn(fmul_rn(v.x, inv), w.x);
+    v.y = fmul_rn(fmul_rn(v.y, inv), w.y);
+    v.z = fmul_rn(fmul_rn(v.z, inv), w.z);
+    v.w = fmul_rn(fmul_rn(v.w, inv), w.w);
+    r4[i] = v;
+  }
+  __syncthreads();
+  // logits: wave w takes experts w, w + 4, ...
+  for (int e = wave; e < E; e += 4) {
+    float acc = 0.0f;
+    if constexpr (RT == T_F32) {
+      const float* wr = reinterpret_cast<const float*>(router.a + (int64_t)e * router.a_row);
+      for (int64_t i = lane; i < K; i += 64) acc += row[i] * wr[i];
+    } else {
+      const __half* wr = reinterpret_cast<const __half*>(router.a + (int64_t)e * router.a_row);
+      for (int64_t i = lane; i < K; i += 64) acc += row[i] * __half2float(wr[i]);
+    }
+    acc = wave_sum(acc);
+    if (lane == 0) logit[e] = acc;
+  }
+  __syncthreads();
+  if (wave != 0) return;
+  float p[4];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int e = lane + 64 * j;
+    p[j] = e < E ? logit[e] : -INFINITY;
+    mx = fmaxf(mx, p[j]);
+  }
+  mx = wave_max(mx);
+  float sum = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int e = lane + 64 * j;
+    p[j] = e < E ? expf(p[j] - mx) : 0.0f;
+    sum += p[j];
+  }
+  sum = wave_sum(sum);
+  const float isum = sum > 0.0f ? 1.0f / sum : 0.0f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) p[j] = (lane + 64 * j < E) ? p[j] * isum : -1.0f;
+  float mass = 0.0f;
+  float wsel[8];
+  int32_t esel[8];
+  for (int q = 0; q < k; ++q) {
+    float bv = -1.0f;
+    int be = 0x7fffffff;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (p[j] > bv) { bv = p[j]; be = lane + 64 * j; }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const float ov = __shfl_xor(bv, o, 64);
+      const int oe = __shfl_xor(be, o, 64);
+      if (ov > bv || (ov == bv && oe < be)) { bv = ov; be = oe; }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (lane + 64 * j == be) p[j] = -1.0f;  // taken
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (j == q) { wsel[j] = bv; esel[j] = (be >= 0 && be < E) ? be : 0; }
+    mass += bv;
+  }
+  if (!(mass > 0.0f)) mass = 1.0f;
+  if (lane == 0) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if (j < k) {
+        ids[t * k + j] = esel[j];
+        wout[t * k + j] = wsel[j] / mass;
+      }
+    }
+  }
+}
+
+// One block. Thread e counts and lists expert e's (token, slot) entries in
+// token order; thread 0 forms the prefix sums between the two passes.
+__global__ void __launch_bounds__(256) k_pf_moe_lists(const int32_t* __restrict__ ids, int64_t M, int k,
+                                                      int E, int32_t* counts, int32_t* offsets,
+                                                      int32_t* list, int32_t* inv) {
+  __shared__ int32_t cnt[256], off[256];
+  const int e = threadIdx.x;
+  const int64_t n = M * k;
+  if (e < E) {
+    int32_t c = 0;
+    for (int64_t i = 0; i < n; ++i) c += (ids[i] == e) ? 1 : 0;
+    cnt[e] = c;
+  }
+  __syncthreads();
+  if (e == 0) {
+    int32_t acc = 0;
+    for (int j = 0; j < E; ++j) {
+      off[j] = acc;
+      acc += cnt[j];
+    }
+  }
+  __syncthreads();
+  if (e < E) {
+    counts[e] = cnt[e];
+    offsets[e] = off[e];
+    int32_t pos = off[e];
+    for (int64_t i = 0; i < n; ++i) {
+      if (ids[i] == e) {
+        list[pos] = (int32_t)(i / k);
+        inv[i] = pos;
+        ++pos;
+      }
+    }
+  }
+}
+
+// One block per token: x[t] += w y in slot order (each slot one expert).
+__global__ void __launch_bounds__(256) k_pf_moe_combine(float* __restrict__ x, int64_t D, int k,
+                                                        const float* __restrict__ w,
+                                                        const int32_t* __restrict__ inv,
+                                                        const float* __restrict__ y) {
+  const int64_t t = blockIdx.x;
+  float* xr = x + t * D;
+  for (int64_t i = threadIdx.x; i < D; i += 256) {
+    float v = xr[i];
+    for (int q = 0; q < k; ++q) v = v + w[t * k + q] * y[(int64_t)inv[t * k + q] * D + i];
+    xr[i] = v;
+  }
+}
+
 }  // namespace
 
 // ---- launchers ------------------------------------------------------------------------------
@@ -1065,7 +1267,8 @@ hipError_t pf_gemm_go(PfGemmArgs a, hipStream_t s) {
     a.seg[k].tile0 = ntiles;
     ntiles += (int)((a.seg[k].rows + per_tile - 1) / per_tile);
   }
-  dim3 grid((unsigned)ntiles, (unsigned)(a.mpad / (16 * MT)), (unsigned)a.ksplit);
+  if (a.gtab && a.gbm != 16 * MT) return hipErrorInvalidValue;
+  dim3 grid((unsigned)ntiles, (unsigned)(a.gtab ? a.ntab : a.mpad / (16 * MT)), (unsigned)a.ksplit);
   UAII_LAUNCH((k_pf_gemm<FMT, EPI, MT, NT>), grid, dim3(PF_WAVES * 64), 0, s, a);
   return hipGetLastError();
 }
@@ -1078,7 +1281,8 @@ hipError_t pf_gemm_dma_go(PfGemmArgs a, hipStream_t s) {
     a.seg[k].tile0 = ntiles;
     ntiles += (int)((a.seg[k].rows + per_tile - 1) / per_tile);
   }
-  dim3 grid((unsigned)ntiles, (unsigned)(a.mpad / (16 * MT)), (unsigned)a.ksplit);
+  if (a.gtab && a.gbm != 16 * MT) return hipErrorInvalidValue;
+  dim3 grid((unsigned)ntiles, (unsigned)(a.gtab ? a.ntab : a.mpad / (16 * MT)), (unsigned)a.ksplit);
   UAII_LAUNCH((k_pf_gemm_dma<FMT, EPI, MT>), grid, dim3(PF_WAVES * 64), 0, s, a);
   return hipGetLastError();
 }
@@ -1095,6 +1299,13 @@ hipError_t pf_gemm_tile(const PfGemmArgs& a, hipStream_t s) {
   const int64_t mid = (rows / 128) * (a.mpad / 64);
   constexpr bool wide = FMT == T_Q4_0 || FMT == T_Q8_0;
   const int want = UAII_PF_TILE;
+  if (a.gtab) {  // expert groups: the tile height their table was built for
+    if constexpr (wide) {
+      if (UAII_PF_DMA) return pf_gemm_dma_go<FMT, EPI, 4>(a, s);
+      return pf_gemm_go<FMT, EPI, 4, 2>(a, s);
+    }
+    return pf_gemm_go<FMT, EPI, 2, 2>(a, s);
+  }
   if constexpr (wide) {
     if (UAII_PF_DMA) {
       if (want == 2 || (want == 0 && mid >= 256)) return pf_gemm_dma_go<FMT, EPI, 4>(a, s);
@@ -1136,10 +1347,24 @@ int pf_gemm_ksplit(const PfGemmArgs& a, int cus) {
   return ks;
 }
 
+int pf_gemm_group_rows(int type) { return (type == T_Q4_0 || type == T_Q8_0) ? 64 : 32; }
+
 hipError_t launch_pf_gemm(PfGemmArgs a, hipStream_t s) {
   if (a.ksplit < 1) a.ksplit = 1;
+  if (a.sx_ld <= 0) a.sx_ld = a.mpad;
+  if (!a.arow && !a.gtab && a.sx_ld != a.mpad) return hipErrorInvalidValue;
   if (a.nseg < 1 || a.nseg > 3 || a.M <= 0 || a.M > a.mpad || a.mpad % 64 || a.K % 64)
     return hipErrorInvalidValue;
+  if (a.gtab) {
+    // every table entry lies inside [0, M) and names an expert below ngroups (the
+    // caller builds it on the host); here the launch itself is checked
+    if (a.ntab < 1 || a.ngroups < 1 || a.ksplit != 1 || a.nseg != 1 ||
+        a.gbm != pf_gemm_group_rows(a.seg[0].w.type) || (!a.arow && a.sx_ld < a.mpad))
+      return hipErrorInvalidValue;
+    const PfSeg& sg = a.seg[0];
+    if (sg.rows * a.ngroups > sg.w.rows || (a.epi == EPI_SWIGLU && sg.rows * a.ngroups > sg.w2.rows))
+      return hipErrorInvalidValue;
+  }
   const int type = a.seg[0].w.type;
   if (!pf_supported(type)) return hipErrorInvalidValue;
   const int64_t kq = (type == T_Q4_K || type == T_Q6_K) ? 256 : 64;  // K granule of a block's range
@@ -1189,6 +1414,50 @@ hipError_t launch_pf_attn(const PfAttnArgs& a, hipStream_t s) {
   dim3 grid((unsigned)((a.M + QT - 1) / QT), (unsigned)(a.n_kv * (G / GW)));
   if (a.hd == 64) UAII_LAUNCH(k_pf_attn<64>, grid, dim3(256), 0, s, a);
   else UAII_LAUNCH(k_pf_attn<128>, grid, dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+bool pf_router_supported(int type) { return type == T_F32 || type == T_F16; }
+
+hipError_t launch_pf_moe_route(const float* x, int64_t M, int64_t K, const float* norm_w, float eps,
+                               const DevWeight& router, int E, int k, int32_t* ids, float* w,
+                               hipStream_t s) {
+  if (M <= 0 || K % 4 || !norm_w || E < 1 || E > 256 || k < 1 || k > 8 || k > E ||
+      router.rows < E || router.cols != K || !pf_router_supported(router.type))
+    return hipErrorInvalidValue;
+  const size_t lds = (size_t)K * 4;
+  if ((int64_t)lds > lds_limit()) return hipErrorInvalidValue;
+  if (router.type == T_F32) {
+    if (lds > 64 * 1024) {
+      const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_pf_moe_route<T_F32>),
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+      if (e != hipSuccess) return e;
+    }
+    UAII_LAUNCH(k_pf_moe_route<T_F32>, dim3((unsigned)M), dim3(256), lds, s, x, K, norm_w, eps, router, E,
+                k, ids, w);
+  } else {
+    if (lds > 64 * 1024) {
+      const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_pf_moe_route<T_F16>),
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+      if (e != hipSuccess) return e;
+    }
+    UAII_LAUNCH(k_pf_moe_route<T_F16>, dim3((unsigned)M), dim3(256), lds, s, x, K, norm_w, eps, router, E,
+                k, ids, w);
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_pf_moe_lists(const int32_t* ids, int64_t M, int k, int E, int32_t* counts,
+                               int32_t* offsets, int32_t* list, int32_t* inv, hipStream_t s) {
+  if (M <= 0 || k < 1 || k > 8 || E < 1 || E > 256) return hipErrorInvalidValue;
+  UAII_LAUNCH(k_pf_moe_lists, dim3(1), dim3(256), 0, s, ids, M, k, E, counts, offsets, list, inv);
+  return hipGetLastError();
+}
+
+hipError_t launch_pf_moe_combine(float* x, int64_t M, int64_t D, int k, const float* w,
+                                 const int32_t* inv, const float* y, hipStream_t s) {
+  if (M <= 0 || D <= 0 || k < 1 || k > 8) return hipErrorInvalidValue;
+  UAII_LAUNCH(k_pf_moe_combine, dim3((unsigned)M), dim3(256), 0, s, x, D, k, w, inv, y);
   return hipGetLastError();
 }
 

@@ -168,6 +168,16 @@ struct PfGemmArgs {
   // next launch_pf_prep of y adds the partials (z in order) into y
   int ksplit;
   float* part;
+  // optional activation-row map: output row t reads activation row arow[t]
+  // (MoE experts gather their tokens); rows are those of ahi/alo/sx/rs
+  const int32_t* arow;
+  int64_t sx_ld;  // row stride of sx (the activations' padded row count); 0: mpad
+  // optional expert grouping (MoE): grid row y computes output rows
+  // [gtab[3y + 1], gtab[3y + 2]) against expert gtab[3y] of the weight stacks,
+  // whose rows e * seg.rows .. (e + 1) * seg.rows - 1 are that expert's;
+  // at most gbm rows per entry (pf_gemm_group_rows of the format)
+  const int32_t* gtab;
+  int ntab, ngroups, gbm;
 };
 
 struct PfQkvArgs {
@@ -196,6 +206,22 @@ struct PfAttnArgs {
   int64_t ldo;
 };
 
+// MoE prompt rows (transformer.cpp:446-612 applied to M tokens):
+// router logits of RMSNorm(x[t]) . Wr^T (Wr F32 or F16, [E][K]), softmax, top-k
+// (ties: lower expert), weights renormalised: ids[t][k], w[t][k].
+hipError_t launch_pf_moe_route(const float* x, int64_t M, int64_t K, const float* norm_w, float eps,
+                               const DevWeight& router, int E, int k, int32_t* ids, float* w,
+                               hipStream_t s);
+// Per-expert token lists from ids[M][k]: counts[E], offsets[E] (prefix sums),
+// list[offsets[e] + j] = token of the j-th (token, slot) routed to e (token
+// order), inv[t * k + slot] = its packed row.
+hipError_t launch_pf_moe_lists(const int32_t* ids, int64_t M, int k, int E, int32_t* counts,
+                               int32_t* offsets, int32_t* list, int32_t* inv, hipStream_t s);
+// x[t] += w[t][0] y[inv[t][0]], then + w[t][1] y[inv[t][1]], ... (slot order).
+hipError_t launch_pf_moe_combine(float* x, int64_t M, int64_t D, int k, const float* w,
+                                 const int32_t* inv, const float* y, hipStream_t s);
+bool pf_router_supported(int type);
+
 bool pf_supported(int type);
 bool pf_attn_supported(int head_dim, int n_heads, int n_kv);
 int64_t pf_mpad(int64_t m);
@@ -207,6 +233,8 @@ hipError_t launch_pf_prep(float* x, int64_t ldx, int64_t M, const float* norm_w,
 hipError_t launch_pf_gemm(PfGemmArgs a, hipStream_t s);
 // K split launch_pf_gemm can take for `a` (EPI_ADD only; 1 = none) on `cus` CUs.
 int pf_gemm_ksplit(const PfGemmArgs& a, int cus);
+// rows per entry of an expert-grouped GEMM's table for this block format
+int pf_gemm_group_rows(int type);
 hipError_t launch_pf_qkv(const PfQkvArgs& a, hipStream_t s);
 hipError_t launch_pf_attn(const PfAttnArgs& a, hipStream_t s);
 

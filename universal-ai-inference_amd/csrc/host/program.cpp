@@ -270,8 +270,7 @@ Error DecoderProgram::build(const DecoderSpec& spec, const ProgramOptions& opts)
   if (want > 0) UAII_TRY(ensure_capacity(want));
 
   // the matrix-core prompt path: block formats it decodes, dense FFNs, f16 cache
-  pf_ok_ = opts_.kv_f16 && !moe_ &&
-           pf_attn_supported((int)d.head_dim, (int)d.n_heads, (int)d.n_kv_heads) &&
+  pf_ok_ = opts_.kv_f16 && pf_attn_supported((int)d.head_dim, (int)d.n_heads, (int)d.n_kv_heads) &&
            d.dim % 64 == 0 && d.q_dim % 64 == 0;
   for (int64_t li = 0; pf_ok_ && li < d.n_layers; ++li) {
     const Layer& L = *layers_[(size_t)li];
@@ -279,7 +278,15 @@ Error DecoderProgram::build(const DecoderSpec& spec, const ProgramOptions& opts)
     std::vector<const DeviceWeight*> ws = {&L.wq, &L.wk, &L.wv, &L.wo};
     if (ls.ffn == LayerSpec::kSwiGLU) ws.insert(ws.end(), {&L.gate, &L.up, &L.down});
     if (ls.ffn == LayerSpec::kGelu) ws.insert(ws.end(), {&L.up, &L.down});
-    if ((ls.ffn == LayerSpec::kSwiGLU || ls.ffn == LayerSpec::kGelu) && ls.inter % 64) pf_ok_ = false;
+    if (ls.ffn == LayerSpec::kMoE) {
+      ws.insert(ws.end(), {&L.gate_exps, &L.up_exps, &L.down_exps});
+      if (L.shared) {
+        ws.insert(ws.end(), {&L.gate_sh, &L.up_sh, &L.down_sh});
+        if (L.inter_sh % 64) pf_ok_ = false;
+      }
+      if (!pf_router_supported(L.gate_inp.view.type)) pf_ok_ = false;
+    }
+    if (ls.ffn != LayerSpec::kNone && ls.inter % 64) pf_ok_ = false;
     for (const DeviceWeight* w : ws) pf_ok_ = pf_ok_ && pf_supported(w->view.type);
   }
   if (const char* env = std::getenv("UAII_PREFILL")) {
@@ -294,10 +301,12 @@ Error DecoderProgram::ensure_prefill_buffers(int64_t chunk) {
   for (void* p : pf_allocs_) (void)hipFree(p);
   pf_allocs_.clear();
   const DecoderSpec& d = spec_;
-  int64_t inter = 1;
+  int64_t inter = 1, inter_sh = 0;
   for (const LayerSpec& ls : d.layers) inter = std::max(inter, ls.inter);
-  const int64_t mpad = pf_mpad(chunk);
-  const int64_t kmax = std::max({d.dim, d.q_dim, inter});
+  for (const auto& L : layers_) inter_sh = std::max(inter_sh, L->inter_sh);
+  const int64_t topk = moe_ ? std::min<int64_t>(d.top_k, d.n_experts) : 1;
+  const int64_t mpad = pf_mpad(chunk * topk);  // MoE: the experts' hidden rows
+  const int64_t kmax = std::max({d.dim, d.q_dim, inter, inter_sh});
   auto alloc = [&](size_t bytes, void** p) -> Error {
     UAII_HIP(hipMalloc(p, std::max<size_t>(bytes, 256)));
     pf_allocs_.push_back(*p);
@@ -310,11 +319,29 @@ Error DecoderProgram::ensure_prefill_buffers(int64_t chunk) {
   UAII_TRY(alloc(4 * C * (size_t)d.q_dim, (void**)&pf_attn_));
   UAII_TRY(alloc(4 * C * (size_t)inter, (void**)&pf_h_));
   UAII_TRY(alloc(4 * 4 * C * (size_t)d.dim, (void**)&pf_part_));
+  if (moe_) {
+    const size_t CK = C * (size_t)topk;
+    UAII_TRY(alloc(4 * CK, (void**)&pf_moe_ids_));
+    UAII_TRY(alloc(4 * CK, (void**)&pf_moe_w_));
+    UAII_TRY(alloc(4 * 2 * (size_t)d.n_experts, (void**)&pf_moe_cnt_));  // counts | offsets
+    UAII_TRY(alloc(4 * CK, (void**)&pf_moe_list_));
+    UAII_TRY(alloc(4 * CK, (void**)&pf_moe_inv_));
+    UAII_TRY(alloc(4 * CK * (size_t)d.dim, (void**)&pf_moe_y_));
+    // two grouped-GEMM row tables, each at most CK / 32 + E entries of 3
+    pf_tab_cap_ = 2 * 3 * ((int64_t)CK / 32 + d.n_experts + 1);
+    UAII_TRY(alloc(4 * (size_t)pf_tab_cap_, (void**)&pf_moe_tab_));
+    // routed experts' hidden rows [chunk * k][inter]; the shared expert's [chunk][inter_sh]
+    (void)hipFree(pf_h_);
+    pf_allocs_.erase(std::find(pf_allocs_.begin(), pf_allocs_.end(), (void*)pf_h_));
+    UAII_TRY(alloc(4 * CK * (size_t)inter, (void**)&pf_h_));
+    if (inter_sh > 0) UAII_TRY(alloc(4 * C * (size_t)inter_sh, (void**)&pf_hsh_));
+  }
   UAII_TRY(alloc(2 * (size_t)mpad * (size_t)kmax, (void**)&pf_act_.hi));
   UAII_TRY(alloc(2 * (size_t)mpad * (size_t)kmax, (void**)&pf_act_.lo));
   UAII_TRY(alloc(4 * (size_t)(kmax / 32) * (size_t)mpad, (void**)&pf_act_.sx));
   UAII_TRY(alloc(4 * (size_t)mpad, (void**)&pf_act_.rs));
   pf_act_.mpad = mpad;
+  pf_act_rows_ = mpad;
   pf_chunk_ = chunk;
   pf_kmax_ = kmax;
   return Error::success();
@@ -365,11 +392,121 @@ Error DecoderProgram::pf_gemm(const DeviceWeight* w[3], const int64_t cols0[3], 
 }
 
 Error DecoderProgram::pf_prep(float* x, int64_t K, int64_t m, const float* norm_w) {
+  if (pf_mpad(m) > pf_act_rows_ || K > pf_kmax_)
+    return Error::make(ErrorCode::Internal, "prefill activation rows exceed their buffer");
+  pf_act_.mpad = pf_mpad(m);
   PfAct act = pf_act_;
   act.K = K;
   const int pend = (x == pf_x_) ? pf_pending_ : 0;
   UAII_HIP(launch_pf_prep(x, K, m, norm_w, spec_.rms_eps, act, stream_, pend ? pf_part_ : nullptr, pend));
   if (pend) pf_pending_ = 0;
+  return Error::success();
+}
+
+// MoE FFN over the chunk's rows (transformer.cpp:446-612, shared expert
+// gguf.cpp:1107-1128): router + top-k per token, per-expert token lists, one
+// gate/up GEMM per expert over its gathered tokens, one prep of all routed
+// hidden rows, one down GEMM per expert, then x += w y in slot order and the
+// shared expert's down as a residual add.
+template <class Prep, class Gemm>
+Error DecoderProgram::prefill_moe(const Layer& L, const LayerSpec& ls, int64_t m, Prep&& prep, Gemm&& gemm) {
+  const DecoderSpec& d = spec_;
+  hipStream_t s = stream_;
+  const int E = (int)d.n_experts;
+  const int k = (int)std::min<int64_t>(d.top_k, d.n_experts);
+  const int64_t I = ls.inter;
+  UAII_TRY(prep(pf_x_, d.dim, m, L.ffn_norm));
+  UAII_TRY(timed("pf_moe_route", 4.0 * (double)(m * d.dim + E * d.dim), 2.0 * (double)(m * E * d.dim), [&] {
+    return launch_pf_moe_route(pf_x_, m, d.dim, L.ffn_norm, d.rms_eps, L.gate_inp.view, E, k, pf_moe_ids_,
+                               pf_moe_w_, s);
+  }));
+  UAII_TRY(timed("pf_moe_route", 0.0, 0.0, [&] {
+    return launch_pf_moe_lists(pf_moe_ids_, m, k, E, pf_moe_cnt_, pf_moe_cnt_ + E, pf_moe_list_, pf_moe_inv_, s);
+  }));
+  std::vector<int32_t> co((size_t)(2 * E));
+  UAII_HIP(hipMemcpyAsync(co.data(), pf_moe_cnt_, 8 * (size_t)E, hipMemcpyDeviceToHost, s));
+  UAII_HIP(hipStreamSynchronize(s));
+  // per-expert row tables of the two grouped launches: {expert, row0, row_end}
+  // per grid row, rows in the packed (expert-major) order of the lists
+  const int bm_gu = pf_gemm_group_rows(L.gate_exps.view.type);
+  const int bm_dn = pf_gemm_group_rows(L.down_exps.view.type);
+  std::vector<int32_t>& tab = pf_tab_host_;
+  tab.clear();
+  int n_used = 0;
+  auto add_table = [&](int bm) {
+    const int first = (int)(tab.size() / 3);
+    for (int e = 0; e < E; ++e) {
+      const int32_t c = co[(size_t)e], off = co[(size_t)(E + e)];
+      for (int32_t r = 0; r < c; r += bm) {
+        tab.push_back(e);
+        tab.push_back(off + r);
+        tab.push_back(off + c);
+      }
+    }
+    return first;
+  };
+  for (int e = 0; e < E; ++e) n_used += co[(size_t)e] > 0 ? 1 : 0;
+  const int t_gu = add_table(bm_gu);
+  const int n_gu = (int)(tab.size() / 3) - t_gu;
+  const int t_dn = add_table(bm_dn);
+  const int n_dn = (int)(tab.size() / 3) - t_dn;
+  if ((int64_t)tab.size() > pf_tab_cap_)
+    return Error::make(ErrorCode::Internal, "MoE prefill row table exceeds its buffer");
+  UAII_HIP(hipMemcpyAsync(pf_moe_tab_, tab.data(), 4 * tab.size(), hipMemcpyHostToDevice, s));
+  auto grouped = [&](int64_t K, int epi, int bm, int t0, int nt) {
+    PfGemmArgs g{};
+    g.nseg = 1;
+    g.epi = epi;
+    g.M = m * k;
+    g.K = K;
+    g.mpad = pf_mpad(m * k);
+    g.ahi = pf_act_.hi;
+    g.alo = pf_act_.lo;
+    g.sx = pf_act_.sx;
+    g.rs = pf_act_.rs;
+    g.sx_ld = pf_act_.mpad;
+    g.gtab = pf_moe_tab_ + 3 * t0;
+    g.ntab = nt;
+    g.ngroups = E;
+    g.gbm = bm;
+    return g;
+  };
+  {
+    // gathered token rows x gate / up of their experts -> routed hidden rows
+    PfGemmArgs g = grouped(d.dim, EPI_SWIGLU, bm_gu, t_gu, n_gu);
+    g.arow = pf_moe_list_;
+    g.y = pf_h_;
+    g.ldy = I;
+    g.seg[0].w = L.gate_exps.view;
+    g.seg[0].w2 = L.up_exps.view;
+    g.seg[0].rows = I;
+    const double bytes = 2.0 * (double)L.gate_exps.bytes * n_used / E;
+    UAII_TRY(timed("pf_moe_gate_up", bytes, 4.0 * (double)(m * k * I * d.dim), [&] { return launch_pf_gemm(g, s); }));
+  }
+  const int64_t c00[3] = {0, 0, 0};
+  if (L.shared) {  // the shared expert reads the same normalised rows
+    const DeviceWeight* wg[3] = {&L.gate_sh, nullptr, nullptr};
+    UAII_TRY(gemm("pf_gemm_shared_gate_up", wg, c00, 1, &L.up_sh, EPI_SWIGLU, m, pf_hsh_, L.inter_sh));
+  }
+  // the routed tokens' hidden rows, packed by expert
+  UAII_TRY(prep(pf_h_, I, m * k, nullptr));
+  {
+    PfGemmArgs g = grouped(I, EPI_STORE, bm_dn, t_dn, n_dn);
+    g.y = pf_moe_y_;
+    g.ldy = d.dim;
+    g.seg[0].w = L.down_exps.view;
+    g.seg[0].rows = d.dim;
+    const double bytes = (double)L.down_exps.bytes * n_used / E;
+    UAII_TRY(timed("pf_moe_down", bytes, 2.0 * (double)(m * k * I * d.dim), [&] { return launch_pf_gemm(g, s); }));
+  }
+  UAII_TRY(timed("pf_moe_combine", 4.0 * (double)(m * d.dim * (k + 2)), 0.0, [&] {
+    return launch_pf_moe_combine(pf_x_, m, d.dim, k, pf_moe_w_, pf_moe_inv_, pf_moe_y_, s);
+  }));
+  if (L.shared) {
+    UAII_TRY(prep(pf_hsh_, L.inter_sh, m, nullptr));
+    const DeviceWeight* wd[3] = {&L.down_sh, nullptr, nullptr};
+    UAII_TRY(gemm("pf_gemm_shared_down", wd, c00, 1, nullptr, EPI_ADD, m, pf_x_, d.dim));
+  }
   return Error::success();
 }
 
@@ -497,6 +634,8 @@ Error DecoderProgram::prefill(int64_t n) {
         UAII_TRY(prep(pf_h_, ls.inter, m, nullptr));
         const DeviceWeight* wd[3] = {&L.down, nullptr, nullptr};
         UAII_TRY(gemm("pf_gemm_down", wd, c00, 1, nullptr, EPI_ADD, m, pf_x_, d.dim));
+      } else if (ls.ffn == LayerSpec::kMoE) {
+        UAII_TRY(prefill_moe(L, ls, m, prep, gemm));
       }
     }
   }

@@ -108,6 +108,8 @@ class DecoderProgram {
   Error pf_gemm(const DeviceWeight* w[3], const int64_t cols0[3], int nw, const DeviceWeight* w2,
                 int epi, int64_t m, float* y, int64_t ldy);
   Error pf_prep(float* x, int64_t K, int64_t m, const float* norm_w);
+  template <class Prep, class Gemm>
+  Error prefill_moe(const Layer& L, const LayerSpec& ls, int64_t m, Prep&& prep, Gemm&& gemm);
   Error encode_step(bool want_logits);
   void free_dynamic();
 
@@ -158,9 +160,16 @@ class DecoderProgram {
   float *pf_x_ = nullptr, *pf_qkv_ = nullptr, *pf_q_ = nullptr, *pf_attn_ = nullptr,
         *pf_h_ = nullptr;
   float* pf_part_ = nullptr;  // [4][chunk][dim]: K-split partials of a residual-add GEMM
+  // MoE prompt rows: routing [chunk][k], per-expert lists, expert outputs
+  int32_t *pf_moe_ids_ = nullptr, *pf_moe_cnt_ = nullptr, *pf_moe_list_ = nullptr,
+          *pf_moe_inv_ = nullptr, *pf_moe_tab_ = nullptr;
+  int64_t pf_tab_cap_ = 0;             // int32 entries of pf_moe_tab_
+  std::vector<int32_t> pf_tab_host_;   // the grouped GEMMs' row tables before upload
+  float *pf_moe_w_ = nullptr, *pf_moe_y_ = nullptr, *pf_hsh_ = nullptr;
   int pf_pending_ = 0;        // splits in pf_part_ still to be added into pf_x_
   int cus_ = 0;
-  uaii_hip::PfAct pf_act_{};
+  uaii_hip::PfAct pf_act_{};  // mpad: rows of the last prep (the GEMMs' tiling)
+  int64_t pf_act_rows_ = 0;   // row capacity of pf_act_
   std::vector<void*> pf_allocs_;
 };
 
