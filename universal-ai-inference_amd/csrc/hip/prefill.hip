@@ -326,6 +326,9 @@ __device__ inline void pf_decode(const PfRaw<FMT>& r, int64_t st, int s, int g, 
 #define UAII_PF_TILE 0  // wave tile: 0 chosen per launch, 2 64x32, 3 32x32
 #endif
 constexpr int PF_WAVES = 4;   // waves per block, side by side along N
+#ifndef UAII_PF_KTILE
+#define UAII_PF_KTILE 1  // Q4_K takes the 64 x 32 wave tile too (0: always 32 x 32)
+#endif
 #ifndef UAII_PF_ROW
 #define UAII_PF_ROW 40
 #endif
@@ -416,20 +419,38 @@ __global__ void __launch_bounds__(PF_WAVES * 64, 2) k_pf_gemm(PfGemmArgs a) {
   // compile-time constants
   uint4 stg[PPT];
   PfRaw<FMT> raw[3][NT];
+  // this thread's activation pieces at stage 0 of the block's K range (a stage
+  // adds 64 halfs); row offsets and the row map are read once, not per stage
+  const __half* abase[PPT];
+#pragma unroll
+  for (int u = 0; u < PPT; ++u) {
+    const int c = threadIdx.x + u * PF_WAVES * 64;
+    const int q = c & 3, r = (c >> 2) % BM, kbh = (c >> 2) / BM;  // kbh = block * 2 + hi/lo
+    abase[u] = ((kbh & 1) ? a.alo : a.ahi) + arow_of(m0 + r) * K + (2 * sbase + (kbh >> 1)) * 32 + q * 8;
+  }
+  // Q4_K: the activation block sums of the stage's two blocks, staged beside the
+  // activations (threads < 2 BM, one value each) instead of read from memory
+  // inside the compute, where the wait for them would also wait for every load
+  // in flight
+  __shared__ float sxs[OFF ? 2 * 2 * BM : 1];
+  float stg_sx = 0.0f;
+  const float* sxbase = nullptr;
+  if constexpr (OFF) {
+    const int t = threadIdx.x < 2 * BM ? threadIdx.x : 0;
+    sxbase = a.sx + (2 * sbase + t / BM) * a.sx_ld + arow_of(m0 + t % BM);
+  }
   auto load_stage = [&](uint4 (&dst)[PPT], int64_t st) __attribute__((always_inline)) {
 #pragma unroll
     for (int u = 0; u < PPT; ++u) {
-      const int c = threadIdx.x + u * PF_WAVES * 64;
-      const int q = c & 3, r = (c >> 2) % BM, kbh = (c >> 2) / BM;  // kbh = block * 2 + hi/lo
-      const __half* src = ((kbh & 1) ? a.alo : a.ahi) + arow_of(m0 + r) * K + (2 * (sbase + st) + (kbh >> 1)) * 32 + q * 8;
       // element-wise: a whole-struct copy here is turned into a memcpy into a
       // stack array (scratch memory)
-      const uint4 v = *reinterpret_cast<const uint4*>(src);
+      const uint4 v = *reinterpret_cast<const uint4*>(abase[u] + st * 64);
       dst[u].x = v.x;
       dst[u].y = v.y;
       dst[u].z = v.z;
       dst[u].w = v.w;
     }
+    if constexpr (OFF) stg_sx = sxbase[st * 2 * a.sx_ld];
   };
   auto store_stage = [&](const uint4 (&src)[PPT], int buf) __attribute__((always_inline)) {
 #pragma unroll
@@ -438,6 +459,9 @@ __global__ void __launch_bounds__(PF_WAVES * 64, 2) k_pf_gemm(PfGemmArgs a) {
       const int q = c & 3, r = (c >> 2) % BM, kbh = (c >> 2) / BM;
       _Float16* dst = lds + (((buf * 4) + kbh) * BM + r) * PF_ROW + q * 8;
       *reinterpret_cast<uint4*>(dst) = src[u];
+    }
+    if constexpr (OFF) {
+      if (threadIdx.x < 2 * BM) sxs[buf * 2 * BM + threadIdx.x] = stg_sx;
     }
   };
   auto load_w = [&](PfRaw<FMT>(&dst)[NT], int64_t st) __attribute__((always_inline)) {
@@ -464,14 +488,8 @@ __global__ void __launch_bounds__(PF_WAVES * 64, 2) k_pf_gemm(PfGemmArgs a) {
         const _Float16* pl = ph + BM * PF_ROW;
         f4_t sxv = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
         if constexpr (OFF) {
-          if (a.arow || a.gtab) {
-            const float* sxr = a.sx + (2 * st + s) * a.sx_ld;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) sxv[r] = sxr[arow_of(m0 + 16 * i + 4 * g + r)];
-          } else {
-            const float4 s4 = *reinterpret_cast<const float4*>(a.sx + (2 * st + s) * a.mpad + m0 + 16 * i + 4 * g);
-            sxv = f4_t{s4.x, s4.y, s4.z, s4.w};
-          }
+          const float4 s4 = *reinterpret_cast<const float4*>(sxs + (buf * 2 + s) * BM + 16 * i + 4 * g);
+          sxv = f4_t{s4.x, s4.y, s4.z, s4.w};
         }
         if constexpr (KS == 32) {
           const h8_t ahi = *reinterpret_cast<const h8_t*>(ph + 8 * g);
@@ -1288,9 +1306,10 @@ hipError_t pf_gemm_dma_go(PfGemmArgs a, hipStream_t s) {
 }
 
 // Wave tile per launch: 64 x 32 (measured best at M = 512 for the 8B shapes,
-// ahead of 64 x 64 and 32 x 32) unless that leaves the grid under one block per
-// CU, or the format's weight ring does not fit the registers of two waves per
-// SIMD at that tile (Q4_K, Q6_K); then 32 x 32.
+// ahead of 64 x 64 and 32 x 32; for Q4_K 232 against 196 TFLOP/s on the 1B
+// gate/up) unless that leaves the grid under one block per CU, or the format's
+// weight ring does not fit the registers of two waves per SIMD at that tile
+// (Q6_K); then 32 x 32.
 template <int FMT, int EPI>
 hipError_t pf_gemm_tile(const PfGemmArgs& a, hipStream_t s) {
   int64_t rows = 0;
@@ -1312,6 +1331,9 @@ hipError_t pf_gemm_tile(const PfGemmArgs& a, hipStream_t s) {
       return pf_gemm_dma_go<FMT, EPI, 2>(a, s);
     }
     if (want == 2 || (want == 0 && mid >= 256)) return pf_gemm_go<FMT, EPI, 4, 2>(a, s);
+  }
+  if constexpr (FMT == T_Q4_K) {
+    if (UAII_PF_KTILE && (want == 2 || (want == 0 && mid >= 256))) return pf_gemm_go<FMT, EPI, 4, 2>(a, s);
   }
   return pf_gemm_go<FMT, EPI, 2, 2>(a, s);
 }
@@ -1337,8 +1359,9 @@ int pf_gemm_ksplit(const PfGemmArgs& a, int cus) {
   int64_t rows = 0;
   for (int k = 0; k < a.nseg; ++k) rows += a.seg[k].rows;
   const bool wide = type == T_Q4_0 || type == T_Q8_0;
+  const bool tall = wide || (type == T_Q4_K && UAII_PF_KTILE);  // formats with the 64 x 32 wave tile
   const int64_t mid = (rows / 128) * (a.mpad / 64);
-  const bool big_tile = wide && (UAII_PF_TILE == 2 || (UAII_PF_TILE == 0 && mid >= 256));
+  const bool big_tile = tall && (UAII_PF_TILE == 2 || (UAII_PF_TILE == 0 && mid >= 256));
   const int64_t tiles = (rows + PF_WAVES * 32 - 1) / (PF_WAVES * 32);
   const int64_t blocks = tiles * (a.mpad / (big_tile ? 64 : 32));
   const int64_t kq = wide ? 64 : 256;
