@@ -1323,6 +1323,9 @@ hipError_t pf_gemm_tile(const PfGemmArgs& a, hipStream_t s) {
       if (UAII_PF_DMA) return pf_gemm_dma_go<FMT, EPI, 4>(a, s);
       return pf_gemm_go<FMT, EPI, 4, 2>(a, s);
     }
+    if constexpr (FMT == T_Q4_K) {
+      if (UAII_PF_KTILE) return pf_gemm_go<FMT, EPI, 4, 2>(a, s);
+    }
     return pf_gemm_go<FMT, EPI, 2, 2>(a, s);
   }
   if constexpr (wide) {
@@ -1370,7 +1373,9 @@ int pf_gemm_ksplit(const PfGemmArgs& a, int cus) {
   return ks;
 }
 
-int pf_gemm_group_rows(int type) { return (type == T_Q4_0 || type == T_Q8_0) ? 64 : 32; }
+int pf_gemm_group_rows(int type) {
+  return (type == T_Q4_0 || type == T_Q8_0 || (type == T_Q4_K && UAII_PF_KTILE)) ? 64 : 32;
+}
 
 hipError_t launch_pf_gemm(PfGemmArgs a, hipStream_t s) {
   if (a.ksplit < 1) a.ksplit = 1;
