@@ -559,7 +559,8 @@ __global__ void __launch_bounds__(PF_WAVES * 64, 2) k_pf_gemm(PfGemmArgs a) {
         if (n >= seg.rows) continue;
         const float v = acc[i][j][r] * rs;
         if constexpr (EPI == EPI_STORE) {
-          yrow[n] = v;
+          if (a.ksplit > 1) a.part[((int64_t)blockIdx.z * a.M + t) * a.ldy + seg.col0 + n] = v;
+          else yrow[n] = v;
         } else if constexpr (EPI == EPI_ADD) {
           if (a.ksplit > 1) a.part[((int64_t)blockIdx.z * a.M + t) * a.ldy + seg.col0 + n] = v;
           else yrow[n] = yrow[n] + v;
@@ -767,7 +768,8 @@ __global__ void __launch_bounds__(PF_WAVES * 64, 2) k_pf_gemm_dma(PfGemmArgs a) 
         if (n >= seg.rows) continue;
         const float v = acc[i][j][r] * rs;
         if constexpr (EPI == EPI_STORE) {
-          yrow[n] = v;
+          if (a.ksplit > 1) a.part[((int64_t)blockIdx.z * a.M + t) * a.ldy + seg.col0 + n] = v;
+          else yrow[n] = v;
         } else if constexpr (EPI == EPI_ADD) {
           if (a.ksplit > 1) a.part[((int64_t)blockIdx.z * a.M + t) * a.ldy + seg.col0 + n] = v;
           else yrow[n] = yrow[n] + v;
@@ -792,6 +794,14 @@ __global__ void __launch_bounds__(256) k_pf_qkv(PfQkvArgs a) {
   const int64_t t = blockIdx.x;
   const int pos = a.p0 + (int)t;
   const float* row = a.qkv + t * a.ldq;
+  // value x of this row: the GEMM's output, or the sum of its K-split partials
+  // in split order
+  auto val = [&](int x) -> float {
+    if (a.nsplit <= 1) return row[x];
+    float v = a.part[t * a.ldq + x];
+    for (int z = 1; z < a.nsplit; ++z) v = v + a.part[((int64_t)z * a.M + t) * a.ldq + x];
+    return v;
+  };
   const int hd = a.head_dim, half = hd / 2;
   const int npair = (a.q_dim + a.kv_dim) / 2;
   for (int u = threadIdx.x; u < npair; u += blockDim.x) {
@@ -801,7 +811,7 @@ __global__ void __launch_bounds__(256) k_pf_qkv(PfQkvArgs a) {
     const int r0 = head * hd + (a.rope_mode == 2 ? p : 2 * p);
     const int r1 = r0 + (a.rope_mode == 2 ? half : 1);
     const int base = isq ? 0 : a.q_dim;
-    float v0 = row[base + r0], v1 = row[base + r1];
+    float v0 = val(base + r0), v1 = val(base + r1);
     const float* bias = isq ? a.bq : a.bk;
     if (bias) { v0 = v0 + bias[r0]; v1 = v1 + bias[r1]; }
     const float2 cs = a.rope[(int64_t)pos * half + p];
@@ -823,7 +833,7 @@ __global__ void __launch_bounds__(256) k_pf_qkv(PfQkvArgs a) {
     }
   }
   for (int r = threadIdx.x; r < a.kv_dim; r += blockDim.x) {
-    float v = row[a.q_dim + a.kv_dim + r];
+    float v = val(a.q_dim + a.kv_dim + r);
     if (a.bv) v = v + a.bv[r];
     const int64_t o = ((int64_t)(r / hd) * a.max_seq + pos) * hd + (r % hd);
     if (a.kv_f16) reinterpret_cast<__half*>(a.vcache)[o] = __float2half(v);
@@ -1353,10 +1363,11 @@ hipError_t pf_gemm_epi(const PfGemmArgs& a, hipStream_t s) {
 }
 }  // namespace
 
-// K split for a residual-add launch: enough blocks for two per CU (each block's
-// K range a whole number of stages and, for the K-quants, super-blocks).
+// K split for a residual-add or plain-store launch: enough blocks for two per CU
+// (each block's K range a whole number of stages and, for the K-quants,
+// super-blocks).
 int pf_gemm_ksplit(const PfGemmArgs& a, int cus) {
-  if (a.epi != EPI_ADD || a.nseg < 1) return 1;
+  if ((a.epi != EPI_ADD && a.epi != EPI_STORE) || a.nseg < 1) return 1;
   const int type = a.seg[0].w.type;
   if (!pf_supported(type)) return 1;
   int64_t rows = 0;
@@ -1397,7 +1408,7 @@ hipError_t launch_pf_gemm(PfGemmArgs a, hipStream_t s) {
   if (!pf_supported(type)) return hipErrorInvalidValue;
   const int64_t kq = (type == T_Q4_K || type == T_Q6_K) ? 256 : 64;  // K granule of a block's range
   if (a.K % (kq * a.ksplit)) return hipErrorInvalidValue;
-  if (a.ksplit > 1 && (a.epi != EPI_ADD || !a.part)) return hipErrorInvalidValue;
+  if (a.ksplit > 1 && ((a.epi != EPI_ADD && a.epi != EPI_STORE) || !a.part)) return hipErrorInvalidValue;
   for (int k = 0; k < a.nseg; ++k) {
     const PfSeg& sg = a.seg[k];
     if (sg.w.type != type || sg.w.cols != a.K || sg.rows <= 0 || sg.rows > sg.w.rows)

@@ -192,6 +192,9 @@ struct PfQkvArgs {
   void* vcache;
   int kv_f16;
   int64_t max_seq;
+  // K-split GEMM output instead of qkv when nsplit > 1: [nsplit][M][ldq]
+  const float* part;
+  int nsplit;
 };
 
 struct PfAttnArgs {

@@ -318,7 +318,9 @@ Error DecoderProgram::ensure_prefill_buffers(int64_t chunk) {
   UAII_TRY(alloc(4 * C * (size_t)d.q_dim, (void**)&pf_q_));
   UAII_TRY(alloc(4 * C * (size_t)d.q_dim, (void**)&pf_attn_));
   UAII_TRY(alloc(4 * C * (size_t)inter, (void**)&pf_h_));
-  UAII_TRY(alloc(4 * 4 * C * (size_t)d.dim, (void**)&pf_part_));
+  // K-split partials: the residual stream's, or the QKV group's
+  pf_part_cols_ = std::max(d.dim, d.q_dim + 2 * d.kv_dim);
+  UAII_TRY(alloc(4 * 4 * C * (size_t)pf_part_cols_, (void**)&pf_part_));
   if (moe_) {
     const size_t CK = C * (size_t)topk;
     UAII_TRY(alloc(4 * CK, (void**)&pf_moe_ids_));
@@ -350,7 +352,8 @@ Error DecoderProgram::ensure_prefill_buffers(int64_t chunk) {
 // One MFMA GEMM launch per run of consecutive weights of the same block format
 // (q, k and v may differ, e.g. Q6_K attn_v beside Q4_K attn_q).
 Error DecoderProgram::pf_gemm(const DeviceWeight* w[3], const int64_t cols0[3], int nw,
-                              const DeviceWeight* w2, int epi, int64_t m, float* y, int64_t ldy) {
+                              const DeviceWeight* w2, int epi, int64_t m, float* y, int64_t ldy,
+                              int store_split) {
   for (int i = 0; i < nw;) {
     PfGemmArgs a{};
     a.epi = epi;
@@ -372,23 +375,63 @@ Error DecoderProgram::pf_gemm(const DeviceWeight* w[3], const int64_t cols0[3], 
       sg.col0 = cols0[j];
       ++j;
     }
+    if (cus_ == 0) {
+      int dev = 0;
+      UAII_HIP(hipGetDevice(&dev));
+      UAII_HIP(hipDeviceGetAttribute(&cus_, hipDeviceAttributeMultiprocessorCount, dev));
+    }
     // a residual add into the stream of a single-format launch may split K; its
     // partials are added by the next prep of the stream (pf_prep)
     a.ksplit = 1;
     if (epi == EPI_ADD && y == pf_x_ && i == 0 && j == nw && pf_pending_ == 0) {
-      if (cus_ == 0) {
-        int dev = 0;
-        UAII_HIP(hipGetDevice(&dev));
-        UAII_HIP(hipDeviceGetAttribute(&cus_, hipDeviceAttributeMultiprocessorCount, dev));
-      }
       a.ksplit = pf_gemm_ksplit(a, cus_);
       a.part = pf_part_;
     }
+    // a split store: every launch of the group writes partials with the same split
+    if (store_split > 1) {
+      a.ksplit = store_split;
+      a.part = pf_part_;
+    }
     UAII_HIP(launch_pf_gemm(a, stream_));
-    if (a.ksplit > 1) pf_pending_ = a.ksplit;
+    if (epi == EPI_ADD && a.ksplit > 1) pf_pending_ = a.ksplit;
     i = j;
   }
   return Error::success();
+}
+
+// K split shared by the launches of a plain-store group (QKV): the largest any
+// launch of the group asks for, halved until every launch's K range allows it.
+int DecoderProgram::pf_store_split(const DeviceWeight* w[3], int nw, int64_t m, int64_t ldy) {
+  if (cus_ == 0) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus_, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+      return 1;
+  }
+  if ((int64_t)4 * pf_chunk_ * pf_part_cols_ < 4 * m * ldy) return 1;
+  int ks = 1;
+  int64_t kq = 64;
+  for (int i = 0; i < nw;) {
+    PfGemmArgs a{};
+    a.epi = EPI_STORE;
+    a.M = m;
+    a.K = w[i]->view.cols;
+    a.mpad = pf_act_.mpad;
+    int j = i;
+    while (j < nw && w[j]->view.type == w[i]->view.type) {
+      PfSeg& sg = a.seg[a.nseg++];
+      sg.w = w[j]->view;
+      sg.rows = w[j]->view.rows;
+      ++j;
+    }
+    const int t = w[i]->view.type;
+    if (t == T_Q4_K || t == T_Q6_K) kq = 256;
+    ks = std::max(ks, pf_gemm_ksplit(a, cus_));
+    i = j;
+  }
+  const int64_t K = w[0]->view.cols;
+  while (ks > 1 && K % (kq * ks) != 0) ks /= 2;
+  return ks;
 }
 
 Error DecoderProgram::pf_prep(float* x, int64_t K, int64_t m, const float* norm_w) {
@@ -548,7 +591,8 @@ Error DecoderProgram::prefill(int64_t n) {
     *bytes += 4.0 * (double)m * (double)w[0]->view.cols + 4.0 * (double)m * (double)outs;
   };
   auto gemm = [&](const char* name, const DeviceWeight** w, const int64_t* cols0, int nw,
-                  const DeviceWeight* w2, int epi, int64_t m, float* y, int64_t ldy) -> Error {
+                  const DeviceWeight* w2, int epi, int64_t m, float* y, int64_t ldy,
+                  int store_split = 1) -> Error {
     double bytes = 0.0, flops = 0.0;
     gemm_cost(w, nw, m, ldy, &bytes, &flops);
     if (w2) {
@@ -557,7 +601,7 @@ Error DecoderProgram::prefill(int64_t n) {
     }
     Error err = Error::success();
     Error launched = timed(name, bytes, flops, [&]() -> hipError_t {
-      err = pf_gemm(w, cols0, nw, w2, epi, m, y, ldy);
+      err = pf_gemm(w, cols0, nw, w2, epi, m, y, ldy, store_split);
       return err.ok() ? hipSuccess : hipErrorInvalidValue;
     });
     if (!err.ok()) return err;
@@ -578,8 +622,11 @@ Error DecoderProgram::prefill(int64_t n) {
       UAII_TRY(prep(pf_x_, d.dim, m, L.attn_norm));
       const DeviceWeight* qkv[3] = {&L.wq, &L.wk, &L.wv};
       const int64_t qkv_cols[3] = {0, d.q_dim, d.q_dim + d.kv_dim};
-      UAII_TRY(gemm("pf_gemm_qkv", qkv, qkv_cols, 3, nullptr, EPI_STORE, m, pf_qkv_, ldqkv));
+      const int qkv_split = pf_store_split(qkv, 3, m, ldqkv);
+      UAII_TRY(gemm("pf_gemm_qkv", qkv, qkv_cols, 3, nullptr, EPI_STORE, m, pf_qkv_, ldqkv, qkv_split));
       PfQkvArgs qa{};
+      qa.part = pf_part_;
+      qa.nsplit = qkv_split;
       qa.qkv = pf_qkv_;
       qa.ldq = ldqkv;
       qa.M = m;

@@ -106,7 +106,8 @@ class DecoderProgram {
   Error collect_timings();
   Error ensure_prefill_buffers(int64_t chunk);
   Error pf_gemm(const DeviceWeight* w[3], const int64_t cols0[3], int nw, const DeviceWeight* w2,
-                int epi, int64_t m, float* y, int64_t ldy);
+                int epi, int64_t m, float* y, int64_t ldy, int store_split = 1);
+  int pf_store_split(const DeviceWeight* w[3], int nw, int64_t m, int64_t ldy);
   Error pf_prep(float* x, int64_t K, int64_t m, const float* norm_w);
   template <class Prep, class Gemm>
   Error prefill_moe(const Layer& L, const LayerSpec& ls, int64_t m, Prep&& prep, Gemm&& gemm);
@@ -164,6 +165,7 @@ class DecoderProgram {
   int32_t *pf_moe_ids_ = nullptr, *pf_moe_cnt_ = nullptr, *pf_moe_list_ = nullptr,
           *pf_moe_inv_ = nullptr, *pf_moe_tab_ = nullptr;
   int64_t pf_tab_cap_ = 0;             // int32 entries of pf_moe_tab_
+  int64_t pf_part_cols_ = 0;           // columns per row of pf_part_
   std::vector<int32_t> pf_tab_host_;   // the grouped GEMMs' row tables before upload
   float *pf_moe_w_ = nullptr, *pf_moe_y_ = nullptr, *pf_hsh_ = nullptr;
   int pf_pending_ = 0;        // splits in pf_part_ still to be added into pf_x_
