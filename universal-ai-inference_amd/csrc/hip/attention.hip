@@ -313,9 +313,8 @@ __device__ inline float adot2(uint32_t a, uint32_t b, float c) {
 
 __device__ inline uint32_t ah_bits(_Float16 h) { return (uint32_t)__builtin_bit_cast(uint16_t, h); }
 
-template <int HD, int G, int TK>
-__global__ void __launch_bounds__(256) k_attn_h16(AttnArgs a) {
-  constexpr int NW = 4;
+template <int HD, int G, int TK, int NW>
+__global__ void __launch_bounds__(NW * 64) k_attn_h16(AttnArgs a) {
   static_assert(TK == 16 || TK == 32, "tile of 16 or 32 keys");
   static_assert(TK >= 64 / (HD / 32), "at least one key per lane group in the scores");
   constexpr int LK = HD / 32;            // lanes per key (scores)
@@ -338,11 +337,12 @@ __global__ void __launch_bounds__(256) k_attn_h16(AttnArgs a) {
   const float scale = 1.0f / sqrtf((float)HD);
 
   // q of the group first: waiting for it does not wait for the K/V loads below
-  constexpr int QPT = (G * HD + 255) / 256;
+  constexpr int NT = NW * 64;
+  constexpr int QPT = (G * HD + NT - 1) / NT;
   float qv[QPT];
 #pragma unroll
   for (int k = 0; k < QPT; ++k) {
-    const int i = tid + 256 * k;
+    const int i = tid + NT * k;
     qv[k] = (i < G * HD) ? a.q[(int64_t)h * G * HD + i] : 0.0f;
   }
 
@@ -375,7 +375,7 @@ __global__ void __launch_bounds__(256) k_attn_h16(AttnArgs a) {
   // q * scale -> f16 (hi, lo) pairs in LDS
 #pragma unroll
   for (int k = 0; k < QPT; ++k) {
-    const int i = tid + 256 * k;
+    const int i = tid + NT * k;
     const float v = qv[k] * scale;
     const _Float16 hi = (_Float16)v;
     const _Float16 lo = (_Float16)(v - (float)hi);
@@ -496,7 +496,7 @@ __global__ void __launch_bounds__(256) k_attn_h16(AttnArgs a) {
   __syncthreads();
   const int64_t pstride = HD + 2;
   float* part = a.part + ((int64_t)h * SB + sblk) * G * pstride;
-  for (int i = tid; i < G * HD; i += 256) {
+  for (int i = tid; i < G * HD; i += NT) {
     const int g = i / HD, d = i % HD;
     float M = -INFINITY;
 #pragma unroll
@@ -519,15 +519,16 @@ __global__ void __launch_bounds__(256) k_attn_h16(AttnArgs a) {
 // Tiles of 32 keys per wave: a block covers 128 keys per pass. (16-key tiles
 // with twice the splits measured slower end to end: more blocks and a wider
 // merge cost more than the shorter per-block chain saves.)
+// (Eight waves of 16-key tiles per block measured within 2 % of this.)
 template <int HD>
 bool launch_h16(const AttnArgs& a, int G, hipStream_t s) {
-  constexpr int TK = 32;
+  constexpr int TK = 32, NW = 4;
   dim3 grid(a.n_kv, a.splits);
   switch (G) {
-    case 1: UAII_LAUNCH((k_attn_h16<HD, 1, TK>), grid, dim3(256), 0, s, a); return true;
-    case 2: UAII_LAUNCH((k_attn_h16<HD, 2, TK>), grid, dim3(256), 0, s, a); return true;
-    case 4: UAII_LAUNCH((k_attn_h16<HD, 4, TK>), grid, dim3(256), 0, s, a); return true;
-    case 8: UAII_LAUNCH((k_attn_h16<HD, 8, TK>), grid, dim3(256), 0, s, a); return true;
+    case 1: UAII_LAUNCH((k_attn_h16<HD, 1, TK, NW>), grid, dim3(NW * 64), 0, s, a); return true;
+    case 2: UAII_LAUNCH((k_attn_h16<HD, 2, TK, NW>), grid, dim3(NW * 64), 0, s, a); return true;
+    case 4: UAII_LAUNCH((k_attn_h16<HD, 4, TK, NW>), grid, dim3(NW * 64), 0, s, a); return true;
+    case 8: UAII_LAUNCH((k_attn_h16<HD, 8, TK, NW>), grid, dim3(NW * 64), 0, s, a); return true;
     default: return false;
   }
 }
