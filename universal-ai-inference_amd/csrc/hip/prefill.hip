@@ -1140,15 +1140,34 @@ __global__ void __launch_bounds__(256) k_pf_moe_route(const float* __restrict__ 
     r4[i] = v;
   }
   __syncthreads();
-  // logits: wave w takes experts w, w + 4, ...
+  // logits: wave w takes experts w, w + 4, ...; each lane 4 consecutive inputs
+  // per step, the router loads of 8 steps issued before their arithmetic (one
+  // memory round trip per 8 steps, not per step)
+  constexpr int RB = 8;
   for (int e = wave; e < E; e += 4) {
     float acc = 0.0f;
-    if constexpr (RT == T_F32) {
-      const float* wr = reinterpret_cast<const float*>(router.a + (int64_t)e * router.a_row);
-      for (int64_t i = lane; i < K; i += 64) acc += row[i] * wr[i];
-    } else {
-      const __half* wr = reinterpret_cast<const __half*>(router.a + (int64_t)e * router.a_row);
-      for (int64_t i = lane; i < K; i += 64) acc += row[i] * __half2float(wr[i]);
+    const uint8_t* wr = router.a + (int64_t)e * router.a_row;
+    for (int base = 0; base < nv; base += 64 * RB) {
+      float4 wv[RB];
+#pragma unroll
+      for (int j = 0; j < RB; ++j) {
+        const int i = min(base + 64 * j + lane, nv - 1);
+        if constexpr (RT == T_F32) {
+          wv[j] = reinterpret_cast<const float4*>(wr)[i];
+        } else {
+          const uint2 h = reinterpret_cast<const uint2*>(wr)[i];
+          wv[j] = make_float4(h2f((uint16_t)(h.x & 0xffff)), h2f((uint16_t)(h.x >> 16)),
+                              h2f((uint16_t)(h.y & 0xffff)), h2f((uint16_t)(h.y >> 16)));
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < RB; ++j) {
+        const int i = base + 64 * j + lane;
+        if (i < nv) {
+          const float4 xv = r4[i];
+          acc += xv.x * wv[j].x + xv.y * wv[j].y + xv.z * wv[j].z + xv.w * wv[j].w;
+        }
+      }
     }
     acc = wave_sum(acc);
     if (lane == 0) logit[e] = acc;

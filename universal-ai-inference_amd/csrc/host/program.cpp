@@ -938,19 +938,27 @@ Error DecoderProgram::encode_step(bool want_logits) {
       // the device (transformer.cpp:446-481)
       const int64_t E = d.n_experts, I = ls.inter;
       const int k = (int)std::min<int64_t>(d.top_k, E);
-      GemvArgs r{};
-      r.nseg = 1;
-      r.epi = EPI_STORE;
-      r.K = d.dim;
-      r.x = x_;
-      r.norm_w = L.ffn_norm;
-      r.eps = d.rms_eps;
-      r.y = moe_logits_;
-      r.seg[0].w = L.gate_inp.view;
-      r.seg[0].rows = E;
-      r.state = state_;
-      UAII_TRY(timed("moe_router", gemv_bytes(L.gate_inp.view), [&] { return launch_gemv(r, s); }));
-      UAII_TRY(timed("moe_route", 0.0, [&] { return launch_moe_route(moe_logits_, (int)E, k, moe_ids_, moe_w_, s); }));
+      if (L.ffn_norm && pf_router_supported(L.gate_inp.view.type) && E <= 256 && k <= 8 && d.dim % 4 == 0) {
+        // one block: RMSNorm, the E router logits and the top-k in one launch
+        UAII_TRY(timed("moe_route", gemv_bytes(L.gate_inp.view), [&] {
+          return launch_pf_moe_route(x_, 1, d.dim, L.ffn_norm, d.rms_eps, L.gate_inp.view, (int)E, k, moe_ids_,
+                                     moe_w_, s);
+        }));
+      } else {
+        GemvArgs r{};
+        r.nseg = 1;
+        r.epi = EPI_STORE;
+        r.K = d.dim;
+        r.x = x_;
+        r.norm_w = L.ffn_norm;
+        r.eps = d.rms_eps;
+        r.y = moe_logits_;
+        r.seg[0].w = L.gate_inp.view;
+        r.seg[0].rows = E;
+        r.state = state_;
+        UAII_TRY(timed("moe_router", gemv_bytes(L.gate_inp.view), [&] { return launch_gemv(r, s); }));
+        UAII_TRY(timed("moe_route", 0.0, [&] { return launch_moe_route(moe_logits_, (int)E, k, moe_ids_, moe_w_, s); }));
+      }
       // gate/up of the k chosen experts (+ the shared expert): one segment each,
       // rows of expert moe_ids_[t], outputs at h_[t * I]
       const int nsegs = k + (L.shared ? 1 : 0);
