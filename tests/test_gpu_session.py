@@ -52,6 +52,10 @@ SMALL = {
                                     vocab=700, ctx_len=256, type_default=uaii_amd.Q4_0,
                                     n_experts=8, top_k=2, router_std=1.0 / 16, shared_ffn=192,
                                     seed=36),
+    # MoE top-3 of 6, Q4_0: one two-expert down launch and one single, in order
+    "moe_top3": synth.ModelConfig(n_layers=2, dim=256, n_heads=4, n_kv_heads=2, ffn=384,
+                                  vocab=800, ctx_len=256, type_default=uaii_amd.Q4_0, n_experts=6,
+                                  top_k=3, router_std=1.0 / 16, seed=38),
     # dense GELU MLP and Q/K/V biases
     "gelu_bias": synth.ModelConfig(n_layers=2, dim=512, n_heads=8, n_kv_heads=4, ffn=1024,
                                    vocab=1500, ctx_len=256, type_default=uaii_amd.Q8_0, gelu=True,

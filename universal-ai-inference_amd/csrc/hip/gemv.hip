@@ -918,20 +918,31 @@ __global__ void __launch_bounds__(W * 64) k_gemv(GemvArgs a) {
   __shared__ float kred[2][W][RPW_MAX];
   __shared__ float bval[W];
   __shared__ int32_t bidx[W];
+  // EPI_ADD2: the block's waves form two halves, half h computing the rows of
+  // segment h (same output rows, own input staged in its own LDS region)
+  constexpr bool PAIR = EPI == EPI_ADD2;
+  constexpr int HW = PAIR ? W / 2 : W;  // waves per segment in a block
+  __shared__ float pexch[2][PAIR ? HW : 1][RPW_MAX];
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int half = PAIR ? wave / HW : 0, hw = PAIR ? wave % HW : wave;
 
-  // segment lookup (uniform per block)
+  // segment lookup (uniform per block; per half for EPI_ADD2)
   int si = 0;
-  for (int k = 1; k < a.nseg; ++k) if ((int)blockIdx.x >= a.seg[k].block0) si = k;
+  if constexpr (PAIR) {
+    si = half;
+  } else {
+    for (int k = 1; k < a.nseg; ++k) if ((int)blockIdx.x >= a.seg[k].block0) si = k;
+  }
   const GemvSeg& seg = a.seg[si];
-  const int nblk = (si + 1 < a.nseg ? a.seg[si + 1].block0 : (int)gridDim.x) - seg.block0;
+  const int nblk = PAIR ? (int)gridDim.x
+                        : (si + 1 < a.nseg ? a.seg[si + 1].block0 : (int)gridDim.x) - seg.block0;
 
   constexpr int RPW = rpw_of(FMT);
   const int ks = a.ksplit;
-  const int nrs = W / ks;  // row sets per block
+  const int nrs = HW / ks;  // row sets per block (per half)
   const int64_t ngroups = (seg.rows + nrs * RPW - 1) / (nrs * RPW);
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  const int rs = wave / ks, kp = wave % ks;
+  const int rs = hw / ks, kp = hw % ks;
 
   Walk wk;
   wk.nch = seg.w.a_row / 16;
@@ -943,7 +954,10 @@ __global__ void __launch_bounds__(W * 64) k_gemv(GemvArgs a) {
 
   const float* xin = seg.x ? seg.x : a.x;
   const int64_t ebase = seg.expert ? (int64_t)seg.expert[0] * seg.expert_rows : 0;
-  const int64_t g0 = (int64_t)blockIdx.x - seg.block0;
+  const int64_t g0 = (int64_t)blockIdx.x - (PAIR ? 0 : seg.block0);
+  // this half's staged input (the LDS holds one region per segment for EPI_ADD2)
+  const int64_t region = pair_fmt<FMT>() ? wk.nch * 34 : a.K;
+  float* const xs = xsm + (PAIR ? half * region : 0);
   const int64_t mine = (g0 < ngroups) ? (ngroups - g0 + nblk - 1) / nblk : 0;
   const int64_t nunits = mine * wk.steps;
 
@@ -953,7 +967,25 @@ __global__ void __launch_bounds__(W * 64) k_gemv(GemvArgs a) {
   // input loads first, then the first unit's weight loads, then the staging
   // arithmetic (which waits for the input only)
   UnitBuf<FMT> U0;
-  if constexpr (pair_fmt<FMT>()) {
+  if constexpr (PAIR) {
+    // both inputs staged by the whole block, one after the other (for the pair
+    // formats before the first weight loads: their staging registers and a
+    // unit's would not fit together under the 16-wave block's register limit)
+    if constexpr (!pair_fmt<FMT>())
+      if (nunits > 0) load_unit<FMT, EPI>(a, seg, ebase, wk, unit_l0(0), 0, lane, U0);
+#pragma unroll 1
+    for (int h = 0; h < 2; ++h) {
+      if constexpr (pair_fmt<FMT>()) {
+        PairStage ps;
+        stage_pairs_issue<FMT>(a, a.seg[h].x, wk.nch, ps);
+        stage_pairs_finish<FMT>(a, a.seg[h].x, wk.nch, ps, xsm + h * region, red);
+      } else {
+        stage_x<FMT>(a, a.seg[h].x, wk.nch, xsm + h * region, red);
+      }
+    }
+    if constexpr (pair_fmt<FMT>())
+      if (nunits > 0) load_unit<FMT, EPI>(a, seg, ebase, wk, unit_l0(0), 0, lane, U0);
+  } else if constexpr (pair_fmt<FMT>()) {
     PairStage ps;
     stage_pairs_issue<FMT>(a, xin, wk.nch, ps);
     if (nunits > 0) load_unit<FMT, EPI>(a, seg, ebase, wk, unit_l0(0), 0, lane, U0);
@@ -994,30 +1026,54 @@ __global__ void __launch_bounds__(W * 64) k_gemv(GemvArgs a) {
         }
       }
     }
-    if (kp == 0) epilogue<EPI, RPW>(a, seg, ((g0 + i * nblk) * nrs + rs) * RPW, lane, acc, best_v, best_i);
+    if constexpr (PAIR) {
+      // half 1 hands its dots to half 0, which adds both in segment order
+      const int par = (int)(i & 1);
+      if (kp == 0 && half == 1 && lane == 0) {
+#pragma unroll
+        for (int r = 0; r < RPW; ++r) pexch[par][rs][r] = acc[r];
+      }
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+      __builtin_amdgcn_s_barrier();
+      if (kp == 0 && half == 0 && lane < RPW) {
+        float v0 = 0.0f, v1 = 0.0f;
+#pragma unroll
+        for (int r = 0; r < RPW; ++r) if (r == lane) { v0 = acc[r]; v1 = pexch[par][rs][r]; }
+        const int64_t l = ((g0 + i * nblk) * nrs + rs) * RPW + lane;
+        if (l < seg.rows) {
+          const int64_t o = seg.row_base + l;
+          float v = a.y[o] + a.seg[0].scale[0] * v0;  // transformer.cpp:600-608, expert by expert
+          v = v + a.seg[1].scale[0] * v1;
+          a.y[o] = v;
+          if (a.tap) a.tap[o] = v;
+        }
+      }
+    } else if (kp == 0) {
+      epilogue<EPI, RPW>(a, seg, ((g0 + i * nblk) * nrs + rs) * RPW, lane, acc, best_v, best_i);
+    }
 #pragma unroll
     for (int r = 0; r < RPW; ++r) acc[r] = 0.0f;
   };
   // first batch: unit 0 (already in flight) and, for NB = 2, unit 1
   if constexpr (NB == 1) {
     if (nunits > 0) {
-      compute_unit<FMT>(wk, 0, lane, xsm, U0, acc);
+      compute_unit<FMT>(wk, 0, lane, xs, U0, acc);
       finish(0);
     }
     for (int64_t u = 1; u < nunits; ++u) {
       UnitBuf<FMT> V;
       load_unit<FMT, EPI>(a, seg, ebase, wk, unit_l0(u), unit_step(u), lane, V);
-      compute_unit<FMT>(wk, unit_step(u), lane, xsm, V, acc);
+      compute_unit<FMT>(wk, unit_step(u), lane, xs, V, acc);
       finish(u);
     }
   } else {
     if (nunits > 0) {
       UnitBuf<FMT> U1;
       if (nunits > 1) load_unit<FMT, EPI>(a, seg, ebase, wk, unit_l0(1), unit_step(1), lane, U1);
-      compute_unit<FMT>(wk, 0, lane, xsm, U0, acc);
+      compute_unit<FMT>(wk, 0, lane, xs, U0, acc);
       finish(0);
       if (nunits > 1) {
-        compute_unit<FMT>(wk, unit_step(1), lane, xsm, U1, acc);
+        compute_unit<FMT>(wk, unit_step(1), lane, xs, U1, acc);
         finish(1);
       }
     }
@@ -1026,10 +1082,10 @@ __global__ void __launch_bounds__(W * 64) k_gemv(GemvArgs a) {
       const bool two = u + 1 < nunits;  // block-uniform
       load_unit<FMT, EPI>(a, seg, ebase, wk, unit_l0(u), unit_step(u), lane, V0);
       if (two) load_unit<FMT, EPI>(a, seg, ebase, wk, unit_l0(u + 1), unit_step(u + 1), lane, V1);
-      compute_unit<FMT>(wk, unit_step(u), lane, xsm, V0, acc);
+      compute_unit<FMT>(wk, unit_step(u), lane, xs, V0, acc);
       finish(u);
       if (two) {
-        compute_unit<FMT>(wk, unit_step(u + 1), lane, xsm, V1, acc);
+        compute_unit<FMT>(wk, unit_step(u + 1), lane, xs, V1, acc);
         finish(u + 1);
       }
     }
@@ -1128,7 +1184,11 @@ KernelFn pick_fmt(int type) {
 // WPB_QKV for the QKV epilogue, WPB_LONG for the residual add.
 KernelFn pick(int epi, int type, int w) {
   if (w == WPB_QKV) return epi == EPI_QKV ? pick_fmt<EPI_QKV, WPB_QKV>(type) : nullptr;
-  if (w == WPB_LONG) return epi == EPI_ADD ? pick_fmt<EPI_ADD, WPB_LONG>(type) : nullptr;
+  if (w == WPB_LONG) {
+    if (epi == EPI_ADD) return pick_fmt<EPI_ADD, WPB_LONG>(type);
+    if (epi == EPI_ADD2) return pick_fmt<EPI_ADD2, WPB_LONG>(type);
+    return nullptr;
+  }
   if (w != WPB) return nullptr;
   switch (epi) {
     case EPI_STORE: return pick_fmt<EPI_STORE, WPB>(type);
@@ -1143,6 +1203,7 @@ KernelFn pick(int epi, int type, int w) {
 
 // Waves per block for a launch of epilogue `epi` whose rows split K over `ks` waves.
 int pick_waves(int epi, int ks) {
+  if (epi == EPI_ADD2) return WPB_LONG;
   if (epi == EPI_ADD && ks == 4) return WPB_LONG;
   if (epi == EPI_QKV) return WPB_QKV;
   return WPB;
@@ -1153,7 +1214,7 @@ int pick_waves(int epi, int ks) {
 // Raise each instantiation's dynamic-LDS limit to what the device allows per
 // block (where the runtime accepts the attribute; otherwise its default holds).
 hipError_t prepare_gemv() {
-  const int epis[] = {EPI_STORE, EPI_ADD, EPI_QKV, EPI_SWIGLU, EPI_LOGITS, EPI_GELU};
+  const int epis[] = {EPI_STORE, EPI_ADD, EPI_QKV, EPI_SWIGLU, EPI_LOGITS, EPI_GELU, EPI_ADD2};
   const int types[] = {T_Q4_0, T_Q8_0, T_Q4_K, T_Q6_K, T_Q4_1, T_Q5_0,
                        T_Q5_1, T_Q5_K, T_Q2_K, T_Q3_K, T_F32,  T_F16};
   const int lim = lds_limit();
@@ -1232,12 +1293,21 @@ struct Plan {
 // rest loop), shared out by group count.
 Plan make_plan(const GemvArgs& a) {
   Plan p;
-  p.lds = lds_bytes(a.seg[0].w.type, a.K);
+  const bool pair = a.epi == EPI_ADD2;  // two segments over the same rows, one staged input each
+  p.lds = (pair ? 2 : 1) * lds_bytes(a.seg[0].w.type, a.K);
   p.ks = pick_ksplit(a.seg[0].w);
   p.waves = pick_waves(a.epi, p.ks);
   p.fn = pick(a.epi, a.seg[0].w.type, p.waves);
   if (!p.fn) return p;
-  const int rpg = (p.waves / p.ks) * rpw_of(a.seg[0].w.type);
+  const int rpg = (p.waves / (pair ? 2 : 1) / p.ks) * rpw_of(a.seg[0].w.type);
+  if (pair) {
+    const int64_t g = (a.seg[0].rows + rpg - 1) / rpg;
+    const int per_cu = resident_blocks(p.fn, p.lds, p.waves);
+    p.per[0] = (int)std::min<int64_t>(g, (int64_t)cu_count() * per_cu);
+    p.per[1] = 0;
+    p.blocks = p.per[0];
+    return p;
+  }
   int64_t total = 0;
   for (int k = 0; k < a.nseg; ++k) total += (a.seg[k].rows + rpg - 1) / rpg;
   const int per_cu = UAII_GEMV_BLOCKS_PER_CU > 0 ? UAII_GEMV_BLOCKS_PER_CU : resident_blocks(p.fn, p.lds, p.waves);
@@ -1291,6 +1361,14 @@ int gemv_grid(const GemvArgs& in) {
 hipError_t launch_gemv(const GemvArgs& in, hipStream_t s) {
   if (in.K % 4) return hipErrorInvalidValue;
   if (in.epi == EPI_LOGITS && in.nseg != 1) return hipErrorInvalidValue;
+  if (in.epi == EPI_ADD2) {
+    // one launch (one type), the same output rows, each segment its own input,
+    // expert and weight
+    const GemvSeg &s0 = in.seg[0], &s1 = in.seg[1];
+    if (in.nseg != 2 || s0.w.type != s1.w.type || s0.rows != s1.rows || s0.row_base != s1.row_base ||
+        !s0.x || !s1.x || !s0.scale || !s1.scale)
+      return hipErrorInvalidValue;
+  }
   for (int k = 0; k < in.nseg; ++k) {
     if (in.epi == EPI_SWIGLU && in.seg[k].w2.type != in.seg[k].w.type) return hipErrorInvalidValue;
     if ((in.epi == EPI_SWIGLU || in.epi == EPI_QKV) && (in.seg[k].rows % 2)) return hipErrorInvalidValue;

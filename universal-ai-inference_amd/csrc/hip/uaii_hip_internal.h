@@ -25,6 +25,10 @@ enum Epilogue : int {
   EPI_SWIGLU = 3,  // rows (gate i, up i) -> y[i] = silu(g) * u
   EPI_LOGITS = 4,  // y[row] = dot, block argmax partials (+ final argmax/advance kernel)
   EPI_GELU = 5,    // y[row] = gelu(dot) (tanh form, elementwise.cpp:57-71)
+  // two MoE experts' down rows in one launch: segments 0 and 1 cover the same
+  // output rows with their own input (seg.x), expert and weight (seg.scale);
+  // y[row] = (y[row] + s0 * dot0) + s1 * dot1, the order of two EPI_ADD launches
+  EPI_ADD2 = 6,
 };
 
 // Persistent decode state shared by the step kernels (device memory).

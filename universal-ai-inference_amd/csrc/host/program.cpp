@@ -1000,6 +1000,27 @@ Error DecoderProgram::encode_step(bool want_logits) {
         dn.epi = EPI_ADD;
         dn.y = x_;
         dn.state = state_;
+        if (t + 1 < k) {
+          // two routed experts in one launch, added in their order
+          dn.nseg = 2;
+          dn.epi = EPI_ADD2;
+          dn.K = I;
+          dn.x = h_ + (int64_t)t * I;
+          for (int h = 0; h < 2; ++h) {
+            GemvSeg& sg = dn.seg[h];
+            sg.x = h_ + (int64_t)(t + h) * I;
+            sg.w = L.down_exps.view;
+            sg.rows = d.dim;
+            sg.expert = moe_ids_ + t + h;
+            sg.expert_rows = d.dim;
+            sg.scale = moe_w_ + t + h;
+          }
+          if (t + 2 == nsegs) dn.tap = tap_r2_ + li * d.dim;
+          const double bytes = 2.0 * gemv_bytes(L.down_exps.view) / (double)E;
+          UAII_TRY(timed("moe_down", bytes, [&] { return launch_gemv(dn, s); }));
+          ++t;
+          continue;
+        }
         if (t + 1 == nsegs) dn.tap = tap_r2_ + li * d.dim;
         double bytes;
         if (t < k) {
