@@ -484,9 +484,15 @@ struct Walk {
   int steps;       // steps per row group (the same for every wave of the block)
 };
 
+struct EpiIn {
+  float v0, v1;  // EPI_ADD: residual, expert weight (1 when absent); EPI_QKV: bias pair
+  float2 cs;     // EPI_QKV: rotation of the pair
+};
+
 template <int FMT>
 struct UnitBuf {
   Raw r[2][rpw_of(FMT)];
+  EpiIn e;  // the group's epilogue inputs (epi_load)
 };
 
 // Wave-uniform row pointers of logical rows l0 .. l0+R-1 of a segment.
@@ -508,9 +514,42 @@ __device__ inline void unit_rows(const GemvArgs& a, const GemvSeg& seg, int64_t 
   }
 }
 
+// Global inputs of one row group's epilogue, read by epi_load with the group's
+// weights (reading them after the dot would add a dependent round trip to
+// memory at the end of every group): EPI_ADD the residual value of this lane's
+// row (lanes < R) and the MoE expert weight; EPI_QKV the bias pair and the RoPE
+// (cos, sin) of this lane's pair (lanes < R/2). Every load is unconditional
+// (clamped rows, a valid stand-in pointer where an input is absent), so the
+// compiler's waits for the weight loads stay exact.
+template <int EPI, int R>
+__device__ inline void epi_load(const GemvArgs& a, const GemvSeg& seg, int64_t lrow0, int lane, int pos, EpiIn& e) {
+  if constexpr (EPI == EPI_ADD) {
+    const int64_t l = min(lrow0 + min(lane, R - 1), seg.rows - 1);
+    e.v0 = a.y[seg.row_base + l];
+    const float* sp = seg.scale ? seg.scale : a.y;
+    e.v1 = sp[0];
+  } else if constexpr (EPI == EPI_QKV) {
+    const int64_t l = min(lrow0 + 2 * min(lane, R / 2 - 1), seg.rows - 2);
+    const int64_t r0 = (seg.kind == 2) ? l : qkv_phys(l, a.rope_mode, a.head_dim);
+    const int64_t r1 = (seg.kind == 2) ? l + 1 : qkv_phys(l + 1, a.rope_mode, a.head_dim);
+    const float* bp = seg.bias ? seg.bias : a.y;
+    e.v0 = bp[seg.bias ? r0 : 0];
+    e.v1 = bp[seg.bias ? r1 : 0];
+    const int64_t p = (a.rope_mode == 2) ? (r0 % a.head_dim) : ((r0 % a.head_dim) >> 1);
+    e.cs = a.rope[(int64_t)pos * (a.head_dim / 2) + p];
+  }
+}
+
+// Position of the token being decoded (QKV epilogue only), read once per launch.
+template <int EPI>
+__device__ inline int epi_pos(const GemvArgs& a) {
+  if constexpr (EPI == EPI_QKV) return a.state->pos;
+  return 0;
+}
+
 template <int FMT, int EPI>
 __device__ inline void load_unit(const GemvArgs& a, const GemvSeg& seg, int64_t ebase, const Walk& wk,
-                                 int64_t l0, int step, int lane, UnitBuf<FMT>& U) {
+                                 int64_t l0, int step, int lane, int pos, UnitBuf<FMT>& U) {
   constexpr int R = rpw_of(FMT);
   RowPtr P[R];
   unit_rows<EPI, R>(a, seg, ebase, l0, P);
@@ -526,6 +565,7 @@ __device__ inline void load_unit(const GemvArgs& a, const GemvSeg& seg, int64_t 
 #pragma unroll
     for (int r = 0; r < R; ++r) load_raw<FMT>(P[r], t, U.r[j][r]);
   }
+  epi_load<EPI, R>(a, seg, l0, lane, pos, U.e);
 }
 
 template <int FMT>
@@ -828,7 +868,7 @@ __device__ inline void stage_pairs_finish(const GemvArgs& a, const float* xin, i
 // of logical rows lrow0 .. lrow0+R-1.
 template <int EPI, int R>
 __device__ inline void epilogue(const GemvArgs& a, const GemvSeg& seg, int64_t lrow0, int lane,
-                                const float* acc, float& best_v, int32_t& best_i) {
+                                const float* acc, const EpiIn& e, int pos, float& best_v, int32_t& best_i) {
   if constexpr (EPI == EPI_STORE || EPI == EPI_ADD || EPI == EPI_LOGITS || EPI == EPI_GELU) {
     if (lane < R) {
       float v = 0.0f;
@@ -838,8 +878,8 @@ __device__ inline void epilogue(const GemvArgs& a, const GemvSeg& seg, int64_t l
       if (l < seg.rows) {
         const int64_t o = seg.row_base + l;
         if constexpr (EPI == EPI_ADD) {
-          if (seg.scale) v = seg.scale[0] * v;  // MoE expert weight (transformer.cpp:600-608)
-          v = a.y[o] + v;
+          if (seg.scale) v = e.v1 * v;  // MoE expert weight (transformer.cpp:600-608)
+          v = e.v0 + v;
         }
         if constexpr (EPI == EPI_GELU) {
           // tanh-form GELU (elementwise.cpp:57-71)
@@ -879,12 +919,10 @@ __device__ inline void epilogue(const GemvArgs& a, const GemvSeg& seg, int64_t l
       if (l < seg.rows) {
         const int64_t r0 = (seg.kind == 2) ? l : qkv_phys(l, a.rope_mode, a.head_dim);
         const int64_t r1 = (seg.kind == 2) ? l + 1 : qkv_phys(l + 1, a.rope_mode, a.head_dim);
-        if (seg.bias) { v0 = v0 + seg.bias[r0]; v1 = v1 + seg.bias[r1]; }
-        const int pos = a.state->pos;
+        if (seg.bias) { v0 = v0 + e.v0; v1 = v1 + e.v1; }
         if (seg.kind != 2) {
           // rotate pair p of its head by the host-built angle table
-          const int64_t p = (a.rope_mode == 2) ? (r0 % a.head_dim) : ((r0 % a.head_dim) >> 1);
-          const float2 cs = a.rope[(int64_t)pos * (a.head_dim / 2) + p];
+          const float2 cs = e.cs;
           const float n0 = v0 * cs.x - v1 * cs.y;
           const float n1 = v0 * cs.y + v1 * cs.x;
           v0 = n0; v1 = n1;
@@ -954,6 +992,7 @@ __global__ void __launch_bounds__(W * 64) k_gemv(GemvArgs a) {
 
   const float* xin = seg.x ? seg.x : a.x;
   const int64_t ebase = seg.expert ? (int64_t)seg.expert[0] * seg.expert_rows : 0;
+  const int pos = epi_pos<EPI>(a);
   const int64_t g0 = (int64_t)blockIdx.x - (PAIR ? 0 : seg.block0);
   // this half's staged input (the LDS holds one region per segment for EPI_ADD2)
   const int64_t region = pair_fmt<FMT>() ? wk.nch * 34 : a.K;
@@ -972,7 +1011,7 @@ __global__ void __launch_bounds__(W * 64) k_gemv(GemvArgs a) {
     // formats before the first weight loads: their staging registers and a
     // unit's would not fit together under the 16-wave block's register limit)
     if constexpr (!pair_fmt<FMT>())
-      if (nunits > 0) load_unit<FMT, EPI>(a, seg, ebase, wk, unit_l0(0), 0, lane, U0);
+      if (nunits > 0) load_unit<FMT, EPI>(a, seg, ebase, wk, unit_l0(0), 0, lane, pos, U0);
 #pragma unroll 1
     for (int h = 0; h < 2; ++h) {
       if constexpr (pair_fmt<FMT>()) {
@@ -984,14 +1023,14 @@ __global__ void __launch_bounds__(W * 64) k_gemv(GemvArgs a) {
       }
     }
     if constexpr (pair_fmt<FMT>())
-      if (nunits > 0) load_unit<FMT, EPI>(a, seg, ebase, wk, unit_l0(0), 0, lane, U0);
+      if (nunits > 0) load_unit<FMT, EPI>(a, seg, ebase, wk, unit_l0(0), 0, lane, pos, U0);
   } else if constexpr (pair_fmt<FMT>()) {
     PairStage ps;
     stage_pairs_issue<FMT>(a, xin, wk.nch, ps);
-    if (nunits > 0) load_unit<FMT, EPI>(a, seg, ebase, wk, unit_l0(0), 0, lane, U0);
+    if (nunits > 0) load_unit<FMT, EPI>(a, seg, ebase, wk, unit_l0(0), 0, lane, pos, U0);
     stage_pairs_finish<FMT>(a, xin, wk.nch, ps, xsm, red);
   } else {
-    if (nunits > 0) load_unit<FMT, EPI>(a, seg, ebase, wk, unit_l0(0), 0, lane, U0);
+    if (nunits > 0) load_unit<FMT, EPI>(a, seg, ebase, wk, unit_l0(0), 0, lane, pos, U0);
     stage_x<FMT>(a, xin, wk.nch, xsm, red);
   }
 
@@ -1002,7 +1041,7 @@ __global__ void __launch_bounds__(W * 64) k_gemv(GemvArgs a) {
   for (int r = 0; r < RPW; ++r) acc[r] = 0.0f;
 
   // unit u -> (group index i = u / steps, step = u % steps); row group g0 + i * nblk
-  auto finish = [&](int64_t u) {
+  auto finish = [&](int64_t u, const EpiIn& e) {
     const int64_t i = u / wk.steps;
     if (u - i * wk.steps != wk.steps - 1) return;
 #pragma unroll
@@ -1049,7 +1088,7 @@ __global__ void __launch_bounds__(W * 64) k_gemv(GemvArgs a) {
         }
       }
     } else if (kp == 0) {
-      epilogue<EPI, RPW>(a, seg, ((g0 + i * nblk) * nrs + rs) * RPW, lane, acc, best_v, best_i);
+      epilogue<EPI, RPW>(a, seg, ((g0 + i * nblk) * nrs + rs) * RPW, lane, acc, e, pos, best_v, best_i);
     }
 #pragma unroll
     for (int r = 0; r < RPW; ++r) acc[r] = 0.0f;
@@ -1058,35 +1097,35 @@ __global__ void __launch_bounds__(W * 64) k_gemv(GemvArgs a) {
   if constexpr (NB == 1) {
     if (nunits > 0) {
       compute_unit<FMT>(wk, 0, lane, xs, U0, acc);
-      finish(0);
+      finish(0, U0.e);
     }
     for (int64_t u = 1; u < nunits; ++u) {
       UnitBuf<FMT> V;
-      load_unit<FMT, EPI>(a, seg, ebase, wk, unit_l0(u), unit_step(u), lane, V);
+      load_unit<FMT, EPI>(a, seg, ebase, wk, unit_l0(u), unit_step(u), lane, pos, V);
       compute_unit<FMT>(wk, unit_step(u), lane, xs, V, acc);
-      finish(u);
+      finish(u, V.e);
     }
   } else {
     if (nunits > 0) {
       UnitBuf<FMT> U1;
-      if (nunits > 1) load_unit<FMT, EPI>(a, seg, ebase, wk, unit_l0(1), unit_step(1), lane, U1);
+      if (nunits > 1) load_unit<FMT, EPI>(a, seg, ebase, wk, unit_l0(1), unit_step(1), lane, pos, U1);
       compute_unit<FMT>(wk, 0, lane, xs, U0, acc);
-      finish(0);
+      finish(0, U0.e);
       if (nunits > 1) {
         compute_unit<FMT>(wk, unit_step(1), lane, xs, U1, acc);
-        finish(1);
+        finish(1, U1.e);
       }
     }
     for (int64_t u = 2; u < nunits; u += 2) {
       UnitBuf<FMT> V0, V1;
       const bool two = u + 1 < nunits;  // block-uniform
-      load_unit<FMT, EPI>(a, seg, ebase, wk, unit_l0(u), unit_step(u), lane, V0);
-      if (two) load_unit<FMT, EPI>(a, seg, ebase, wk, unit_l0(u + 1), unit_step(u + 1), lane, V1);
+      load_unit<FMT, EPI>(a, seg, ebase, wk, unit_l0(u), unit_step(u), lane, pos, V0);
+      if (two) load_unit<FMT, EPI>(a, seg, ebase, wk, unit_l0(u + 1), unit_step(u + 1), lane, pos, V1);
       compute_unit<FMT>(wk, unit_step(u), lane, xs, V0, acc);
-      finish(u);
+      finish(u, V0.e);
       if (two) {
         compute_unit<FMT>(wk, unit_step(u + 1), lane, xs, V1, acc);
-        finish(u + 1);
+        finish(u + 1, V1.e);
       }
     }
   }
