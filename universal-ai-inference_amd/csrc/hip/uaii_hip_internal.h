@@ -135,6 +135,55 @@ int attention_splits(int64_t max_seq);
 hipError_t launch_attention_decode(const AttnArgs& a, hipStream_t s);
 hipError_t prepare_attention();
 
+// ---- all transformer layers of one decode step in one persistent launch -----------
+
+// Weights of one dense SwiGLU layer (device copy of the table, one entry per layer).
+struct LayerW {
+  DevWeight wq, wk, wv, wo, gate, up, down;
+  const float* attn_norm;
+  const float* ffn_norm;
+  const float *bq, *bk, *bv;  // optional QKV biases
+};
+
+// Device-wide counters of k_layers (zero before the first launch; every launch
+// leaves them zero again except `fail`). Each counter sits on its own 128-byte line.
+struct LayersSync {
+  unsigned long long w[16 * (16 + 64)];
+};
+
+struct LayersArgs {
+  const LayerW* layers;  // [n_layers], device memory
+  int n_layers;
+  int64_t dim, q_dim, kv_dim, inter;
+  int n_heads, n_kv, head_dim, rope_mode;
+  float eps;
+  float* x;            // residual stream [dim]
+  float* qkv;          // raw projections [q_dim + 2 kv_dim]
+  float* attn;         // attention output [q_dim]
+  float* h;            // SwiGLU activation [inter]
+  float* part;         // attention split partials [n_kv][splits][G][hd + 2]
+  int splits;          // key splits per kv head (set by launch_layers)
+  void* kv;            // f16 cache: layer l K at kv + 2 l layer_bytes, V at + layer_bytes
+  int64_t max_seq;
+  const float2* rope;  // [max_seq][hd / 2]
+  const StepState* state;
+  float* tap_r1;       // [n_layers][dim] residual after attention, or null
+  float* tap_r2;       // [n_layers][dim] residual after the FFN, or null
+  LayersSync* sync;
+  const uint8_t* pad;  // >= 1 KiB of device memory read by the padding DMA lines
+  unsigned long long timeout;  // s_memrealtime ticks a device-wide wait may take
+};
+
+// Whether launch_layers can run a model of this shape (all seven matrices of
+// every layer of one type; see layers.hip for the shape rules).
+bool layers_supported(int type, int n_layers, int64_t dim, int64_t q_dim, int64_t kv_dim, int64_t inter,
+                      int n_heads, int n_kv, int head_dim);
+// Attention splits per kv head the launch uses (partial buffer sizing).
+int layers_splits(int n_kv);
+// Once per process, outside stream capture: the kernel's LDS limit and fit check.
+hipError_t prepare_layers(int head_dim, int G);
+hipError_t launch_layers(const LayersArgs& a, int type, hipStream_t s);
+
 // ---- prefill (M > 1 prompt tokens, matrix cores) ---------------------------------------
 
 // Activation rows prepared for the MFMA GEMM: x * 2^e = hi + lo in f16 (each

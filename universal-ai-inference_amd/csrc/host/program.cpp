@@ -292,6 +292,54 @@ Error DecoderProgram::build(const DecoderSpec& spec, const ProgramOptions& opts)
   if (const char* env = std::getenv("UAII_PREFILL")) {
     if (std::string(env) == "0") pf_ok_ = false;
   }
+  UAII_TRY(build_layers(alloc));
+  return Error::success();
+}
+
+// The one-launch layer kernel (UAII_LAYERS=1; off by default: on the 8B
+// decode it measures 350 tok/s against 428 for the per-layer launches) takes
+// dense SwiGLU models whose seven layer matrices share one block format, with
+// an f16 KV cache.
+template <class Alloc>
+Error DecoderProgram::build_layers(Alloc&& alloc) {
+  const DecoderSpec& d = spec_;
+  const char* env = std::getenv("UAII_LAYERS");
+  lay_ok_ = env && std::string(env) == "1" && opts_.kv_f16 && !moe_ && d.n_layers > 0;
+  if (!lay_ok_) return Error::success();
+  const int64_t inter = d.layers[0].inter;
+  lay_type_ = layers_[0]->wq.view.type;
+  for (int64_t li = 0; lay_ok_ && li < d.n_layers; ++li) {
+    const Layer& L = *layers_[(size_t)li];
+    const LayerSpec& ls = d.layers[(size_t)li];
+    if (ls.ffn != LayerSpec::kSwiGLU || ls.inter != inter || !L.attn_norm || !L.ffn_norm) lay_ok_ = false;
+    for (const DeviceWeight* w : {&L.wq, &L.wk, &L.wv, &L.wo, &L.gate, &L.up, &L.down})
+      if (w->view.type != lay_type_) lay_ok_ = false;
+  }
+  lay_ok_ = lay_ok_ && layers_supported(lay_type_, (int)d.n_layers, d.dim, d.q_dim, d.kv_dim, inter,
+                                        (int)d.n_heads, (int)d.n_kv_heads, (int)d.head_dim);
+  if (!lay_ok_) return Error::success();
+  std::vector<LayerW> tab((size_t)d.n_layers);
+  lay_wbytes_ = 0.0;
+  for (int64_t li = 0; li < d.n_layers; ++li) {
+    const Layer& L = *layers_[(size_t)li];
+    LayerW& t = tab[(size_t)li];
+    t.wq = L.wq.view; t.wk = L.wk.view; t.wv = L.wv.view; t.wo = L.wo.view;
+    t.gate = L.gate.view; t.up = L.up.view; t.down = L.down.view;
+    t.attn_norm = L.attn_norm; t.ffn_norm = L.ffn_norm;
+    t.bq = L.bq; t.bk = L.bk; t.bv = L.bv;
+    for (const DeviceWeight* w : {&L.wq, &L.wk, &L.wv, &L.wo, &L.gate, &L.up, &L.down})
+      lay_wbytes_ += gemv_bytes(w->view);
+  }
+  UAII_TRY(alloc(sizeof(LayerW) * tab.size(), (void**)&lay_tab_));
+  UAII_HIP(hipMemcpy(lay_tab_, tab.data(), sizeof(LayerW) * tab.size(), hipMemcpyHostToDevice));
+  UAII_TRY(alloc(sizeof(LayersSync), (void**)&lay_sync_));
+  UAII_TRY(alloc(1024, (void**)&lay_pad_));
+  UAII_TRY(alloc(4 * (size_t)(d.q_dim + 2 * d.kv_dim), (void**)&lay_qkv_));
+  const int G = (int)(d.n_heads / d.n_kv_heads);
+  const size_t part = (size_t)d.n_kv_heads * (size_t)layers_splits((int)d.n_kv_heads) * (size_t)G *
+                      (size_t)(d.head_dim + 2);
+  UAII_TRY(alloc(4 * part, (void**)&lay_part_));
+  UAII_HIP(prepare_layers((int)d.head_dim, G));
   return Error::success();
 }
 
@@ -704,8 +752,11 @@ Error DecoderProgram::ensure_capacity(int64_t max_seq) {
   const DecoderSpec& d = spec_;
   const size_t elem = opts_.kv_f16 ? 2 : 4;
   kv_bytes_ = (size_t)d.n_layers * 2 * (size_t)d.kv_dim * (size_t)max_seq * elem;
-  UAII_HIP(hipMalloc(&kv_, kv_bytes_));
-  UAII_HIP(hipMemsetAsync(kv_, 0, kv_bytes_, stream_));
+  // slack past the end: the layer kernel fetches whole tiles of keys, masking
+  // the ones past the cached length
+  const size_t kv_slack = 64 << 10;
+  UAII_HIP(hipMalloc(&kv_, kv_bytes_ + kv_slack));
+  UAII_HIP(hipMemsetAsync(kv_, 0, kv_bytes_ + kv_slack, stream_));
   UAII_HIP(hipMalloc((void**)&ids_, sizeof(int32_t) * (size_t)(max_seq + 2)));
   UAII_HIP(hipMemsetAsync(ids_, 0, sizeof(int32_t) * (size_t)(max_seq + 2), stream_));
   const int hd = (int)d.head_dim;
@@ -785,6 +836,14 @@ Error DecoderProgram::read_ids(int64_t* out, int64_t n) {
   std::vector<int32_t> ids((size_t)n);
   UAII_HIP(hipStreamSynchronize(stream_));
   UAII_HIP(hipMemcpy(ids.data(), ids_, (size_t)n * 4, hipMemcpyDeviceToHost));
+  if (lay_sync_) {
+    unsigned long long fail = 0;
+    UAII_HIP(hipMemcpy(&fail, lay_sync_->w, sizeof(fail), hipMemcpyDeviceToHost));
+    if (fail) {
+      UAII_HIP(hipMemset(lay_sync_, 0, sizeof(LayersSync)));
+      return Error::make(ErrorCode::Internal, "decode layer kernel: a device-wide wait timed out");
+    }
+  }
   for (int64_t i = 0; i < n; ++i) out[i] = ids[(size_t)i];
   return Error::success();
 }
@@ -825,7 +884,37 @@ Error DecoderProgram::encode_step(bool want_logits) {
   if (opts_.profile) {
     UAII_HIP(hipMemcpy(&pos_host, &state_->pos, 4, hipMemcpyDeviceToHost));
   }
-  for (int64_t li = 0; li < d.n_layers; ++li) {
+  if (lay_ok_) {
+    LayersArgs la{};
+    la.layers = lay_tab_;
+    la.n_layers = (int)d.n_layers;
+    la.dim = d.dim;
+    la.q_dim = d.q_dim;
+    la.kv_dim = d.kv_dim;
+    la.inter = d.layers[0].inter;
+    la.n_heads = (int)d.n_heads;
+    la.n_kv = (int)d.n_kv_heads;
+    la.head_dim = (int)d.head_dim;
+    la.rope_mode = d.rope_mode;
+    la.eps = d.rms_eps;
+    la.x = x_;
+    la.qkv = lay_qkv_;
+    la.attn = attn_;
+    la.h = h_;
+    la.part = lay_part_;
+    la.kv = kv_;
+    la.max_seq = max_ctx_;
+    la.rope = rope_;
+    la.state = state_;
+    la.tap_r1 = tap_r1_;
+    la.tap_r2 = tap_r2_;
+    la.sync = lay_sync_;
+    la.pad = lay_pad_;
+    la.timeout = 20000000ull;  // 0.2 s of the 100 MHz s_memrealtime clock per wait
+    const double kv_read = 2.0 * (double)pos_host * (double)d.kv_dim * (double)elem * (double)d.n_layers;
+    UAII_TRY(timed("layers", lay_wbytes_ + kv_read, [&] { return launch_layers(la, lay_type_, s); }));
+  }
+  for (int64_t li = 0; !lay_ok_ && li < d.n_layers; ++li) {
     const Layer& L = *layers_[(size_t)li];
     const LayerSpec& ls = d.layers[(size_t)li];
     uint8_t* kbase = static_cast<uint8_t*>(kv_) + (size_t)li * 2 * layer_kv;

@@ -112,6 +112,8 @@ class DecoderProgram {
   template <class Prep, class Gemm>
   Error prefill_moe(const Layer& L, const LayerSpec& ls, int64_t m, Prep&& prep, Gemm&& gemm);
   Error encode_step(bool want_logits);
+  template <class Alloc>
+  Error build_layers(Alloc&& alloc);
   void free_dynamic();
 
   DecoderSpec spec_;
@@ -148,6 +150,17 @@ class DecoderProgram {
   float2* rope_ = nullptr;
   float* attn_part_ = nullptr;
   int attn_splits_ = 1;
+
+  // all layers of a decode step in one launch (layers.hip): eligibility, the
+  // device layer table, device-wide counters and the launch's own buffers
+  bool lay_ok_ = false;
+  int lay_type_ = 0;
+  uaii_hip::LayerW* lay_tab_ = nullptr;
+  uaii_hip::LayersSync* lay_sync_ = nullptr;
+  uint8_t* lay_pad_ = nullptr;
+  float* lay_qkv_ = nullptr;
+  float* lay_part_ = nullptr;
+  double lay_wbytes_ = 0.0;  // weight bytes the launch streams
 
   hipGraphExec_t graph_[2] = {nullptr, nullptr};
   std::map<std::string, KernelTiming> timing_;
