@@ -232,55 +232,65 @@ __device__ __forceinline__ Plan make_plan(const LayersArgs& a, int b, int nblk, 
 // stall the issue of a stage.
 constexpr int PT = 14;
 
-// The loaders' position in the stage sequence: layer l, stage r of the layer
-// (phases end at Plan::e0..e3 and T), ring slot; advanced one stage at a time.
-// No table lookups here: an array the compiler placed in scratch memory would
-// add a vector-memory load, counted by vmcnt, to the loaders' path.
-struct Cursor {
-  int l, r, slot;
+// ---- loader side -------------------------------------------------------------------------------
+//
+// The stages of a phase (and of each matrix within the QKV phase) are a run
+// whose lines advance by fixed strides, so the loaders keep, per run, the
+// source of each of their lines and add the stride per stage; only at the
+// start of a run (7-8 per layer) do they work out addresses from the layer
+// table. (Working them out per stage took ~1.1 us of a loader's time per
+// 0.7 us stage.)
+struct Seg {
+  const uint8_t* p16[LX4];       // this wave's 1 KiB lines
+  const uint8_t* p4[LX1];        // and 256-byte lines
+  uint32_t o16[LX4], o4[LX1];    // byte offset in the stage, or ~0u for a padding line
+  int64_t s16, s4;               // per-stage advance of the real lines
+  int left;                      // stages left in the run
 };
 
-// ---- loader side: the DMA lines of one stage ------------------------------------------------
-
-// ring_lds / pad_lds: LDS byte addresses of the ring and of the padding line.
-template <int HD, int NS>
-__device__ __forceinline__ void issue_stage(const LayersArgs& a, const uint64_t* ptab, const Plan& p,
-                                            const Cursor& c, uint32_t ring_lds, uint32_t pad_lds, int b,
-                                            int nblk, int lw, int lane) {
-  const int l = c.l;
-  const uint32_t dst = ring_lds + (uint32_t)(c.slot * SB);
+// The run that starts at stage r of layer l (phases end at Plan::e0..e3 and T).
+template <int HD>
+__device__ __forceinline__ void seg_setup(const LayersArgs& a, const uint64_t* ptab, const Plan& p, int l, int r,
+                                          int lw, Seg& sg) {
   const uint64_t* pt = ptab + l * PT;
   // 1 KiB lines: j < c16 from A0 + 1024 j, then from A1; 256-byte lines likewise
-  const uint8_t *A0 = nullptr, *A1 = nullptr, *B0 = nullptr, *B1 = nullptr;
-  int n16 = 0, c16 = 0, n4 = 0, c4 = 0;
-  // (fields read one by one: the constant-address-space table cannot be copied whole)
-  auto single = [&](int m, int64_t row0, const Geo& ge) {
+  const uint8_t *A0 = a.pad, *A1 = a.pad, *B0 = a.pad, *B1 = a.pad;
+  int n16 = 0, c16 = 0, n4 = 0, c4 = 0, run = 1;
+  int64_t da = 0, db = 0;
+  auto single = [&](int m, int64_t row0, const Geo& ge, int stages) {
     A0 = reinterpret_cast<const uint8_t*>(pt[2 * m]) + row0 * ge.arow;
     B0 = reinterpret_cast<const uint8_t*>(pt[2 * m + 1]) + row0 * ge.brow;
     n16 = c16 = ge.nl;
     n4 = c4 = ge.sl;
+    da = ge.R * ge.arow;
+    db = ge.R * ge.brow;
+    run = stages;
   };
-  if (c.r < p.e0) {
-    const int r = c.r;
+  if (r < p.e0) {
     const int64_t row0 = (p.fq + r) * p.gq.R;
-    if (row0 < a.q_dim) single(0, row0, p.gq);
-    else if (row0 < a.q_dim + a.kv_dim) single(1, row0 - a.q_dim, p.gq);
-    else single(2, row0 - a.q_dim - a.kv_dim, p.gq);
-  } else if (c.r < p.e1) {
-    const int r = c.r - p.e0;
+    const int left = p.e0 - r;
+    if (row0 < a.q_dim) {
+      single(0, row0, p.gq, min((int64_t)left, (a.q_dim - row0) / p.gq.R));
+    } else if (row0 < a.q_dim + a.kv_dim) {
+      single(1, row0 - a.q_dim, p.gq, min((int64_t)left, (a.q_dim + a.kv_dim - row0) / p.gq.R));
+    } else {
+      single(2, row0 - a.q_dim - a.kv_dim, p.gq, left);
+    }
+  } else if (r < p.e1) {
     constexpr int KT = 4096 / HD;
     const int64_t layer_bytes = a.kv_dim * a.max_seq * 2;
     const uint8_t* kb = static_cast<const uint8_t*>(a.kv) + (int64_t)l * 2 * layer_bytes;
-    const int64_t off = ((int64_t)p.ah * a.max_seq + p.k0 + (int64_t)r * KT) * HD * 2;
+    const int64_t off = ((int64_t)p.ah * a.max_seq + p.k0 + (int64_t)(r - p.e0) * KT) * HD * 2;
     A0 = kb + off;
     A1 = kb + layer_bytes + off;
     n16 = 16;
     c16 = 8;
-  } else if (c.r < p.e2) {
-    single(3, (p.fo + (c.r - p.e1)) * p.go.R, p.go);
-  } else if (c.r < p.e3) {
-    const int r = c.r - p.e2;
-    const int64_t j0 = (p.fg + r) * (p.gg.R / 2);
+    da = KT * HD * 2;
+    run = p.e1 - r;
+  } else if (r < p.e2) {
+    single(3, (p.fo + (r - p.e1)) * p.go.R, p.go, p.e2 - r);
+  } else if (r < p.e3) {
+    const int64_t j0 = (p.fg + (r - p.e2)) * (p.gg.R / 2);
     A0 = reinterpret_cast<const uint8_t*>(pt[8]) + j0 * p.gg.arow;
     A1 = reinterpret_cast<const uint8_t*>(pt[10]) + j0 * p.gg.arow;
     B0 = reinterpret_cast<const uint8_t*>(pt[9]) + j0 * p.gg.brow;
@@ -289,30 +299,42 @@ __device__ __forceinline__ void issue_stage(const LayersArgs& a, const uint64_t*
     c16 = p.gg.nl / 2;
     n4 = p.gg.sl;
     c4 = p.gg.sl / 2;
+    da = (p.gg.R / 2) * p.gg.arow;
+    db = (p.gg.R / 2) * p.gg.brow;
+    run = p.e3 - r;
   } else {
-    single(6, (p.fd + (c.r - p.e3)) * p.gd.R, p.gd);
+    single(6, (p.fd + (r - p.e3)) * p.gd.R, p.gd, p.T - r);
   }
 #pragma unroll
   for (int u = 0; u < LX4; ++u) {
     const int j = lw + NLW * u;
-    const uint8_t* src = a.pad + 16 * lane;
-    uint32_t to = pad_lds;
-    if (j < n16) {
-      src = (j < c16 ? A0 + (int64_t)j * 1024 : A1 + (int64_t)(j - c16) * 1024) + 16 * lane;
-      to = dst + (uint32_t)(j * 1024);
-    }
-    dma16(src, __builtin_amdgcn_readfirstlane(to));
+    sg.p16[u] = j < n16 ? (j < c16 ? A0 + (int64_t)j * 1024 : A1 + (int64_t)(j - c16) * 1024) : a.pad;
+    sg.o16[u] = j < n16 ? (uint32_t)(j * 1024) : ~0u;
   }
 #pragma unroll
   for (int u = 0; u < LX1; ++u) {
     const int j = lw + NLW * u;
-    const uint8_t* src = a.pad + 4 * lane;
-    uint32_t to = pad_lds;
-    if (j < n4) {
-      src = (j < c4 ? B0 + (int64_t)j * 256 : B1 + (int64_t)(j - c4) * 256) + 4 * lane;
-      to = dst + (uint32_t)(SQ + j * 256);
-    }
-    dma4(src, __builtin_amdgcn_readfirstlane(to));
+    sg.p4[u] = j < n4 ? (j < c4 ? B0 + (int64_t)j * 256 : B1 + (int64_t)(j - c4) * 256) : a.pad;
+    sg.o4[u] = j < n4 ? (uint32_t)(SQ + j * 256) : ~0u;
+  }
+  sg.s16 = da;
+  sg.s4 = db;
+  sg.left = run;
+}
+
+// One stage's lines into the stage at LDS address slot_lds; the run advances.
+__device__ __forceinline__ void issue_fast(Seg& sg, uint32_t slot_lds, uint32_t pad_lds, int lane) {
+#pragma unroll
+  for (int u = 0; u < LX4; ++u) {
+    const bool real = sg.o16[u] != ~0u;
+    dma16(sg.p16[u] + 16 * lane, real ? slot_lds + sg.o16[u] : pad_lds);
+    if (real) sg.p16[u] += sg.s16;
+  }
+#pragma unroll
+  for (int u = 0; u < LX1; ++u) {
+    const bool real = sg.o4[u] != ~0u;
+    dma4(sg.p4[u] + 4 * lane, real ? slot_lds + sg.o4[u] : pad_lds);
+    if (real) sg.p4[u] += sg.s4;
   }
 }
 
@@ -404,12 +426,31 @@ __device__ __forceinline__ float dot_q4(uint4 qv, uint32_t sbits, const XP& xp) 
 // Phase input: this compute wave's chunk column of src (optionally RMSNorm'd,
 // norm.cpp:89-130: x * (1 / sqrt(mean(x^2) + eps)) * w, two roundings). Every
 // wave of the block calls it (one block barrier when norm_w is set).
-__device__ __forceinline__ void stage_in(const float* src, const float* norm_w, float eps, int64_t K, const Geo& ge,
-                                bool comp, int wave, int lane, float* red, XP& xp) {
+// The RMSNorm weights of this wave's chunk, loaded ahead of the device-wide
+// wait that precedes their phase (they do not depend on it).
+__device__ __forceinline__ void load_norm(const float* norm_w, const Geo& ge, bool comp, int wave, int lane,
+                                          float* w) {
+  const int c = wave % ge.ncp;
+  const int64_t t = (int64_t)c * 64 + lane;
+  if (comp && c < ge.ncol && norm_w) {
+    const float4* w4 = reinterpret_cast<const float4*>(norm_w + 32 * t);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const float4 f = w4[k];
+      w[4 * k] = f.x; w[4 * k + 1] = f.y; w[4 * k + 2] = f.z; w[4 * k + 3] = f.w;
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < 32; ++k) w[k] = 0.0f;
+  }
+}
+
+// w: this wave's RMSNorm weights from load_norm (norm set) or unused.
+__device__ __forceinline__ void stage_in(const float* src, bool norm, const float* w, float eps, int64_t K,
+                                         const Geo& ge, bool comp, int wave, int lane, float* red, XP& xp) {
   const int c = wave % ge.ncp;
   const bool act = comp && c < ge.ncol;
   float v[32];
-  float w[32];
   const int64_t t = (int64_t)c * 64 + lane;
   if (act) {
 #pragma unroll
@@ -417,23 +458,15 @@ __device__ __forceinline__ void stage_in(const float* src, const float* norm_w, 
       const float4 f = ldf4(src, 32 * t + 4 * k);
       v[4 * k] = f.x; v[4 * k + 1] = f.y; v[4 * k + 2] = f.z; v[4 * k + 3] = f.w;
     }
-    if (norm_w) {
-      const float4* w4 = reinterpret_cast<const float4*>(norm_w + 32 * t);
-#pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const float4 f = w4[k];
-        w[4 * k] = f.x; w[4 * k + 1] = f.y; w[4 * k + 2] = f.z; w[4 * k + 3] = f.w;
-      }
-    }
   } else {
 #pragma unroll
-    for (int k = 0; k < 32; ++k) { v[k] = 0.0f; w[k] = 0.0f; }
+    for (int k = 0; k < 32; ++k) v[k] = 0.0f;
   }
-  if (norm_w) {
+  if (norm) {
     float ss = 0.0f;
 #pragma unroll
     for (int k = 0; k < 32; ++k) ss += v[k] * v[k];
-    ss = wave_sum(ss);
+    ss = wave_total(ss);
     if (comp && wave < ge.ncp && c < ge.ncol && lane == 0) red[c] = ss;
     block_sync();
     float tot = 0.0f;
@@ -617,19 +650,19 @@ __global__ void __launch_bounds__(NTH, 1) k_layers(LayersArgs a) {
   u64 nbar = 0;
   bool dead = false;
 
-  // loaders: the next stage to fetch; everyone: the slot of the stage consumed next
-  Cursor cur{0, 0, 0};
+  // loaders: the run being fetched and the position (layer il, stage ir, slot
+  // islot) of the next stage; everyone: the slot of the stage consumed next
+  Seg sg;
+  int il = 0, ir = 0, islot = 0;
   const uint32_t ring_lds = lds_addr(ring), pad_lds_addr = lds_addr(pad_lds);
   int cslot = 0;
   int64_t issued = 0;
   auto issue_next = [&]() __attribute__((always_inline)) {
-    issue_stage<HD, NS>(a, ptab, p, cur, ring_lds, pad_lds_addr, b, nblk, lw, lane);
+    issue_fast(sg, ring_lds + (uint32_t)(islot * SB), pad_lds_addr, lane);
     ++issued;
-    if (++cur.r == p.T) { cur.r = 0; ++cur.l; }
-    cur.slot = cur.slot + 1 == NS ? 0 : cur.slot + 1;
-    cur.l = __builtin_amdgcn_readfirstlane(cur.l);
-    cur.r = __builtin_amdgcn_readfirstlane(cur.r);
-    cur.slot = __builtin_amdgcn_readfirstlane(cur.slot);
+    islot = islot + 1 == NS ? 0 : islot + 1;
+    if (++ir == p.T) { ir = 0; ++il; }
+    if (--sg.left == 0 && issued < p.total) seg_setup<HD>(a, ptab, p, il, ir, lw, sg);
   };
   // Stage gi: the loaders wait for their lines of it (at most NS-2 later stages
   // outstanding), one block barrier, then they refill the slot of stage gi-1,
@@ -683,13 +716,15 @@ __global__ void __launch_bounds__(NTH, 1) k_layers(LayersArgs a) {
   }
   wait_vm<0>();
   block_sync();
-  if (!comp) {
+  if (!comp && p.total > 0) {
+    seg_setup<HD>(a, ptab, p, 0, 0, lw, sg);
     for (int k = 0; k < NS - 1; ++k)
       if (issued < p.total) issue_next();
   }
 
   int64_t g = 0;
   XP xp;
+  float wpre[32];  // RMSNorm weights of the next normalised phase
   for (int l = 0; l < a.n_layers; ++l) {
     // per-lane values are recomputed inside each layer instead of being kept
     // live (or spilled) across the whole loop
@@ -701,7 +736,8 @@ __global__ void __launch_bounds__(NTH, 1) k_layers(LayersArgs a) {
     const float* bv = lws[l].bv;
 
     // ---- Q, K, V projections (raw, + bias) ----
-    stage_in(a.x, attn_norm, a.eps, a.dim, p.gq, comp, wave, lane, red, xp);
+    if (l == 0) load_norm(attn_norm, p.gq, comp, wave, lane, wpre);
+    stage_in(a.x, attn_norm != nullptr, wpre, a.eps, a.dim, p.gq, comp, wave, lane, red, xp);
     for (int i = 0; i < p.nq; ++i, ++g) {
       const uint8_t* st = stage_begin(g);
       if (comp) gemv_stage(st, p.gq, i, xp, part, wave, lane);
@@ -857,7 +893,7 @@ __global__ void __launch_bounds__(NTH, 1) k_layers(LayersArgs a) {
       for (int t = tid; t < p.no * p.go.R; t += NCW * 64)
         resid[t] = ldf(a.x, (p.fo + t / p.go.R) * p.go.R + t % p.go.R);
     }
-    stage_in(a.attn, nullptr, 0.0f, a.q_dim, p.go, comp, wave, lane, red, xp);
+    stage_in(a.attn, false, wpre, 0.0f, a.q_dim, p.go, comp, wave, lane, red, xp);
     for (int i = 0; i < p.no; ++i, ++g) {
       const uint8_t* st = stage_begin(g);
       if (comp) gemv_stage(st, p.go, i, xp, part, wave, lane);
@@ -873,10 +909,11 @@ __global__ void __launch_bounds__(NTH, 1) k_layers(LayersArgs a) {
         if (a.tap_r1) a.tap_r1[(int64_t)l * a.dim + gr] = v;
       }
     }
+    load_norm(ffn_norm, p.gg, comp, wave, lane, wpre);
     grid_sync();
 
     // ---- gate / up, SwiGLU ----
-    stage_in(a.x, ffn_norm, a.eps, a.dim, p.gg, comp, wave, lane, red, xp);
+    stage_in(a.x, ffn_norm != nullptr, wpre, a.eps, a.dim, p.gg, comp, wave, lane, red, xp);
     for (int i = 0; i < p.ng; ++i, ++g) {
       const uint8_t* st = stage_begin(g);
       if (comp) gemv_stage(st, p.gg, i, xp, part, wave, lane);
@@ -899,7 +936,7 @@ __global__ void __launch_bounds__(NTH, 1) k_layers(LayersArgs a) {
       for (int t = tid; t < p.nd * p.gd.R; t += NCW * 64)
         resid[t] = ldf(a.x, (p.fd + t / p.gd.R) * p.gd.R + t % p.gd.R);
     }
-    stage_in(a.h, nullptr, 0.0f, a.inter, p.gd, comp, wave, lane, red, xp);
+    stage_in(a.h, false, wpre, 0.0f, a.inter, p.gd, comp, wave, lane, red, xp);
     for (int i = 0; i < p.nd; ++i, ++g) {
       const uint8_t* st = stage_begin(g);
       if (comp) gemv_stage(st, p.gd, i, xp, part, wave, lane);
@@ -915,7 +952,10 @@ __global__ void __launch_bounds__(NTH, 1) k_layers(LayersArgs a) {
         if (a.tap_r2) a.tap_r2[(int64_t)l * a.dim + gr] = v;
       }
     }
-    if (l + 1 < a.n_layers) grid_sync();
+    if (l + 1 < a.n_layers) {
+      load_norm(lws[l + 1].attn_norm, p.gq, comp, wave, lane, wpre);
+      grid_sync();
+    }
   }
 
   // every DMA landed (none is outstanding once the last stage was consumed)

@@ -297,7 +297,7 @@ Error DecoderProgram::build(const DecoderSpec& spec, const ProgramOptions& opts)
 }
 
 // The one-launch layer kernel (UAII_LAYERS=1; off by default: on the 8B
-// decode it measures 350 tok/s against 428 for the per-layer launches) takes
+// decode it measures 362 tok/s against 428 for the per-layer launches) takes
 // dense SwiGLU models whose seven layer matrices share one block format, with
 // an f16 KV cache.
 template <class Alloc>
