@@ -49,9 +49,10 @@ def maxrel(a, b):
     return float(np.abs(np.asarray(a, np.float64) - b).max() / max(np.abs(b).max(), 1e-30))
 
 
-def run(path, cfg, prompt, n_new, layers=True, profile=False):
-    old = os.environ.get("UAII_LAYERS")
+def run(path, cfg, prompt, n_new, layers=True, profile=False, ring="1"):
+    saved = {k: os.environ.get(k) for k in ("UAII_LAYERS", "UAII_RING")}
     os.environ["UAII_LAYERS"] = "1" if layers else "0"
+    os.environ["UAII_RING"] = ring
     try:
         with uaii_amd.Session(path, kv_f16=True, profile=profile) as s:
             ids = s.generate(prompt, n_new)
@@ -61,10 +62,11 @@ def run(path, cfg, prompt, n_new, layers=True, profile=False):
                 taps[f"r2_{li}"] = s.get(f"blk.{li}.resid2")
             summary = s.profile_summary() if profile else ""
     finally:
-        if old is None:
-            del os.environ["UAII_LAYERS"]
-        else:
-            os.environ["UAII_LAYERS"] = old
+        for k, v in saved.items():
+            if v is None:
+                del os.environ[k]
+            else:
+                os.environ[k] = v
     return ids, taps, summary
 
 
@@ -118,3 +120,32 @@ def test_layers_long_context():
     ids2, _, _ = run(path, cfg, short, 8)
     want2, _ = oracle.Model(path).generate(short, 8, kv_f16=True)
     assert np.array_equal(ids2, want2)
+
+
+@pytest.mark.parametrize("mode", ["1", "2"])
+@pytest.mark.parametrize("name", [n for n in CFGS if n != "g1_hd64_long"])
+def test_ring_gemv_match_oracle(name, mode):
+    """Per-layer launches with Q4_0 GEMVs on the LDS-ring kernel: mode 1 (default) the
+    O and down projections, mode 2 also QKV (RoPE mode 0 only) and gate/up."""
+    cfg = CFGS[name]
+    path = synth.cached_model(cfg)
+    prompt = np.random.default_rng(cfg.seed + 3).integers(0, cfg.vocab, 40).astype(np.int64)
+    print(name, mode, flush=True)
+    ids, taps, _ = run(path, cfg, prompt, 24, layers=False, ring=mode)
+    want_ids, want = oracle.Model(path).generate(prompt, 24, kv_f16=True)
+    assert np.array_equal(ids, want_ids)
+    assert maxrel(taps["logits"], want["logits"]) < 2e-3
+    for li in range(cfg.n_layers):
+        assert maxrel(taps[f"r1_{li}"], want["resid1"][li]) < 2e-3
+        assert maxrel(taps[f"r2_{li}"], want["resid2"][li]) < 2e-3
+
+
+def test_ring_gemv_matches_gemv():
+    cfg = CFGS["g4_hd128"]
+    path = synth.cached_model(cfg)
+    prompt = np.random.default_rng(cfg.seed + 11).integers(0, cfg.vocab, 5).astype(np.int64)
+    ids, taps, _ = run(path, cfg, prompt, 40, layers=False, ring="2")
+    ids0, taps0, _ = run(path, cfg, prompt, 40, layers=False, ring="0")
+    assert np.array_equal(ids, ids0)
+    for k in taps:
+        assert maxrel(taps[k], taps0[k]) < 1e-4, k

@@ -445,7 +445,53 @@ __device__ __forceinline__ void load_norm(const float* norm_w, const Geo& ge, bo
   }
 }
 
-// w: this wave's RMSNorm weights from load_norm (norm set) or unused.
+// This wave's chunk of src (zeros for an idle column).
+template <bool SC1>
+__device__ __forceinline__ void stage_load(const float* src, const Geo& ge, bool comp, int wave, int lane, float* v) {
+  const int c = wave % ge.ncp;
+  const int64_t t = (int64_t)c * 64 + lane;
+  if (comp && c < ge.ncol) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const float4 f = SC1 ? ldf4(src, 32 * t + 4 * k) : reinterpret_cast<const float4*>(src)[8 * t + k];
+      v[4 * k] = f.x; v[4 * k + 1] = f.y; v[4 * k + 2] = f.z; v[4 * k + 3] = f.w;
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < 32; ++k) v[k] = 0.0f;
+  }
+}
+
+// RMSNorm (one block barrier when norm) and the pairs of the loaded chunk v.
+__device__ __forceinline__ void stage_finish(float* v, bool norm, const float* w, float eps, int64_t K, const Geo& ge,
+                                             bool comp, int wave, int lane, float* red, XP& xp) {
+  const int c = wave % ge.ncp;
+  const bool act = comp && c < ge.ncol;
+  if (norm) {
+    float ss = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 32; ++k) ss += v[k] * v[k];
+    ss = wave_total(ss);
+    if (comp && wave < ge.ncp && c < ge.ncol && lane == 0) red[c] = ss;
+    block_sync();
+    float tot = 0.0f;
+    for (int k = 0; k < ge.ncol; ++k) tot += red[k];
+    const float inv = 1.0f / sqrtf(tot / (float)K + eps);
+#pragma unroll
+    for (int k = 0; k < 32; ++k) v[k] = fmul_rn(fmul_rn(v[k], inv), w[k]);
+  }
+  if (act) {
+    make_pairs(v, xp);
+  } else {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) xp.p[k] = make_uint4(0u, 0u, 0u, 0u);
+    xp.c = make_float2(0.0f, 0.0f);
+  }
+}
+
+// w: this wave's RMSNorm weights from load_norm (norm set) or unused. SC1:
+// src was written in this launch by other blocks (device-coherent loads).
+template <bool SC1 = true>
 __device__ __forceinline__ void stage_in(const float* src, bool norm, const float* w, float eps, int64_t K,
                                          const Geo& ge, bool comp, int wave, int lane, float* red, XP& xp) {
   const int c = wave % ge.ncp;
@@ -455,7 +501,7 @@ __device__ __forceinline__ void stage_in(const float* src, bool norm, const floa
   if (act) {
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
-      const float4 f = ldf4(src, 32 * t + 4 * k);
+      const float4 f = SC1 ? ldf4(src, 32 * t + 4 * k) : reinterpret_cast<const float4*>(src)[8 * t + k];
       v[4 * k] = f.x; v[4 * k + 1] = f.y; v[4 * k + 2] = f.z; v[4 * k + 3] = f.w;
     }
   } else {
@@ -973,6 +1019,223 @@ __global__ void __launch_bounds__(NTH, 1) k_layers(LayersArgs a) {
   }
 }
 
+// ---- one GEMV through the ring (decode, between ordinary launches) -----------------------------
+
+constexpr int RING_NS = 8;
+constexpr int RING_PRO = 2;
+
+// Wait until at most k stages' DMA lines (k * ND instructions) are outstanding.
+__device__ __forceinline__ void wait_stages(int k) {
+  switch (k) {
+    case 0: wait_vm<0>(); break;
+    case 1: wait_vm<ND>(); break;
+    case 2: wait_vm<2 * ND>(); break;
+    case 3: wait_vm<3 * ND>(); break;
+    case 4: wait_vm<4 * ND>(); break;
+    case 5: wait_vm<5 * ND>(); break;
+    case 6: wait_vm<6 * ND>(); break;
+    default: wait_vm<7 * ND>(); break;
+  }
+}
+
+// Partial row sums of two consecutive stages (the second only if `two`): all
+// four rows' bytes are read before any dot, so the dependent chains of the
+// reductions overlap.
+__device__ __forceinline__ void gemv_stage2(const uint8_t* st0, const uint8_t* st1, bool two, const Geo& ge,
+                                            int si, const XP& xp, float* part, int wave, int lane) {
+  const int c = wave % ge.ncp, rg = wave / ge.ncp;
+  if (c >= ge.ncol) return;
+  const int t = c * 64 + lane;
+  uint4 qv[4];
+  uint32_t sb[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const uint8_t* st = k < 2 ? st0 : (two ? st1 : st0);
+    const int r = 2 * rg + (k & 1);
+    qv[k] = *reinterpret_cast<const uint4*>(st + r * ge.arow + 16 * t);
+    sb[k] = *reinterpret_cast<const uint16_t*>(st + SQ + r * ge.brow + 2 * t);
+  }
+  float d[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) d[k] = dot_q4(qv[k], sb[k], xp);
+#pragma unroll
+  for (int k = 0; k < 4; ++k) d[k] = group_sum<16>(d[k]);
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const float v = (rl(d[k], 0) + rl(d[k], 16)) + (rl(d[k], 32) + rl(d[k], 48));
+    const int r = 2 * rg + (k & 1);
+    if (lane == 0 && (k < 2 || two)) part[((si + (k >> 1)) * ge.R + r) * ge.ncol + c] = v;
+  }
+}
+
+// Stages of a ring GEMV (R rows each; EPI_SWIGLU: R/2 gate + R/2 up rows).
+__device__ __forceinline__ int64_t ring_stages_of(const RingArgs& a, const Geo& ge) {
+  if (a.epi == EPI_SWIGLU) return a.rows[0] / (ge.R / 2);
+  int64_t rows = 0;
+  for (int k = 0; k < a.nseg; ++k) rows += a.rows[k];
+  return rows / ge.R;
+}
+
+// The run of stages that starts at global stage gs and ends at the block's
+// last stage gend or at a segment boundary.
+__device__ __forceinline__ void ring_seg(const RingArgs& a, const Geo& ge, int64_t gs, int64_t gend, int lw,
+                                         Seg& sg) {
+  const uint8_t *A0 = a.pad, *A1 = a.pad, *B0 = a.pad, *B1 = a.pad;
+  int n16, c16, n4, c4;
+  int64_t da, db, run;
+  if (a.epi == EPI_SWIGLU) {
+    const int64_t j0 = gs * (ge.R / 2);
+    A0 = a.w[0].a + j0 * ge.arow;
+    A1 = a.w[1].a + j0 * ge.arow;
+    B0 = a.w[0].b + j0 * ge.brow;
+    B1 = a.w[1].b + j0 * ge.brow;
+    n16 = ge.nl; c16 = ge.nl / 2;
+    n4 = ge.sl; c4 = ge.sl / 2;
+    da = (ge.R / 2) * ge.arow;
+    db = (ge.R / 2) * ge.brow;
+    run = gend - gs;
+  } else {
+    int64_t row0 = gs * ge.R;
+    int k = 0;
+    while (k + 1 < a.nseg && row0 >= a.rows[k]) { row0 -= a.rows[k]; ++k; }
+    const DevWeight& w = a.w[k];
+    A0 = w.a + row0 * ge.arow;
+    B0 = w.b + row0 * ge.brow;
+    n16 = c16 = ge.nl;
+    n4 = c4 = ge.sl;
+    da = ge.R * ge.arow;
+    db = ge.R * ge.brow;
+    run = min(gend - gs, (a.rows[k] - row0) / ge.R);
+  }
+#pragma unroll
+  for (int u = 0; u < LX4; ++u) {
+    const int j = lw + NLW * u;
+    sg.p16[u] = j < n16 ? (j < c16 ? A0 + (int64_t)j * 1024 : A1 + (int64_t)(j - c16) * 1024) : a.pad;
+    sg.o16[u] = j < n16 ? (uint32_t)(j * 1024) : ~0u;
+  }
+#pragma unroll
+  for (int u = 0; u < LX1; ++u) {
+    const int j = lw + NLW * u;
+    sg.p4[u] = j < n4 ? (j < c4 ? B0 + (int64_t)j * 256 : B1 + (int64_t)(j - c4) * 256) : a.pad;
+    sg.o4[u] = j < n4 ? (uint32_t)(SQ + j * 256) : ~0u;
+  }
+  sg.s16 = da;
+  sg.s4 = db;
+  sg.left = (int)run;
+}
+
+__global__ void __launch_bounds__(NTH, 1) k_ring_gemv(RingArgs a) {
+  constexpr int NS = RING_NS;
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  __shared__ float red[64];
+  uint8_t* ring = lds;
+  float* part = reinterpret_cast<float*>(lds + NS * SB + 1024);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const bool comp = wave < NCW;
+  const int lw = wave - NCW;
+  const int nblk = gridDim.x, b = blockIdx.x;
+  const Geo ge = geo_of(a.K);
+  const int64_t T = ring_stages_of(a, ge);
+  const int n = share(T, b, nblk);
+  const int64_t f = first_stage(T, b, nblk);
+  const uint32_t ring_lds = lds_addr(ring), pad_lds = lds_addr(lds + NS * SB);
+
+  Seg sg;
+  int issued = 0, islot = 0, cslot = 0;
+  auto issue_next = [&]() __attribute__((always_inline)) {
+    issue_fast(sg, ring_lds + (uint32_t)(islot * SB), pad_lds, lane);
+    ++issued;
+    islot = islot + 1 == NS ? 0 : islot + 1;
+    if (--sg.left == 0 && issued < n) ring_seg(a, ge, f + issued, f + n, lw, sg);
+  };
+  // The input vector's loads go out first, then the first RING_PRO stages:
+  // every CU's first requests of a launch complete only when the whole grid's
+  // burst has been served, so a small first burst gets the first data (and the
+  // input) back sooner. Stages then go in pairs; each pair waits for its two
+  // stages, and the loaders refill up to 4 stages per pair (the ring deepens
+  // to NS-2 stages ahead).
+  float w[32];
+  load_norm(a.norm_w, ge, comp, wave, lane, w);
+  float v[32];
+  stage_load<false>(a.x, ge, comp, wave, lane, v);
+  block_sync();
+  if (!comp && n > 0) {
+    ring_seg(a, ge, f, f + n, lw, sg);
+    for (int k = 0; k < RING_PRO; ++k)
+      if (issued < n) issue_next();
+  }
+  XP xp;
+  stage_finish(v, a.norm_w != nullptr, w, a.eps, a.K, ge, comp, wave, lane, red, xp);
+  for (int i = 0; i < n; i += 2) {
+    if (!comp) wait_stages(issued - min(i + 2, n));
+    block_sync();
+    if (!comp) {
+      const int cap = min(n, i + NS);  // stages below i + NS have a free slot
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        if (issued < cap) issue_next();
+    }
+    const uint8_t* st0 = ring + cslot * SB;
+    cslot = cslot + 1 == NS ? 0 : cslot + 1;
+    const uint8_t* st1 = ring + cslot * SB;
+    cslot = cslot + 1 == NS ? 0 : cslot + 1;
+    if (comp) gemv_stage2(st0, st1, i + 1 < n, ge, i, xp, part, wave, lane);
+  }
+  block_sync();
+  if (!comp) return;
+  // epilogues (gemv.hip's, on the block's rows)
+  if (a.epi == EPI_SWIGLU) {
+    const int hr = ge.R / 2;
+    for (int t = tid; t < n * hr; t += NCW * 64) {
+      const int i = t / hr, r = t % hr;
+      const float gv = row_sum(part, ge, i, r), uv = row_sum(part, ge, i, r + hr);
+      a.y[(f + i) * hr + r] = gv / (1.0f + expf(-gv)) * uv;  // silu(g) * u (elementwise.cpp:73-84)
+    }
+  } else if (a.epi == EPI_QKV) {
+    const int pos = a.state->pos;
+    const int hr = ge.R / 2;
+    for (int t = tid; t < n * hr; t += NCW * 64) {
+      const int i = t / hr, r0 = 2 * (t % hr);
+      int64_t l = (f + i) * ge.R + r0;
+      int k = 0;
+      while (k + 1 < a.nseg && l >= a.rows[k]) { l -= a.rows[k]; ++k; }
+      float v0 = row_sum(part, ge, i, r0), v1 = row_sum(part, ge, i, r0 + 1);
+      if (a.bias[k]) { v0 = v0 + a.bias[k][l]; v1 = v1 + a.bias[k][l + 1]; }
+      const int64_t hd = a.head_dim;
+      if (k != 2) {  // RoPE mode 0 on q and k (transformer.cpp:144-220)
+        const float2 cs = a.rope[(int64_t)pos * (hd / 2) + ((l % hd) >> 1)];
+        const float n0 = v0 * cs.x - v1 * cs.y;
+        const float n1 = v0 * cs.y + v1 * cs.x;
+        v0 = n0; v1 = n1;
+      }
+      if (k == 0) {
+        a.y[l] = v0;
+        a.y[l + 1] = v1;
+      } else {  // K after RoPE and raw V into the cache at pos (kv_cache.hpp:80-120)
+        void* cache = k == 1 ? a.kcache : a.vcache;
+        const int64_t o0 = ((l / hd) * a.max_seq + pos) * hd + (l % hd);
+        if (a.kv_f16) {
+          reinterpret_cast<__half*>(cache)[o0] = __float2half(v0);
+          reinterpret_cast<__half*>(cache)[o0 + 1] = __float2half(v1);
+        } else {
+          reinterpret_cast<float*>(cache)[o0] = v0;
+          reinterpret_cast<float*>(cache)[o0 + 1] = v1;
+        }
+      }
+    }
+  } else {
+    for (int t = tid; t < n * ge.R; t += NCW * 64) {
+      const int i = t / ge.R, r = t % ge.R;
+      const int64_t gr = (f + i) * ge.R + r;
+      float v = row_sum(part, ge, i, r);
+      if (a.epi == EPI_ADD) v = a.y[gr] + v;
+      a.y[gr] = v;
+      if (a.tap) a.tap[gr] = v;
+    }
+  }
+}
+
 int dev_cus() {
   int dev = 0, n = 0;
   if (hipGetDevice(&dev) != hipSuccess) return 0;
@@ -1056,6 +1319,54 @@ bool layers_supported(int type, int n_layers, int64_t dim, int64_t q_dim, int64_
   if (head_dim == 128) lds = G == 8 ? layers_lds<128, 8>(n_layers) : layers_lds<128, 4>(n_layers);
   else lds = G == 8 ? layers_lds<64, 8>(n_layers) : layers_lds<64, 4>(n_layers);
   return lds <= layers_lds_cap();
+}
+
+bool ring_gemv_supported(const RingArgs& a) {
+  if (a.nseg < 1 || a.nseg > 3 || a.K <= 0 || a.K % 2048 || a.K > 16384 || !a.x || !a.y || !a.pad) return false;
+  if (a.epi != EPI_STORE && a.epi != EPI_ADD && a.epi != EPI_QKV && a.epi != EPI_SWIGLU) return false;
+  if (a.epi == EPI_SWIGLU && a.nseg != 2) return false;
+  if (a.epi == EPI_QKV && (a.nseg != 3 || a.head_dim < 2 || a.head_dim % 2 || !a.rope || !a.state || !a.kcache ||
+                           !a.vcache))
+    return false;
+  const Geo ge = geo_of(a.K);
+  int64_t T = 0;
+  for (int k = 0; k < a.nseg; ++k) {
+    const DevWeight& w = a.w[k];
+    if (w.type != T_Q4_0 || w.cols != a.K || w.a_row != ge.arow || w.b_row != ge.brow) return false;
+    const int64_t unit = a.epi == EPI_SWIGLU ? ge.R / 2 : ge.R;
+    const int64_t rows = a.epi == EPI_SWIGLU ? a.rows[0] : a.rows[k];
+    if (rows <= 0 || rows % unit || w.rows < rows) return false;
+    if (a.epi != EPI_SWIGLU) T += rows / ge.R;
+  }
+  if (a.epi == EPI_SWIGLU) T = a.rows[0] / (ge.R / 2);
+  if (a.epi == EPI_QKV && a.head_dim % 2) return false;
+  const int nblk = dev_cus();
+  if (nblk < 1) return false;
+  const int64_t most = (T + nblk - 1) / nblk;
+  if (most * ge.R * ge.ncol > PART_MAX) return false;
+  return (size_t)RING_NS * SB + 1024 + PART_MAX * 4 <= layers_lds_cap();
+}
+
+hipError_t prepare_ring_gemv() {
+  static std::once_flag once;
+  static hipError_t prep = hipSuccess;
+  std::call_once(once, [] {
+    const size_t lds = (size_t)RING_NS * SB + 1024 + PART_MAX * 4;
+    prep = hipFuncSetAttribute((const void*)k_ring_gemv, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    int per_cu = 0;
+    if (prep == hipSuccess) prep = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_ring_gemv, NTH, lds);
+    if (prep == hipSuccess && per_cu < 1) prep = hipErrorInvalidConfiguration;
+  });
+  return prep;
+}
+
+hipError_t launch_ring_gemv(const RingArgs& a, hipStream_t s) {
+  if (!ring_gemv_supported(a)) return hipErrorInvalidValue;
+  const hipError_t prep = prepare_ring_gemv();
+  if (prep != hipSuccess) return prep;
+  const size_t lds = (size_t)RING_NS * SB + 1024 + PART_MAX * 4;
+  UAII_LAUNCH(k_ring_gemv, dim3(dev_cus()), dim3(NTH), lds, s, a);
+  return hipGetLastError();
 }
 
 hipError_t prepare_layers(int head_dim, int G) {

@@ -184,6 +184,38 @@ int layers_splits(int n_kv);
 hipError_t prepare_layers(int head_dim, int G);
 hipError_t launch_layers(const LayersArgs& a, int type, hipStream_t s);
 
+// ---- one decode GEMV with its weights streamed through an LDS ring ----------------
+
+// Loader waves fetch the block's rows global -> LDS while compute waves take
+// stages out of LDS (layers.hip), so the dot products never hold back the next
+// loads. Q4_0 only; see ring_gemv_supported for the shapes.
+struct RingArgs {
+  DevWeight w[3];        // stacked row segments (Q, K, V), or gate (0) / up (1) for EPI_SWIGLU
+  int64_t rows[3];       // rows per segment (EPI_SWIGLU: rows[0] = output size)
+  int nseg;
+  int epi;               // EPI_STORE, EPI_ADD, EPI_QKV (RoPE mode 0), EPI_SWIGLU
+  int64_t K;
+  const float* x;        // input [K]
+  const float* norm_w;   // RMSNorm weight or null
+  float eps;
+  float* y;              // output (EPI_QKV: q)
+  float* tap;            // EPI_ADD: copy of each written value, or null
+  // EPI_QKV
+  const float* bias[3];
+  void* kcache;          // layer base [n_kv][max_seq][hd]
+  void* vcache;
+  int kv_f16;
+  int64_t max_seq;
+  int head_dim;
+  const float2* rope;    // [max_seq][hd / 2]
+  const StepState* state;
+  const uint8_t* pad;    // >= 1 KiB of device memory read by the padding DMA lines
+};
+
+bool ring_gemv_supported(const RingArgs& a);
+hipError_t prepare_ring_gemv();
+hipError_t launch_ring_gemv(const RingArgs& a, hipStream_t s);
+
 // ---- prefill (M > 1 prompt tokens, matrix cores) ---------------------------------------
 
 // Activation rows prepared for the MFMA GEMM: x * 2^e = hi + lo in f16 (each

@@ -293,6 +293,16 @@ Error DecoderProgram::build(const DecoderSpec& spec, const ProgramOptions& opts)
     if (std::string(env) == "0") pf_ok_ = false;
   }
   UAII_TRY(build_layers(alloc));
+  UAII_TRY(alloc(1024, (void**)&ring_pad_));
+  {
+    // the ring kernel measures faster for the residual-add GEMVs (O, down) and
+    // slower for QKV and gate/up (whose RMSNorm staging the first loads wait
+    // behind); UAII_RING=2 takes all four, 0 none
+    const char* env = std::getenv("UAII_RING");
+    ring_mode_ = env ? std::atoi(env) : 1;
+    if (prepare_ring_gemv() != hipSuccess) ring_mode_ = 0;
+    (void)hipGetLastError();
+  }
   return Error::success();
 }
 
@@ -940,7 +950,30 @@ Error DecoderProgram::encode_step(bool want_logits) {
     a.rope = rope_;
     a.state = state_;
     const double qkv_bytes = gemv_bytes(L.wq.view) + gemv_bytes(L.wk.view) + gemv_bytes(L.wv.view);
-    UAII_TRY(timed("gemv_qkv", qkv_bytes, [&] { return launch_gemv(a, s); }));
+    RingArgs rq{};
+    rq.w[0] = L.wq.view; rq.w[1] = L.wk.view; rq.w[2] = L.wv.view;
+    rq.rows[0] = d.q_dim; rq.rows[1] = d.kv_dim; rq.rows[2] = d.kv_dim;
+    rq.nseg = 3;
+    rq.epi = EPI_QKV;
+    rq.K = d.dim;
+    rq.x = x_;
+    rq.norm_w = L.attn_norm;
+    rq.eps = d.rms_eps;
+    rq.y = q_;
+    rq.bias[0] = L.bq; rq.bias[1] = L.bk; rq.bias[2] = L.bv;
+    rq.kcache = kbase;
+    rq.vcache = vbase;
+    rq.kv_f16 = opts_.kv_f16 ? 1 : 0;
+    rq.max_seq = max_ctx_;
+    rq.head_dim = (int)d.head_dim;
+    rq.rope = rope_;
+    rq.state = state_;
+    rq.pad = ring_pad_;
+    if (ring_mode_ >= 2 && d.rope_mode == 0 && ring_gemv_supported(rq)) {
+      UAII_TRY(timed("gemv_qkv", qkv_bytes, [&] { return launch_ring_gemv(rq, s); }));
+    } else {
+      UAII_TRY(timed("gemv_qkv", qkv_bytes, [&] { return launch_gemv(a, s); }));
+    }
 
     AttnArgs at{};
     at.q = q_;
@@ -970,7 +1003,21 @@ Error DecoderProgram::encode_step(bool want_logits) {
     o.seg[0].w = L.wo.view;
     o.seg[0].rows = d.dim;
     o.state = state_;
-    UAII_TRY(timed("gemv_o", gemv_bytes(L.wo.view), [&] { return launch_gemv(o, s); }));
+    RingArgs ro{};
+    ro.w[0] = L.wo.view;
+    ro.rows[0] = d.dim;
+    ro.nseg = 1;
+    ro.epi = EPI_ADD;
+    ro.K = d.q_dim;
+    ro.x = attn_;
+    ro.y = x_;
+    ro.tap = o.tap;
+    ro.pad = ring_pad_;
+    if (ring_mode_ >= 1 && ring_gemv_supported(ro)) {
+      UAII_TRY(timed("gemv_o", gemv_bytes(L.wo.view), [&] { return launch_ring_gemv(ro, s); }));
+    } else {
+      UAII_TRY(timed("gemv_o", gemv_bytes(L.wo.view), [&] { return launch_gemv(o, s); }));
+    }
 
     if (ls.ffn == LayerSpec::kSwiGLU) {
       GemvArgs g{};
@@ -985,8 +1032,24 @@ Error DecoderProgram::encode_step(bool want_logits) {
       g.seg[0].w2 = L.up.view;
       g.seg[0].rows = 2 * ls.inter;
       g.state = state_;
-      UAII_TRY(timed("gemv_gate_up", gemv_bytes(L.gate.view) + gemv_bytes(L.up.view),
-                     [&] { return launch_gemv(g, s); }));
+      RingArgs rg{};
+      rg.w[0] = L.gate.view;
+      rg.w[1] = L.up.view;
+      rg.rows[0] = ls.inter;
+      rg.nseg = 2;
+      rg.epi = EPI_SWIGLU;
+      rg.K = d.dim;
+      rg.x = x_;
+      rg.norm_w = L.ffn_norm;
+      rg.eps = d.rms_eps;
+      rg.y = h_;
+      rg.pad = ring_pad_;
+      const double gu_bytes = gemv_bytes(L.gate.view) + gemv_bytes(L.up.view);
+      if (ring_mode_ >= 2 && ring_gemv_supported(rg)) {
+        UAII_TRY(timed("gemv_gate_up", gu_bytes, [&] { return launch_ring_gemv(rg, s); }));
+      } else {
+        UAII_TRY(timed("gemv_gate_up", gu_bytes, [&] { return launch_gemv(g, s); }));
+      }
       GemvArgs dn{};
       dn.nseg = 1;
       dn.epi = EPI_ADD;
@@ -997,7 +1060,21 @@ Error DecoderProgram::encode_step(bool want_logits) {
       dn.seg[0].w = L.down.view;
       dn.seg[0].rows = d.dim;
       dn.state = state_;
-      UAII_TRY(timed("gemv_down", gemv_bytes(L.down.view), [&] { return launch_gemv(dn, s); }));
+      RingArgs rd{};
+      rd.w[0] = L.down.view;
+      rd.rows[0] = d.dim;
+      rd.nseg = 1;
+      rd.epi = EPI_ADD;
+      rd.K = ls.inter;
+      rd.x = h_;
+      rd.y = x_;
+      rd.tap = dn.tap;
+      rd.pad = ring_pad_;
+      if (ring_mode_ >= 1 && ring_gemv_supported(rd)) {
+        UAII_TRY(timed("gemv_down", gemv_bytes(L.down.view), [&] { return launch_ring_gemv(rd, s); }));
+      } else {
+        UAII_TRY(timed("gemv_down", gemv_bytes(L.down.view), [&] { return launch_gemv(dn, s); }));
+      }
     } else if (ls.ffn == LayerSpec::kGelu) {
       GemvArgs g{};
       g.nseg = 1;

@@ -161,6 +161,10 @@ class DecoderProgram {
   float* lay_qkv_ = nullptr;
   float* lay_part_ = nullptr;
   double lay_wbytes_ = 0.0;  // weight bytes the launch streams
+  // decode GEMVs through the LDS ring (layers.hip) where the shapes allow:
+  // 0 none, 1 the residual-add GEMVs (O, down), 2 also QKV and gate/up
+  int ring_mode_ = 0;
+  uint8_t* ring_pad_ = nullptr;
 
   hipGraphExec_t graph_[2] = {nullptr, nullptr};
   std::map<std::string, KernelTiming> timing_;
