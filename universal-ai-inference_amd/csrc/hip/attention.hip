@@ -11,8 +11,10 @@
 // max / sum / output for all G query heads of the group (K/V read once per
 // group). Each block writes (o, m, l) partials; a second small kernel merges the
 // splits of every query head. (A last-block ticket merge inside the split kernel
-// needs a device-scope release per block, i.e. an L2 write-back on CDNA4, which
-// costs more than the extra launch.)
+// costs more than the extra launch: with a device-scope release per block, an L2
+// write-back on CDNA4; with write-through (sc1) partial stores and sc1 loads in
+// the merging block, 409 against 451 tok/s on the 8B decode, the merge code
+// raising the kernel to 214 VGPRs.)
 
 #include "common.h"
 #include "uaii_hip_internal.h"
