@@ -25,6 +25,31 @@ namespace {
 constexpr int NT = 256;    // threads per block
 constexpr int MAXG = 16;   // max q heads per kv head
 
+// Wave reductions on DPP moves instead of LDS permutes: within each 16-lane row
+// xor 1 and xor 2 (quad_perm), then the half-row and row mirrors; across the 4
+// rows with readlane (the result is wave-uniform).
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float lane_val(float v, int k) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), k));
+}
+__device__ __forceinline__ float wave_max_dpp(float v) {
+  v = fmaxf(v, dpp_mov<0xB1>(v));   // quad_perm [1,0,3,2]
+  v = fmaxf(v, dpp_mov<0x4E>(v));   // quad_perm [2,3,0,1]
+  v = fmaxf(v, dpp_mov<0x141>(v));  // row_half_mirror
+  v = fmaxf(v, dpp_mov<0x140>(v));  // row_mirror
+  return fmaxf(fmaxf(lane_val(v, 0), lane_val(v, 16)), fmaxf(lane_val(v, 32), lane_val(v, 48)));
+}
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  v += dpp_mov<0xB1>(v);
+  v += dpp_mov<0x4E>(v);
+  v += dpp_mov<0x141>(v);
+  v += dpp_mov<0x140>(v);
+  return (lane_val(v, 0) + lane_val(v, 16)) + (lane_val(v, 32) + lane_val(v, 48));
+}
+
 template <bool F16>
 __device__ inline float ld_kv(const void* p, int64_t i) {
   if constexpr (F16) return __half2float(reinterpret_cast<const __half*>(p)[i]);
@@ -320,6 +345,7 @@ __global__ void __launch_bounds__(NW * 64) k_attn_h16(AttnArgs a) {
   static_assert(TK == 16 || TK == 32, "tile of 16 or 32 keys");
   static_assert(TK >= 64 / (HD / 32), "at least one key per lane group in the scores");
   constexpr int LK = HD / 32;            // lanes per key (scores)
+  static_assert(LK == 2 || LK == 4, "score lanes reduced with quad_perm moves");
   constexpr int KPI = 64 / LK;           // keys per K instruction
   constexpr int KJ = TK / KPI;           // keys per lane per tile (scores)
   constexpr int LV = HD / 8;             // lanes per key (P.V)
@@ -426,8 +452,8 @@ __global__ void __launch_bounds__(NW * 64) k_attn_h16(AttnArgs a) {
 #pragma unroll
       for (int g = 0; g < G; ++g) {
         float t = sc[j][g];
-#pragma unroll
-        for (int o2 = 1; o2 < LK; o2 <<= 1) t += __shfl_xor(t, o2, 64);
+        t += dpp_mov<0xB1>(t);                  // xor 1
+        if constexpr (LK == 4) t += dpp_mov<0x4E>(t);  // xor 2
         sc[j][g] = (t0 + kk + KPI * j < b1) ? t : -INFINITY;
       }
     }
@@ -438,7 +464,7 @@ __global__ void __launch_bounds__(NW * 64) k_attn_h16(AttnArgs a) {
       float mx = sc[0][g];
 #pragma unroll
       for (int j = 1; j < KJ; ++j) mx = fmaxf(mx, sc[j][g]);
-      const float mnew = fmaxf(m[g], wave_max(mx));
+      const float mnew = fmaxf(m[g], wave_max_dpp(mx));
       float ps = 0.0f;
 #pragma unroll
       for (int j = 0; j < KJ; ++j) {
@@ -448,7 +474,7 @@ __global__ void __launch_bounds__(NW * 64) k_attn_h16(AttnArgs a) {
         if (kq == 0) p_s[wave][g][(key % VPI) * VJ + key / VPI] = pv;
       }
       alpha[g] = (m[g] == -INFINITY) ? 0.0f : expf(m[g] - mnew);
-      l[g] = l[g] * alpha[g] + wave_sum(kq == 0 ? ps : 0.0f);
+      l[g] = l[g] * alpha[g] + wave_sum_dpp(kq == 0 ? ps : 0.0f);
       m[g] = mnew;
     }
     __builtin_amdgcn_wave_barrier();
@@ -548,10 +574,10 @@ __global__ void __launch_bounds__(256) k_attn_merge(AttnArgs a) {
   if (threadIdx.x < 64) {
     const int k = threadIdx.x;
     const float mk = (k < SB) ? hp[(int64_t)k * G * pstride + hd] : -INFINITY;
-    const float M = wave_max(mk);
+    const float M = wave_max_dpp(mk);
     const float wk = (k < SB && mk != -INFINITY) ? expf(mk - M) : 0.0f;
     const float lk = (k < SB) ? hp[(int64_t)k * G * pstride + hd + 1] : 0.0f;
-    const float den = wave_sum(wk * lk);
+    const float den = wave_sum_dpp(wk * lk);
     w[k] = wk;
     if (k == 0) inv_den = den > 0.0f ? 1.0f / den : 0.0f;
   }
