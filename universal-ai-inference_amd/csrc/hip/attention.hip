@@ -25,31 +25,6 @@ namespace {
 constexpr int NT = 256;    // threads per block
 constexpr int MAXG = 16;   // max q heads per kv head
 
-// Wave reductions on DPP moves instead of LDS permutes: within each 16-lane row
-// xor 1 and xor 2 (quad_perm), then the half-row and row mirrors; across the 4
-// rows with readlane (the result is wave-uniform).
-template <int CTRL>
-__device__ __forceinline__ float dpp_mov(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
-}
-__device__ __forceinline__ float lane_val(float v, int k) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), k));
-}
-__device__ __forceinline__ float wave_max_dpp(float v) {
-  v = fmaxf(v, dpp_mov<0xB1>(v));   // quad_perm [1,0,3,2]
-  v = fmaxf(v, dpp_mov<0x4E>(v));   // quad_perm [2,3,0,1]
-  v = fmaxf(v, dpp_mov<0x141>(v));  // row_half_mirror
-  v = fmaxf(v, dpp_mov<0x140>(v));  // row_mirror
-  return fmaxf(fmaxf(lane_val(v, 0), lane_val(v, 16)), fmaxf(lane_val(v, 32), lane_val(v, 48)));
-}
-__device__ __forceinline__ float wave_sum_dpp(float v) {
-  v += dpp_mov<0xB1>(v);
-  v += dpp_mov<0x4E>(v);
-  v += dpp_mov<0x141>(v);
-  v += dpp_mov<0x140>(v);
-  return (lane_val(v, 0) + lane_val(v, 16)) + (lane_val(v, 32) + lane_val(v, 48));
-}
-
 template <bool F16>
 __device__ inline float ld_kv(const void* p, int64_t i) {
   if constexpr (F16) return __half2float(reinterpret_cast<const __half*>(p)[i]);

@@ -646,7 +646,7 @@ __device__ inline void stage_x(const GemvArgs& a, const float* xin, int64_t nch,
     }
     if (w_in_regs) {
       // single batch: finish the norm from registers after the reduction
-      ss = wave_sum(ss);
+      ss = wave_sum_dpp(ss);
       if ((tid & 63) == 0) red[tid >> 6] = ss;
       __syncthreads();
       float tot = 0.0f;
@@ -675,7 +675,7 @@ __device__ inline void stage_x(const GemvArgs& a, const float* xin, int64_t nch,
     return;
   }
   // RMSNorm with K > 4 * 4 * blockDim: second pass over LDS with batched weight loads
-  ss = wave_sum(ss);
+  ss = wave_sum_dpp(ss);
   if ((tid & 63) == 0) red[tid >> 6] = ss;
   __syncthreads();
   float tot = 0.0f;
@@ -824,7 +824,7 @@ __device__ inline void stage_pairs_finish(const GemvArgs& a, const float* xin, i
               (v.z * v.z + v.w * v.w);
       }
     }
-    ss = wave_sum(ss);
+    ss = wave_sum_dpp(ss);
     if ((tid & 63) == 0) red[tid >> 6] = ss;
     __syncthreads();
     float tot = 0.0f;
@@ -1045,7 +1045,7 @@ __global__ void __launch_bounds__(W * 64) k_gemv(GemvArgs a) {
     const int64_t i = u / wk.steps;
     if (u - i * wk.steps != wk.steps - 1) return;
 #pragma unroll
-    for (int r = 0; r < RPW; ++r) acc[r] = wave_sum(acc[r]);
+    for (int r = 0; r < RPW; ++r) acc[r] = wave_sum_dpp(acc[r]);
     if (ks > 1) {
       const int par = (int)(i & 1);
       if (lane == 0) {
