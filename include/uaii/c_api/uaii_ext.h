@@ -76,7 +76,8 @@ UAII_CAPI_API void uaii_sample_params_init(uaii_sample_params* params);
 
 /** uaii_session_generate with the reference's sampler (Session::generate's
  * SampleParams argument, session.cpp:910-1046): non-greedy draws are made on
- * the host from each step's probs row with a seeded mt19937_64. */
+ * the host from each step's logits row (session.cpp:974-978) with a seeded
+ * mt19937_64. */
 UAII_CAPI_API uaii_status uaii_session_generate_sampled(uaii_session* session,
                                                         const int64_t* prompt_tokens,
                                                         size_t prompt_n, int64_t max_new_tokens,

@@ -431,8 +431,9 @@ struct RefRunner {
 namespace {
 
 // Generate through the reference kernels with the reference's sampler
-// (session.cpp:989-1044): greedy when `sp` is greedy, else a seeded
-// mt19937_64 over the probs row.
+// (session.cpp:989-1044): greedy over the probs row when `sp` is greedy, else a
+// seeded mt19937_64 over the logits row (want_logits = !sample.greedy(),
+// session.cpp:974-978).
 int generate_with(const char* path, int max_layers, const std::int64_t* prompt,
                   std::int64_t n_prompt, std::int64_t max_new, const runtime::SampleParams& sp,
                   std::int64_t* out, std::int64_t* out_n, float* taps_logits, float* taps_resid2) {
@@ -450,8 +451,8 @@ int generate_with(const char* path, int max_layers, const std::int64_t* prompt,
   }
   for (std::int64_t t = 0; t < max_new; ++t) {
     std::int64_t next = 0;
-    err = runtime::sample_token_f32(R.probs->f32.data(), static_cast<std::size_t>(R.V), sp, hist,
-                                    &rng, &next);
+    const float* scores = sp.greedy() ? R.probs->f32.data() : R.logits->f32.data();
+    err = runtime::sample_token_f32(scores, static_cast<std::size_t>(R.V), sp, hist, &rng, &next);
     if (!err.ok()) { g_err = err.message(); return -1; }
     hist.push_back(next);
     if (t + 1 >= max_new) break;

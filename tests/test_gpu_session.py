@@ -176,8 +176,8 @@ def test_generate_edge_cases():
                          ids=lambda p: f"T{p[0]}_p{p[1]}_k{p[2]}_r{p[3]}")
 def test_generate_sampled_matches_reference(prm):
     """Seeded temperature / top-k / top-p / repetition-penalty sampling: the device
-    probs row through the host sampler gives the ids the reference's kernels and
-    sampler give (session.cpp:989-1044). Top-k without top-p is left out here: it
+    logits row through the host sampler gives the ids the reference's kernels and
+    sampler give (logits when sampling, session.cpp:974-978; loop :989-1044). Top-k without top-p is left out here: it
     draws in std::nth_element's arrangement of the kept ids, which depends on the
     exact bits of the whole row (ulp-level differences in tiny probabilities
     reorder it), so that case is pinned on identical rows in test_sampling.py."""
@@ -192,3 +192,31 @@ def test_generate_sampled_matches_reference(prm):
     want = oracle.ref_generate_sampled(path, prompt, 24, t, tp, tk, rp, 7)
     assert np.array_equal(ids, want)
     assert len(set(ids[12:].tolist())) > 1
+
+
+@pytest.mark.parametrize("prm", [(0.05, 1.0, 0, 1.0), (0.7, 0.9, 0, 1.3)], ids=lambda p: f"T{p[0]}_p{p[1]}_r{p[3]}")
+def test_generate_sampled_draws_from_logits(prm):
+    """The first sampled token is the reference sampler's draw over the device's
+    logits row after the prompt (session.cpp:974-978: logits, not probs, when
+    sampling), bit for bit: the same row bits, seed and penalty history must give
+    the same id for every seed. A loop that sampled the probs row would draw from
+    a different row and, at these temperatures, a near-uniform distribution."""
+    cfg = SMALL["gqa_q4_0"]
+    path = synth.cached_model(cfg)
+    prompt = prompt_for(cfg, 10, 5)
+    t, tp, tk, rp = prm
+    with uaii_amd.Session(path) as s:
+        s.generate(prompt, 1)
+        logits = s.get("logits")
+        drawn = []
+        for seed in range(24):
+            ids = s.generate_sampled(prompt, 1, uaii_amd.sample_params(t, tp, tk, rp, seed=seed))
+            want = uaii_amd.sample_token(logits, uaii_amd.sample_params(t, tp, tk, rp, seed=seed), prompt.tolist())
+            assert int(ids[-1]) == want, seed
+            drawn.append(want)
+    if t <= 0.1:
+        # softmax(logits / 0.05) puts ~0.96 on the top logit's token here; the
+        # softmax of a probs row would be near uniform over the vocabulary
+        assert drawn.count(int(np.argmax(logits))) >= 16
+    else:
+        assert len(set(drawn)) > 1

@@ -21,14 +21,17 @@ PARAMS = [
 
 
 def rows(vocab, n, seed):
+    """Logits rows (what the session samples from, session.cpp:974-978) of two
+    spreads, plus a probability row, which the sampler must treat like any other
+    row of scores."""
     rng = np.random.default_rng(seed)
     for i in range(n):
-        if i % 2:
+        if i % 3 == 2:
             x = rng.normal(0, 3, vocab).astype(np.float32)
             e = np.exp(x - x.max())
-            yield (e / e.sum()).astype(np.float32)  # a probs row, as the session samples from
+            yield (e / e.sum()).astype(np.float32)
         else:
-            yield rng.normal(0, 2, vocab).astype(np.float32)
+            yield rng.normal(0, 2 + 4 * (i % 3), vocab).astype(np.float32)
 
 
 @pytest.mark.parametrize("vocab", [50, 3000, 32000])
@@ -46,13 +49,23 @@ def test_sampler_matches_reference(vocab, prm):
             assert got == want, (i, seed)
 
 
-def test_sampler_distribution_follows_probs():
-    """With temperature 1 and no truncation, a probs row is re-softmaxed once
-    (the reference samples from `probs`); the empirical frequencies over many
-    seeds follow softmax(probs)."""
-    probs = np.array([0.5, 0.3, 0.2], np.float32)
-    want = np.exp(probs) / np.exp(probs).sum()
-    counts = np.zeros(3)
-    for seed in range(3000):
-        counts[uaii_amd.sample_token(probs, uaii_amd.sample_params(1.0, 1.0, 0, 1.0, seed=seed))] += 1
-    assert np.abs(counts / counts.sum() - want).max() < 0.03
+def test_sampler_distribution_follows_softmax_of_logits():
+    """The sampler softmaxes the row it is given (sampling.cpp:80-92), and the
+    session gives it the logits: at temperature T with no truncation the draw
+    frequencies over many seeds follow softmax(logits / T). Sampling a row that
+    had already been softmaxed would flatten them (here to about 0.39/0.33/0.28
+    at T = 1), which this bar rejects."""
+    logits = np.array([2.0, 0.0, -1.0], np.float32)
+    for T in (1.0, 0.5):
+        z = logits.astype(np.float64) / T
+        want = np.exp(z - z.max()) / np.exp(z - z.max()).sum()
+        counts = np.zeros(3)
+        n = 4000
+        for seed in range(n):
+            counts[uaii_amd.sample_token(logits, uaii_amd.sample_params(T, 1.0, 0, 1.0, seed=seed))] += 1
+        freq = counts / n
+        # 5 standard deviations of a binomial frequency
+        assert np.all(np.abs(freq - want) < 5 * np.sqrt(want * (1 - want) / n) + 1e-3), (T, freq, want)
+    flat = np.exp(logits - logits.max()) / np.exp(logits - logits.max()).sum()
+    resoft = np.exp(flat) / np.exp(flat).sum()
+    assert abs(resoft[0] - 0.84) > 0.3  # the probs-reading mistake is far outside the bar

@@ -90,9 +90,11 @@ Error Session::generate(const std::vector<int64_t>& prompt, int64_t max_new,
   const bool per_token = (bool)on_new_token || !stop_ids.empty();
   auto is_stop = [&](int64_t t) { return std::find(stop_ids.begin(), stop_ids.end(), t) != stop_ids.end(); };
   if (!sample.greedy()) {
-    // Non-greedy: the reference samples from the `probs` row on the host with a
-    // seeded mt19937_64 (session.cpp:989-995, :1018-1026); each step's probs come
-    // back from the device and the chosen id is fed to the next step.
+    // Non-greedy: the reference samples the pre-softmax `logits` row on the host
+    // (want_logits = !sample.greedy(), session.cpp:974-978) with a seeded
+    // mt19937_64 (:989-995, :1018-1026); each step's logits come back from the
+    // device and the chosen id is fed to the next step. The sampler applies its
+    // own softmax, so the device's softmax kernel does not run on this path.
     std::mt19937_64 rng;
     if (sample.has_seed) {
       rng.seed(sample.seed);
@@ -101,11 +103,11 @@ Error Session::generate(const std::vector<int64_t>& prompt, int64_t max_new,
       rng.seed((static_cast<uint64_t>(rd()) << 32) ^ static_cast<uint64_t>(rd()));
     }
     out->assign(prompt.begin(), prompt.end());
-    std::vector<float> probs;
+    std::vector<float> logits;
     for (int64_t t = 0; t < max_new; ++t) {
-      UAII_TRY(p.read_tap("probs", &probs));
+      UAII_TRY(p.read_tap("logits", &logits));
       int64_t next = 0;
-      UAII_TRY(sample_token_f32(probs.data(), probs.size(), sample, *out, &rng, &next));
+      UAII_TRY(sample_token_f32(logits.data(), logits.size(), sample, *out, &rng, &next));
       out->push_back(next);
       if (on_new_token && !on_new_token(next)) return Error::success();
       if (is_stop(next)) return Error::success();
