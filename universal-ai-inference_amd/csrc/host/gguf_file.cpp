@@ -146,6 +146,10 @@ Error GgufFile::open(const std::string& path) {
   c.p += 4;
   c.u(4);  // version
   const uint64_t n_tensors = c.u(8), n_kv = c.u(8);
+  // every tensor info takes at least 24 bytes (name length, rank, type, offset),
+  // so a count beyond that cannot be real (and must not size an allocation)
+  if (n_tensors > (uint64_t)len_ / 24 || n_kv > (uint64_t)len_ / 12)
+    return Error::make(ErrorCode::InvalidArgument, "truncated binary read");
   for (uint64_t i = 0; i < n_kv; ++i) {
     std::string key = c.str();
     const uint32_t t = (uint32_t)c.u(4);
@@ -165,15 +169,28 @@ Error GgufFile::open(const std::string& path) {
     if (c.bad) return Error::make(ErrorCode::InvalidArgument, "truncated binary read");
     tensors_.push_back(std::move(t));
   }
-  const size_t data_off = ((size_t)(c.p - map_) + 31) & ~(size_t)31;
+  const uint64_t data_off = ((uint64_t)(c.p - map_) + 31) & ~(uint64_t)31;
   for (size_t i = 0; i < tensors_.size(); ++i) {
     GgufTensor& t = tensors_[i];
+    // element count, byte size and end offset with every product and sum checked
+    // for uint64 wrap-around: a crafted header must not pass the end-of-file test
     uint64_t n = 1;
-    for (auto d : t.ne) n *= d;
-    t.nbytes = gguf_nbytes(t.type, n);
-    t.data = map_ + data_off + t.offset;
-    if (gguf_type_supported(t.type) && data_off + t.offset + t.nbytes > len_)
+    bool wrap = false;
+    for (auto d : t.ne) wrap = wrap || __builtin_mul_overflow(n, d, &n) || d > (uint64_t)INT64_MAX;
+    const int be = block_elems(t.type);
+    uint64_t end = 0;
+    if (!wrap && be) {
+      if (n % (uint64_t)be)
+        return Error::make(ErrorCode::InvalidArgument,
+                           "tensor " + t.name + " element count is not a multiple of its block size");
+      wrap = __builtin_mul_overflow(n / (uint64_t)be, (uint64_t)block_bytes(t.type), &t.nbytes) ||
+             __builtin_add_overflow(data_off, t.offset, &end) || __builtin_add_overflow(end, t.nbytes, &end);
+    }
+    if (wrap || n > (uint64_t)INT64_MAX)
+      return Error::make(ErrorCode::InvalidArgument, "tensor " + t.name + " size overflows");
+    if (t.offset > (uint64_t)len_ || (be && end > (uint64_t)len_))
       return Error::make(ErrorCode::InvalidArgument, "tensor " + t.name + " extends past end of file");
+    t.data = map_ + data_off + t.offset;
     index_[t.name] = i;
   }
   return Error::success();

@@ -165,6 +165,11 @@ Error DecoderProgram::build(const DecoderSpec& spec, const ProgramOptions& opts)
     return Error::make(ErrorCode::InvalidArgument, "model dims must be multiples of 4");
 
   auto up = [&](const GgufTensor* t, DeviceWeight* w) -> Error {
+    // the rows the upload copies must be exactly the bytes the file holds for
+    // this tensor (the parser bounded those by the end of the mapping)
+    if (t->cols() <= 0 || t->rows() <= 0 ||
+        (uint64_t)t->rows() * gguf_nbytes(t->type, (uint64_t)t->cols()) != t->nbytes)
+      return Error::make(ErrorCode::InvalidArgument, "tensor " + t->name + " shape does not match its bytes");
     return upload_weight(t->type, t->data, t->rows(), t->cols(), stream_, w);
   };
   UAII_TRY(up(d.tok_embd, &tok_embd_));
@@ -830,30 +835,38 @@ Error DecoderProgram::seek(int64_t pos) {
   return Error::success();
 }
 
+// After the stream has drained: a device-wide wait of the one-launch layer
+// kernel that timed out leaves the fail word set and the step's results
+// meaningless; report it (once) to whichever read-back comes first.
+Error DecoderProgram::check_layers_fail() {
+  if (!lay_sync_) return Error::success();
+  unsigned long long fail = 0;
+  UAII_HIP(hipMemcpy(&fail, lay_sync_->w, sizeof(fail), hipMemcpyDeviceToHost));
+  if (fail) {
+    UAII_HIP(hipMemset(lay_sync_, 0, sizeof(LayersSync)));
+    return Error::make(ErrorCode::Internal, "decode layer kernel: a device-wide wait timed out");
+  }
+  return Error::success();
+}
+
 Error DecoderProgram::read_state(StepState* st) {
   UAII_HIP(hipStreamSynchronize(stream_));
+  UAII_TRY(check_layers_fail());
   UAII_HIP(hipMemcpy(st, state_, sizeof(StepState), hipMemcpyDeviceToHost));
   return Error::success();
 }
 
 Error DecoderProgram::synchronize() {
   UAII_HIP(hipStreamSynchronize(stream_));
-  return Error::success();
+  return check_layers_fail();
 }
 
 Error DecoderProgram::read_ids(int64_t* out, int64_t n) {
   if (n > max_ctx_ + 1) return Error::make(ErrorCode::InvalidArgument, "read_ids beyond capacity");
   std::vector<int32_t> ids((size_t)n);
   UAII_HIP(hipStreamSynchronize(stream_));
+  UAII_TRY(check_layers_fail());
   UAII_HIP(hipMemcpy(ids.data(), ids_, (size_t)n * 4, hipMemcpyDeviceToHost));
-  if (lay_sync_) {
-    unsigned long long fail = 0;
-    UAII_HIP(hipMemcpy(&fail, lay_sync_->w, sizeof(fail), hipMemcpyDeviceToHost));
-    if (fail) {
-      UAII_HIP(hipMemset(lay_sync_, 0, sizeof(LayersSync)));
-      return Error::make(ErrorCode::Internal, "decode layer kernel: a device-wide wait timed out");
-    }
-  }
   for (int64_t i = 0; i < n; ++i) out[i] = ids[(size_t)i];
   return Error::success();
 }
@@ -1280,6 +1293,7 @@ Error DecoderProgram::read_tap(const std::string& name, std::vector<float>* out)
   }
   out->resize(n);
   UAII_HIP(hipStreamSynchronize(stream_));
+  UAII_TRY(check_layers_fail());
   UAII_HIP(hipMemcpy(out->data(), src, n * 4, hipMemcpyDeviceToHost));
   return Error::success();
 }

@@ -104,6 +104,7 @@ class DecoderProgram {
   template <class F>
   Error timed(const char* name, double bytes, double flops, F&& launch);
   Error collect_timings();
+  Error check_layers_fail();
   Error ensure_prefill_buffers(int64_t chunk);
   Error pf_gemm(const DeviceWeight* w[3], const int64_t cols0[3], int nw, const DeviceWeight* w2,
                 int epi, int64_t m, float* y, int64_t ldy, int store_split = 1);
