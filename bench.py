@@ -48,6 +48,23 @@ def measured_traffic(kernel: str, algo_bytes: float):
     return None
 
 
+def cpu_info():
+    """Host CPU model, logical CPUs of the machine, and the CPUs this process may run on."""
+    model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        usable = os.cpu_count() or 0
+    return model, os.cpu_count() or 0, usable
+
+
 def cpu_baseline(path: str, start_pos: int, n_steps: int, threads: int):
     """Reference CPU path on a bounded decode window (rank 0, N=1)."""
     sys.path.insert(0, str(ROOT))
@@ -60,14 +77,41 @@ def cpu_baseline(path: str, start_pos: int, n_steps: int, threads: int):
         R.uref_time_decode_window.argtypes = [C.c_char_p, C.c_int64, C.c_int64]
         secs = R.uref_time_decode_window(path.encode(), start_pos, n_steps)
         kind = "reference"
+        what = ("the reference's own CPU kernels (quant_gemm_f32 Path B, rmsnorm, rope, attention_kv_f32, "
+                "softmax; compiled from its sources into oracle/_ref) driven op by op by this build's "
+                "restatement of the gguf.cpp decode graph, not the reference's Session::run")
     else:
         secs = oracle.Model(path).time_decode_window(start_pos, n_steps, threads)
         kind = "port"
+        what = "the C restatement of the reference's CPU path (oracle/uaii_oracle.c)"
     if secs <= 0:
         raise RuntimeError("cpu baseline failed")
+    model, ncpu, usable = cpu_info()
     return {"value": n_steps / secs, "unit": "tok/s", "cores": threads, "kind": kind,
+            "threads": threads, "nproc": ncpu, "usable_cpus": usable, "cpu_model": model,
             "sample": f"{n_steps} decode steps at ctx {start_pos}..{start_pos + n_steps} "
-                      f"(KV filled with deterministic values), {secs:.1f} s wall"}
+                      f"(KV filled with deterministic values), {secs:.1f} s wall; {what}"}
+
+
+def parity_check(path: str, n_prompt: int, n_new: int, layers: int, threads: int):
+    """Greedy ids of the benchmarked GGUF file truncated to its first `layers`
+    layers (UAII_MAX_LAYERS, gguf.cpp:785-799): the device session (f16 KV, the
+    prompt on the matrix cores) against the CPU oracle with an f16 KV cache."""
+    sys.path.insert(0, str(ROOT))
+    import numpy as np
+    import oracle  # checker only
+    import uaii_amd
+    prompt = np.random.default_rng(1234).integers(0, 32000, n_prompt).astype(np.int64)
+    os.environ["UAII_MAX_LAYERS"] = str(layers)
+    try:
+        with uaii_amd.Session(path, kv_f16=True, max_context=n_prompt + n_new + 8) as s:
+            got = s.generate(prompt, n_new)
+    finally:
+        del os.environ["UAII_MAX_LAYERS"]
+    want, _ = oracle.Model(path, max_layers=layers).generate(prompt, n_new, kv_f16=True, nthreads=threads,
+                                                             taps=False)
+    return {"layers": layers, "prompt": n_prompt, "decoded": n_new,
+            "ids_match": bool(np.array_equal(got, want)), "against": "oracle (f16 KV)"}
 
 
 def main() -> int:
@@ -82,6 +126,7 @@ def main() -> int:
     ap.add_argument("--cpu-threads", type=int, default=16)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-profile", action="store_true")
+    ap.add_argument("--no-parity", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); "
@@ -185,11 +230,12 @@ def main() -> int:
     dt = time.perf_counter() - t0
     tok_s = K / dt
     log(f"decode {K} steps in {dt:.3f}s -> {tok_s:.1f} tok/s ({1e3 * dt / K:.3f} ms/step)")
-    ids = sess.read_ids(ctx)
+    ids = sess.read_ids(ctx + 1)  # the prompt, then every generated id
     best, second = sess.last_margin()
 
     kernels = {}
     roofline = None
+    P = 0
     if not args.no_profile:
         P = min(args.profile_steps, K)
         sess.seek(n_prompt + W)
@@ -200,7 +246,8 @@ def main() -> int:
         kernels = json.loads(sess.profile_summary())
         sess.set_profiling(False)
         ids2 = sess.read_ids(n_prompt + W + P + 1)
-        replay_ok = bool(np.array_equal(ids2, ids[: n_prompt + W + P + 1]))
+        replay_ok = bool(len(ids2) == n_prompt + W + P + 1 and
+                         np.array_equal(ids2, ids[: n_prompt + W + P + 1]))
         log(f"profiled replay of {P} steps reproduces the ids: {replay_ok}")
         # dominant kernel by device time
         dom = max(kernels, key=lambda k: kernels[k]["total_ms"])
@@ -220,6 +267,15 @@ def main() -> int:
                     "kernel_ms_per_step": round(step_ms, 4),
                     "profiled_steps": P, "profiled_replay_ids_match": replay_ok}
     sess.close()
+
+    parity = None
+    if not args.no_parity:
+        try:
+            parity = parity_check(path, 16, 8, 2, args.cpu_threads)
+            log(f"parity {parity}")
+        except Exception as e:
+            log(f"parity check failed to run: {e}")
+            parity = {"error": str(e)}
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -245,8 +301,9 @@ def main() -> int:
         "argmax_margin_last": round(best - second, 6),
         "roofline": roofline,
         "kernels": {n: {"avg_us": round(v["avg_us"], 2), "gbps": round(v["gbps"], 1),
-                        "launches_per_step": v["launches"] / max(1, args.profile_steps)}
+                        "launches_per_step": v["launches"] / max(1, P)}
                     for n, v in kernels.items()},
+        "parity": parity,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
