@@ -1019,10 +1019,38 @@ static int state_init(orc_state* s, orc_model* m, int64_t max_seq, int kv_f16) {
 
 /* MoE FFN on f32 expert stacks (transformer.cpp:522-612): for each selected
  * expert, gate/up rows summed over D, SiLU*up, down rows summed over I, then
- * Y += w*out, experts in descending-prob order. */
+ * Y += w*out, experts in descending-prob order. Rows run on parallel_for; each
+ * row's sum is one thread's sequential loop, so the result does not depend on
+ * the thread count. */
+typedef struct {
+  const float *xin, *G, *U, *Dn;
+  float *hid, *y;
+  int64_t D, I;
+  float w;
+} moe_ctx;
+
+static void moe_gate_up_row(void* v, int64_t i, float* scratch) {
+  (void)scratch;
+  moe_ctx* c = (moe_ctx*)v;
+  float gs = 0.0f, us = 0.0f;
+  for (int64_t d = 0; d < c->D; d++) {
+    gs += c->xin[d] * c->G[i * c->D + d];
+    us += c->xin[d] * c->U[i * c->D + d];
+  }
+  float sig = 1.0f / (1.0f + expf(-gs));
+  c->hid[i] = (gs * sig) * us;
+}
+
+static void moe_down_row(void* v, int64_t o, float* scratch) {
+  (void)scratch;
+  moe_ctx* c = (moe_ctx*)v;
+  float acc = 0.0f;
+  for (int64_t i = 0; i < c->I; i++) acc += c->hid[i] * c->Dn[o * c->I + i];
+  c->y[o] += c->w * acc;
+}
+
 static void moe_ffn(orc_state* s, const orc_layer* L, const float* xin, float* y,
                     int nthreads) {
-  (void)nthreads;
   orc_model* m = s->m;
   int64_t D = m->dim, I = L->gate_exps.rows, E = L->gate_exps.n3;
   float probs[256];
@@ -1033,23 +1061,10 @@ static void moe_ffn(orc_state* s, const orc_layer* L, const float* xin, float* y
   for (int64_t o = 0; o < D; o++) y[o] = 0.0f;
   for (int t = 0; t < (int)(m->top_k < E ? m->top_k : E); t++) {
     int e = ids[t];
-    const float* Ge = L->gate_exps.f32 + (int64_t)e * I * D;
-    const float* Ue = L->up_exps.f32 + (int64_t)e * I * D;
-    const float* De = L->down_exps.f32 + (int64_t)e * D * I;
-    for (int64_t i = 0; i < I; i++) {
-      float gs = 0.0f, us = 0.0f;
-      for (int64_t d = 0; d < D; d++) {
-        gs += xin[d] * Ge[i * D + d];
-        us += xin[d] * Ue[i * D + d];
-      }
-      float sig = 1.0f / (1.0f + expf(-gs));
-      s->hid[i] = (gs * sig) * us;
-    }
-    for (int64_t o = 0; o < D; o++) {
-      float acc = 0.0f;
-      for (int64_t i = 0; i < I; i++) acc += s->hid[i] * De[o * I + i];
-      y[o] += w[t] * acc;
-    }
+    moe_ctx c = {xin, L->gate_exps.f32 + (int64_t)e * I * D, L->up_exps.f32 + (int64_t)e * I * D,
+                 L->down_exps.f32 + (int64_t)e * D * I, s->hid, y, D, I, w[t]};
+    parallel_for(I, nthreads, 0, moe_gate_up_row, &c);
+    parallel_for(D, nthreads, 0, moe_down_row, &c);
   }
 }
 
@@ -1151,7 +1166,9 @@ int orc_generate(orc_model* m, const int64_t* prompt, int64_t n_prompt, int64_t 
   /* prefill: one run() per prompt token (session.cpp:1006-1016) */
   for (int64_t i = 0; i < n_prompt; i++) {
     int last = (i == n_prompt - 1);
-    if (forward(&s, prompt[i], pos, nthreads, last ? taps : NULL, 1)) { state_free(&s); return -1; }
+    /* the LM head of the earlier prompt tokens is computed by the reference and
+     * never read; skipping it here changes no value that is read */
+    if (forward(&s, prompt[i], pos, nthreads, last ? taps : NULL, last)) { state_free(&s); return -1; }
     pos++;
     out[n++] = prompt[i];
   }

@@ -1,0 +1,145 @@
+"""Every BASELINE workload shape under GPU parity, through the C ABI.
+
+* Decode attention at the headline context: max_seq 4096 gives 32 key splits
+  per kv head (the merge of 32 partials), checked against the oracle's
+  attention_kv_f32 restatement (transformer.cpp:222-433) at 1, 2049, 4090 and
+  4096 keys, 32 or 64 query heads over 8 kv heads, head_dim 64 / 128, f16 and
+  f32 caches.
+* The Llama-3-8B shape (Q4_0 and Q8_0), two layers of it at full width with a
+  4096-position KV cache: a 96-token prompt on the matrix cores, then 64 greedy
+  tokens; ids identical to the oracle with an fp16 cache, logits and the
+  residual taps within 2e-3 of it, and of the oracle's f32-cache path (the
+  reference's own cache type) over a shorter run.
+* The Llama-3.2-1B shape at full depth (16 layers, Q4_K + Q6_K, tied):
+  128-token prompt, 64 greedy tokens.
+* The Mixtral shape (8 experts, top-2, Q4_K, d 4096, ffn 14336), one layer:
+  64-token prompt, 32 greedy tokens against the oracle's Path A MoE (the only
+  path on which the reference's experts run, transformer.cpp:522-612).
+
+Reference loop for every model: session.cpp:1006-1044 (prompt, then greedy
+argmax over probs, lowest index on ties).
+"""
+import dataclasses
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+import uaii_amd
+from uaii_amd import synth, DeviceBuffer, check_hip
+
+pytestmark = pytest.mark.gpu
+
+THREADS = max(1, min(16, os.cpu_count() or 1))
+
+SHAPES = {
+    "8b_q4_0": dataclasses.replace(synth.PRESETS["8b"], n_layers=2),
+    "8b_q8_0": dataclasses.replace(synth.PRESETS["8b_q8"], n_layers=2),
+    "1b": synth.PRESETS["1b"],
+    "mx": dataclasses.replace(synth.PRESETS["mx"], n_layers=1),
+}
+
+
+def maxrel(a, b):
+    return float(np.abs(np.asarray(a, np.float64) - b).max() / max(np.abs(b).max(), 1e-30))
+
+
+@pytest.mark.parametrize("kv_f16", [1, 0])
+@pytest.mark.parametrize("heads", [(32, 8, 128), (64, 8, 128), (32, 8, 64)], ids=str)
+@pytest.mark.parametrize("n_keys", [1, 2049, 4090, 4096])
+def test_attention_decode_32_splits(hip, kv_f16, heads, n_keys):
+    nh, nkv, hd = heads
+    max_seq = 4096
+    rng = np.random.default_rng(n_keys * 13 + nh + hd)
+    q = rng.standard_normal(nh * hd).astype(np.float32)
+    k = rng.standard_normal((nkv, max_seq, hd)).astype(np.float32)
+    v = rng.standard_normal((nkv, max_seq, hd)).astype(np.float32)
+    if kv_f16:
+        k, v = k.astype(np.float16), v.astype(np.float16)
+    dq, dk, dv = DeviceBuffer.from_array(q), DeviceBuffer.from_array(k), DeviceBuffer.from_array(v)
+    do = DeviceBuffer(nh * hd * 4)
+    check_hip(hip.uaii_hip_attention_decode(dq.ptr, dk.ptr, dv.ptr, kv_f16, max_seq, nh, nkv, hd,
+                                            n_keys, do.ptr, None))
+    got = do.to_array(np.float32, nh * hd)
+    # oracle layout [seq][kv_dim]: the past n_keys - 1 keys, then the current one
+    kf = k.astype(np.float32).transpose(1, 0, 2).reshape(max_seq, nkv * hd)
+    vf = v.astype(np.float32).transpose(1, 0, 2).reshape(max_seq, nkv * hd)
+    past = max(n_keys - 1, 1)
+    kc, vc = np.ascontiguousarray(kf[:past]), np.ascontiguousarray(vf[:past])
+    kn, vn = np.ascontiguousarray(kf[n_keys - 1]), np.ascontiguousarray(vf[n_keys - 1])
+    want = np.zeros(nh * hd, np.float32)
+    oracle.oracle().orc_attention_decode(oracle._fp(q), oracle._fp(kc), oracle._fp(vc), n_keys - 1,
+                                         oracle._fp(kn), oracle._fp(vn), oracle._fp(want), nh, nkv, hd)
+    assert maxrel(got, want) < 1e-5
+    if n_keys == 1:
+        assert maxrel(got, np.repeat(vf[0].reshape(nkv, hd), nh // nkv, axis=0).reshape(-1)) < 1e-6
+
+
+def run_device(path, prompt, n_new, n_layers, kv_f16=True, max_context=0):
+    with uaii_amd.Session(path, kv_f16=kv_f16, max_context=max_context) as s:
+        if kv_f16:
+            assert s.prefill_supported(), "the prompt should run on the matrix cores"
+        ids = s.generate(prompt, n_new)
+        taps = {k: s.get(k) for k in ("logits", "normed")}
+        for li in range(n_layers):
+            taps[f"r1_{li}"] = s.get(f"blk.{li}.resid1")
+            taps[f"r2_{li}"] = s.get(f"blk.{li}.resid2")
+    return ids, taps
+
+
+def check_taps(taps, want, n_layers, bar=2e-3):
+    errs = {"logits": maxrel(taps["logits"], want["logits"]),
+            "normed": maxrel(taps["normed"], want["normed"])}
+    for li in range(n_layers):
+        errs[f"r1_{li}"] = maxrel(taps[f"r1_{li}"], want["resid1"][li])
+        errs[f"r2_{li}"] = maxrel(taps[f"r2_{li}"], want["resid2"][li])
+    print("max rel errors", {k: f"{v:.2e}" for k, v in errs.items()}, flush=True)
+    for k, e in errs.items():
+        assert e < bar, (k, e)
+
+
+@pytest.mark.parametrize("name", ["8b_q4_0", "8b_q8_0"])
+def test_8b_shape_two_layers(name):
+    cfg = SHAPES[name]
+    path = synth.cached_model(cfg, nthreads=THREADS)
+    prompt = np.random.default_rng(cfg.seed + 100).integers(0, cfg.vocab, 96).astype(np.int64)
+    m = oracle.Model(path)
+    assert m.n_layers == 2 and m.dim == 4096 and m.ffn == 14336 and m.vocab == 128256
+    ids, taps = run_device(path, prompt, 64, 2, max_context=4096)
+    want_ids, want = m.generate(prompt, 64, kv_f16=True, nthreads=THREADS)
+    print(name, "gpu", ids[96:].tolist(), flush=True)
+    print(name, "cpu", want_ids[96:].tolist(), flush=True)
+    assert np.array_equal(ids, want_ids)
+    check_taps(taps, want, 2)
+    # the reference's f32 KV cache: the device's fp16 cache within the same bars
+    ids8, taps8 = run_device(path, prompt, 8, 2, max_context=4096)
+    want_ids32, want32 = m.generate(prompt, 8, kv_f16=False, nthreads=THREADS)
+    assert np.array_equal(ids8, want_ids32)
+    check_taps(taps8, want32, 2)
+
+
+def test_1b_shape_full_depth():
+    cfg = SHAPES["1b"]
+    path = synth.cached_model(cfg, nthreads=THREADS)
+    prompt = np.random.default_rng(cfg.seed + 100).integers(0, cfg.vocab, 128).astype(np.int64)
+    ids, taps = run_device(path, prompt, 64, cfg.n_layers)
+    want_ids, want = oracle.Model(path).generate(prompt, 64, kv_f16=True, nthreads=THREADS)
+    print("1b gpu", ids[128:].tolist(), flush=True)
+    print("1b cpu", want_ids[128:].tolist(), flush=True)
+    assert np.array_equal(ids, want_ids)
+    check_taps(taps, want, cfg.n_layers)
+
+
+def test_mixtral_shape_one_layer():
+    cfg = SHAPES["mx"]
+    path = synth.cached_model(cfg, nthreads=THREADS)
+    prompt = np.random.default_rng(cfg.seed + 100).integers(0, cfg.vocab, 64).astype(np.int64)
+    ids, taps = run_device(path, prompt, 32, 1)
+    m = oracle.Model(path)
+    assert m.n_experts == 8 and m.top_k == 2 and m.ffn == 14336
+    want_ids, want = m.generate(prompt, 32, kv_f16=True, nthreads=THREADS)
+    print("mx gpu", ids[64:].tolist(), flush=True)
+    print("mx cpu", want_ids[64:].tolist(), flush=True)
+    assert np.array_equal(ids, want_ids)
+    check_taps(taps, want, 1)

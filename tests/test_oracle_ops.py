@@ -148,7 +148,6 @@ def test_softmax_argmax_silu():
         assert R.uref_argmax(fp(x2), x2.size) == 100
         s = np.zeros_like(x)
         assert R.uref_silu(fp(x), fp(s), x.size) == 0
-        assert np.array_equal(s, np.array([O().orc_silu(float(v)) for v in x[:0]] or s, np.float32)) or True
         mine = np.array([O().orc_silu(float(v)) for v in x[:2000]], np.float32)
         assert np.array_equal(mine, s[:2000])
 
