@@ -108,6 +108,21 @@ UAII_HIP_API int uaii_hip_attention_decode(const float* q, const void* kcache,
                                            int n_heads, int n_kv_heads, int head_dim,
                                            int64_t n_keys, float* out, void* stream);
 
+/* uaii_hip_attention_decode without any allocation. No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * stream capture, allocation-free serving loops). Same arguments, kernels and
+ * results as uaii_hip_attention_decode; the split partials live in a fixed
+ * 2 MiB device array per GPU (held until the process ends) instead of a
+ * hipMalloc'd buffer, so n_kv_heads * splits * (n_heads / n_kv_heads) *
+ * (head_dim + 2) * 4 bytes must fit in 2 MiB (splits = min(32, ceil(max_seq /
+ * 128))); larger calls return -3 and launch nothing. Calls that overlap on one
+ * GPU share that array and race. */
+UAII_HIP_API int uaii_hip_attention_decode_noalloc(const float* q, const void* kcache,
+                                                   const void* vcache, int kv_f16,
+                                                   int64_t max_seq, int n_heads, int n_kv_heads,
+                                                   int head_dim, int64_t n_keys, float* out,
+                                                   void* stream);
+
 /* Causal attention of m queries at positions p0 .. p0 + m - 1 (q, out:
  * [m][n_heads * head_dim]) over an f16 cache holding keys 0 .. p0 + m - 1;
  * head_dim 64 or 128 (attention_kv_f32 applied to each query in turn,

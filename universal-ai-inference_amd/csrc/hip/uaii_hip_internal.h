@@ -134,6 +134,9 @@ struct AttnArgs {
 int attention_splits(int64_t max_seq);
 hipError_t launch_attention_decode(const AttnArgs& a, hipStream_t s);
 hipError_t prepare_attention();
+// Resolves the allocation-free attention scratch of the current device (noalloc.hip).
+hipError_t prepare_noalloc();
+size_t noalloc_scratch_bytes();
 
 // ---- all transformer layers of one decode step in one persistent launch -----------
 

@@ -17,6 +17,7 @@ namespace {
 
 constexpr int kErrArg = -1;      // invalid argument
 constexpr int kErrNotImpl = -2;  // not implemented
+constexpr int kErrScratch = -3;  // larger than the allocation-free scratch
 
 std::mutex g_scratch_mu;
 void* g_scratch = nullptr;       // attention partials for uaii_hip_attention_decode
@@ -50,7 +51,9 @@ int uaii_hip_init(int device) {
   if (e != hipSuccess) return (int)e;
   e = prepare_gemv();
   if (e != hipSuccess) return (int)e;
-  return (int)prepare_attention();
+  e = prepare_attention();
+  if (e != hipSuccess) return (int)e;
+  return (int)prepare_noalloc();
 }
 
 int uaii_hip_device_count(int* count) {
@@ -61,6 +64,8 @@ int uaii_hip_device_count(int* count) {
 const char* uaii_hip_error_string(int code) {
   if (code == kErrArg) return "invalid argument";
   if (code == kErrNotImpl) return "not implemented";
+  if (code == kErrScratch)
+    return "the call needs more device scratch than the allocation-free entry point holds";
   return hipGetErrorString(static_cast<hipError_t>(code));
 }
 
