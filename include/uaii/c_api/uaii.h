@@ -63,17 +63,22 @@ typedef struct uaii_session_options {
   uint32_t struct_size;          /* sizeof(uaii_session_options) */
   const char* backend;           /* "rocm" (only backend of this library) */
   const char* weights_dir;       /* prefix for relative model paths (may be NULL) */
-  uaii_weight_init weight_init;  /* accepted for ABI parity; GGUF weights must load */
+  uaii_weight_init weight_init;  /* accepted; every weight of a GGUF decoder must load */
   int enable_fusion;             /* accepted; the device program is always fused */
-  int enable_memory_reuse;       /* accepted; no f32 weight slots exist on device */
+  int enable_memory_reuse;       /* non-zero (default): weights take the values of the
+                                    reference's f32 weight load (its Path A: Q4_0 nibbles
+                                    in pairwise order); 0 with keep_quantized_weights:
+                                    those of its packed decode (Path B) */
   int enable_profiler;           /* non-zero: per-step device timing is recorded */
   const char* profile_trace_path;
-  uint64_t budget_bytes;         /* device byte budget; 0 = unlimited */
+  uint64_t budget_bytes;         /* device byte budget; 0 = unlimited; exceeding it
+                                    fails with UAII_ERR_INVALID_ARGUMENT */
   int enable_streaming;          /* must be 0: the whole model is HBM resident */
   int allow_missing_weights;
   const char* weights_sandbox;
   int compute_dtype;             /* uaii_compute_dtype: KV cache storage */
-  int keep_quantized_weights;    /* must be non-zero: weights stay block-packed */
+  int keep_quantized_weights;    /* 0: Path A values as with enable_memory_reuse; the
+                                    device keeps weights block-packed either way */
   int64_t max_context;           /* 0 = GGUF {arch}.context_length */
 } uaii_session_options;
 

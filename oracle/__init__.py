@@ -12,6 +12,8 @@ Parity status per oracle function (what pins it):
   orc_half_to_float      exhaustive 65536-value check vs numpy float16 + _ref
   orc_dequant_row        reference Q4_0 known-answer block, hand-built closed-form
                          blocks for every format, synth round-trip bounds, _ref
+  orc_load_row_f32       _ref's gguf_load_tensor_f32 (the reference loader itself)
+                         on whole tensors of every format, bit for bit
   orc_quant_gemm         benchmark-pattern known answer in f64, _ref
   orc_rmsnorm            unit-RMS invariant with w=1, numpy f64, _ref
   orc_rope               pos 0 identity, pair-norm preservation, numpy f64, _ref
@@ -80,11 +82,18 @@ def oracle():
         L.orc_moe_topk.argtypes = [f, i64, C.c_int, C.POINTER(C.c_int), f]
         L.orc_model_open.restype = vp
         L.orc_model_open.argtypes = [C.c_char_p, C.c_int]
+        L.orc_model_open_ex.restype = vp
+        L.orc_model_open_ex.argtypes = [C.c_char_p, C.c_int, C.c_int]
+        L.orc_load_row_f32.restype = C.c_int
+        L.orc_load_row_f32.argtypes = [C.c_int, vp, i64, f]
         L.orc_model_close.restype = None
         L.orc_model_close.argtypes = [vp]
         L.orc_last_error.restype = C.c_char_p
         L.orc_model_hparams.restype = None
         L.orc_model_hparams.argtypes = [vp, C.POINTER(i64)]
+        L.orc_model_tensor.restype = C.c_int
+        L.orc_model_tensor.argtypes = [vp, C.c_char_p, C.POINTER(C.c_int), C.POINTER(i64),
+                                       C.POINTER(C.c_void_p)]
         L.orc_model_fparams.restype = None
         L.orc_model_fparams.argtypes = [vp, f]
         L.orc_generate.restype = C.c_int
@@ -131,6 +140,10 @@ def ref():
         L.uref_generate.restype = C.c_int
         L.uref_generate.argtypes = [C.c_char_p, C.c_int, C.POINTER(i64), i64, i64, C.POINTER(i64),
                                     C.POINTER(i64), f, f]
+        L.uref_generate_path_a.restype = C.c_int
+        L.uref_generate_path_a.argtypes = L.uref_generate.argtypes
+        L.uref_load_tensor_f32.restype = C.c_int
+        L.uref_load_tensor_f32.argtypes = [C.c_char_p, C.c_char_p, f, i64, C.POINTER(i64)]
         _r = L
     return _r
 
@@ -147,6 +160,18 @@ def dequant(gguf_type: int, packed, rows: int, cols: int, use_ref: bool = False)
         rc = fn(gguf_type, C.c_void_p(p.ctypes.data + r * rb), cols, _fp(out[r]))
         if rc != 0:
             raise OracleError("dequant failed")
+    return out
+
+
+def load_f32(gguf_type: int, packed, rows: int, cols: int):
+    """Rows as the reference's f32 weight load gives them (orc_load_row_f32)."""
+    import numpy as np
+    p = np.ascontiguousarray(packed, dtype=np.uint8)
+    out = np.empty((rows, cols), dtype=np.float32)
+    rb = oracle().orc_row_bytes(gguf_type, cols)
+    for r in range(rows):
+        if oracle().orc_load_row_f32(gguf_type, C.c_void_p(p.ctypes.data + r * rb), cols, _fp(out[r])):
+            raise OracleError("load_f32 failed")
     return out
 
 
@@ -169,11 +194,16 @@ def quant_gemm(gguf_type: int, a, packed, n: int, nthreads: int = 0, use_ref: bo
 
 
 class Model:
-    """An oracle model (orc_model_open) with greedy generate and taps."""
+    """An oracle model (orc_model_open_ex) with greedy generate and taps.
 
-    def __init__(self, path: str, max_layers: int = 0):
+    path_a=True runs the reference's Path A (weights as its f32 load gives them,
+    f32 GEMM): what the reference does under its default options
+    (enable_memory_reuse=1) or keep_quantized_weights=0. MoE models run Path A
+    either way."""
+
+    def __init__(self, path: str, max_layers: int = 0, path_a: bool = False):
         self.path = str(path)
-        self.h = oracle().orc_model_open(self.path.encode(), max_layers)
+        self.h = oracle().orc_model_open_ex(self.path.encode(), max_layers, int(path_a))
         if not self.h:
             raise OracleError(oracle().orc_last_error().decode())
         hp = (C.c_int64 * 12)()
@@ -204,6 +234,19 @@ class Model:
             raise OracleError(oracle().orc_last_error().decode())
         return out[: n.value], bufs
 
+    def tensor(self, name: str):
+        """(GGUF type, rows, cols, a copy of the raw bytes) of one tensor."""
+        import numpy as np
+        t = C.c_int()
+        ne = (C.c_int64 * 3)()
+        data = C.c_void_p()
+        if oracle().orc_model_tensor(self.h, name.encode(), C.byref(t), ne, C.byref(data)) != 0:
+            raise OracleError(f"tensor not found: {name}")
+        cols, rows = ne[0], ne[1] * ne[2]
+        nbytes = rows * oracle().orc_row_bytes(t.value, cols)
+        raw = np.ctypeslib.as_array((C.c_uint8 * nbytes).from_address(data.value)).copy()
+        return t.value, rows, cols, raw
+
     def time_decode_window(self, start_pos: int, n_steps: int, nthreads: int = 0) -> float:
         s = oracle().orc_time_decode_window(self.h, start_pos, n_steps, nthreads)
         if s < 0:
@@ -223,8 +266,9 @@ class Model:
 
 
 def ref_generate(path: str, prompt, max_new: int, max_layers: int = 0, n_layers: int = 0,
-                 dim: int = 0, vocab: int = 0):
-    """Greedy generate through the reference's compiled kernels (needs _ref)."""
+                 dim: int = 0, vocab: int = 0, path_a: bool = False):
+    """Greedy generate through the reference's compiled kernels (needs _ref);
+    path_a=True loads every weight with the reference's gguf_load_tensor_f32."""
     import numpy as np
     R = ref()
     if R is None:
@@ -234,12 +278,26 @@ def ref_generate(path: str, prompt, max_new: int, max_layers: int = 0, n_layers:
     n = C.c_int64()
     logits = np.zeros(max(vocab, 1), np.float32)
     resid2 = np.zeros(max(n_layers * dim, 1), np.float32)
-    rc = R.uref_generate(str(path).encode(), max_layers, p.ctypes.data_as(C.POINTER(C.c_int64)),
+    fn = R.uref_generate_path_a if path_a else R.uref_generate
+    rc = fn(str(path).encode(), max_layers, p.ctypes.data_as(C.POINTER(C.c_int64)),
                          len(p), max_new, out.ctypes.data_as(C.POINTER(C.c_int64)), C.byref(n),
                          _fp(logits) if vocab else None, _fp(resid2) if n_layers else None)
     if rc != 0:
         raise OracleError(R.uref_last_error().decode())
     return out[: n.value], logits, resid2.reshape(max(n_layers, 1), -1) if n_layers else None
+
+
+def ref_load_tensor_f32(path: str, name: str):
+    """A whole GGUF tensor through the reference's gguf_load_tensor_f32 (needs _ref)."""
+    import numpy as np
+    R = ref()
+    n = C.c_int64()
+    if R.uref_load_tensor_f32(str(path).encode(), name.encode(), None, 0, C.byref(n)) != 0:
+        raise OracleError(R.uref_last_error().decode())
+    out = np.zeros(n.value, np.float32)
+    if R.uref_load_tensor_f32(str(path).encode(), name.encode(), _fp(out), n.value, C.byref(n)) != 0:
+        raise OracleError(R.uref_last_error().decode())
+    return out
 
 
 def ref_sample_token(row, temperature, top_p, top_k, rep, seed, penalty=()):

@@ -9,10 +9,14 @@
 // re-drives the reference kernels in the order the reference GGUF graph wires
 // them (libs/uaii-loaders/src/gguf.cpp:935-1209) with the dispatch decisions of
 // libs/uaii-kernels/src/dispatch.cpp:82-237 and the token loop of
-// libs/uaii-runtime/src/session.cpp:910-1164. GGUF header parsing is borrowed
-// from the C oracle (uaii_oracle.c), whose own parity is tested separately.
+// libs/uaii-runtime/src/session.cpp:910-1164. GGUF header parsing for the
+// graph wiring is borrowed from the C oracle (uaii_oracle.c), whose own parity is
+// tested separately; weights that the reference holds as f32 (norms, biases,
+// routers, every weight on Path A) come from the reference's own loader
+// (gguf_read_header + gguf_load_tensor_f32, libs/uaii-loaders/src/gguf.cpp).
 
 #include "uaii/kernels/kernels.hpp"
+#include "uaii/loaders/gguf.hpp"
 #include "uaii/kernels/quant_gemm.hpp"
 #include "uaii/quant/gguf_dequant.hpp"
 #include "uaii/runtime/kv_cache.hpp"
@@ -194,10 +198,10 @@ struct Weight {
 };
 
 // Path B keeps block-quant weights packed (session.cpp:342-358); Path A and
-// non-block types are dequantized to f32 with the reference's own decoder
-// (gguf.cpp:445-556, which delegates to dequant_gguf_row for K-quants; for Q8_0
-// and Q4_0-ggml layout the values are identical).
-bool bind_weight(orc_model* m, const std::string& name, bool f32_always, bool path_a, Weight* w) {
+// non-block types are f32, as the reference's own loader gives them
+// (gguf_load_tensor_f32, gguf.cpp:445-556, the load of session.cpp:434-443).
+bool bind_weight(orc_model* m, const loaders::GgufFile& gf, const std::string& name,
+                 bool f32_always, bool path_a, Weight* w) {
   int type = 0;
   std::int64_t ne[3];
   const std::uint8_t* data = nullptr;
@@ -220,20 +224,11 @@ bool bind_weight(orc_model* m, const std::string& name, bool f32_always, bool pa
     w->view.quant_cols = rank == 3 ? 0 : cols;
     w->view.nbytes = quant::packed_nbytes(f, static_cast<std::size_t>(rows * cols));
   } else {
-    w->f32.resize(static_cast<std::size_t>(rows * cols));
-    const std::size_t rb = quant::packed_nbytes(f, static_cast<std::size_t>(cols));
-    for (std::int64_t r = 0; r < rows; ++r) {
-      if (f == quant::QuantFormat::F32) {
-        std::memcpy(&w->f32[r * cols], data + r * cols * 4, cols * 4);
-      } else if (f == quant::QuantFormat::F16) {
-        for (std::int64_t c = 0; c < cols; ++c) {
-          std::uint16_t h;
-          std::memcpy(&h, data + (r * cols + c) * 2, 2);
-          w->f32[r * cols + c] = orc_half_to_float(h);
-        }
-      } else {
-        (void)quant::dequant_gguf_row(f, data + r * rb, cols, &w->f32[r * cols]);
-      }
+    Shape sh;
+    const Error e = loaders::gguf_load_tensor_f32(gf, name, &w->f32, &sh);
+    if (!e.ok() || w->f32.size() != static_cast<std::size_t>(rows * cols)) {
+      g_err = "gguf_load_tensor_f32 " + name + ": " + e.message();
+      return false;
     }
     w->view.dtype = DType::F32;
     w->view.data = w->f32.data();
@@ -263,6 +258,7 @@ struct RefRunner {
                ctx = 0, qd = 0, kvd = 0, ff = 1;
   float theta = 0.f, eps = 0.f;
   bool path_a = false;
+  loaders::GgufFile gf;
   Weight emb, onorm, lm;
   std::vector<Weight> W;
   runtime::KvCache kv;
@@ -275,9 +271,11 @@ struct RefRunner {
   }
 
   Error open(const char* path, int max_layers, std::int64_t kv_max_override,
-             std::int64_t total_hint, std::int64_t n_prompt) {
+             std::int64_t total_hint, std::int64_t n_prompt, bool force_path_a = false) {
     m = orc_model_open(path, max_layers);
     if (!m) return Error::make(ErrorCode::NotFound, orc_last_error());
+    Error he = loaders::gguf_read_header(path, &gf);
+    if (!he.ok()) return he;
     std::int64_t hp[12];
     float fp[2];
     orc_model_hparams(m, hp);
@@ -285,13 +283,13 @@ struct RefRunner {
     L = hp[0]; D = hp[1]; H = hp[2]; HKV = hp[3]; hd = hp[4]; V = hp[5];
     E = hp[7]; topk = hp[8]; rope_mode = hp[9]; ctx = hp[10];
     theta = fp[0]; eps = fp[1];
-    path_a = E > 0;
+    path_a = force_path_a || E > 0;
     qd = H * hd; kvd = HKV * hd;
     W.resize(static_cast<std::size_t>(L * NW));
-    bind_weight(m, "token_embd.weight", false, path_a, &emb);
-    bind_weight(m, "output_norm.weight", true, path_a, &onorm);
-    if (!bind_weight(m, "output.weight", false, path_a, &lm)) {
-      bind_weight(m, "token_embd.weight", false, path_a, &lm);  // tied (gguf.cpp:813-816)
+    bind_weight(m, gf, "token_embd.weight", false, path_a, &emb);
+    bind_weight(m, gf, "output_norm.weight", true, path_a, &onorm);
+    if (!bind_weight(m, gf, "output.weight", false, path_a, &lm)) {
+      bind_weight(m, gf, "token_embd.weight", false, path_a, &lm);  // tied (gguf.cpp:813-816)
     }
     // per layer: 0 attn_norm .. 8 ffn_down, 9-12 MoE router/experts, 13-15 q/k/v
     // biases, 16-18 shared expert gate/up/down (gguf.cpp:1107-1128)
@@ -306,7 +304,7 @@ struct RefRunner {
         std::string nm = "blk." + std::to_string(li) + "." + names[kk];
         if (kk < 13 || kk >= 16) nm += ".weight";
         const bool f32_always = (kk == 0 || kk == 5 || (kk >= 9 && kk < 16));
-        bind_weight(m, nm, f32_always, path_a, &W[li * NW + kk]);
+        bind_weight(m, gf, nm, f32_always, path_a, &W[li * NW + kk]);
       }
     }
     for (std::int64_t li = 0; li < L; ++li) {
@@ -436,9 +434,10 @@ namespace {
 // session.cpp:974-978).
 int generate_with(const char* path, int max_layers, const std::int64_t* prompt,
                   std::int64_t n_prompt, std::int64_t max_new, const runtime::SampleParams& sp,
-                  std::int64_t* out, std::int64_t* out_n, float* taps_logits, float* taps_resid2) {
+                  std::int64_t* out, std::int64_t* out_n, float* taps_logits, float* taps_resid2,
+                  bool path_a = false) {
   RefRunner R;
-  Error err = R.open(path, max_layers, 0, n_prompt + max_new, n_prompt);
+  Error err = R.open(path, max_layers, 0, n_prompt + max_new, n_prompt, path_a);
   if (!err.ok()) { g_err = err.message(); return -1; }
   std::vector<std::int64_t> hist;
   std::mt19937_64 rng{0};
@@ -486,6 +485,31 @@ int uref_generate(const char* path, int max_layers, const std::int64_t* prompt,
                   std::int64_t* out_n, float* taps_logits, float* taps_resid2) {
   return generate_with(path, max_layers, prompt, n_prompt, max_new, runtime::SampleParams{}, out,
                        out_n, taps_logits, taps_resid2);
+}
+
+// Greedy generate on Path A (every weight f32 from gguf_load_tensor_f32, f32
+// GEMM): the reference's route under its default options (session.cpp:259-367).
+int uref_generate_path_a(const char* path, int max_layers, const std::int64_t* prompt,
+                         std::int64_t n_prompt, std::int64_t max_new, std::int64_t* out,
+                         std::int64_t* out_n, float* taps_logits, float* taps_resid2) {
+  return generate_with(path, max_layers, prompt, n_prompt, max_new, runtime::SampleParams{}, out,
+                       out_n, taps_logits, taps_resid2, true);
+}
+
+// One whole GGUF tensor through the reference's f32 load (gguf.cpp:445-556).
+int uref_load_tensor_f32(const char* path, const char* name, float* out, std::int64_t cap,
+                         std::int64_t* out_n) {
+  loaders::GgufFile gf;
+  Error e = loaders::gguf_read_header(path, &gf);
+  std::vector<float> v;
+  Shape sh;
+  if (e.ok()) e = loaders::gguf_load_tensor_f32(gf, name, &v, &sh);
+  if (!e.ok()) { g_err = e.message(); return -1; }
+  *out_n = static_cast<std::int64_t>(v.size());
+  if (out == nullptr) return 0;
+  if (cap < *out_n) { g_err = "capacity"; return -1; }
+  std::memcpy(out, v.data(), v.size() * 4);
+  return 0;
 }
 
 // The same with the reference sampler: temperature / top_p / top_k / repetition

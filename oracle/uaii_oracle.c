@@ -308,6 +308,22 @@ int orc_dequant_row(int t, const uint8_t* p, int64_t cols, float* out) {
   return 0;
 }
 
+/* Row values of the reference's f32 weight load (gguf.cpp:445-556). */
+int orc_load_row_f32(int t, const uint8_t* p, int64_t cols, float* out) {
+  if (t != ORC_Q4_0) return orc_dequant_row(t, p, cols, out);
+  if (!p || !out || cols % 32) return -1;
+  for (int64_t b = 0; b < cols / 32; b++) {
+    const uint8_t* blk = p + b * 18;
+    const float d = rdh(blk);
+    for (int i = 0; i < 32; i += 2) { /* gguf.cpp:514-520 */
+      const uint8_t byte = blk[2 + i / 2];
+      out[b * 32 + i] = d * (float)((int)(byte & 0x0f) - 8);
+      out[b * 32 + i + 1] = d * (float)((int)(byte >> 4) - 8);
+    }
+  }
+  return 0;
+}
+
 /* ------------------------------------------------------------------ threads */
 
 typedef struct {
@@ -690,12 +706,15 @@ static size_t tensor_bytes(const orc_tensor* t) {
   return orc_row_bytes(t->type, (int64_t)n);
 }
 
-static float* dequant_all(const orc_w* w) {
+/* f32 copy of a weight: the f32 load's values on Path A, else the dequant's */
+static float* dequant_all(const orc_w* w, int path_a) {
   int64_t per = w->rows * w->cols;
   float* f = (float*)malloc((size_t)(per * w->n3) * 4);
   size_t rb = orc_row_bytes(w->type, w->cols);
-  for (int64_t r = 0; r < w->rows * w->n3; r++)
-    orc_dequant_row(w->type, w->data + r * rb, w->cols, f + r * w->cols);
+  for (int64_t r = 0; r < w->rows * w->n3; r++) {
+    if (path_a) orc_load_row_f32(w->type, w->data + r * rb, w->cols, f + r * w->cols);
+    else orc_dequant_row(w->type, w->data + r * rb, w->cols, f + r * w->cols);
+  }
   return f;
 }
 
@@ -712,13 +731,17 @@ static int bind_w(orc_model* m, const char* name, orc_w* w, int want_f32) {
   w->rows = t->n_dims > 1 ? (int64_t)t->ne[1] : 1;
   w->n3 = t->n_dims > 2 ? (int64_t)t->ne[2] : 1;
   w->data = t->data;
-  if (want_f32 || t->type == ORC_F32 || t->type == ORC_F16) w->f32 = dequant_all(w);
+  if (want_f32 || t->type == ORC_F32 || t->type == ORC_F16) w->f32 = dequant_all(w, m->path_a);
   return 1;
 }
 
 static void free_w(orc_w* w) { free(w->f32); w->f32 = NULL; }
 
 orc_model* orc_model_open(const char* path, int max_layers) {
+  return orc_model_open_ex(path, max_layers, 0);
+}
+
+orc_model* orc_model_open_ex(const char* path, int max_layers, int path_a) {
   int fd = open(path, O_RDONLY);
   if (fd < 0) { set_err("cannot open gguf"); return NULL; }
   struct stat st;
@@ -824,7 +847,7 @@ orc_model* orc_model_open(const char* path, int max_layers) {
   }
   if (m->n_layers > 512) m->n_layers = 512;
   if (max_layers > 0 && m->n_layers > max_layers) m->n_layers = max_layers;
-  m->path_a = find_t(m, "blk.0.ffn_gate_exps.weight") != NULL || m->n_experts > 0;
+  m->path_a = path_a || find_t(m, "blk.0.ffn_gate_exps.weight") != NULL || m->n_experts > 0;
 
   if (bind_w(m, "token_embd.weight", &m->tok_embd, 0) < 0) goto fail;
   if (!m->tied && bind_w(m, "output.weight", &m->output, m->path_a) < 0) goto fail;
@@ -832,7 +855,7 @@ orc_model* orc_model_open(const char* path, int max_layers) {
     /* lm_head reuses the embedding weight (gguf.cpp:813-816); own f32 copy if needed */
     m->output = m->tok_embd;
     int need = m->path_a || m->tok_embd.type == ORC_F32 || m->tok_embd.type == ORC_F16;
-    m->output.f32 = need ? dequant_all(&m->tok_embd) : NULL;
+    m->output.f32 = need ? dequant_all(&m->tok_embd, m->path_a) : NULL;
   }
   m->has_out_norm = bind_w(m, "output_norm.weight", &m->out_norm, 1);
   if (m->has_out_norm < 0) goto fail;
@@ -1075,9 +1098,11 @@ static int forward(orc_state* s, int64_t token, int64_t pos, int nthreads, orc_t
   int64_t D = m->dim, hd = m->head_dim, qd = m->n_heads * hd, kvd = m->n_kv * hd;
   if (token < 0 || token >= m->tok_embd.rows) { set_err("embedding token id out of range"); return -1; }
   if (pos >= s->max_seq) { set_err("KvCache capacity exceeded"); return -1; }
-  /* Embedding (transformer.cpp:61-142): one dequantized row */
+  /* Embedding (transformer.cpp:61-142): one dequantized row (Path A: the row of
+   * the f32-loaded table) */
   size_t erb = orc_row_bytes(m->tok_embd.type, D);
-  orc_dequant_row(m->tok_embd.type, m->tok_embd.data + token * erb, D, s->x);
+  if (m->path_a) orc_load_row_f32(m->tok_embd.type, m->tok_embd.data + token * erb, D, s->x);
+  else orc_dequant_row(m->tok_embd.type, m->tok_embd.data + token * erb, D, s->x);
   if (tp && tp->hidden) memcpy(tp->hidden, s->x, (size_t)D * 4);
   for (int64_t li = 0; li < m->n_layers; li++) {
     orc_layer* L = &m->L[li];

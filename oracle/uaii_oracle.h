@@ -44,6 +44,15 @@ int orc_block_bytes(int type);
  * closed-form hand-built blocks for each format, and oracle/_ref. */
 int orc_dequant_row(int type, const uint8_t* packed, int64_t cols, float* out);
 
+/* One row as the reference's f32 weight load gives it (gguf_load_tensor_f32,
+ * libs/uaii-loaders/src/gguf.cpp:445-556), the values every weight takes on
+ * Path A: Q4_0 byte j of a block gives elements 2j (low nibble) and 2j+1 (high
+ * nibble) (gguf.cpp:514-520); Q8_0, F32 and F16 decode as orc_dequant_row, and
+ * the other block formats go through it (gguf.cpp:528-546).
+ * Pinned: against the reference's gguf_load_tensor_f32 on whole GGUF tensors
+ * (oracle/_ref, tests/test_oracle_path_a.py). */
+int orc_load_row_f32(int type, const uint8_t* packed, int64_t cols, float* out);
+
 /* C[M,N] = A[M,K] * dequant(B[N,K])^T, per-row dequant then sequential f32 dot
  * (libs/uaii-kernels/src/quant_gemm.cpp:22-70). nthreads<=0 -> all cores.
  * Pinned: benchmark pattern known answer (benchmarks/src/uaii_bench.cpp:505-518)
@@ -89,6 +98,12 @@ typedef struct orc_model orc_model;
  * derivation gguf.cpp:801-1246). max_layers>0 caps the layer count like
  * UAII_MAX_LAYERS (gguf.cpp:785-799). Returns NULL on failure (orc_last_error()). */
 orc_model* orc_model_open(const char* path, int max_layers);
+/* The same; path_a != 0 runs every model on the reference's Path A (all weights
+ * loaded as f32 by gguf_load_tensor_f32 and multiplied by the f32 GEMM), which
+ * the reference takes under its default options (enable_memory_reuse=1:
+ * session.cpp:259-367, :420-443) or keep_quantized_weights=0. MoE models take
+ * Path A either way (their expert kernel reads f32 only, transformer.cpp:551-554). */
+orc_model* orc_model_open_ex(const char* path, int max_layers, int path_a);
 void orc_model_close(orc_model* m);
 const char* orc_last_error(void);
 

@@ -87,8 +87,6 @@ def test_create_fails_before_compute(tmp_path):
     tiny = synth.cached_model(synth.PRESETS["tiny"]).encode()
     rc, msg, h = _create(tiny, backend=b"cpu")
     assert rc == 7 and "rocm" in msg and not h.value
-    rc, msg, _ = _create(tiny, keep_quantized_weights=0)
-    assert rc == 7
     rc, msg, _ = _create(tiny, struct_size=0)
     assert rc == 6
     rc, msg, _ = _create(tiny, struct_size=C.sizeof(uaii_amd.SessionOptions) + 8)

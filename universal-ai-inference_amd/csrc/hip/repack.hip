@@ -48,9 +48,23 @@ __device__ inline void cp(uint8_t* dst, const uint8_t* src, int n) {
   for (int i = 0; i < n; ++i) dst[i] = src[i];
 }
 
-// One thread per GGUF block.
+// Q4_0 payload whose ggml decode (element k = low nibble of byte k, element
+// k + 16 = its high nibble) gives the values of the reference's f32 load, which
+// takes elements 2j and 2j + 1 from the low and high nibbles of byte j
+// (libs/uaii-loaders/src/gguf.cpp:514-520).
+__device__ inline void q4_0_from_pairwise(uint8_t* dst, const uint8_t* qs) {
+  for (int k = 0; k < 16; ++k) {
+    const int sh = 4 * (k & 1);
+    const uint32_t lo = (qs[k >> 1] >> sh) & 15u;        // element k
+    const uint32_t hi = (qs[8 + (k >> 1)] >> sh) & 15u;  // element k + 16
+    dst[k] = (uint8_t)(lo | (hi << 4));
+  }
+}
+
+// One thread per GGUF block. q4_0_pairwise: Q4_0 blocks take the values of the
+// reference's f32 load instead of its packed decode.
 __global__ void k_repack(DevWeight w, const uint8_t* __restrict__ src, int64_t nblocks_row,
-                         int64_t total_blocks) {
+                         int64_t total_blocks, int q4_0_pairwise) {
   const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (gid >= total_blocks) return;
   const int64_t r = gid / nblocks_row, i = gid % nblocks_row;
@@ -63,7 +77,11 @@ __global__ void k_repack(DevWeight w, const uint8_t* __restrict__ src, int64_t n
   switch (w.type) {
     case T_F32: cp(a + i * 4, s, 4); break;
     case T_F16: cp(a + i * 2, s, 2); break;
-    case T_Q4_0: cp(b + i * 2, s, 2); cp(a + i * 16, s + 2, 16); break;
+    case T_Q4_0:
+      cp(b + i * 2, s, 2);
+      if (q4_0_pairwise) q4_0_from_pairwise(a + i * 16, s + 2);
+      else cp(a + i * 16, s + 2, 16);
+      break;
     case T_Q4_1: cp(b + i * 4, s, 4); cp(a + i * 16, s + 4, 16); break;
     case T_Q5_0: cp(c + i * 2, s, 2); cp(b + i * 4, s + 2, 4); cp(a + i * 16, s + 6, 16); break;
     case T_Q5_1: cp(c + i * 4, s, 4); cp(b + i * 4, s + 4, 4); cp(a + i * 16, s + 8, 16); break;
@@ -100,13 +118,14 @@ __global__ void k_dequant(DevWeight w, int64_t row0, int64_t nrows, float* __res
 
 }  // namespace
 
-hipError_t launch_repack(const DevWeight& w, const uint8_t* src_dev, hipStream_t s) {
+hipError_t launch_repack(const DevWeight& w, const uint8_t* src_dev, hipStream_t s, bool q4_0_pairwise) {
   const int64_t nbr = w.cols / block_elems(w.type);
   const int64_t total = nbr * w.rows;
   if (total == 0) return hipSuccess;
   const int threads = 256;
   const int64_t grid = (total + threads - 1) / threads;
-  hipLaunchKernelGGL(k_repack, dim3((unsigned)grid), dim3(threads), 0, s, w, src_dev, nbr, total);
+  hipLaunchKernelGGL(k_repack, dim3((unsigned)grid), dim3(threads), 0, s, w, src_dev, nbr, total,
+                     q4_0_pairwise ? 1 : 0);
   return hipGetLastError();
 }
 

@@ -12,7 +12,10 @@ namespace uaii_hip {
 // Bytes per row of the split arrays a, b, c, d for `type` at `cols`.
 void split_row_bytes(int type, int64_t cols, int64_t out[4]);
 
-hipError_t launch_repack(const DevWeight& w, const uint8_t* src_dev, hipStream_t s);
+// q4_0_pairwise: Q4_0 rows take the values of the reference's f32 weight load
+// (gguf.cpp:514-520) rather than its packed decode (gguf_dequant.cpp:117-134).
+hipError_t launch_repack(const DevWeight& w, const uint8_t* src_dev, hipStream_t s,
+                         bool q4_0_pairwise = false);
 hipError_t launch_dequant(const DevWeight& w, int64_t row0, int64_t nrows, float* out,
                           hipStream_t s);
 

@@ -48,7 +48,7 @@ DeviceWeight::~DeviceWeight() {
 }
 
 Error upload_weight(int type, const uint8_t* host, int64_t rows, int64_t cols, hipStream_t s,
-                    DeviceWeight* out) {
+                    DeviceWeight* out, bool f32_load) {
   const int be = block_elems(type);
   if (be == 0) return Error::make(ErrorCode::NotImplemented, "unsupported GGUF type " + std::to_string(type));
   if (rows <= 0 || cols <= 0 || cols % be)
@@ -85,7 +85,7 @@ Error upload_weight(int type, const uint8_t* host, int64_t rows, int64_t cols, h
       DevWeight sub = v;
       sub.rows = n;
       sub.a += r0 * v.a_row; sub.b += r0 * v.b_row; sub.c += r0 * v.c_row; sub.d += r0 * v.d_row;
-      st = launch_repack(sub, static_cast<const uint8_t*>(stage), s);
+      st = launch_repack(sub, static_cast<const uint8_t*>(stage), s, f32_load);
     }
     if (st == hipSuccess) st = hipStreamSynchronize(s);
     err = hip_error(st, "weight upload");
@@ -113,6 +113,17 @@ void DecoderProgram::free_dynamic() {
   }
   kv_ = nullptr; ids_ = nullptr; rope_ = nullptr; attn_part_ = nullptr;
   max_ctx_ = 0;
+  used_dyn_ = 0;
+}
+
+Error DecoderProgram::charge(uint64_t& pool, uint64_t bytes) {
+  const uint64_t used = used_static_ + used_dyn_ + used_pf_;
+  if (opts_.budget_bytes != 0 && used + bytes > opts_.budget_bytes)
+    return Error::make(ErrorCode::InvalidArgument,
+                       "memory budget exceeded: used=" + std::to_string(used) + " need=" +
+                           std::to_string(bytes) + " limit=" + std::to_string(opts_.budget_bytes));
+  pool += bytes;
+  return Error::success();
 }
 
 Error DecoderProgram::upload_f32(const GgufTensor* t, float** out) {
@@ -120,6 +131,7 @@ Error DecoderProgram::upload_f32(const GgufTensor* t, float** out) {
   if (!t) return Error::success();
   uint64_t n = 1;
   for (auto d : t->ne) n *= d;
+  UAII_TRY(charge(used_static_, n * 4));
   std::vector<float> h(n);
   if (t->type == T_F32) {
     std::memcpy(h.data(), t->data, n * 4);
@@ -164,13 +176,20 @@ Error DecoderProgram::build(const DecoderSpec& spec, const ProgramOptions& opts)
   if (d.dim % 4 || d.q_dim % 4)
     return Error::make(ErrorCode::InvalidArgument, "model dims must be multiples of 4");
 
+  // Path A values (the reference's f32 weight load) when asked, and for MoE
+  // models, whose expert kernel the reference runs on f32 weights only
+  // (transformer.cpp:551-554)
+  bool moe_model = d.n_experts > 0;
+  for (const LayerSpec& s : d.layers) moe_model = moe_model || s.ffn == LayerSpec::kMoE;
+  const bool f32_load = opts_.f32_weight_load || moe_model;
   auto up = [&](const GgufTensor* t, DeviceWeight* w) -> Error {
     // the rows the upload copies must be exactly the bytes the file holds for
     // this tensor (the parser bounded those by the end of the mapping)
     if (t->cols() <= 0 || t->rows() <= 0 ||
         (uint64_t)t->rows() * gguf_nbytes(t->type, (uint64_t)t->cols()) != t->nbytes)
       return Error::make(ErrorCode::InvalidArgument, "tensor " + t->name + " shape does not match its bytes");
-    return upload_weight(t->type, t->data, t->rows(), t->cols(), stream_, w);
+    UAII_TRY(upload_weight(t->type, t->data, t->rows(), t->cols(), stream_, w, f32_load));
+    return charge(used_static_, w->bytes);
   };
   UAII_TRY(up(d.tok_embd, &tok_embd_));
   if (!d.tied) UAII_TRY(up(d.output, &output_));
@@ -238,6 +257,7 @@ Error DecoderProgram::build(const DecoderSpec& spec, const ProgramOptions& opts)
 
   // activations and step state
   auto alloc = [&](size_t bytes, void** p) -> Error {
+    UAII_TRY(charge(used_static_, std::max<size_t>(bytes, 256)));
     UAII_HIP(hipMalloc(p, std::max<size_t>(bytes, 256)));
     UAII_HIP(hipMemset(*p, 0, std::max<size_t>(bytes, 256)));
     allocs_.push_back(*p);
@@ -363,6 +383,7 @@ Error DecoderProgram::ensure_prefill_buffers(int64_t chunk) {
   UAII_HIP(hipStreamSynchronize(stream_));
   for (void* p : pf_allocs_) (void)hipFree(p);
   pf_allocs_.clear();
+  used_pf_ = 0;
   const DecoderSpec& d = spec_;
   int64_t inter = 1, inter_sh = 0;
   for (const LayerSpec& ls : d.layers) inter = std::max(inter, ls.inter);
@@ -371,6 +392,7 @@ Error DecoderProgram::ensure_prefill_buffers(int64_t chunk) {
   const int64_t mpad = pf_mpad(chunk * topk);  // MoE: the experts' hidden rows
   const int64_t kmax = std::max({d.dim, d.q_dim, inter, inter_sh});
   auto alloc = [&](size_t bytes, void** p) -> Error {
+    UAII_TRY(charge(used_pf_, std::max<size_t>(bytes, 256)));
     UAII_HIP(hipMalloc(p, std::max<size_t>(bytes, 256)));
     pf_allocs_.push_back(*p);
     return Error::success();
@@ -770,17 +792,19 @@ Error DecoderProgram::ensure_capacity(int64_t max_seq) {
   // slack past the end: the layer kernel fetches whole tiles of keys, masking
   // the ones past the cached length
   const size_t kv_slack = 64 << 10;
+  const int hd = (int)d.head_dim;
+  attn_splits_ = attention_splits(max_seq);
+  const int G = (int)(d.n_heads / d.n_kv_heads);
+  const size_t part = (size_t)d.n_kv_heads * attn_splits_ * G * (size_t)(hd + 2);
+  UAII_TRY(charge(used_dyn_, kv_bytes_ + kv_slack + sizeof(int32_t) * (size_t)(max_seq + 2) +
+                                 sizeof(float2) * (size_t)max_seq * (size_t)(hd / 2) + part * 4));
   UAII_HIP(hipMalloc(&kv_, kv_bytes_ + kv_slack));
   UAII_HIP(hipMemsetAsync(kv_, 0, kv_bytes_ + kv_slack, stream_));
   UAII_HIP(hipMalloc((void**)&ids_, sizeof(int32_t) * (size_t)(max_seq + 2)));
   UAII_HIP(hipMemsetAsync(ids_, 0, sizeof(int32_t) * (size_t)(max_seq + 2), stream_));
-  const int hd = (int)d.head_dim;
   std::vector<float2> tab = rope_table(d.rope_theta, hd, max_seq);
   UAII_HIP(hipMalloc((void**)&rope_, tab.size() * sizeof(float2)));
   UAII_HIP(hipMemcpy(rope_, tab.data(), tab.size() * sizeof(float2), hipMemcpyHostToDevice));
-  attn_splits_ = attention_splits(max_seq);
-  const int G = (int)(d.n_heads / d.n_kv_heads);
-  const size_t part = (size_t)d.n_kv_heads * attn_splits_ * G * (size_t)(hd + 2);
   UAII_HIP(hipMalloc((void**)&attn_part_, part * 4));
   UAII_HIP(hipStreamSynchronize(stream_));
   max_ctx_ = max_seq;

@@ -33,14 +33,25 @@ struct DeviceWeight {
 };
 
 // Upload `rows` GGUF rows of `cols` values and re-lay them out on the device.
+// f32_load: the rows take the values the reference's f32 weight load gives them
+// (gguf_load_tensor_f32, which orders Q4_0 nibbles pairwise) instead of those of
+// its packed decode; the storage stays block-packed either way.
 Error upload_weight(int type, const uint8_t* host, int64_t rows, int64_t cols, hipStream_t s,
-                    DeviceWeight* out);
+                    DeviceWeight* out, bool f32_load = false);
 
 struct ProgramOptions {
+  // Weights carry the values of the reference's Path A, its f32 weight load
+  // (session.cpp:420-443 -> gguf_load_tensor_f32), rather than of its packed
+  // quant_gemm path. MoE models always do: the reference runs them on Path A only.
+  bool f32_weight_load = false;
   bool kv_f16 = false;        // KV cache storage dtype
   bool use_graph = true;      // replay the captured step graph
   bool profile = false;       // per-kernel HIP event timing (direct launches)
   int64_t max_context = 0;    // 0: GGUF context_length
+  // Device bytes the program may hold (weights, KV cache, activations, prompt
+  // buffers); 0 = unlimited. Exceeding it is InvalidArgument "memory budget
+  // exceeded", as the reference's MemoryBudget::reserve (libs/uaii-memory/src/budget.cpp:6-19).
+  uint64_t budget_bytes = 0;
 };
 
 struct KernelTiming {
@@ -98,6 +109,9 @@ class DecoderProgram {
   };
 
   Error upload_f32(const GgufTensor* t, float** out);
+  // Count `bytes` against the device budget in `pool` (static, dynamic or prompt buffers).
+  Error charge(uint64_t& pool, uint64_t bytes);
+  uint64_t used_static_ = 0, used_dyn_ = 0, used_pf_ = 0;
   // Profiling mode: each launch group records a start/stop event pair on its own
   // kernel dispatches (hipExtLaunchKernelGGL through UAII_LAUNCH), with no
   // synchronisation between kernels; collect_timings() reads the pairs.

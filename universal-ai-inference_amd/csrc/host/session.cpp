@@ -16,10 +16,6 @@ Error Session::create(const std::string& gguf_path, SessionOptions options) {
                        "backend '" + options_.backend_name +
                            "' is not provided by this library (it implements 'rocm')");
   }
-  if (!options_.keep_quantized_weights) {
-    return Error::make(ErrorCode::NotImplemented,
-                       "keep_quantized_weights=0 is not supported: device weights stay block-packed");
-  }
   if (options_.enable_streaming) {
     return Error::make(ErrorCode::NotImplemented,
                        "weight streaming is not supported: the model is HBM resident");
@@ -30,6 +26,13 @@ Error Session::create(const std::string& gguf_path, SessionOptions options) {
   UAII_TRY(file_.open(path));
   UAII_TRY(derive_decoder(file_, &spec_));
   ProgramOptions po;
+  // The reference holds every weight as f32 from gguf_load_tensor_f32 (Path A)
+  // when memory reuse is on (each weight's slot is sized for f32, so the packed
+  // copy is refused: session.cpp:259-367, :420-443) or when quantized weights are
+  // not kept (:342-366); only memory_reuse=0 with keep_quantized_weights=1 keeps
+  // them packed (Path B). The values differ for Q4_0 (gguf.cpp:514-520); device
+  // storage stays packed on both paths.
+  po.f32_weight_load = options_.enable_memory_reuse || !options_.keep_quantized_weights;
   po.kv_f16 = options_.kv_f16;
   // UAII_NO_GRAPH=1 launches the step kernels directly instead of replaying the
   // captured graph (same kernels; for tools that cannot follow stream capture).
@@ -37,6 +40,7 @@ Error Session::create(const std::string& gguf_path, SessionOptions options) {
   po.use_graph = options_.use_graph && !(ng && ng[0] == '1');
   po.profile = options_.enable_profiler;
   po.max_context = options_.max_context;
+  po.budget_bytes = options_.budget_bytes;
   program_ = std::make_unique<DecoderProgram>();
   UAII_TRY(program_->build(spec_, po));
   ready_ = true;

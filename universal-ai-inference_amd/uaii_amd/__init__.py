@@ -253,12 +253,21 @@ class Session:
     """uaii_session_* through the C ABI."""
 
     def __init__(self, path: str, *, kv_f16: bool = False, max_context: int = 0,
-                 profile: bool = False, backend: str = "rocm"):
+                 profile: bool = False, backend: str = "rocm", memory_reuse: bool = False,
+                 keep_quantized: bool = True, budget_bytes: int = 0):
+        """memory_reuse / keep_quantized select the reference's weight path: the
+        defaults here (memory_reuse off, quantized weights kept) are its packed
+        Path B, the quant_gemm path; memory_reuse=True (the C ABI's default, as in
+        the reference) or keep_quantized=False give the values of its Path A (the
+        f32 weight load, Q4_0 nibbles in pairwise order)."""
         L = lib()
         opts = SessionOptions()
         L.uaii_session_options_init(C.byref(opts))
         self._backend = backend.encode()
         opts.backend = self._backend
+        opts.enable_memory_reuse = 1 if memory_reuse else 0
+        opts.keep_quantized_weights = 1 if keep_quantized else 0
+        opts.budget_bytes = budget_bytes
         opts.compute_dtype = 1 if kv_f16 else 0
         opts.max_context = max_context
         opts.enable_profiler = 1 if profile else 0
