@@ -35,6 +35,7 @@ namespace {
 #define UAII_GEMV_BATCH 1
 #endif
 
+
 // Waves per block (measured per role on the 8B decode step): 4 in general; 8 for
 // the QKV epilogue (6144 rows of K = 4096: more row sets share one staged
 // input); 16 for the K-split long rows of the residual-add GEMV (the down
@@ -965,6 +966,12 @@ __global__ void __launch_bounds__(W * 64) k_gemv(GemvArgs a) {
   const int lane = threadIdx.x & 63;
   const int half = PAIR ? wave / HW : 0, hw = PAIR ? wave % HW : wave;
 
+  // The input's loads go out first, from the leading fields of the arguments
+  // (for a pair format a row of K values is K / 32 chunks): the launch's input
+  // is its first memory request, before the segment and group setup below.
+  PairStage ps0;
+  if constexpr (pair_fmt<FMT>() && !PAIR) stage_pairs_issue<FMT>(a, a.x, a.K >> 5, ps0);
+
   // segment lookup (uniform per block; per half for EPI_ADD2)
   int si = 0;
   if constexpr (PAIR) {
@@ -979,32 +986,34 @@ __global__ void __launch_bounds__(W * 64) k_gemv(GemvArgs a) {
   constexpr int RPW = rpw_of(FMT);
   const int ks = a.ksplit;
   const int nrs = HW / ks;  // row sets per block (per half)
-  const int64_t ngroups = (seg.rows + nrs * RPW - 1) / (nrs * RPW);
   const int rs = hw / ks, kp = hw % ks;
 
   Walk wk;
-  wk.nch = seg.w.a_row / 16;
-  const int ncol = (int)((wk.nch + 63) / 64);
-  const int per = (ncol + ks - 1) / ks;
+  wk.nch = seg.w.a_row >> 4;
+  const int ncol = (int)((wk.nch + 63) >> 6);
+  const int per = seg.per;
   wk.cbeg = kp * per;
   wk.cend = min(ncol, wk.cbeg + per);
-  wk.steps = (per + 1) / 2;
+  wk.steps = (per + 1) >> 1;
 
   const float* xin = seg.x ? seg.x : a.x;
   const int64_t ebase = seg.expert ? (int64_t)seg.expert[0] * seg.expert_rows : 0;
   const int pos = epi_pos<EPI>(a);
-  const int64_t g0 = (int64_t)blockIdx.x - (PAIR ? 0 : seg.block0);
+  const int g0 = (int)blockIdx.x - (PAIR ? 0 : seg.block0);
   // this half's staged input (the LDS holds one region per segment for EPI_ADD2)
   const int64_t region = pair_fmt<FMT>() ? wk.nch * 34 : a.K;
   float* const xs = xsm + (PAIR ? half * region : 0);
-  const int64_t mine = (g0 < ngroups) ? (ngroups - g0 + nblk - 1) / nblk : 0;
-  const int64_t nunits = mine * wk.steps;
+  // groups g0, g0 + nblk, ... below ngroups (counts computed on the host)
+  const int mine = (g0 < seg.ngroups) ? seg.gq + (g0 < seg.gr ? 1 : 0) : 0;
+  const int nunits = mine * wk.steps;
 
-  auto unit_l0 = [&](int64_t u) { return ((g0 + (u / wk.steps) * nblk) * nrs + rs) * RPW; };
-  auto unit_step = [&](int64_t u) { return (int)(u % wk.steps); };
+  auto unit_l0 = [&](int u) {
+    return ((int64_t)(g0 + (u / wk.steps) * nblk) * nrs + rs) * RPW;
+  };
+  auto unit_step = [&](int u) { return u % wk.steps; };
 
-  // input loads first, then the first unit's weight loads, then the staging
-  // arithmetic (which waits for the input only)
+  // input loads first; the first unit's weight loads go out before the staging
+  // arithmetic for the register-staged formats, after it for the pair formats
   UnitBuf<FMT> U0;
   if constexpr (PAIR) {
     // both inputs staged by the whole block, one after the other (for the pair
@@ -1025,10 +1034,16 @@ __global__ void __launch_bounds__(W * 64) k_gemv(GemvArgs a) {
     if constexpr (pair_fmt<FMT>())
       if (nunits > 0) load_unit<FMT, EPI>(a, seg, ebase, wk, unit_l0(0), 0, lane, pos, U0);
   } else if constexpr (pair_fmt<FMT>()) {
-    PairStage ps;
-    stage_pairs_issue<FMT>(a, xin, wk.nch, ps);
+    // The weight loads go out only after the input is staged. The input vector
+    // was just written by the previous launch; every CU's request for it is
+    // served behind whatever the grid has already asked of memory, so issuing
+    // the first unit's weights ahead of it (here, or once this wave's own input
+    // has arrived, or after a short sleep) delayed the input to 6-10 us after
+    // the launch against ~3 us, measured by per-wave clock stamps on the 8B
+    // decode (gate/up 19.3 -> 17.9 us, LM head 61 -> 55 us, QKV unchanged;
+    // 461 -> 471 tok/s).
+    stage_pairs_finish<FMT>(a, xin, wk.nch, ps0, xsm, red);
     if (nunits > 0) load_unit<FMT, EPI>(a, seg, ebase, wk, unit_l0(0), 0, lane, pos, U0);
-    stage_pairs_finish<FMT>(a, xin, wk.nch, ps, xsm, red);
   } else {
     if (nunits > 0) load_unit<FMT, EPI>(a, seg, ebase, wk, unit_l0(0), 0, lane, pos, U0);
     stage_x<FMT>(a, xin, wk.nch, xsm, red);
@@ -1041,8 +1056,8 @@ __global__ void __launch_bounds__(W * 64) k_gemv(GemvArgs a) {
   for (int r = 0; r < RPW; ++r) acc[r] = 0.0f;
 
   // unit u -> (group index i = u / steps, step = u % steps); row group g0 + i * nblk
-  auto finish = [&](int64_t u, const EpiIn& e) {
-    const int64_t i = u / wk.steps;
+  auto finish = [&](int u, const EpiIn& e) {
+    const int i = u / wk.steps;
     if (u - i * wk.steps != wk.steps - 1) return;
 #pragma unroll
     for (int r = 0; r < RPW; ++r) acc[r] = wave_sum_dpp(acc[r]);
@@ -1078,7 +1093,7 @@ __global__ void __launch_bounds__(W * 64) k_gemv(GemvArgs a) {
         float v0 = 0.0f, v1 = 0.0f;
 #pragma unroll
         for (int r = 0; r < RPW; ++r) if (r == lane) { v0 = acc[r]; v1 = pexch[par][rs][r]; }
-        const int64_t l = ((g0 + i * nblk) * nrs + rs) * RPW + lane;
+        const int64_t l = ((int64_t)(g0 + i * nblk) * nrs + rs) * RPW + lane;
         if (l < seg.rows) {
           const int64_t o = seg.row_base + l;
           float v = a.y[o] + a.seg[0].scale[0] * v0;  // transformer.cpp:600-608, expert by expert
@@ -1088,7 +1103,7 @@ __global__ void __launch_bounds__(W * 64) k_gemv(GemvArgs a) {
         }
       }
     } else if (kp == 0) {
-      epilogue<EPI, RPW>(a, seg, ((g0 + i * nblk) * nrs + rs) * RPW, lane, acc, e, pos, best_v, best_i);
+      epilogue<EPI, RPW>(a, seg, ((int64_t)(g0 + i * nblk) * nrs + rs) * RPW, lane, acc, e, pos, best_v, best_i);
     }
 #pragma unroll
     for (int r = 0; r < RPW; ++r) acc[r] = 0.0f;
@@ -1099,7 +1114,7 @@ __global__ void __launch_bounds__(W * 64) k_gemv(GemvArgs a) {
       compute_unit<FMT>(wk, 0, lane, xs, U0, acc);
       finish(0, U0.e);
     }
-    for (int64_t u = 1; u < nunits; ++u) {
+    for (int u = 1; u < nunits; ++u) {
       UnitBuf<FMT> V;
       load_unit<FMT, EPI>(a, seg, ebase, wk, unit_l0(u), unit_step(u), lane, pos, V);
       compute_unit<FMT>(wk, unit_step(u), lane, xs, V, acc);
@@ -1116,7 +1131,7 @@ __global__ void __launch_bounds__(W * 64) k_gemv(GemvArgs a) {
         finish(1, U1.e);
       }
     }
-    for (int64_t u = 2; u < nunits; u += 2) {
+    for (int u = 2; u < nunits; u += 2) {
       UnitBuf<FMT> V0, V1;
       const bool two = u + 1 < nunits;  // block-uniform
       load_unit<FMT, EPI>(a, seg, ebase, wk, unit_l0(u), unit_step(u), lane, pos, V0);
@@ -1428,12 +1443,35 @@ hipError_t launch_gemv(const GemvArgs& in, hipStream_t s) {
     const Plan p = make_plan(a);
     if (!p.fn) return hipErrorInvalidValue;
     a.ksplit = p.ks;
+    const bool pair = a.epi == EPI_ADD2;
+    if (!pair) {
+      // one input for the run, at GemvArgs::x (the kernel issues it first)
+      const float* x = a.seg[0].x ? a.seg[0].x : a.x;
+      for (int k = 0; k < a.nseg; ++k) {
+        if (a.seg[k].x && a.seg[k].x != x) return hipErrorInvalidValue;
+        a.seg[k].x = nullptr;
+      }
+      a.x = x;
+    }
     int blocks = 0;
     for (int k = 0; k < a.nseg; ++k) {
       a.seg[k].block0 = blocks;
       blocks += p.per[k];
     }
     if (blocks == 0) return hipSuccess;
+    // the kernel's integer setup: row groups, groups per block, chunk columns per wave
+    const int rpg = (p.waves / (pair ? 2 : 1) / p.ks) * rpw_of(a.seg[0].w.type);
+    for (int k = 0; k < a.nseg; ++k) {
+      GemvSeg& g = a.seg[k];
+      const int64_t ngroups = (g.rows + rpg - 1) / rpg;
+      const int nblk = pair ? blocks : p.per[k];
+      if (ngroups > INT32_MAX || nblk <= 0) return hipErrorInvalidValue;
+      g.ngroups = (int32_t)ngroups;
+      g.gq = (int32_t)(ngroups / nblk);
+      g.gr = (int32_t)(ngroups % nblk);
+      const int64_t ncol = (g.w.a_row / 16 + 63) / 64;
+      g.per = (int32_t)((ncol + p.ks - 1) / p.ks);
+    }
     if ((int64_t)p.lds > lds_limit() - 1024) return hipErrorInvalidValue;
     if (a.epi == EPI_LOGITS && blocks > a.part_cap) return hipErrorInvalidValue;
     UAII_LAUNCH(p.fn, dim3(blocks), dim3(p.waves * 64), p.lds, s, a);

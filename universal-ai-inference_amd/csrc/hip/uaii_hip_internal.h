@@ -59,16 +59,24 @@ struct GemvSeg {
   int64_t expert_rows;
   const float* scale;  // EPI_ADD: y += *scale * dot (device memory), or null
   const float* x;      // this segment's input vector, or null for GemvArgs::x
+  // set by launch_gemv (the kernel's integer setup, done once on the host):
+  // row groups of the segment, groups per block (gq, plus one for blocks below
+  // gr), and 64-chunk columns per wave of a K split
+  int32_t ngroups, gq, gr, per;
 };
 
+// The fields a GEMV block needs first (its input and RMSNorm weight) lead the
+// struct, so the launch's first scalar-cache line holds them and the input
+// loads go out before anything else is read.
 struct GemvArgs {
-  GemvSeg seg[3];
-  int nseg;
-  int epi;
-  int64_t K;
   const float* x;        // input vector [K]
   const float* norm_w;   // RMSNorm weight [K] (prologue) or null
+  int64_t K;
   float eps;
+  int nseg;
+  int epi;
+  // set by launch_gemv: waves of a block that split one row set's K (1, 2 or 4)
+  int ksplit;
   float* y;              // EPI_STORE/ADD/QKV(q)/SWIGLU/LOGITS output
   float* tap;            // optional copy of each written value (EPI_ADD)
   float* xtap;           // optional copy of the staged (normalised) input, block 0
@@ -87,8 +95,7 @@ struct GemvArgs {
   int32_t* ids;          // token history [max_seq + 1]
   // shared
   StepState* state;
-  // set by launch_gemv: waves of a block that split one row set's K (1, 2 or 4)
-  int ksplit;
+  GemvSeg seg[3];
 };
 
 hipError_t launch_gemv(const GemvArgs& a, hipStream_t s);
