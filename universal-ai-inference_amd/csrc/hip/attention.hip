@@ -334,9 +334,11 @@ __global__ void __launch_bounds__(NW * 64) k_attn_h16(AttnArgs a) {
   const int h = blockIdx.x, sblk = blockIdx.y, SB = gridDim.y;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int64_t n = a.fixed_len > 0 ? (int64_t)a.fixed_len : (int64_t)a.state->pos + 1;
-  const int64_t CB = (n + SB - 1) / SB;
-  const int64_t b0 = (int64_t)sblk * CB, b1 = (b0 + CB < n) ? b0 + CB : n;
+  // key range of this block in 32-bit arithmetic (positions < max_seq < 2^31):
+  // the K/V loads wait for it, and a 64-bit division is a long emulated sequence
+  const int n = a.fixed_len > 0 ? a.fixed_len : a.state->pos + 1;
+  const int CB = (int)(((unsigned)n + (unsigned)SB - 1u) / (unsigned)SB);
+  const int b0 = sblk * CB, b1 = (b0 + CB < n) ? b0 + CB : n;
   const float scale = 1.0f / sqrtf((float)HD);
 
   // q of the group first: waiting for it does not wait for the K/V loads below
@@ -355,24 +357,24 @@ __global__ void __launch_bounds__(NW * 64) k_attn_h16(AttnArgs a) {
   const int vd = lane % LV, vk = lane / LV;   // P.V: dims [8 vd, 8 vd + 8) of key vk + VPI j
 
   uint4 kr[KJ][4], vr[VJ];
-  auto load_tile = [&](int64_t t0) {
+  auto load_tile = [&](int t0) {
 #pragma unroll
     for (int j = 0; j < KJ; ++j) {
-      int64_t key = t0 + kk + KPI * j;
+      int key = t0 + kk + KPI * j;
       key = key < b1 ? key : b1 - 1;  // in bounds; masked below
-      const uint4* src = reinterpret_cast<const uint4*>(kc + key * HD + 32 * kq);
+      const uint4* src = reinterpret_cast<const uint4*>(kc + (int64_t)key * HD + 32 * kq);
 #pragma unroll
       for (int c = 0; c < 4; ++c) kr[j][c] = src[c];
     }
 #pragma unroll
     for (int j = 0; j < VJ; ++j) {
-      int64_t key = t0 + vk + VPI * j;
+      int key = t0 + vk + VPI * j;
       key = key < b1 ? key : b1 - 1;
-      vr[j] = *reinterpret_cast<const uint4*>(vc + key * HD + 8 * vd);
+      vr[j] = *reinterpret_cast<const uint4*>(vc + (int64_t)key * HD + 8 * vd);
     }
   };
 
-  const int64_t first = b0 + (int64_t)wave * TK;
+  const int first = b0 + wave * TK;
   if (first < b1) load_tile(first);
 
   // q * scale -> f16 (hi, lo) pairs in LDS
@@ -398,7 +400,7 @@ __global__ void __launch_bounds__(NW * 64) k_attn_h16(AttnArgs a) {
     for (int e = 0; e < 8; ++e) o[g][e] = 0.0f;
   }
 
-  for (int64_t t0 = first; t0 < b1; t0 += NW * TK) {
+  for (int t0 = first; t0 < b1; t0 += NW * TK) {
     if (t0 != first) load_tile(t0);
     // scores
     float sc[KJ][G];

@@ -1069,7 +1069,7 @@ __device__ __forceinline__ void gemv_stage2(const uint8_t* st0, const uint8_t* s
 }
 
 // Stages of a ring GEMV (R rows each; EPI_SWIGLU: R/2 gate + R/2 up rows).
-__device__ __forceinline__ int64_t ring_stages_of(const RingArgs& a, const Geo& ge) {
+__host__ __device__ __forceinline__ int64_t ring_stages_of(const RingArgs& a, const Geo& ge) {
   if (a.epi == EPI_SWIGLU) return a.rows[0] / (ge.R / 2);
   int64_t rows = 0;
   for (int k = 0; k < a.nseg; ++k) rows += a.rows[k];
@@ -1134,11 +1134,17 @@ __global__ void __launch_bounds__(NTH, 1) k_ring_gemv(RingArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const bool comp = wave < NCW;
   const int lw = wave - NCW;
-  const int nblk = gridDim.x, b = blockIdx.x;
+  const int b = blockIdx.x;
   const Geo ge = geo_of(a.K);
-  const int64_t T = ring_stages_of(a, ge);
-  const int n = share(T, b, nblk);
-  const int64_t f = first_stage(T, b, nblk);
+  // The input vector's loads go out first (its fields lead the arguments),
+  // ahead of the stage bookkeeping below.
+  float w[32];
+  load_norm(a.norm_w, ge, comp, wave, lane, w);
+  float v[32];
+  stage_load<false>(a.x, ge, comp, wave, lane, v);
+  // this block's run of stages (counts from the host): f .. f + n - 1
+  const int n = a.tq + (b < a.tr ? 1 : 0);
+  const int64_t f = (int64_t)b * a.tq + (b < a.tr ? b : a.tr);
   const uint32_t ring_lds = lds_addr(ring), pad_lds = lds_addr(lds + NS * SB);
 
   Seg sg;
@@ -1149,16 +1155,11 @@ __global__ void __launch_bounds__(NTH, 1) k_ring_gemv(RingArgs a) {
     islot = islot + 1 == NS ? 0 : islot + 1;
     if (--sg.left == 0 && issued < n) ring_seg(a, ge, f + issued, f + n, lw, sg);
   };
-  // The input vector's loads go out first, then the first RING_PRO stages:
-  // every CU's first requests of a launch complete only when the whole grid's
-  // burst has been served, so a small first burst gets the first data (and the
-  // input) back sooner. Stages then go in pairs; each pair waits for its two
-  // stages, and the loaders refill up to 4 stages per pair (the ring deepens
-  // to NS-2 stages ahead).
-  float w[32];
-  load_norm(a.norm_w, ge, comp, wave, lane, w);
-  float v[32];
-  stage_load<false>(a.x, ge, comp, wave, lane, v);
+  // After the input's loads, the first RING_PRO stages: every CU's first
+  // requests of a launch complete only when the whole grid's burst has been
+  // served, so a small first burst gets the first data (and the input) back
+  // sooner. Stages then go in pairs; each pair waits for its two stages, and the
+  // loaders refill up to 4 stages per pair (the ring deepens to NS-2 stages ahead).
   block_sync();
   if (!comp && n > 0) {
     ring_seg(a, ge, f, f + n, lw, sg);
@@ -1360,12 +1361,18 @@ hipError_t prepare_ring_gemv() {
   return prep;
 }
 
-hipError_t launch_ring_gemv(const RingArgs& a, hipStream_t s) {
-  if (!ring_gemv_supported(a)) return hipErrorInvalidValue;
+hipError_t launch_ring_gemv(const RingArgs& in, hipStream_t s) {
+  if (!ring_gemv_supported(in)) return hipErrorInvalidValue;
   const hipError_t prep = prepare_ring_gemv();
   if (prep != hipSuccess) return prep;
   const size_t lds = (size_t)RING_NS * SB + 1024 + PART_MAX * 4;
-  UAII_LAUNCH(k_ring_gemv, dim3(dev_cus()), dim3(NTH), lds, s, a);
+  const int nblk = dev_cus();
+  if (nblk <= 0) return hipErrorInvalidDevice;
+  RingArgs a = in;
+  const int64_t T = ring_stages_of(a, geo_of(a.K));
+  a.tq = (int32_t)(T / nblk);
+  a.tr = (int32_t)(T % nblk);
+  UAII_LAUNCH(k_ring_gemv, dim3(nblk), dim3(NTH), lds, s, a);
   return hipGetLastError();
 }
 

@@ -127,18 +127,19 @@ hipError_t launch_copy(const void* src, void* dst, int64_t n16, hipStream_t s);
 
 // ---- attention -----------------------------------------------------------------
 
+// Everything a block needs to issue its first loads sits in the first 64 bytes.
 struct AttnArgs {
   const float* q;        // [n_heads * hd] (post-RoPE)
+  const StepState* state;  // keys 0..state->pos inclusive
   const void* kcache;    // layer base [n_kv][max_seq][hd]
   const void* vcache;
-  int kv_f16;
   int64_t max_seq;
-  int n_heads, n_kv, hd;
-  const StepState* state;  // keys 0..state->pos inclusive
   int fixed_len;           // >0: use this key count instead of state->pos + 1
+  int kv_f16;
+  int n_heads, n_kv, hd;
+  int splits;
   float* out;            // [n_heads * hd]
   float* part;           // [n_kv][splits][group][hd + 2]
-  int splits;
 };
 
 int attention_splits(int64_t max_seq);
@@ -202,15 +203,18 @@ hipError_t launch_layers(const LayersArgs& a, int type, hipStream_t s);
 // Loader waves fetch the block's rows global -> LDS while compute waves take
 // stages out of LDS (layers.hip), so the dot products never hold back the next
 // loads. Q4_0 only; see ring_gemv_supported for the shapes.
+// The input fields lead (the kernel loads its input before anything else).
 struct RingArgs {
-  DevWeight w[3];        // stacked row segments (Q, K, V), or gate (0) / up (1) for EPI_SWIGLU
-  int64_t rows[3];       // rows per segment (EPI_SWIGLU: rows[0] = output size)
-  int nseg;
-  int epi;               // EPI_STORE, EPI_ADD, EPI_QKV (RoPE mode 0), EPI_SWIGLU
-  int64_t K;
   const float* x;        // input [K]
   const float* norm_w;   // RMSNorm weight or null
+  int64_t K;
   float eps;
+  int nseg;
+  int epi;               // EPI_STORE, EPI_ADD, EPI_QKV (RoPE mode 0), EPI_SWIGLU
+  // set by launch_ring_gemv: stages per block (tq, plus one for blocks below tr)
+  int32_t tq, tr;
+  DevWeight w[3];        // stacked row segments (Q, K, V), or gate (0) / up (1) for EPI_SWIGLU
+  int64_t rows[3];       // rows per segment (EPI_SWIGLU: rows[0] = output size)
   float* y;              // output (EPI_QKV: q)
   float* tap;            // EPI_ADD: copy of each written value, or null
   // EPI_QKV
