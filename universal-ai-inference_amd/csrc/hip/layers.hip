@@ -1022,7 +1022,10 @@ __global__ void __launch_bounds__(NTH, 1) k_layers(LayersArgs a) {
 // ---- one GEMV through the ring (decode, between ordinary launches) -----------------------------
 
 constexpr int RING_NS = 8;
-constexpr int RING_PRO = 2;
+#ifndef UAII_RING_PRO
+#define UAII_RING_PRO 1
+#endif
+constexpr int RING_PRO = UAII_RING_PRO;
 
 // Wait until at most k stages' DMA lines (k * ND instructions) are outstanding.
 __device__ __forceinline__ void wait_stages(int k) {
