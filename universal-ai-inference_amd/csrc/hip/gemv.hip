@@ -41,7 +41,14 @@ namespace {
 // input); 16 for the K-split long rows of the residual-add GEMV (the down
 // projection, whose staged input is as large as a 4-wave block's weight bytes).
 constexpr int WPB = 4;
-constexpr int WPB_QKV = 8;
+#ifndef UAII_WPB_QKV
+#define UAII_WPB_QKV 8
+#endif
+#ifndef UAII_WPB_SWIGLU
+#define UAII_WPB_SWIGLU 4
+#endif
+constexpr int WPB_QKV = UAII_WPB_QKV;
+constexpr int WPB_SWIGLU = UAII_WPB_SWIGLU;
 constexpr int WPB_LONG = 16;
 constexpr int NB = UAII_GEMV_BATCH;
 static_assert(NB == 1 || NB == 2, "UAII_GEMV_BATCH must be 1 or 2");
@@ -768,10 +775,11 @@ __device__ inline void emit_pair_item(const GemvArgs& a, int64_t nch, int64_t it
               fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
     psum = ((u.x + u.y) + (u.z + u.w)) + ((v.x + v.y) + (v.z + v.w));
   }
-  m = fmaxf(m, __shfl_xor(m, 1, 64));
-  m = fmaxf(m, __shfl_xor(m, 2, 64));
-  psum += __shfl_xor(psum, 1, 64);
-  psum += __shfl_xor(psum, 2, 64);
+  // the chunk's four lanes (quad xor 1, 2) on DPP moves, not LDS permutes
+  m = fmaxf(m, dpp_mov<0xB1>(m));
+  m = fmaxf(m, dpp_mov<0x4E>(m));
+  psum += dpp_mov<0xB1>(psum);
+  psum += dpp_mov<0x4E>(psum);
   if (!valid) return;
   const int64_t i0 = 8 * t + w;
   if (tap) {
@@ -1042,8 +1050,14 @@ __global__ void __launch_bounds__(W * 64) k_gemv(GemvArgs a) {
     // the launch against ~3 us, measured by per-wave clock stamps on the 8B
     // decode (gate/up 19.3 -> 17.9 us, LM head 61 -> 55 us, QKV unchanged;
     // 461 -> 471 tok/s).
+#ifdef UAII_GEMV_EARLY
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wave's input has arrived
+    if (nunits > 0) load_unit<FMT, EPI>(a, seg, ebase, wk, unit_l0(0), 0, lane, pos, U0);
+    stage_pairs_finish<FMT>(a, xin, wk.nch, ps0, xsm, red);
+#else
     stage_pairs_finish<FMT>(a, xin, wk.nch, ps0, xsm, red);
     if (nunits > 0) load_unit<FMT, EPI>(a, seg, ebase, wk, unit_l0(0), 0, lane, pos, U0);
+#endif
   } else {
     if (nunits > 0) load_unit<FMT, EPI>(a, seg, ebase, wk, unit_l0(0), 0, lane, pos, U0);
     stage_x<FMT>(a, xin, wk.nch, xsm, red);
@@ -1237,7 +1251,8 @@ KernelFn pick_fmt(int type) {
 // Kernel for (epilogue, format, waves per block): WPB for every epilogue,
 // WPB_QKV for the QKV epilogue, WPB_LONG for the residual add.
 KernelFn pick(int epi, int type, int w) {
-  if (w == WPB_QKV) return epi == EPI_QKV ? pick_fmt<EPI_QKV, WPB_QKV>(type) : nullptr;
+  if (epi == EPI_SWIGLU && w == WPB_SWIGLU) return pick_fmt<EPI_SWIGLU, WPB_SWIGLU>(type);
+  if (epi == EPI_QKV && w == WPB_QKV) return pick_fmt<EPI_QKV, WPB_QKV>(type);
   if (w == WPB_LONG) {
     if (epi == EPI_ADD) return pick_fmt<EPI_ADD, WPB_LONG>(type);
     if (epi == EPI_ADD2) return pick_fmt<EPI_ADD2, WPB_LONG>(type);
@@ -1260,6 +1275,7 @@ int pick_waves(int epi, int ks) {
   if (epi == EPI_ADD2) return WPB_LONG;
   if (epi == EPI_ADD && ks == 4) return WPB_LONG;
   if (epi == EPI_QKV) return WPB_QKV;
+  if (epi == EPI_SWIGLU) return WPB_SWIGLU;
   return WPB;
 }
 
@@ -1274,7 +1290,7 @@ hipError_t prepare_gemv() {
   const int lim = lds_limit();
   for (int e : epis) {
     for (int t : types) {
-      for (int w : {WPB, WPB_QKV, WPB_LONG}) {
+      for (int w : {WPB, WPB_QKV, WPB_SWIGLU, WPB_LONG}) {
         const KernelFn fn = pick(e, t, w);
         if (!fn) continue;
         (void)hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, lim - 1024);
