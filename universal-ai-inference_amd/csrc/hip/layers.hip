@@ -1023,7 +1023,7 @@ __global__ void __launch_bounds__(NTH, 1) k_layers(LayersArgs a) {
 
 constexpr int RING_NS = 8;
 #ifndef UAII_RING_PRO
-#define UAII_RING_PRO 1
+#define UAII_RING_PRO 2
 #endif
 constexpr int RING_PRO = UAII_RING_PRO;
 
@@ -1172,7 +1172,12 @@ __global__ void __launch_bounds__(NTH, 1) k_ring_gemv(RingArgs a) {
   XP xp;
   stage_finish(v, a.norm_w != nullptr, w, a.eps, a.K, ge, comp, wave, lane, red, xp);
   for (int i = 0; i < n; i += 2) {
-    if (!comp) wait_stages(issued - min(i + 2, n));
+    if (!comp) {
+      // stages i and i + 1 are in flight (a one-stage first burst leaves i + 1
+      // to here), then wait until both have landed
+      while (issued < min(i + 2, n)) issue_next();
+      wait_stages(issued - min(i + 2, n));
+    }
     block_sync();
     if (!comp) {
       const int cap = min(n, i + NS);  // stages below i + NS have a free slot
