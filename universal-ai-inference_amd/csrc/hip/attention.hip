@@ -541,38 +541,29 @@ bool launch_h16(const AttnArgs& a, int G, hipStream_t s) {
 
 // Merge the SB block partials of every query head (one block per head):
 // out = sum_s w_s o_s / sum_s w_s l_s with w_s = exp(m_s - max_s m_s).
-constexpr int MERGE_NT = 320;  // head_dim <= 256 value columns + one wave for (m, l)
-__global__ void __launch_bounds__(MERGE_NT) k_attn_merge(AttnArgs a) {
+__global__ void __launch_bounds__(256) k_attn_merge(AttnArgs a) {
   __shared__ float w[64];
   __shared__ float inv_den;
   const int hq = blockIdx.x, hd = a.hd, G = a.n_heads / a.n_kv, SB = a.splits;
-  const int kvh = hq / G, g = hq % G, t = threadIdx.x;
+  const int kvh = hq / G, g = hq % G;
   const int64_t pstride = hd + 2;
   const float* hp = a.part + ((int64_t)kvh * SB * G + g) * pstride;  // split k at + k*G*pstride
-  // One memory round trip: every load goes out before any arithmetic. Threads
-  // below hd take column t of every split; the last wave takes the (m, l) pairs.
-  float v[64];
-  if (t < hd) {
-#pragma unroll
-    for (int k = 0; k < 64; ++k) v[k] = (k < SB) ? hp[(int64_t)k * G * pstride + t] : 0.0f;
-  }
-  if (t >= MERGE_NT - 64) {
-    const int k = t - (MERGE_NT - 64);
+  if (threadIdx.x < 64) {
+    const int k = threadIdx.x;
     const float mk = (k < SB) ? hp[(int64_t)k * G * pstride + hd] : -INFINITY;
-    const float lk = (k < SB) ? hp[(int64_t)k * G * pstride + hd + 1] : 0.0f;
     const float M = wave_max_dpp(mk);
     const float wk = (k < SB && mk != -INFINITY) ? expf(mk - M) : 0.0f;
+    const float lk = (k < SB) ? hp[(int64_t)k * G * pstride + hd + 1] : 0.0f;
     const float den = wave_sum_dpp(wk * lk);
     w[k] = wk;
     if (k == 0) inv_den = den > 0.0f ? 1.0f / den : 0.0f;
   }
   __syncthreads();
-  if (t < hd) {
+  for (int d = threadIdx.x; d < hd; d += blockDim.x) {
     float num = 0.0f;
-#pragma unroll
-    for (int k = 0; k < 64; ++k)
-      if (k < SB) num += w[k] * v[k];
-    a.out[(int64_t)hq * hd + t] = num * inv_den;
+#pragma unroll 16
+    for (int k = 0; k < SB; ++k) num += w[k] * hp[(int64_t)k * G * pstride + d];
+    a.out[(int64_t)hq * hd + d] = num * inv_den;
   }
 }
 
@@ -621,7 +612,7 @@ hipError_t launch_attention_decode(const AttnArgs& a, hipStream_t s) {
     if (ok) {
       const hipError_t st = hipGetLastError();
       if (st != hipSuccess) return st;
-      UAII_LAUNCH(k_attn_merge, dim3(a.n_heads), dim3(MERGE_NT), 0, s, a);
+      UAII_LAUNCH(k_attn_merge, dim3(a.n_heads), dim3(256), 0, s, a);
       return hipGetLastError();
     }
   }
@@ -638,7 +629,7 @@ hipError_t launch_attention_decode(const AttnArgs& a, hipStream_t s) {
   }
   const hipError_t st = hipGetLastError();
   if (st != hipSuccess) return st;
-  UAII_LAUNCH(k_attn_merge, dim3(a.n_heads), dim3(MERGE_NT), 0, s, a);
+  UAII_LAUNCH(k_attn_merge, dim3(a.n_heads), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 
