@@ -44,10 +44,19 @@ typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
 typedef float f4_t __attribute__((ext_vector_type(4)));
 
 __device__ inline h2_t as_h2(uint32_t u) { return __builtin_bit_cast(h2_t, u); }
+// (v & m) | c in one v_and_or_b32. Written out because gfx9's three-operand
+// encoding takes no literal constants, so the compiler splits the expression
+// into v_and + v_or; here the mask sits in a scalar register and the constant
+// in a vector register, both loop-invariant.
+__device__ inline uint32_t and_or(uint32_t v, uint32_t m, uint32_t c) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(v), "s"(m), "v"(c));
+  return r;
+}
 // low nibbles of bytes 0 and 2 as f16 (1024 + q)
-__device__ inline uint32_t nib_pair(uint32_t v) { return (v & 0x000F000Fu) | 0x64006400u; }
+__device__ inline uint32_t nib_pair(uint32_t v) { return and_or(v, 0x000F000Fu, 0x64006400u); }
 // bytes 0 and 2 as f16 (1024 + b)
-__device__ inline uint32_t byte_pair(uint32_t v) { return (v & 0x00FF00FFu) | 0x64006400u; }
+__device__ inline uint32_t byte_pair(uint32_t v) { return and_or(v, 0x00FF00FFu, 0x64006400u); }
 
 __device__ inline h8_t cat8(h2_t a, h2_t b, h2_t c, h2_t d) {
   return h8_t{a.x, a.y, b.x, b.y, c.x, c.y, d.x, d.y};
@@ -332,6 +341,15 @@ constexpr int PF_WAVES = 4;   // waves per block, side by side along N
 #ifndef UAII_PF_ROW
 #define UAII_PF_ROW 40
 #endif
+#ifndef UAII_PF_KS_BPC
+#define UAII_PF_KS_BPC 2  // K split target: four-wave block equivalents per CU
+#endif
+#ifndef UAII_PF_DW
+#define UAII_PF_DW 8  // waves per block of the direct-to-LDS kernel (4 or 8)
+#endif
+#ifndef UAII_PF_XCD
+#define UAII_PF_XCD 1  // XCD-aware block order in the direct-to-LDS kernel
+#endif
 constexpr int PF_ROW = UAII_PF_ROW;  // halfs per staged 32-k row (32 + 8 pad)
 
 // LDS: [buffer 2][block 2][hi/lo 2][BM rows][PF_ROW halfs]
@@ -343,17 +361,18 @@ constexpr int pf_lds_halfs() { return 2 * 2 * 2 * 16 * MT * PF_ROW; }
 struct PfRange {
   int64_t m0, mend, mfirst, wrow0;
 };
-__device__ inline PfRange pf_range(const PfGemmArgs& a, int bm, int64_t seg_rows) {
+__device__ inline PfRange pf_range(const PfGemmArgs& a, int bm, int64_t seg_rows, int gy = -1) {
+  if (gy < 0) gy = blockIdx.y;
   PfRange r;
   if (a.gtab) {
-    const int32_t* e = a.gtab + 3 * blockIdx.y;
+    const int32_t* e = a.gtab + 3 * gy;
     r.wrow0 = (int64_t)e[0] * seg_rows;
     r.m0 = e[1];
     r.mend = e[2];
     r.mfirst = r.m0;
   } else {
     r.wrow0 = 0;
-    r.m0 = (int64_t)blockIdx.y * bm;
+    r.m0 = (int64_t)gy * bm;
     r.mend = a.M;
     r.mfirst = 0;
   }
@@ -585,9 +604,15 @@ __global__ void __launch_bounds__(PF_WAVES * 64, 2) k_pf_gemm(PfGemmArgs a) {
 // ring of three LDS stages keeps two stages of loads outstanding. The loads are
 // issued from inline assembly and their completion is waited for with explicit
 // vmcnt counts: the compiler would otherwise wait for every outstanding LDS
-// load before each LDS read. Each activation row's four 16-byte pieces are
-// stored XOR-swizzled (piece p of row r in slot p ^ swz(r)) so the fragment
-// reads of 16 consecutive rows hit distinct banks.
+// load before each LDS read. Both operands stay row-major in LDS (the lanes
+// of one DMA instruction that share a row fetch its contiguous bytes), with
+// the 16-byte pieces of each row XOR-permuted so that the fragment reads are
+// free of bank conflicts on gfx950: activation piece p of row r sits in slot
+// p ^ ((r >> 1) & 3); weight part p of row r (32- or 64-byte rows) in slot
+// p ^ ((r >> 3) & 1) for Q4_0, p ^ ((r >> 2) & 3) for Q8_0. Measured with
+// SQ_LDS_BANK_CONFLICT: unpermuted rows cost 4 conflict cycles per 16-byte
+// activation read and 2 (Q4_0) or 6 (Q8_0) per 8-byte weight read, as does
+// the permutation p ^ (((r >> 1) ^ (r >> 3)) & 3) for the activations.
 
 __device__ inline void dma16(const void* g, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(g) : "memory", "m0");
@@ -595,98 +620,154 @@ __device__ inline void dma16(const void* g, uint32_t lds) {
 __device__ inline void dma4(const void* g, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, off" ::"s"(lds), "v"(g) : "memory", "m0");
 }
+// The same 16-byte copy from a wave-uniform base (scalar registers) plus the
+// lane's 32-bit byte offset: no per-lane 64-bit address arithmetic per stage.
+__device__ inline void dma16s(const void* sbase, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds), "v"(voff), "s"(sbase)
+               : "memory", "m0");
+}
+// A pointer the wave holds in common, made visibly uniform so that it lives in
+// scalar registers.
+__device__ inline const uint8_t* uniform_ptr(const void* p) {
+  const uint64_t u = (uint64_t)(uintptr_t)p;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)u);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(u >> 32));
+  return reinterpret_cast<const uint8_t*>((uintptr_t)(((uint64_t)hi << 32) | lo));
+}
 __device__ inline uint32_t lds_addr(const void* p) {
   return __builtin_amdgcn_readfirstlane(
       (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p);
 }
-__device__ inline int pf_swz(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
+__device__ inline int pf_swz(int r) { return (r >> 1) & 3; }
+template <int FMT>
+__device__ inline int pf_wswz(int r) { return FMT == T_Q4_0 ? (r >> 3) & 1 : (r >> 2) & 3; }
 
 template <int FMT>
 constexpr int dma_qbytes() { return FMT == T_Q8_0 ? 64 : 32; }  // payload bytes per row per stage
 template <int MT>
 constexpr int dma_a_bytes() { return 2 * 2 * 16 * MT * 64; }      // [block][hi/lo][row][64 B]
-template <int FMT>
-constexpr int dma_w_bytes() { return PF_WAVES * 32 * (dma_qbytes<FMT>() + 8); }  // per wave: 32 rows
-template <int FMT, int MT>
-constexpr int dma_stage_bytes() { return dma_a_bytes<MT>() + dma_w_bytes<FMT>(); }
+// per wave: the payload of its 16 NT rows, then a 256-byte scale area (a dword per row)
+template <int FMT, int NT>
+constexpr int dma_wave_w_bytes() { return 16 * NT * dma_qbytes<FMT>() + 256; }
+// Waves per block of the direct-to-LDS kernel, side by side along N: 8, so
+// that with two blocks per CU each SIMD holds four waves.
+constexpr int PF_DW = UAII_PF_DW;
+template <int FMT, int MT, int NT>
+constexpr int dma_stage_bytes() { return dma_a_bytes<MT>() + PF_DW * dma_wave_w_bytes<FMT, NT>(); }
+// Activation DMA instructions per wave and stage: the 4 MT (block, hi/lo,
+// subtile) copies spread over the waves
+template <int MT>
+constexpr int dma_a_per_wave() { return 4 * MT / PF_DW; }
 // DMA instructions each wave issues per stage (the vmcnt unit)
-template <int FMT, int MT>
-constexpr int dma_per_stage() { return MT + dma_qbytes<FMT>() / 32 + 1; }
+template <int FMT, int MT, int NT>
+constexpr int dma_per_stage() { return dma_a_per_wave<MT>() + 16 * NT * dma_qbytes<FMT>() / 1024 + 1; }
+// Weight subtiles per wave: 2 (32 rows). 64-row waves (4) spilled registers at
+// the 64 x 64 wave tile.
+template <int FMT>
+constexpr int dma_nt() { return 2; }
 
-template <int FMT, int EPI, int MT>
-__global__ void __launch_bounds__(PF_WAVES * 64, 2) k_pf_gemm_dma(PfGemmArgs a) {
-  constexpr int NT = 2;
+template <int FMT, int EPI, int MT, int NT>
+__global__ void __launch_bounds__(PF_DW * 64, 2) k_pf_gemm_dma(PfGemmArgs a) {
+  static_assert(NT == 2 || NT == 4, "weight subtiles per wave");
+  static_assert((4 * MT) % PF_DW == 0, "activation copies per wave");
+  constexpr int NA = dma_a_per_wave<MT>();
   constexpr int BM = 16 * MT;
-  constexpr int NQ = (EPI == EPI_SWIGLU) ? 1 : NT;
+  constexpr int NQ = (EPI == EPI_SWIGLU) ? NT / 2 : NT;
+  constexpr int NR = 16 * NT;  // weight rows per wave
   constexpr int QB = dma_qbytes<FMT>();
-  constexpr int SB = dma_stage_bytes<FMT, MT>();
-  constexpr int ND = dma_per_stage<FMT, MT>();
+  constexpr int WB = dma_wave_w_bytes<FMT, NT>();
+  constexpr int SB = dma_stage_bytes<FMT, MT, NT>();
+  constexpr int ND = dma_per_stage<FMT, MT, NT>();
   static_assert(ND <= 15, "vmcnt immediate");
   __shared__ __attribute__((aligned(16))) uint8_t lds[3 * SB];
 
-  const int tile = blockIdx.x;
+  // Grid position. Blocks go to the XCDs round-robin in dispatch order; with
+  // the column-tile count a multiple of 8, XCD x takes the column tiles
+  // 8 c + x, and within an XCD the blocks are renumbered row tile fastest, so
+  // that the blocks resident on one XCD share their weight columns in its L2.
+  int tile = blockIdx.x, gy = blockIdx.y;
+#if UAII_PF_XCD
+  if ((gridDim.x & 7) == 0) {
+    const int id = blockIdx.y * gridDim.x + blockIdx.x;
+    const int loc = id >> 3;
+    gy = loc % gridDim.y;
+    tile = (loc / gridDim.y) * 8 + (id & 7);
+  }
+#endif
   int si = 0;
   for (int k = 1; k < a.nseg; ++k) if (tile >= a.seg[k].tile0) si = k;
   const PfSeg& seg = a.seg[si];
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int col = lane & 15, g = lane >> 4;
-  const int64_t n0 = ((int64_t)(tile - seg.tile0) * PF_WAVES + wave) * (16 * NQ);
-  const PfRange mr = pf_range(a, BM, seg.rows);
+  const int64_t n0 = ((int64_t)(tile - seg.tile0) * PF_DW + wave) * (16 * NQ);
+  const PfRange mr = pf_range(a, BM, seg.rows, gy);
   const int64_t m0 = mr.m0;
-  const int64_t K = a.K, nst = K / 64 / a.ksplit;  // stages of this block's K range
+  const int64_t K = a.K;
+  const int nst = (int)(K / 64 / a.ksplit);         // stages of this block's K range
   const int64_t sbase = (int64_t)blockIdx.z * nst;  // its first stage
 
-  // this lane's DMA sources. Activations: wave w copies (block w >> 1, hi/lo
-  // w & 1); instruction u covers rows 16u .. 16u + 15, lane -> (row, slot).
+  // this lane's DMA sources. Activations: wave w copies (block (w >> 1) & 1,
+  // hi/lo w & 1) of the row subtiles NA (w >> 2) .. NA (w >> 2) + NA - 1;
+  // instruction u covers rows 16 u' .. 16 u' + 15 of its subtile u', lane ->
+  // (row, slot).
   const int arow_l = lane >> 2, aslot = lane & 3;
   const __half* asrc = (wave & 1) ? a.alo : a.ahi;
-  const int ablk = wave >> 1;
-  // Weights: the wave's 32 rows (subtile j = row / 16; SwiGLU: j = 1 is the up
-  // tensor), QB / 16 lanes per row for the payload, one dword per row of scales.
-  const int wl_per_row = QB / 16;
-  const int wrow_q = lane / wl_per_row, wpart = lane % wl_per_row;  // payload: 2 passes for Q8_0
-  const uint8_t* wsrc_q[QB / 32];
+  const int ablk = (wave >> 1) & 1;
+  const int asub0 = NA * (wave >> 2);
+  // the lane's byte offset of its row's piece (stage independent; the launch
+  // checks that the activation array spans under 2^31 bytes) and the wave's
+  // scalar base, to which stage st adds 128 st bytes (64 k of f16)
+  uint32_t aoff[NA];
 #pragma unroll
-  for (int u = 0; u < QB / 32; ++u) {
-    const int rl = (lane + 64 * u) / wl_per_row;
+  for (int u = 0; u < NA; ++u) {
+    const int r = 16 * (asub0 + u) + arow_l;
+    const int piece = aslot ^ pf_swz(r);
+    aoff[u] = (uint32_t)(pf_arow(a, mr, m0 + r) * K * 2) + (uint32_t)(ablk * 64 + piece * 16);
+  }
+  const uint8_t* abase = uniform_ptr(asrc);
+  // Weights: the wave's 32 rows (subtile j = row / 16; SwiGLU: j = 1 is the up
+  // tensor); a row's stage payload is WP 16-byte parts, and LDS slot
+  // q = 64 u + lane of the payload is slot q % WP of row q / WP. One dword per
+  // row of scales.
+  constexpr int WP = QB / 16;
+  constexpr int NWQ = NR * QB / 1024;  // payload DMA instructions per stage
+  const uint8_t* wsrc_q[NWQ];
+#pragma unroll
+  for (int u = 0; u < NWQ; ++u) {
+    const int q = lane + 64 * u;
+    const int rl = q / WP, part = (q % WP) ^ pf_wswz<FMT>(rl);
     const int j = rl >> 4;
     const DevWeight& w = (EPI == EPI_SWIGLU && j >= NQ) ? seg.w2 : seg.w;
     int64_t r = n0 + 16 * (j % NQ) + (rl & 15);
     r = mr.wrow0 + (r < seg.rows ? r : seg.rows - 1);
-    wsrc_q[u] = w.a + r * w.a_row + 16 * ((lane + 64 * u) % wl_per_row);
+    wsrc_q[u] = w.a + r * w.a_row + 16 * part;
   }
   const uint8_t* wsrc_s;
   {
-    const int rl = lane & 31;
+    const int rl = lane & (NR - 1);
     const int j = rl >> 4;
     const DevWeight& w = (EPI == EPI_SWIGLU && j >= NQ) ? seg.w2 : seg.w;
     int64_t r = n0 + 16 * (j % NQ) + (rl & 15);
     r = mr.wrow0 + (r < seg.rows ? r : seg.rows - 1);
     wsrc_s = w.b + r * w.b_row;
   }
-  (void)wrow_q;
-  (void)wpart;
 
-  auto issue = [&](int64_t stl, int slot) __attribute__((always_inline)) {
+  auto issue = [&](int stl, int slot) __attribute__((always_inline)) {
     const int64_t st = sbase + stl;
     uint8_t* base = lds + slot * SB;
     // activations
 #pragma unroll
-    for (int u = 0; u < MT; ++u) {
-      const int r = 16 * u + arow_l;
-      const int piece = aslot ^ pf_swz(r);
-      const int64_t ar = pf_arow(a, mr, m0 + r);
-      const __half* src = asrc + ar * K + (2 * st + ablk) * 32 + piece * 8;
-      dma16(src, lds_addr(base + ((ablk * 2 + (wave & 1)) * BM + 16 * u) * 64));
-    }
+    for (int u = 0; u < NA; ++u)
+      dma16s(uniform_ptr(abase + st * 128), aoff[u],
+             lds_addr(base + ((ablk * 2 + (wave & 1)) * BM + 16 * (asub0 + u)) * 64));
     // weight payload and scales of this wave's rows
-    uint8_t* wb = base + dma_a_bytes<MT>() + wave * (32 * (QB + 8));
+    uint8_t* wb = base + dma_a_bytes<MT>() + wave * WB;
 #pragma unroll
-    for (int u = 0; u < QB / 32; ++u) dma16(wsrc_q[u] + st * QB, lds_addr(wb + u * 1024));
-    dma4(wsrc_s + st * 4, lds_addr(wb + 32 * QB));
+    for (int u = 0; u < NWQ; ++u) dma16(wsrc_q[u] + st * QB, lds_addr(wb + u * 1024));
+    dma4(wsrc_s + st * 4, lds_addr(wb + NR * QB));
   };
-  auto wait_stage = [&](int64_t st) __attribute__((always_inline)) {
+  auto wait_stage = [&](int st) __attribute__((always_inline)) {
     // stage st is complete when at most the next stage's loads are outstanding
     if (st + 1 < nst) __builtin_amdgcn_s_waitcnt(0x0f70 | ND);  // vmcnt(ND), lgkm/exp untouched
     else __builtin_amdgcn_s_waitcnt(0x0f70);                    // vmcnt(0)
@@ -699,47 +780,71 @@ __global__ void __launch_bounds__(PF_WAVES * 64, 2) k_pf_gemm_dma(PfGemmArgs a) 
 #pragma unroll
     for (int j = 0; j < NT; ++j) acc[i][j] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
-  auto compute = [&](int64_t stl, int slot) __attribute__((always_inline)) {
+  auto compute = [&](int stl, int slot) __attribute__((always_inline)) {
     const int64_t st = sbase + stl;
     const uint8_t* base = lds + slot * SB;
-    const uint8_t* wb = base + dma_a_bytes<MT>() + wave * (32 * (QB + 8));
+    const uint8_t* wb = base + dma_a_bytes<MT>() + wave * WB;
     PfRaw<FMT> rw[NT];
 #pragma unroll
     for (int j = 0; j < NT; ++j) {
+      // block s of the row: part s (Q4_0: 16 bytes, lane half g & 1) or parts
+      // 2 s, 2 s + 1 (Q8_0: 32 bytes, lane quarter g)
       const uint8_t* rowp = wb + (16 * j + col) * QB;
-      if constexpr (FMT == T_Q4_0) {
-        rw[j].q[0] = *reinterpret_cast<const uint2*>(rowp + 8 * (g & 1));
-        rw[j].q[1] = *reinterpret_cast<const uint2*>(rowp + 16 + 8 * (g & 1));
-      } else {
-        rw[j].q[0] = *reinterpret_cast<const uint2*>(rowp + 8 * g);
-        rw[j].q[1] = *reinterpret_cast<const uint2*>(rowp + 32 + 8 * g);
+#pragma unroll
+      for (int sb = 0; sb < 2; ++sb) {
+        const int part = (FMT == T_Q4_0) ? sb : 2 * sb + (g >> 1);
+        rw[j].q[sb] = *reinterpret_cast<const uint2*>(rowp + 16 * (part ^ pf_wswz<FMT>(col)) + 8 * (g & 1));
       }
-      rw[j].d = *reinterpret_cast<const uint32_t*>(wb + 32 * QB + 4 * (16 * j + col));
+      rw[j].d = *reinterpret_cast<const uint32_t*>(wb + NR * QB + 4 * (16 * j + col));
     }
+    // Steps (block sb, subtile i) in order, each fenced from the next so that
+    // the registers live at once stay bounded: a step reads the next step's A
+    // fragments, issues its own matrix-core ops, then applies the previous
+    // step's block scales while those ops run.
+    auto afrag = [&](int sb, int i, h8_t& hi, h8_t& lo) __attribute__((always_inline)) {
+      const int r = 16 * i + col;
+      const int off = r * 64 + 16 * (g ^ pf_swz(r));
+      hi = *reinterpret_cast<const h8_t*>(base + ((sb * 2 + 0) * BM) * 64 + off);
+      lo = *reinterpret_cast<const h8_t*>(base + ((sb * 2 + 1) * BM) * 64 + off);
+    };
+    h8_t nhi, nlo;
+    afrag(0, 0, nhi, nlo);
+    f4_t pp[NT];
+    float psc[NT];
+    PfFrag<FMT> fr[NT];
 #pragma unroll
     for (int sb = 0; sb < 2; ++sb) {
-      PfFrag<FMT> fr[NT];
 #pragma unroll
       for (int j = 0; j < NT; ++j) pf_decode<FMT>(rw[j], st, sb, g, fr[j]);
 #pragma unroll
       for (int i = 0; i < MT; ++i) {
-        const int r = 16 * i + col;
-        const int off = r * 64 + 16 * (g ^ pf_swz(r));
-        const h8_t ahi = *reinterpret_cast<const h8_t*>(base + ((sb * 2 + 0) * BM) * 64 + off);
-        const h8_t alo = *reinterpret_cast<const h8_t*>(base + ((sb * 2 + 1) * BM) * 64 + off);
+        const int step = sb * MT + i;
+        const h8_t ahi = nhi, alo = nlo;
+        if (step + 1 < 2 * MT) afrag((step + 1) / MT, (step + 1) % MT, nhi, nlo);
+        f4_t pc[NT];
+#pragma unroll
+        for (int j = 0; j < NT; ++j) pc[j] = mfma32(ahi, fr[j].b, f4_t{0.0f, 0.0f, 0.0f, 0.0f});
+#pragma unroll
+        for (int j = 0; j < NT; ++j) pc[j] = mfma32(alo, fr[j].b, pc[j]);
+        if (step > 0) {
+#pragma unroll
+          for (int j = 0; j < NT; ++j) acc[(step - 1) % MT][j] += psc[j] * pp[j];
+        }
 #pragma unroll
         for (int j = 0; j < NT; ++j) {
-          f4_t p = mfma32(ahi, fr[j].b, f4_t{0.0f, 0.0f, 0.0f, 0.0f});
-          p = mfma32(alo, fr[j].b, p);
-          acc[i][j] += fr[j].sc[0] * p;
+          pp[j] = pc[j];
+          psc[j] = fr[j].sc[0];
         }
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
+#pragma unroll
+    for (int j = 0; j < NT; ++j) acc[MT - 1][j] += psc[j] * pp[j];
   };
 
   issue(0, 0);
   if (nst > 1) issue(1, 1);
-  for (int64_t st = 0; st < nst; st += 3) {
+  for (int st = 0; st < nst; st += 3) {
     wait_stage(st);
     if (st + 2 < nst) issue(st + 2, 2);
     compute(st, 0);
@@ -1322,7 +1427,8 @@ hipError_t pf_gemm_go(PfGemmArgs a, hipStream_t s) {
 
 template <int FMT, int EPI, int MT>
 hipError_t pf_gemm_dma_go(PfGemmArgs a, hipStream_t s) {
-  const int per_tile = PF_WAVES * 16 * (EPI == EPI_SWIGLU ? 1 : 2);
+  constexpr int NT = dma_nt<FMT>();
+  const int per_tile = PF_DW * 16 * (EPI == EPI_SWIGLU ? NT / 2 : NT);
   int ntiles = 0;
   for (int k = 0; k < a.nseg; ++k) {
     a.seg[k].tile0 = ntiles;
@@ -1330,7 +1436,7 @@ hipError_t pf_gemm_dma_go(PfGemmArgs a, hipStream_t s) {
   }
   if (a.gtab && a.gbm != 16 * MT) return hipErrorInvalidValue;
   dim3 grid((unsigned)ntiles, (unsigned)(a.gtab ? a.ntab : a.mpad / (16 * MT)), (unsigned)a.ksplit);
-  UAII_LAUNCH((k_pf_gemm_dma<FMT, EPI, MT>), grid, dim3(PF_WAVES * 64), 0, s, a);
+  UAII_LAUNCH((k_pf_gemm_dma<FMT, EPI, MT, NT>), grid, dim3(PF_DW * 64), 0, s, a);
   return hipGetLastError();
 }
 
@@ -1395,11 +1501,13 @@ int pf_gemm_ksplit(const PfGemmArgs& a, int cus) {
   const bool tall = wide || (type == T_Q4_K && UAII_PF_KTILE);  // formats with the 64 x 32 wave tile
   const int64_t mid = (rows / 128) * (a.mpad / 64);
   const bool big_tile = tall && (UAII_PF_TILE == 2 || (UAII_PF_TILE == 0 && mid >= 256));
-  const int64_t tiles = (rows + PF_WAVES * 32 - 1) / (PF_WAVES * 32);
+  const int nw = (wide && UAII_PF_DMA) ? PF_DW : PF_WAVES;  // waves per block
+  const int64_t tiles = (rows + nw * 32 - 1) / (nw * 32);     // 32 weight rows per wave
   const int64_t blocks = tiles * (a.mpad / (big_tile ? 64 : 32));
   const int64_t kq = wide ? 64 : 256;
   int ks = 1;
-  while (ks < 4 && blocks * ks < 2 * (int64_t)cus && a.K % (kq * ks * 2) == 0) ks *= 2;
+  const int64_t want = (int64_t)cus * UAII_PF_KS_BPC * PF_WAVES / nw;  // blocks (of PF_WAVES-wave units)
+  while (ks < 4 && blocks * ks < want && a.K % (kq * ks * 2) == 0) ks *= 2;
   return ks;
 }
 
@@ -1413,6 +1521,8 @@ hipError_t launch_pf_gemm(PfGemmArgs a, hipStream_t s) {
   if (!a.arow && !a.gtab && a.sx_ld != a.mpad) return hipErrorInvalidValue;
   if (a.nseg < 1 || a.nseg > 3 || a.M <= 0 || a.M > a.mpad || a.mpad % 64 || a.K % 64)
     return hipErrorInvalidValue;
+  // the direct-to-LDS kernels address activation rows by 32-bit byte offsets
+  if (a.sx_ld * a.K * 2 >= (int64_t(1) << 31)) return hipErrorInvalidValue;
   if (a.gtab) {
     // every table entry lies inside [0, M) and names an expert below ngroups (the
     // caller builds it on the host); here the launch itself is checked
