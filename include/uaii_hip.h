@@ -141,6 +141,13 @@ UAII_HIP_API int uaii_hip_time_gemm(const uaii_hip_weight* w, const float* x, in
 /* Device-to-device copy with the library's plain copy kernel (bytes % 16 == 0). */
 UAII_HIP_API int uaii_hip_time_copy(const void* src, void* dst, size_t bytes, int iters,
                                     float* avg_ms);
+/* Per-launch floor of the decode kernels: a plain read of `bytes` (% 16 == 0)
+ * in their launch shape (one 512-thread block per CU, eight 16-byte loads in
+ * flight per thread), `iters` launches rotating over the `nsrc` buffers so that
+ * a rotation larger than the last-level cache reads HBM every launch.
+ * No counterpart in the reference: measurement only. */
+UAII_HIP_API int uaii_hip_time_read(const void* const* srcs, int nsrc, size_t bytes, int iters,
+                                    float* avg_ms);
 
 #ifdef __cplusplus
 }

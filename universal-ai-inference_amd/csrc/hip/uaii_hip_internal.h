@@ -124,6 +124,9 @@ hipError_t launch_rope(float* x, int64_t rows, int64_t dim, int head_dim, const 
                        int64_t pos_stride, const float2* tab, int mode, hipStream_t s);
 // Plain device copy of n16 16-byte words (the yardstick for HBM rates and counters).
 hipError_t launch_copy(const void* src, void* dst, int64_t n16, hipStream_t s);
+// Plain read of n16 16-byte words, one 512-thread block per CU (the per-launch
+// floor of the decode kernels); `sink` receives a word only by a 2^-32 chance.
+hipError_t launch_read(const void* src, int64_t n16, uint32_t* sink, hipStream_t s);
 
 // ---- attention -----------------------------------------------------------------
 

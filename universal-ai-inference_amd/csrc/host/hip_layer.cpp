@@ -392,4 +392,30 @@ int uaii_hip_time_copy(const void* src, void* dst, size_t bytes, int iters, floa
   return rc;
 }
 
+int uaii_hip_time_read(const void* const* srcs, int nsrc, size_t bytes, int iters, float* avg_ms) {
+  if (!srcs || nsrc <= 0 || iters <= 0 || !avg_ms || bytes % 16 || bytes == 0) return kErrArg;
+  for (int i = 0; i < nsrc; ++i)
+    if (!srcs[i]) return kErrArg;
+  uint32_t* sink = nullptr;
+  hipError_t e = hipMalloc(&sink, 16);
+  if (e != hipSuccess) return (int)e;
+  hipEvent_t e0, e1;
+  (void)hipEventCreate(&e0);
+  (void)hipEventCreate(&e1);
+  const int64_t n16 = (int64_t)(bytes / 16);
+  int rc = (int)uaii_hip::launch_read(srcs[0], n16, sink, nullptr);
+  (void)hipEventRecord(e0, nullptr);
+  for (int i = 0; i < iters && !rc; ++i)
+    rc = (int)uaii_hip::launch_read(srcs[(i + 1) % nsrc], n16, sink, nullptr);
+  (void)hipEventRecord(e1, nullptr);
+  (void)hipEventSynchronize(e1);
+  float ms = 0.0f;
+  (void)hipEventElapsedTime(&ms, e0, e1);
+  *avg_ms = ms / (float)iters;
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  (void)hipFree(sink);
+  return rc;
+}
+
 }  // extern "C"

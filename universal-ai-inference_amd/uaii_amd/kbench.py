@@ -9,6 +9,12 @@ weights from HBM, plus the plain 1 GiB copy kernel. Meant to run alone or under
 memory traffic.
 
     python3 -m uaii_amd.kbench --epi swiglu --type q4_0 --rows 14336 --cols 4096
+
+``--floor`` instead times the per-launch floor: a plain read kernel in the
+decode GEMVs' launch shape over each decode kernel's byte count of the 8B Q4_0
+step (rotating over buffers that together exceed the last-level cache).
+
+    python3 -m uaii_amd.kbench --floor
 """
 from __future__ import annotations
 
@@ -34,7 +40,11 @@ def main(argv=None) -> int:
     ap.add_argument("--copy-mib", type=int, default=1024)
     ap.add_argument("--m", type=int, default=1,
                     help="activation rows: 1 = decode GEMV, > 1 = prefill MFMA GEMM (TFLOP/s)")
+    ap.add_argument("--floor", action="store_true",
+                    help="plain-read per-launch floor over the 8B decode kernels' byte counts")
     a = ap.parse_args(argv)
+    if a.floor:
+        return floor(a.iters)
     names = {v.lower(): k for k, v in TYPE_NAMES.items()}
     t = names[a.type.lower()]
     L = lib()
@@ -95,6 +105,38 @@ def main(argv=None) -> int:
     check_hip(L.uaii_hip_time_copy(src.ptr, dst.ptr, nb, 10, C.byref(ms)), "copy")
     print(f"copy {a.copy_mib} MiB: {ms.value * 1e3:.1f} us, {2 * nb / (ms.value * 1e-3) / 1e9:.0f} GB/s (r+w)",
           flush=True)
+    return 0
+
+
+# Bytes per launch of the 8B Q4_0 decode kernels at ctx 4096 (algorithmic bytes).
+FLOOR_CASES = [("O", 9.44e6), ("QKV", 14.17e6), ("attention K+V", 16.8e6), ("down", 33.0e6),
+               ("gate+up", 66.1e6), ("LM head", 295.5e6)]
+
+
+def floor(iters: int) -> int:
+    """Average time of a plain read of each case's bytes, one launch after
+    another, rotating over enough buffers (> 320 MiB) that every launch reads
+    HBM. Prints one line per case and the per-token sum (32 layers of the five
+    layer reads + the LM head)."""
+    L = lib()
+    check_hip(L.uaii_hip_init(0), "init")
+    total_us = 0.0
+    for name, nbytes in FLOOR_CASES:
+        nb = int(nbytes) // 16 * 16
+        copies = max(2, int(np.ceil(320 * 2 ** 20 / nb)))
+        bufs = [DeviceBuffer(nb) for _ in range(copies)]
+        for b in bufs:
+            b.zero()
+        ptrs = (C.c_void_p * copies)(*[b.ptr for b in bufs])
+        ms = C.c_float()
+        check_hip(L.uaii_hip_time_read(ptrs, copies, nb, iters, C.byref(ms)), "read")
+        us = ms.value * 1e3
+        total_us += us * (1 if name == "LM head" else 32)
+        print(f"floor {name:14s} {nb / 1e6:7.2f} MB: {us:7.2f} us/launch, {nb / us / 1e3:6.0f} GB/s, "
+              f"{copies} buffers", flush=True)
+        del bufs
+    print(f"floor per token (32 x (O + QKV + attention + down + gate+up) + LM head): {total_us / 1e3:.3f} ms "
+          f"= {1e6 / total_us:.0f} tok/s", flush=True)
     return 0
 
 
