@@ -177,7 +177,7 @@ def main() -> int:
         sess.step_async(True)
         sess.sync()
         prefill_s = time.perf_counter() - t0
-        prefill["method"] = "matrix cores (MFMA), 512-token chunks"
+        prefill["method"] = "matrix cores (MFMA), 1024-token chunks"
         if not args.no_profile:
             # the same prefill profiled per kernel; it rebuilds the same KV state
             sess.begin(prompt, ctx)

@@ -49,14 +49,15 @@ def maxrel(a, b):
     return float(np.abs(np.asarray(a, np.float64) - b).max() / max(np.abs(b).max(), 1e-30))
 
 
-def run(path, cfg, prompt, n_new, layers=True, profile=False, ring="1"):
-    saved = {k: os.environ.get(k) for k in ("UAII_LAYERS", "UAII_RING")}
+def run(path, cfg, prompt, n_new, layers=True, profile=False, ring="1", ring_lm="0"):
+    saved = {k: os.environ.get(k) for k in ("UAII_LAYERS", "UAII_RING", "UAII_RING_LM")}
     os.environ["UAII_LAYERS"] = "1" if layers else "0"
     os.environ["UAII_RING"] = ring
+    os.environ["UAII_RING_LM"] = ring_lm
     try:
         with uaii_amd.Session(path, kv_f16=True, profile=profile) as s:
             ids = s.generate(prompt, n_new)
-            taps = {"logits": s.get("logits")}
+            taps = {"logits": s.get("logits"), "normed": s.get("normed")}
             for li in range(cfg.n_layers):
                 taps[f"r1_{li}"] = s.get(f"blk.{li}.resid1")
                 taps[f"r2_{li}"] = s.get(f"blk.{li}.resid2")
@@ -149,3 +150,19 @@ def test_ring_gemv_matches_gemv():
     assert np.array_equal(ids, ids0)
     for k in taps:
         assert maxrel(taps[k], taps0[k]) < 1e-4, k
+
+
+@pytest.mark.parametrize("name", ["g4_hd128", "g1_hd128_ffn6144"])
+def test_ring_lm_head(name):
+    """The LM head on the ring GEMV (UAII_RING_LM=1: final RMSNorm staging, logits,
+    argmax partials per compute wave, then the final argmax + token advance)
+    against the oracle: ids, logits and the normed input."""
+    cfg = CFGS[name]
+    path = synth.cached_model(cfg)
+    prompt = np.random.default_rng(cfg.seed + 3).integers(0, cfg.vocab, 20).astype(np.int64)
+    print(name, flush=True)
+    ids, taps, _ = run(path, cfg, prompt, 32, layers=False, ring_lm="1")
+    want_ids, want = oracle.Model(path).generate(prompt, 32, kv_f16=True)
+    assert np.array_equal(ids, want_ids)
+    assert maxrel(taps["logits"], want["logits"]) < 2e-3
+    assert maxrel(taps["normed"], want["normed"]) < 2e-3

@@ -59,7 +59,8 @@ def oracle_rmsnorm_rows(x, nw, eps=1e-5):
 
 @pytest.mark.parametrize("t", MFMA_TYPES, ids=lambda t: uaii_amd.TYPE_NAMES[t])
 @pytest.mark.parametrize("m,rows,cols", [(1, 256, 256), (3, 96, 512), (77, 1000, 1024),
-                                         (130, 300, 2048), (512, 4096, 4096)], ids=str)
+                                         (130, 300, 2048), (512, 4096, 4096), (1024, 640, 1024)],
+                         ids=str)
 def test_gemm_against_oracle(hip, t, m, rows, cols):
     p = packed(t, rows, cols, seed=rows + cols + m)
     x = synth.normals(71, m, 0, m * cols, 1.0).reshape(m, cols)
@@ -278,3 +279,24 @@ def test_prefill_chunks_and_offsets(monkeypatch, name):
         logits = s.get("logits")
     assert np.array_equal(ids, ref_ids)
     assert maxrel(logits, ref_logits) < 2e-3
+
+
+def test_generate_long_prompt_two_chunks():
+    """An 1100-token prompt: one 1024-token chunk (the default chunk) and a
+    75-token one at p0 = 1024, then 16 greedy tokens, against the oracle."""
+    cfg = synth.ModelConfig(n_layers=2, dim=512, n_heads=8, n_kv_heads=2, ffn=1024, vocab=2000,
+                            ctx_len=2048, type_default=uaii_amd.Q4_0, type_attn_v=uaii_amd.Q8_0,
+                            seed=47)
+    path = synth.cached_model(cfg)
+    prompt = np.random.default_rng(cfg.seed).integers(0, cfg.vocab, 1100).astype(np.int64)
+    with uaii_amd.Session(path, kv_f16=True) as s:
+        assert s.prefill_supported()
+        ids = s.generate(prompt, 16)
+        taps = {k: s.get(k) for k in ("logits", "normed")}
+        r2 = [s.get(f"blk.{li}.resid2") for li in range(cfg.n_layers)]
+    want_ids, want = oracle.Model(path).generate(prompt, 16, kv_f16=True)
+    assert np.array_equal(ids, want_ids)
+    assert maxrel(taps["logits"], want["logits"]) < 2e-3
+    assert maxrel(taps["normed"], want["normed"]) < 2e-3
+    for li in range(cfg.n_layers):
+        assert maxrel(r2[li], want["resid2"][li]) < 2e-3

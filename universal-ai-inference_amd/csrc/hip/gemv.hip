@@ -1500,4 +1500,16 @@ hipError_t launch_gemv(const GemvArgs& in, hipStream_t s) {
   });
 }
 
+hipError_t launch_argmax_final(float* part_val, int32_t* part_idx, int nparts, StepState* state,
+                               int32_t* ids, hipStream_t s) {
+  if (!part_val || !part_idx || !state || !ids || nparts < 1) return hipErrorInvalidValue;
+  GemvArgs a{};
+  a.part_val = part_val;
+  a.part_idx = part_idx;
+  a.state = state;
+  a.ids = ids;
+  UAII_LAUNCH(k_argmax_final, dim3(1), dim3(1024), 0, s, a, nparts);
+  return hipGetLastError();
+}
+
 }  // namespace uaii_hip

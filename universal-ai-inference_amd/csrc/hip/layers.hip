@@ -1171,6 +1171,11 @@ __global__ void __launch_bounds__(NTH, 1) k_ring_gemv(RingArgs a) {
   }
   XP xp;
   stage_finish(v, a.norm_w != nullptr, w, a.eps, a.K, ge, comp, wave, lane, red, xp);
+  if (a.xtap && b == 0 && comp && wave < ge.ncol) {  // the staged input, once (chunk column = wave)
+    float4* dst = reinterpret_cast<float4*>(a.xtap) + 8 * ((int64_t)wave * 64 + lane);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) dst[k] = make_float4(v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]);
+  }
   for (int i = 0; i < n; i += 2) {
     if (!comp) {
       // stages i and i + 1 are in flight (a one-stage first burst leaves i + 1
@@ -1232,6 +1237,29 @@ __global__ void __launch_bounds__(NTH, 1) k_ring_gemv(RingArgs a) {
           reinterpret_cast<float*>(cache)[o0 + 1] = v1;
         }
       }
+    }
+  } else if (a.epi == EPI_LOGITS) {
+    // logits, and this wave's greedy argmax partial: a thread's rows ascend, so
+    // strict '>' keeps the lowest index; lanes combine on (larger value, then
+    // lower index), as k_argmax_final does across the partials
+    float bv = -INFINITY;
+    int32_t bi = 0x7fffffff;
+    for (int t = tid; t < n * ge.R; t += NCW * 64) {
+      const int i = t / ge.R, r = t % ge.R;
+      const int64_t gr = (f + i) * ge.R + r;
+      const float v = row_sum(part, ge, i, r);
+      a.y[gr] = v;
+      if (bi == 0x7fffffff || v > bv) { bv = v; bi = (int32_t)gr; }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const float ov = __shfl_xor(bv, o, 64);
+      const int32_t oi = __shfl_xor(bi, o, 64);
+      if (oi != 0x7fffffff && (bi == 0x7fffffff || ov > bv || (ov == bv && oi < bi))) { bv = ov; bi = oi; }
+    }
+    if (lane == 0) {
+      a.part_val[b * NCW + wave] = bv;
+      a.part_idx[b * NCW + wave] = bi;
     }
   } else {
     for (int t = tid; t < n * ge.R; t += NCW * 64) {
@@ -1330,9 +1358,13 @@ bool layers_supported(int type, int n_layers, int64_t dim, int64_t q_dim, int64_
   return lds <= layers_lds_cap();
 }
 
+int ring_logits_parts() { return dev_cus() * NCW; }
+
 bool ring_gemv_supported(const RingArgs& a) {
   if (a.nseg < 1 || a.nseg > 3 || a.K <= 0 || a.K % 2048 || a.K > 16384 || !a.x || !a.y || !a.pad) return false;
-  if (a.epi != EPI_STORE && a.epi != EPI_ADD && a.epi != EPI_QKV && a.epi != EPI_SWIGLU) return false;
+  if (a.epi != EPI_STORE && a.epi != EPI_ADD && a.epi != EPI_QKV && a.epi != EPI_SWIGLU && a.epi != EPI_LOGITS)
+    return false;
+  if (a.epi == EPI_LOGITS && (a.nseg != 1 || !a.part_val || !a.part_idx || a.rows[0] > INT32_MAX)) return false;
   if (a.epi == EPI_SWIGLU && a.nseg != 2) return false;
   if (a.epi == EPI_QKV && (a.nseg != 3 || a.head_dim < 2 || a.head_dim % 2 || !a.rope || !a.state || !a.kcache ||
                            !a.vcache))

@@ -213,7 +213,7 @@ struct RingArgs {
   int64_t K;
   float eps;
   int nseg;
-  int epi;               // EPI_STORE, EPI_ADD, EPI_QKV (RoPE mode 0), EPI_SWIGLU
+  int epi;               // EPI_STORE, EPI_ADD, EPI_QKV (RoPE mode 0), EPI_SWIGLU, EPI_LOGITS
   // set by launch_ring_gemv: stages per block (tq, plus one for blocks below tr)
   int32_t tq, tr;
   DevWeight w[3];        // stacked row segments (Q, K, V), or gate (0) / up (1) for EPI_SWIGLU
@@ -230,7 +230,19 @@ struct RingArgs {
   const float2* rope;    // [max_seq][hd / 2]
   const StepState* state;
   const uint8_t* pad;    // >= 1 KiB of device memory read by the padding DMA lines
+  // EPI_LOGITS: the staged (normed) input copied to xtap by block 0 when set, and
+  // per compute wave a (max, lowest index) partial of the greedy argmax at
+  // part_val/part_idx[block * 8 + wave] (ring_logits_parts() entries)
+  float* xtap;
+  float* part_val;
+  int32_t* part_idx;
 };
+
+// Argmax partials a ring EPI_LOGITS launch writes (one per compute wave).
+int ring_logits_parts();
+// The final argmax + token advance over `nparts` partials (k_argmax_final).
+hipError_t launch_argmax_final(float* part_val, int32_t* part_idx, int nparts, StepState* state,
+                               int32_t* ids, hipStream_t s);
 
 bool ring_gemv_supported(const RingArgs& a);
 hipError_t prepare_ring_gemv();

@@ -147,6 +147,7 @@ class DecoderProgram {
   float* lm_part_val_ = nullptr;
   int32_t* lm_part_idx_ = nullptr;
   int lm_blocks_ = 0;  // capacity of the LM-head partial buffers
+  bool ring_lm_ = false;  // the LM head on the ring GEMV (UAII_RING_LM=1; off by default)
   // profiling mode: start/stop event pairs and their (kernel name, bytes) per launch group
   struct ProfTag {
     std::string name;
