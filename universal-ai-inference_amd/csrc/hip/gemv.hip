@@ -1050,14 +1050,13 @@ __global__ void __launch_bounds__(W * 64) k_gemv(GemvArgs a) {
     // the launch against ~3 us, measured by per-wave clock stamps on the 8B
     // decode (gate/up 19.3 -> 17.9 us, LM head 61 -> 55 us, QKV unchanged;
     // 461 -> 471 tok/s).
-#ifdef UAII_GEMV_EARLY
-    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wave's input has arrived
-    if (nunits > 0) load_unit<FMT, EPI>(a, seg, ebase, wk, unit_l0(0), 0, lane, pos, U0);
-    stage_pairs_finish<FMT>(a, xin, wk.nch, ps0, xsm, red);
-#else
     stage_pairs_finish<FMT>(a, xin, wk.nch, ps0, xsm, red);
     if (nunits > 0) load_unit<FMT, EPI>(a, seg, ebase, wk, unit_l0(0), 0, lane, pos, U0);
-#endif
+  } else if constexpr (FMT == T_Q8_0) {
+    // input first here too: 8B Q8_0 decode 368.4 -> 372.2 tok/s (QKV 13.0 -> 12.0
+    // us); the same order for the K-quants measured slower (1B 935 -> 917 tok/s)
+    stage_x<FMT>(a, xin, wk.nch, xsm, red);
+    if (nunits > 0) load_unit<FMT, EPI>(a, seg, ebase, wk, unit_l0(0), 0, lane, pos, U0);
   } else {
     if (nunits > 0) load_unit<FMT, EPI>(a, seg, ebase, wk, unit_l0(0), 0, lane, pos, U0);
     stage_x<FMT>(a, xin, wk.nch, xsm, red);
