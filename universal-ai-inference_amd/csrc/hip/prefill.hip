@@ -1038,6 +1038,16 @@ __global__ void __launch_bounds__(256, 2) k_pf_attn(PfAttnArgs a) {
     }
   }
 
+  // scale of the raw scores into base-2 exponent units, and the causal limits
+  // in 32-bit positions (a cache holds < 2^31 keys)
+  float l2s[PA_QW];
+  int qposi[PA_QW];
+#pragma unroll
+  for (int u = 0; u < PA_QW; ++u) {
+    l2s[u] = qrs[u] * 1.4426950408889634f;
+    qposi[u] = (int)qpos[u];
+  }
+  const int64_t qpos0 = a.p0 + qw0;  // the wave's first query position
   f4_t o[PA_QW][ND];
   float mrun[PA_QW], lrun[PA_QW];
 #pragma unroll
@@ -1052,18 +1062,19 @@ __global__ void __launch_bounds__(256, 2) k_pf_attn(PfAttnArgs a) {
   const __half* vbase = reinterpret_cast<const __half*>(a.vcache) + (int64_t)kvh * a.max_seq * HD;
 
   // tile staging: K pieces (key, 8 dims) and V pairs (keys 2k, 2k + 1, 8 dims);
-  // keys past nkeys read as zeros
+  // keys past nkeys read as zeros. Offsets inside a tile are 32-bit and fixed
+  // per thread; only the last tile checks them against nkeys.
   uint4 kreg[KPIECES], vreg[VPAIRS][2];
   auto load_tile = [&](int64_t kt) __attribute__((always_inline)) {
+    const __half* kt_base = reinterpret_cast<const __half*>(uniform_ptr(kbase + kt * HD));
+    const __half* vt_base = reinterpret_cast<const __half*>(uniform_ptr(vbase + kt * HD));
+    const bool full = kt + PA_TK <= nkeys;  // block-uniform
 #pragma unroll
     for (int u = 0; u < KPIECES; ++u) {
       const int c = threadIdx.x + 256 * u;
       const int key = c / (HD / 8), p = c % (HD / 8);
       kreg[u] = make_uint4(0, 0, 0, 0);
-      if (kt + key < nkeys) {
-        const uint4 v = *reinterpret_cast<const uint4*>(kbase + (kt + key) * HD + 8 * p);
-        kreg[u].x = v.x; kreg[u].y = v.y; kreg[u].z = v.z; kreg[u].w = v.w;
-      }
+      if (full || kt + key < nkeys) kreg[u] = *reinterpret_cast<const uint4*>(kt_base + (key * HD + 8 * p));
     }
 #pragma unroll
     for (int u = 0; u < VPAIRS; ++u) {
@@ -1072,10 +1083,8 @@ __global__ void __launch_bounds__(256, 2) k_pf_attn(PfAttnArgs a) {
 #pragma unroll
       for (int e = 0; e < 2; ++e) {
         vreg[u][e] = make_uint4(0, 0, 0, 0);
-        if (kt + 2 * kp + e < nkeys) {
-          const uint4 v = *reinterpret_cast<const uint4*>(vbase + (kt + 2 * kp + e) * HD + 8 * p);
-          vreg[u][e].x = v.x; vreg[u][e].y = v.y; vreg[u][e].z = v.z; vreg[u][e].w = v.w;
-        }
+        if (full || kt + 2 * kp + e < nkeys)
+          vreg[u][e] = *reinterpret_cast<const uint4*>(vt_base + ((2 * kp + e) * HD + 8 * p));
       }
     }
   };
@@ -1111,6 +1120,8 @@ __global__ void __launch_bounds__(256, 2) k_pf_attn(PfAttnArgs a) {
 #pragma unroll
     for (int u = 0; u < PA_QW; ++u) {
       // S^T for 4 key subtiles: lane holds keys kt + 16s + 4g + r of query col
+      // raw scores (q pre-scaled by 2^qe); the running max and the exponentials
+      // are in base 2: score * log2(e) = acc * l2s, p = 2^(acc * l2s - m)
       f4_t sc[4];
 #pragma unroll
       for (int s4 = 0; s4 < 4; ++s4) {
@@ -1121,27 +1132,35 @@ __global__ void __launch_bounds__(256, 2) k_pf_attn(PfAttnArgs a) {
           acc = mfma32(kf, qhi[u][c], acc);
           acc = mfma32(kf, qlo[u][c], acc);
         }
-        sc[s4] = acc * qrs[u];
+        sc[s4] = acc;
+      }
+      // causal mask only on tiles that reach past the wave's first query
+      // (rows past M are never stored and need none)
+      if (kt + PA_TK - 1 > qpos0) {
+#pragma unroll
+        for (int s4 = 0; s4 < 4; ++s4)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int key = (int)kt + 16 * s4 + 4 * g + r;
+            if (key > qposi[u]) sc[s4][r] = -INFINITY;
+          }
       }
       float tmax = -INFINITY;
 #pragma unroll
       for (int s4 = 0; s4 < 4; ++s4)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int64_t key = kt + 16 * s4 + 4 * g + r;
-          if (!qvalid[u] || key > qpos[u]) sc[s4][r] = -INFINITY;
-          tmax = fmaxf(tmax, sc[s4][r]);
-        }
+        for (int r = 0; r < 4; ++r) tmax = fmaxf(tmax, sc[s4][r]);
       tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
       tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-      const float mnew = fmaxf(mrun[u], tmax);
-      const float alpha = (mrun[u] == -INFINITY) ? 0.0f : expf(mrun[u] - mnew);
+      const float mnew = fmaxf(mrun[u], tmax * l2s[u]);
+      const float alpha = (mrun[u] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mrun[u] - mnew);
+      const float mref = (mnew == -INFINITY) ? 0.0f : mnew;  // a fully masked row so far: p = 0
       float psum = 0.0f;
 #pragma unroll
       for (int s4 = 0; s4 < 4; ++s4)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const float p = (sc[s4][r] == -INFINITY) ? 0.0f : expf(sc[s4][r] - mnew);
+          const float p = __builtin_amdgcn_exp2f(fmaf(sc[s4][r], l2s[u], -mref));
           sc[s4][r] = p;
           psum += p;
         }
@@ -1149,8 +1168,10 @@ __global__ void __launch_bounds__(256, 2) k_pf_attn(PfAttnArgs a) {
       psum += __shfl_xor(psum, 32, 64);
       lrun[u] = lrun[u] * alpha + psum;
       mrun[u] = mnew;
+      if (__any(alpha != 1.0f)) {
 #pragma unroll
-      for (int d = 0; d < ND; ++d) o[u][d] *= alpha;
+        for (int d = 0; d < ND; ++d) o[u][d] *= alpha;
+      }
       // O^T += V^T . (2^14 P)^T over two 32-key chunks (p <= 1, so 2^14 p keeps
       // hi and lo normal); lane's keys: 32c + 4g + r (r < 4), 32c + 16 + 4g + (r - 4)
 #pragma unroll
