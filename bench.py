@@ -10,8 +10,10 @@ Also reported: the prompt prefill rate (matrix-core path, with its dominant
 GEMM's fp16 MFMA roofline fraction), per-kernel device time from HIP
 events on the session stream (a profiled replay of the same decode window right
 after the timed region), the dominant kernel's HBM roofline fraction, a
-device-to-device copy rate, and the reference's CPU path timed on a bounded
-window (reference kernels built from the reference sources, oracle/_ref).
+device-to-device copy rate, the reference's CPU path timed on a bounded
+window (reference kernels built from the reference sources, oracle/_ref), and
+the device GEMV at the reference's one published kernel figure (Q4_0 2048x4096
+on its benchmark's inputs) beside the reference kernel timed on this host.
 """
 from __future__ import annotations
 
@@ -93,6 +95,91 @@ def cpu_baseline(path: str, start_pos: int, n_steps: int, threads: int):
                       f"(KV filled with deterministic values), {secs:.1f} s wall; {what}"}
 
 
+PUBLISHED_GEMV = {"shape": "Q4_0 M=1 N=2048 K=4096", "median_ms": 4.495, "trials": 10,
+                  "hardware": "Intel Core i9-14900HX, 32 threads, WSL2",
+                  "source": "benchmarks/results/local_wsl.json:103-111 (uaii_bench.cpp:494-566)"}
+
+
+def published_gemv_inputs(np):
+    """The inputs of the reference's quant GEMV benchmark (uaii_bench.cpp:505-518):
+    Q4_0 blocks in row-major order with d = 1.0 (0x3c00) and qs[i] = (i + block) & 0xff,
+    activations a[i] = 0.01f * ((i % 17) + 1). Returns the packed rows, a, and the
+    exact product (f64 over the ggml nibble order, low nibbles first)."""
+    n, k = 2048, 4096
+    nb = n * k // 32
+    blk = np.zeros((nb, 18), np.uint8)
+    blk[:, 1] = 0x3C
+    blk[:, 2:] = (np.arange(16)[None, :] + np.arange(nb)[:, None]) & 0xFF
+    a = np.float32(0.01) * ((np.arange(k) % 17) + 1).astype(np.float32)
+    qs = blk[:, 2:].astype(np.int64)
+    w = (np.concatenate([qs & 15, qs >> 4], axis=1) - 8).reshape(n, k).astype(np.float64)
+    return blk.reshape(-1), a.astype(np.float32), w @ a.astype(np.float64)
+
+
+def published_gemv(np, uaii_amd, iters: int = 200):
+    """The device GEMV at the reference's one published hot-path shape, on that
+    benchmark's inputs: HIP-event time per launch over the one matrix back to back
+    (the reference benchmark reuses its matrix too) and over copies taken in turn
+    that together exceed the last-level cache (each launch reads HBM), and the
+    result's largest relative error against the exact product."""
+    import ctypes as C
+    L = uaii_amd.lib()
+    packed, a, exact = published_gemv_inputs(np)
+    n, k = 2048, 4096
+    copies = int(np.ceil(320 * 2 ** 20 / packed.nbytes))
+    ws = [uaii_amd.DeviceWeight(uaii_amd.Q4_0, packed, n, k) for _ in range(copies)]
+    x = uaii_amd.DeviceBuffer.from_array(a)
+    y = uaii_amd.DeviceBuffer(4 * n)
+    ms_hot, ms_hbm = C.c_float(), C.c_float()
+    uaii_amd.check_hip(L.uaii_hip_time_gemv(ws[0].h, x.ptr, y.ptr, iters, C.byref(ms_hot)), "time_gemv")
+    hs = (C.c_void_p * copies)(*[w.h for w in ws])
+    uaii_amd.check_hip(L.uaii_hip_time_gemv_rotate(hs, copies, x.ptr, y.ptr, iters, C.byref(ms_hbm)),
+                       "time_gemv_rotate")
+    uaii_amd.check_hip(L.uaii_hip_gemv(ws[0].h, x.ptr, y.ptr, None), "gemv")
+    uaii_amd.check_hip(L.uaii_hip_synchronize())
+    got = y.to_array(np.float32, n).astype(np.float64)
+    err = float(np.abs(got - exact).max() / np.abs(exact).max())
+    for w in ws:
+        w.free()
+    algo = packed.nbytes + 4 * k + 4 * n
+    return {**PUBLISHED_GEMV, "reference_ms": PUBLISHED_GEMV["median_ms"],
+            "gpu_us_same_matrix": round(ms_hot.value * 1e3, 2),
+            "gpu_us_from_hbm": round(ms_hbm.value * 1e3, 2),
+            "gpu_gbps_from_hbm": round(algo / (ms_hbm.value * 1e-3) / 1e9, 1),
+            "algorithmic_bytes": algo, "weight_copies": copies,
+            "max_rel_err_vs_exact": err,
+            "speedup_vs_published": round(PUBLISHED_GEMV["median_ms"] / ms_hbm.value, 1)}
+
+
+def published_gemv_cpu(np, threads: int):
+    """The reference's quant_gemm_f32 (compiled from its sources into oracle/_ref)
+    on the same inputs on this host: median of 10 trials after 5 warm-up calls, as
+    uaii_bench.cpp:84-94 and :643 time it."""
+    sys.path.insert(0, str(ROOT))
+    import oracle  # baseline only
+    import ctypes as C
+    os.environ["UAII_NUM_THREADS"] = str(threads)
+    R = oracle.ref()
+    if R is None:
+        return None
+    packed, a, exact = published_gemv_inputs(np)
+    n, k = 2048, 4096
+    out = np.zeros(n, np.float32)
+    fp = C.POINTER(C.c_float)
+    args = (2, a.ctypes.data_as(fp), 1, k, packed.ctypes.data_as(C.c_void_p), n, out.ctypes.data_as(fp))
+    for _ in range(5):
+        if R.uref_quant_gemm(*args) != 0:
+            raise RuntimeError(R.uref_last_error().decode())
+    samples = []
+    for _ in range(10):
+        t0 = time.perf_counter()
+        R.uref_quant_gemm(*args)
+        samples.append((time.perf_counter() - t0) * 1e3)
+    err = float(np.abs(out.astype(np.float64) - exact).max() / np.abs(exact).max())
+    return {"median_ms": round(float(np.median(samples)), 4), "min_ms": round(min(samples), 4),
+            "threads": threads, "max_rel_err_vs_exact": err}
+
+
 def parity_check(path: str, n_prompt: int, n_new: int, layers: int, threads: int):
     """Greedy ids of the benchmarked GGUF file truncated to its first `layers`
     layers (UAII_MAX_LAYERS, gguf.cpp:785-799): the device session (f16 KV, the
@@ -158,6 +245,8 @@ def main() -> int:
     copy_gbs = 2 * nb / (ms.value * 1e-3) / 1e9
     src.free(), dst.free()
     log(f"d2d copy {copy_gbs:.0f} GB/s (read+write)")
+    pub = published_gemv(np, uaii_amd)
+    log(f"published GEMV shape {pub}")
 
     t = time.time()
     sess = uaii_amd.Session(path, kv_f16=True, max_context=ctx)
@@ -284,6 +373,11 @@ def main() -> int:
             log(f"cpu baseline {cpu}")
         except Exception as e:  # the GPU figure stands on its own
             log(f"cpu baseline unavailable: {e}")
+        try:
+            pub["cpu_reference_here"] = published_gemv_cpu(np, args.cpu_threads)
+            log(f"published GEMV shape on this host {pub['cpu_reference_here']}")
+        except Exception as e:
+            log(f"published GEMV shape on this host unavailable: {e}")
 
     out = {
         "metric": METRIC, "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": K,
@@ -298,6 +392,7 @@ def main() -> int:
         "prefill_tok_s": round(n_prompt / prefill_s, 1),
         "prefill": prefill,
         "copy_gbps": round(copy_gbs, 1),
+        "published_gemv": pub,
         "argmax_margin_last": round(best - second, 6),
         "roofline": roofline,
         "kernels": {n: {"avg_us": round(v["avg_us"], 2), "gbps": round(v["gbps"], 1),

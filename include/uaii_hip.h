@@ -136,6 +136,11 @@ UAII_HIP_API int uaii_hip_attention_prefill(const float* q, const void* kcache,
 /* Average device time of `iters` back-to-back uaii_hip_gemv launches, in ms. */
 UAII_HIP_API int uaii_hip_time_gemv(const uaii_hip_weight* w, const float* x, float* y,
                                     int iters, float* avg_ms);
+/* The same over `nw` weights of one shape taken in turn (uaii_hip_gemv each),
+ * so that a rotation larger than the last-level cache reads HBM every launch.
+ * No counterpart in the reference: measurement only. */
+UAII_HIP_API int uaii_hip_time_gemv_rotate(const uaii_hip_weight* const* ws, int nw,
+                                           const float* x, float* y, int iters, float* avg_ms);
 UAII_HIP_API int uaii_hip_time_gemm(const uaii_hip_weight* w, const float* x, int64_t m,
                                     float* y, int iters, float* avg_ms);
 /* Device-to-device copy with the library's plain copy kernel (bytes % 16 == 0). */

@@ -130,6 +130,30 @@ def test_gemv_bench_pattern_known_answer(hip):
     assert maxrel(got, exact) < 1e-5
 
 
+def test_time_gemv_rotate(hip):
+    """The measurement entry that takes GEMV weights in turn (bench.py's
+    published-shape figure): a positive time, the last launch's output equal to
+    a plain GEMV of that weight, and bad arguments refused."""
+    rng = np.random.default_rng(91)
+    rows, cols = 256, 1024
+    ws = []
+    for _ in range(3):
+        p = rng.integers(0, 256, rows * uaii_amd.row_bytes(uaii_amd.Q4_0, cols), dtype=np.uint8)
+        p.reshape(-1, 18)[:, 1] &= 0x3B
+        ws.append(DeviceWeight(uaii_amd.Q4_0, p, rows, cols))
+    x = DeviceBuffer.from_array(rng.normal(0, 1, cols).astype(np.float32))
+    y, y0 = DeviceBuffer(4 * rows), DeviceBuffer(4 * rows)
+    hs = (C.c_void_p * 3)(*[w.h for w in ws])
+    ms = C.c_float()
+    check_hip(hip.uaii_hip_time_gemv_rotate(hs, 3, x.ptr, y.ptr, 4, C.byref(ms)), "rotate")
+    assert ms.value > 0
+    # launches 1..4 take weights 1, 2, 0, 1: the output is weight 1's
+    check_hip(hip.uaii_hip_gemv(ws[1].h, x.ptr, y0.ptr, None), "gemv")
+    check_hip(hip.uaii_hip_synchronize())
+    assert np.array_equal(y.to_array(np.float32, rows), y0.to_array(np.float32, rows))
+    assert hip.uaii_hip_time_gemv_rotate(hs, 0, x.ptr, y.ptr, 4, C.byref(ms)) != 0
+
+
 @pytest.mark.parametrize("t", [uaii_amd.Q4_0, uaii_amd.Q4_K, uaii_amd.Q6_K],
                          ids=lambda t: uaii_amd.TYPE_NAMES[t])
 def test_gemv_rmsnorm_prologue(hip, t):

@@ -354,6 +354,27 @@ int uaii_hip_time_gemv(const uaii_hip_weight* w, const float* x, float* y, int i
   return rc;
 }
 
+int uaii_hip_time_gemv_rotate(const uaii_hip_weight* const* ws, int nw, const float* x, float* y,
+                              int iters, float* avg_ms) {
+  if (!ws || nw <= 0 || !x || !y || iters <= 0 || !avg_ms) return kErrArg;
+  for (int i = 0; i < nw; ++i)
+    if (!ws[i]) return kErrArg;
+  hipEvent_t e0, e1;
+  (void)hipEventCreate(&e0);
+  (void)hipEventCreate(&e1);
+  int rc = uaii_hip_gemv(ws[0], x, y, nullptr);  // warm
+  (void)hipEventRecord(e0, nullptr);
+  for (int i = 0; i < iters && !rc; ++i) rc = uaii_hip_gemv(ws[(i + 1) % nw], x, y, nullptr);
+  (void)hipEventRecord(e1, nullptr);
+  (void)hipEventSynchronize(e1);
+  float ms = 0.0f;
+  (void)hipEventElapsedTime(&ms, e0, e1);
+  *avg_ms = ms / (float)iters;
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  return rc;
+}
+
 int uaii_hip_time_gemm(const uaii_hip_weight* w, const float* x, int64_t m, float* y, int iters,
                        float* avg_ms) {
   if (!w || !x || !y || iters <= 0 || !avg_ms || m <= 0) return kErrArg;
