@@ -55,6 +55,13 @@ __device__ inline uint32_t and_or(uint32_t v, uint32_t m, uint32_t c) {
 }
 // low nibbles of bytes 0 and 2 as f16 (1024 + q)
 __device__ inline uint32_t nib_pair(uint32_t v) { return and_or(v, 0x000F000Fu, 0x64006400u); }
+// The same with the mask in a vector register: 0x000F000F gives 1024 + q from
+// the low nibbles, 0x00F000F0 gives 1024 + 16 q from the high ones in place
+__device__ inline uint32_t and_or_v(uint32_t v, uint32_t m, uint32_t c) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(v), "v"(m), "v"(c));
+  return r;
+}
 // bytes 0 and 2 as f16 (1024 + b)
 __device__ inline uint32_t byte_pair(uint32_t v) { return and_or(v, 0x00FF00FFu, 0x64006400u); }
 
@@ -151,9 +158,13 @@ __global__ void __launch_bounds__(256) k_pf_prep(float* __restrict__ x, int64_t 
     if (i < nv) {
       const float4 v = r4[i];
       const float y0 = v.x * s, y1 = v.y * s, y2 = v.z * s, y3 = v.w * s;
-      const _Float16 h0 = (_Float16)y0, h1 = (_Float16)y1, h2 = (_Float16)y2, h3 = (_Float16)y3;
-      const _Float16 l0 = (_Float16)(y0 - (float)h0), l1 = (_Float16)(y1 - (float)h1);
-      const _Float16 l2 = (_Float16)(y2 - (float)h2), l3 = (_Float16)(y3 - (float)h3);
+      // hi16 layout: elements 16..31 of the 32-block (float4 slots 4..7) times
+      // 1/16, exactly (a power of two), before the split
+      const float q = (act.hi16 && (i & 7) >= 4) ? 0.0625f : 1.0f;
+      const float z0 = y0 * q, z1 = y1 * q, z2 = y2 * q, z3 = y3 * q;
+      const _Float16 h0 = (_Float16)z0, h1 = (_Float16)z1, h2 = (_Float16)z2, h3 = (_Float16)z3;
+      const _Float16 l0 = (_Float16)(z0 - (float)h0), l1 = (_Float16)(z1 - (float)h1);
+      const _Float16 l2 = (_Float16)(z2 - (float)h2), l3 = (_Float16)(z3 - (float)h3);
       // stored order (k0, k2, k1, k3)
       hi2[i] = make_uint2(__builtin_bit_cast(uint32_t, h2_t{h0, h2}),
                           __builtin_bit_cast(uint32_t, h2_t{h1, h3}));
@@ -271,10 +282,23 @@ __device__ inline void pf_load(const PfRow& p, int64_t st, PfRaw<FMT>& r) {
   }
 }
 
-// Block s (0 or 1) of stage st for lane group g.
-template <int FMT>
+// Block s (0 or 1) of stage st for lane group g. H16 (Q4_0, PfAct::hi16
+// activations): lane groups 2 and 3, which hold elements 16..31, decode their
+// high nibbles in place as 16 (q - 8), exact in f16, and the activations of
+// those elements carry the factor 1/16; this saves the per-lane shift.
+template <int FMT, bool H16 = false>
 __device__ inline void pf_decode(const PfRaw<FMT>& r, int64_t st, int s, int g, PfFrag<FMT>& f) {
-  if constexpr (FMT == T_Q4_0) {
+  if constexpr (FMT == T_Q4_0 && H16) {
+    const bool up = g >= 2;
+    const uint32_t m = up ? 0x00F000F0u : 0x000F000Fu;
+    const _Float16 bv = up ? (_Float16)1152.0f : (_Float16)1032.0f;  // 1024 + 16 * 8 : 1024 + 8
+    const h2_t bias = {bv, bv};
+    const uint32_t c = 0x64006400u;
+    const uint32_t v0 = r.q[s].x, v1 = r.q[s].y;
+    f.b = cat8(as_h2(and_or_v(v0, m, c)) - bias, as_h2(and_or_v(v0 >> 8, m, c)) - bias,
+               as_h2(and_or_v(v1, m, c)) - bias, as_h2(and_or_v(v1 >> 8, m, c)) - bias);
+    f.sc[0] = h2f((uint16_t)(r.d >> (16 * s)));
+  } else if constexpr (FMT == T_Q4_0) {
     const int sh = (g >> 1) * 4;
     const uint32_t v0 = r.q[s].x >> sh, v1 = r.q[s].y >> sh;
     const h2_t bias = {(_Float16)1032.0f, (_Float16)1032.0f};
@@ -666,7 +690,7 @@ constexpr int dma_per_stage() { return dma_a_per_wave<MT>() + 16 * NT * dma_qbyt
 template <int FMT>
 constexpr int dma_nt() { return 2; }
 
-template <int FMT, int EPI, int MT, int NT>
+template <int FMT, int EPI, int MT, int NT, bool H16>
 __global__ void __launch_bounds__(PF_DW * 64, 2) k_pf_gemm_dma(PfGemmArgs a) {
   static_assert(NT == 2 || NT == 4, "weight subtiles per wave");
   static_assert((4 * MT) % PF_DW == 0, "activation copies per wave");
@@ -815,7 +839,7 @@ __global__ void __launch_bounds__(PF_DW * 64, 2) k_pf_gemm_dma(PfGemmArgs a) {
 #pragma unroll
     for (int sb = 0; sb < 2; ++sb) {
 #pragma unroll
-      for (int j = 0; j < NT; ++j) pf_decode<FMT>(rw[j], st, sb, g, fr[j]);
+      for (int j = 0; j < NT; ++j) pf_decode<FMT, H16>(rw[j], st, sb, g, fr[j]);
 #pragma unroll
       for (int i = 0; i < MT; ++i) {
         const int step = sb * MT + i;
@@ -1457,7 +1481,13 @@ hipError_t pf_gemm_dma_go(PfGemmArgs a, hipStream_t s) {
   }
   if (a.gtab && a.gbm != 16 * MT) return hipErrorInvalidValue;
   dim3 grid((unsigned)ntiles, (unsigned)(a.gtab ? a.ntab : a.mpad / (16 * MT)), (unsigned)a.ksplit);
-  UAII_LAUNCH((k_pf_gemm_dma<FMT, EPI, MT, NT>), grid, dim3(PF_DW * 64), 0, s, a);
+  if constexpr (FMT == T_Q4_0) {
+    if (a.hi16) {
+      UAII_LAUNCH((k_pf_gemm_dma<FMT, EPI, MT, NT, true>), grid, dim3(PF_DW * 64), 0, s, a);
+      return hipGetLastError();
+    }
+  }
+  UAII_LAUNCH((k_pf_gemm_dma<FMT, EPI, MT, NT, false>), grid, dim3(PF_DW * 64), 0, s, a);
   return hipGetLastError();
 }
 
@@ -1536,6 +1566,8 @@ int pf_gemm_group_rows(int type) {
   return (type == T_Q4_0 || type == T_Q8_0 || (type == T_Q4_K && UAII_PF_KTILE)) ? 64 : 32;
 }
 
+bool pf_hi16_supported(int type) { return type == T_Q4_0 && UAII_PF_DMA; }
+
 hipError_t launch_pf_gemm(PfGemmArgs a, hipStream_t s) {
   if (a.ksplit < 1) a.ksplit = 1;
   if (a.sx_ld <= 0) a.sx_ld = a.mpad;
@@ -1556,6 +1588,7 @@ hipError_t launch_pf_gemm(PfGemmArgs a, hipStream_t s) {
   }
   const int type = a.seg[0].w.type;
   if (!pf_supported(type)) return hipErrorInvalidValue;
+  if (a.hi16 && !pf_hi16_supported(type)) return hipErrorInvalidValue;
   const int64_t kq = (type == T_Q4_K || type == T_Q6_K) ? 256 : 64;  // K granule of a block's range
   if (a.K % (kq * a.ksplit)) return hipErrorInvalidValue;
   if (a.ksplit > 1 && ((a.epi != EPI_ADD && a.epi != EPI_STORE) || !a.part)) return hipErrorInvalidValue;

@@ -259,6 +259,10 @@ struct PfAct {
   float* rs;      // [mpad]
   int64_t mpad;   // rows allocated (multiple of 64); rows >= M are zero
   int64_t K;
+  // 1: the layout the Q4_0 direct-to-LDS GEMM takes with its high nibbles
+  // decoded in place (elements 16..31 of every 32-block stored times 1/16);
+  // only for activations every consumer of which is such a launch
+  int hi16;
 };
 
 struct PfSeg {
@@ -295,6 +299,7 @@ struct PfGemmArgs {
   // at most gbm rows per entry (pf_gemm_group_rows of the format)
   const int32_t* gtab;
   int ntab, ngroups, gbm;
+  int hi16;       // the activations carry PfAct::hi16's layout (Q4_0 only)
 };
 
 struct PfQkvArgs {
@@ -350,6 +355,8 @@ int64_t pf_mpad(int64_t m);
 hipError_t launch_pf_prep(float* x, int64_t ldx, int64_t M, const float* norm_w, float eps,
                           const PfAct& act, hipStream_t s, const float* part = nullptr,
                           int nsplit = 0);
+// Whether a weight format's prefill GEMM takes PfAct::hi16 activations.
+bool pf_hi16_supported(int type);
 hipError_t launch_pf_gemm(PfGemmArgs a, hipStream_t s);
 // K split launch_pf_gemm can take for `a` (EPI_ADD only; 1 = none) on `cus` CUs.
 int pf_gemm_ksplit(const PfGemmArgs& a, int cus);

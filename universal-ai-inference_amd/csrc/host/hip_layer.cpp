@@ -202,6 +202,7 @@ int gemm_common(const uaii_hip_weight* w, const uaii_hip_weight* w2, const float
   act.rs = reinterpret_cast<float*>(base + 2 * hb + sxb);
   act.mpad = mpad;
   act.K = K;
+  act.hi16 = pf_hi16_supported(v.type) ? 1 : 0;  // this launch is the activations' only consumer
   hipError_t e = launch_pf_prep(const_cast<float*>(x), K, m, norm_w, eps, act, S(stream));
   if (e != hipSuccess) return (int)e;
   PfGemmArgs a{};
@@ -220,6 +221,7 @@ int gemm_common(const uaii_hip_weight* w, const uaii_hip_weight* w2, const float
   if (w2) a.seg[0].w2 = w2->w.view;
   a.seg[0].rows = N;
   a.seg[0].col0 = 0;
+  a.hi16 = act.hi16;
   return (int)launch_pf_gemm(a, S(stream));
 }
 

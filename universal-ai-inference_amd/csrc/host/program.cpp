@@ -317,6 +317,9 @@ Error DecoderProgram::build(const DecoderSpec& spec, const ProgramOptions& opts)
   if (const char* env = std::getenv("UAII_PREFILL")) {
     if (std::string(env) == "0") pf_ok_ = false;
   }
+  // Q4_0 GEMMs take their high nibbles in place (PfAct::hi16) where every
+  // consumer of a prep is one; UAII_PF_H16=0 keeps the shifted decode
+  if (const char* env = std::getenv("UAII_PF_H16")) pf_h16_ = std::string(env) != "0";
   UAII_TRY(build_layers(alloc));
   UAII_TRY(alloc(1024, (void**)&ring_pad_));
   {
@@ -455,6 +458,7 @@ Error DecoderProgram::pf_gemm(const DeviceWeight* w[3], const int64_t cols0[3], 
     a.rs = pf_act_.rs;
     a.y = y;
     a.ldy = ldy;
+    a.hi16 = pf_act_.hi16;
     int j = i;
     while (j < nw && w[j]->view.type == w[i]->view.type) {
       PfSeg& sg = a.seg[a.nseg++];
@@ -523,10 +527,11 @@ int DecoderProgram::pf_store_split(const DeviceWeight* w[3], int nw, int64_t m, 
   return ks;
 }
 
-Error DecoderProgram::pf_prep(float* x, int64_t K, int64_t m, const float* norm_w) {
+Error DecoderProgram::pf_prep(float* x, int64_t K, int64_t m, const float* norm_w, bool hi16) {
   if (pf_mpad(m) > pf_act_rows_ || K > pf_kmax_)
     return Error::make(ErrorCode::Internal, "prefill activation rows exceed their buffer");
   pf_act_.mpad = pf_mpad(m);
+  pf_act_.hi16 = hi16 ? 1 : 0;  // the GEMMs that read these rows take the same layout
   PfAct act = pf_act_;
   act.K = K;
   const int pend = (x == pf_x_) ? pf_pending_ : 0;
@@ -662,10 +667,10 @@ Error DecoderProgram::prefill(int64_t n) {
   const size_t layer_kv = (size_t)d.kv_dim * (size_t)max_ctx_ * 2;
   const int64_t ldqkv = d.q_dim + 2 * d.kv_dim;
   prof_used_ = 0;
-  auto prep = [&](float* x, int64_t K, int64_t m, const float* norm_w) -> Error {
+  auto prep = [&](float* x, int64_t K, int64_t m, const float* norm_w, bool hi16 = false) -> Error {
     Error err = Error::success();
     Error launched = timed("pf_prep", 12.0 * (double)m * (double)K, 0.0, [&]() -> hipError_t {
-      err = pf_prep(x, K, m, norm_w);
+      err = pf_prep(x, K, m, norm_w, hi16);
       return err.ok() ? hipSuccess : hipErrorInvalidValue;
     });
     if (!err.ok()) return err;
@@ -710,8 +715,10 @@ Error DecoderProgram::prefill(int64_t n) {
       const LayerSpec& ls = d.layers[(size_t)li];
       uint8_t* kbase = static_cast<uint8_t*>(kv_) + (size_t)li * 2 * layer_kv;
       uint8_t* vbase = kbase + layer_kv;
+      // each prep's layout: PfAct::hi16 when every GEMM reading it takes it
+      auto h16 = [&](const DeviceWeight& w) { return pf_h16_ && pf_hi16_supported(w.view.type); };
       // attention block (gguf.cpp:1000-1060)
-      UAII_TRY(prep(pf_x_, d.dim, m, L.attn_norm));
+      UAII_TRY(prep(pf_x_, d.dim, m, L.attn_norm, h16(L.wq) && h16(L.wk) && h16(L.wv)));
       const DeviceWeight* qkv[3] = {&L.wq, &L.wk, &L.wv};
       const int64_t qkv_cols[3] = {0, d.q_dim, d.q_dim + d.kv_dim};
       const int qkv_split = pf_store_split(qkv, 3, m, ldqkv);
@@ -756,13 +763,14 @@ Error DecoderProgram::prefill(int64_t n) {
       UAII_TRY(timed("pf_attention", 4.0 * pairs * (double)d.kv_dim, 4.0 * pairs * (double)d.q_dim, [&] {
         return launch_pf_attn(at, s);
       }));
-      UAII_TRY(prep(pf_attn_, d.q_dim, m, nullptr));
+      UAII_TRY(prep(pf_attn_, d.q_dim, m, nullptr, h16(L.wo)));
       const DeviceWeight* wo[3] = {&L.wo, nullptr, nullptr};
       const int64_t c00[3] = {0, 0, 0};
       UAII_TRY(gemm("pf_gemm_o", wo, c00, 1, nullptr, EPI_ADD, m, pf_x_, d.dim));
       // FFN block (gguf.cpp:1130-1173)
       if (ls.ffn == LayerSpec::kSwiGLU || ls.ffn == LayerSpec::kGelu) {
-        UAII_TRY(prep(pf_x_, d.dim, m, L.ffn_norm));
+        const bool ffn16 = ls.ffn == LayerSpec::kSwiGLU ? h16(L.gate) && h16(L.up) : h16(L.up);
+        UAII_TRY(prep(pf_x_, d.dim, m, L.ffn_norm, ffn16));
         if (ls.ffn == LayerSpec::kSwiGLU) {
           const DeviceWeight* wg[3] = {&L.gate, nullptr, nullptr};
           UAII_TRY(gemm("pf_gemm_gate_up", wg, c00, 1, &L.up, EPI_SWIGLU, m, pf_h_, ls.inter));
@@ -770,7 +778,7 @@ Error DecoderProgram::prefill(int64_t n) {
           const DeviceWeight* wu[3] = {&L.up, nullptr, nullptr};
           UAII_TRY(gemm("pf_gemm_up", wu, c00, 1, nullptr, EPI_GELU, m, pf_h_, ls.inter));
         }
-        UAII_TRY(prep(pf_h_, ls.inter, m, nullptr));
+        UAII_TRY(prep(pf_h_, ls.inter, m, nullptr, h16(L.down)));
         const DeviceWeight* wd[3] = {&L.down, nullptr, nullptr};
         UAII_TRY(gemm("pf_gemm_down", wd, c00, 1, nullptr, EPI_ADD, m, pf_x_, d.dim));
       } else if (ls.ffn == LayerSpec::kMoE) {

@@ -123,7 +123,7 @@ class DecoderProgram {
   Error pf_gemm(const DeviceWeight* w[3], const int64_t cols0[3], int nw, const DeviceWeight* w2,
                 int epi, int64_t m, float* y, int64_t ldy, int store_split = 1);
   int pf_store_split(const DeviceWeight* w[3], int nw, int64_t m, int64_t ldy);
-  Error pf_prep(float* x, int64_t K, int64_t m, const float* norm_w);
+  Error pf_prep(float* x, int64_t K, int64_t m, const float* norm_w, bool hi16 = false);
   template <class Prep, class Gemm>
   Error prefill_moe(const Layer& L, const LayerSpec& ls, int64_t m, Prep&& prep, Gemm&& gemm);
   Error encode_step(bool want_logits);
@@ -147,6 +147,7 @@ class DecoderProgram {
   float* lm_part_val_ = nullptr;
   int32_t* lm_part_idx_ = nullptr;
   int lm_blocks_ = 0;  // capacity of the LM-head partial buffers
+  bool pf_h16_ = true;    // Q4_0 prefill GEMMs on PfAct::hi16 activations (UAII_PF_H16=0: off)
   bool ring_lm_ = false;  // the LM head on the ring GEMV (UAII_RING_LM=1; off by default)
   // profiling mode: start/stop event pairs and their (kernel name, bytes) per launch group
   struct ProfTag {
