@@ -101,11 +101,16 @@ def test_gemv_small_all_formats(hip, t):
                          ids=lambda t: uaii_amd.TYPE_NAMES[t])
 @pytest.mark.parametrize("shape", [(4096, 4096), (4096, 14336), (14336, 4096)],
                          ids=lambda s: f"{s[0]}x{s[1]}")
-def test_gemv_config_shapes(hip, t, shape):
-    """Config 2 shapes (N x K) at M=1 against the oracle's CPU dequant-matmul."""
+@pytest.mark.parametrize("act", ["f32", "f16"])
+def test_gemv_config_shapes(hip, t, shape, act):
+    """Config 2 shapes (N x K) at M=1 against the oracle's CPU dequant-matmul, with
+    N(0,1) activations in f32 and as fp16 values (the reference takes f32 rows, so
+    fp16 activations enter as their exact f32 values)."""
     rows, cols = shape
     p = random_packed(t, rows, cols, seed=3)
     x = synth.normals(98, 1, 0, cols, 1.0)
+    if act == "f16":
+        x = x.astype(np.float16).astype(np.float32)
     got = run_gemv(hip, t, rows, cols, x, p)
     want = oracle.quant_gemm(t, x, p, rows, nthreads=0)[0]
     assert maxrel(got, want) < 2e-3
@@ -128,6 +133,40 @@ def test_gemv_bench_pattern_known_answer(hip):
     vals = np.concatenate([(q & 15) - 8, (q >> 4) - 8], axis=1).reshape(rows, cols).astype(np.float64)
     exact = vals @ a.astype(np.float64)
     assert maxrel(got, exact) < 1e-5
+
+
+def test_timing_entries(hip):
+    """The other measurement entries (bench.py, kbench): each returns a positive
+    time, the copy leaves dst equal to src, the timed GEMM leaves the plain GEMM's
+    output, the read floor accepts a rotation of buffers, and each refuses bad
+    arguments."""
+    rng = np.random.default_rng(92)
+    nb = 1 << 20
+    src = DeviceBuffer.from_array(rng.integers(0, 256, nb, dtype=np.uint8))
+    dst = DeviceBuffer(nb)
+    ms = C.c_float()
+    check_hip(hip.uaii_hip_time_copy(src.ptr, dst.ptr, nb, 3, C.byref(ms)), "time_copy")
+    assert ms.value > 0
+    assert np.array_equal(dst.to_array(np.uint8, nb), src.to_array(np.uint8, nb))
+    assert hip.uaii_hip_time_copy(src.ptr, dst.ptr, nb - 4, 3, C.byref(ms)) != 0  # bytes % 16
+    bufs = [DeviceBuffer(nb) for _ in range(3)]
+    ptrs = (C.c_void_p * 3)(*[b.ptr for b in bufs])
+    check_hip(hip.uaii_hip_time_read(ptrs, 3, nb, 4, C.byref(ms)), "time_read")
+    assert ms.value > 0
+    assert hip.uaii_hip_time_read(ptrs, 0, nb, 4, C.byref(ms)) != 0
+    assert hip.uaii_hip_time_read(ptrs, 3, 0, 4, C.byref(ms)) != 0
+    rows, cols, m = 128, 256, 64
+    p = rng.integers(0, 256, rows * uaii_amd.row_bytes(uaii_amd.Q4_0, cols), dtype=np.uint8)
+    p.reshape(-1, 18)[:, 1] &= 0x3B
+    w = DeviceWeight(uaii_amd.Q4_0, p, rows, cols)
+    x = DeviceBuffer.from_array(rng.normal(0, 1, m * cols).astype(np.float32))
+    y, y0 = DeviceBuffer(4 * m * rows), DeviceBuffer(4 * m * rows)
+    check_hip(hip.uaii_hip_time_gemm(w.h, x.ptr, m, y.ptr, 2, C.byref(ms)), "time_gemm")
+    assert ms.value > 0
+    check_hip(hip.uaii_hip_gemm(w.h, x.ptr, m, y0.ptr, None), "gemm")
+    check_hip(hip.uaii_hip_synchronize())
+    assert np.array_equal(y.to_array(np.float32, m * rows), y0.to_array(np.float32, m * rows))
+    assert hip.uaii_hip_time_gemm(w.h, x.ptr, 0, y.ptr, 2, C.byref(ms)) != 0
 
 
 def test_time_gemv_rotate(hip):

@@ -81,12 +81,17 @@ def test_gemm_against_oracle(hip, t, m, rows, cols):
 @pytest.mark.parametrize("t", [uaii_amd.Q4_0, uaii_amd.Q8_0, uaii_amd.Q4_K],
                          ids=lambda t: uaii_amd.TYPE_NAMES[t])
 @pytest.mark.parametrize("shape", [(4096, 14336), (14336, 4096)], ids=lambda s: f"{s[0]}x{s[1]}")
-def test_gemm_config_shapes(hip, t, shape):
-    """Config 2 at M=512; the oracle checks a sample of 24 activation rows."""
+@pytest.mark.parametrize("act", ["f32", "f16"])
+def test_gemm_config_shapes(hip, t, shape, act):
+    """Config 2 at M=512; the oracle checks a sample of 24 activation rows. N(0,1)
+    activations in f32 and as fp16 values (entering as their exact f32 values, the
+    reference's row type)."""
     rows, cols = shape
     m = 512
     p = packed(t, rows, cols, seed=7)
     x = synth.normals(72, m, 0, m * cols, 1.0).reshape(m, cols)
+    if act == "f16":
+        x = x.astype(np.float16).astype(np.float32)
     w = DeviceWeight(t, p, rows, cols)
     got = run_gemm(hip, w, x, rows)
     pick = np.random.default_rng(5).choice(m, 24, replace=False)
