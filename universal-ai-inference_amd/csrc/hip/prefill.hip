@@ -366,7 +366,10 @@ constexpr int PF_WAVES = 4;   // waves per block, side by side along N
 #define UAII_PF_ROW 40
 #endif
 #ifndef UAII_PF_KS_BPC
-#define UAII_PF_KS_BPC 2  // K split target: four-wave block equivalents per CU
+// K split target: four-wave block equivalents per CU. 4 (two 8-wave blocks per
+// CU) measured 26.2k against 25.5k tok/s for 2 on the 8B prompt (down, O and
+// QKV 3-12 % faster, the partial fold in the next prep 1.4 ms slower); 8 25.2k
+#define UAII_PF_KS_BPC 4
 #endif
 #ifndef UAII_PF_DW
 #define UAII_PF_DW 8  // waves per block of the direct-to-LDS kernel (4 or 8)
