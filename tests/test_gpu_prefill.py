@@ -145,6 +145,34 @@ def test_gemm_rmsnorm_add_swiglu(hip, t):
     assert maxrel(dh.to_array(np.float32, m * rows).reshape(m, rows), want) < 1e-4
 
 
+@pytest.mark.parametrize("t", MFMA_TYPES, ids=lambda t: uaii_amd.TYPE_NAMES[t])
+def test_gemm_add_swiglu_wide_tile(hip, t):
+    """The residual-add and SwiGLU launches on a grid large enough for the 64-row
+    wave tile (4096 rows at M = 512), for every matrix-core format (Q6_K's tile
+    spills registers there); the oracle checks 24 sampled activation rows."""
+    rows, cols, m = 4096, 1024, 512
+    x = synth.normals(77, m, 0, m * cols, 2.0).reshape(m, cols)
+    nw = 1.0 + synth.normals(78, 1, 0, cols, 0.1)
+    pick = np.random.default_rng(9).choice(m, 24, replace=False)
+    pick[0], pick[1] = 0, m - 1
+    xn = oracle_rmsnorm_rows(x[pick], nw)
+    pg, pu = packed(t, rows, cols, 31), packed(t, rows, cols, 32)
+    wg, wu = DeviceWeight(t, pg, rows, cols), DeviceWeight(t, pu, rows, cols)
+    g = oracle.quant_gemm(t, xn, pg, rows, nthreads=0).astype(np.float64)
+    u = oracle.quant_gemm(t, xn, pu, rows, nthreads=0).astype(np.float64)
+    assert maxrel(run_gemm(hip, wg, x, rows, norm=nw)[pick], g) < 1e-4
+    dx, dn = DeviceBuffer.from_array(x), DeviceBuffer.from_array(nw)
+    y0 = synth.normals(79, m, 0, m * rows, 1.0).reshape(m, rows)
+    dy = DeviceBuffer.from_array(y0)
+    check_hip(hip.uaii_hip_gemm_add(wg.h, dx.ptr, m, dn.ptr, 1e-5, dy.ptr, None))
+    got = dy.to_array(np.float32, m * rows).reshape(m, rows)[pick]
+    assert maxrel(got, y0[pick] + g) < 1e-4
+    dh = DeviceBuffer(m * rows * 4)
+    check_hip(hip.uaii_hip_gemm_swiglu(wg.h, wu.h, dx.ptr, m, dn.ptr, 1e-5, dh.ptr, None))
+    want = g / (1.0 + np.exp(-g)) * u
+    assert maxrel(dh.to_array(np.float32, m * rows).reshape(m, rows)[pick], want) < 1e-4
+
+
 def test_gemm_other_formats_run_row_by_row(hip):
     """Formats outside the MFMA decoder go through the GEMV per row, same results."""
     t, rows, cols, m = uaii_amd.Q5_K, 200, 512, 5

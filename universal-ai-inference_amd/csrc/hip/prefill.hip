@@ -371,6 +371,13 @@ constexpr int PF_WAVES = 4;   // waves per block, side by side along N
 // QKV 3-12 % faster, the partial fold in the next prep 1.4 ms slower); 8 25.2k
 #define UAII_PF_KS_BPC 4
 #endif
+#ifndef UAII_PF_K6TILE
+// Q6_K takes the 64 x 32 wave tile where the grid allows (0: always 32 x 32).
+// Its residual-add and SwiGLU launches then spill ~28 VGPRs at two waves per
+// SIMD and still measured faster: 1B down 14.3 -> 11.3 ms per prompt, prefill
+// 54.8k -> 61.2k tok/s
+#define UAII_PF_K6TILE 1
+#endif
 #ifndef UAII_PF_DW
 #define UAII_PF_DW 8  // waves per block of the direct-to-LDS kernel (4 or 8)
 #endif
@@ -1496,9 +1503,8 @@ hipError_t pf_gemm_dma_go(PfGemmArgs a, hipStream_t s) {
 
 // Wave tile per launch: 64 x 32 (measured best at M = 512 for the 8B shapes,
 // ahead of 64 x 64 and 32 x 32; for Q4_K 232 against 196 TFLOP/s on the 1B
-// gate/up) unless that leaves the grid under one block per CU, or the format's
-// weight ring does not fit the registers of two waves per SIMD at that tile
-// (Q6_K); then 32 x 32.
+// gate/up; for Q6_K 85 against 67 TFLOP/s on the 1B down, register spills
+// included) unless that leaves the grid under one block per CU; then 32 x 32.
 template <int FMT, int EPI>
 hipError_t pf_gemm_tile(const PfGemmArgs& a, hipStream_t s) {
   int64_t rows = 0;
@@ -1526,6 +1532,9 @@ hipError_t pf_gemm_tile(const PfGemmArgs& a, hipStream_t s) {
   }
   if constexpr (FMT == T_Q4_K) {
     if (UAII_PF_KTILE && (want == 2 || (want == 0 && mid >= 256))) return pf_gemm_go<FMT, EPI, 4, 2>(a, s);
+  }
+  if constexpr (FMT == T_Q6_K) {
+    if (UAII_PF_K6TILE && (want == 2 || (want == 0 && mid >= 256))) return pf_gemm_go<FMT, EPI, 4, 2>(a, s);
   }
   return pf_gemm_go<FMT, EPI, 2, 2>(a, s);
 }
