@@ -72,9 +72,6 @@ __device__ inline h8_t cat8(h2_t a, h2_t b, h2_t c, h2_t d) {
 __device__ inline f4_t mfma32(h8_t a, h8_t b, f4_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
-__device__ inline f4_t mfma16(h4_t a, h4_t b, f4_t c) {
-  return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
-}
 
 __device__ inline float pow2f_i(int e) { return __uint_as_float((uint32_t)(e + 127) << 23); }
 
@@ -205,23 +202,27 @@ struct PfRaw<T_Q4_K> {
 };
 template <>
 struct PfRaw<T_Q6_K> {
-  uint32_t ql[4];  // ql words of (block 0, sub 0), (0, 1), (1, 0), (1, 1)
-  uint32_t qh[2];  // qh words of sub-blocks 0 and 1 (shared by both blocks)
-  uint32_t sc;     // the four int8 sub-block scales
+  uint2 ql[2];     // ql bytes 8 g .. +7 of blocks 0 and 1 (low or high nibbles by stage)
+  uint2 qh;        // qh bytes 8 g .. +7 (shared by both blocks)
+  uint32_t sc;     // the four int8 sub-block scales of the stage
   uint32_t d;
 };
 
 template <int FMT>
 struct PfFrag {
-  h8_t b;         // K=32 formats
-  h4_t b16[2];    // K=16 formats: sub-blocks 0 and 1
-  float sc[2];
+  h8_t b;         // the block's weight integers (Q6_K: the high part of sc (q - 32))
+  h8_t blo;       // Q6_K: the remainder of sc (q - 32) after b (0 or +-1)
+  float sc[1];
   float off;
 };
 
+// Q6_K folds each 16-element sub-block's int8 scale into the MFMA operand:
+// sc (q - 32) is an integer of magnitude <= 4096, which the f16 pair (b, blo)
+// holds exactly, so a 32-element block (two sub-blocks) takes one 16x16x32 MFMA
+// per operand pair and only the super-block scale d remains for the f32 partial.
 template <int FMT>
-__device__ constexpr int pf_ksub() {
-  return FMT == T_Q6_K ? 16 : 32;
+__device__ constexpr bool pf_split_b() {
+  return FMT == T_Q6_K;
 }
 template <int FMT>
 __device__ constexpr bool pf_offset() {
@@ -246,8 +247,8 @@ __device__ inline PfRow pf_row(const DevWeight& w, int64_t row, int g) {
   } else if constexpr (FMT == T_Q8_0 || FMT == T_Q4_K) {
     p.a += 8 * g;
   } else if constexpr (FMT == T_Q6_K) {
-    p.a += 4 * g;
-    p.b += 4 * g;
+    p.a += 8 * g;
+    p.b += 8 * g;
     p.c = w.c + row * w.c_row;
     p.d = w.d + row * w.d_row;
   }
@@ -272,11 +273,9 @@ __device__ inline void pf_load(const PfRow& p, int64_t st, PfRaw<FMT>& r) {
   } else if constexpr (FMT == T_Q6_K) {
     // super-block st / 4, half (st % 4) / 2, elements 64 (st % 2) .. +63 of the half
     const uint8_t* ql = p.a + (st >> 1) * 64;
-    const uint8_t* qh = p.b + (st >> 1) * 32;
-#pragma unroll
-    for (int u = 0; u < 4; ++u) r.ql[u] = *reinterpret_cast<const uint32_t*>(ql + 16 * u);
-    r.qh[0] = *reinterpret_cast<const uint32_t*>(qh);
-    r.qh[1] = *reinterpret_cast<const uint32_t*>(qh + 16);
+    r.ql[0] = *reinterpret_cast<const uint2*>(ql);
+    r.ql[1] = *reinterpret_cast<const uint2*>(ql + 32);
+    r.qh = *reinterpret_cast<const uint2*>(p.b + (st >> 1) * 32);
     r.sc = *reinterpret_cast<const uint32_t*>(p.c + st * 4);
     r.d = ld_u16(p.d + (st >> 2) * 2);
   }
@@ -334,19 +333,29 @@ __device__ inline void pf_decode(const PfRaw<FMT>& r, int64_t st, int s, int g, 
     f.sc[0] = fmul_rn(d, (float)sc);
     f.off = fmul_rn(dmin, (float)mn);
   } else if constexpr (FMT == T_Q6_K) {
-    // element e = 64 (st % 2) + 32 s + 16 t + 4 g + i of the half: ql byte e % 64
-    // (high nibble when e >= 64), qh byte e % 32 at bit 2 (e / 32), scale e / 16
+    // element e = 64 (st % 2) + 32 s + 8 g + i of the half: ql byte e % 64 (high
+    // nibble when e >= 64), qh byte e % 32 at bit 2 (e / 32), sub-block e / 16 of
+    // the stage, i.e. 2 s + g / 2. b = RN(sc (q - 32)) and blo = sc (q - 32) - b
+    // by one fused multiply-add, exact: the integer is at most 4096 in magnitude
     const int nib = (int)(st & 1) * 4;
     const int qsh = 4 * (int)(st & 1) + 2 * s;
     const h2_t bias = {(_Float16)1056.0f, (_Float16)1056.0f};
-    const float d = h2f((uint16_t)r.d);
+    const _Float16 scv = (_Float16)(float)(int8_t)((r.sc >> (8 * (2 * s + (g >> 1)))) & 0xff);
+    const h2_t sc2 = {scv, scv};
+    const uint32_t w[2] = {r.ql[s].x, r.ql[s].y}, hq[2] = {r.qh.x, r.qh.y};
+    h2_t hi[4], lo[4];
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
-      const uint32_t q6 = ((r.ql[2 * s + t] >> nib) & 0x0F0F0F0Fu) | (((r.qh[t] >> qsh) & 0x03030303u) << 4);
+      const uint32_t q6 = ((w[t] >> nib) & 0x0F0F0F0Fu) | (((hq[t] >> qsh) & 0x03030303u) << 4);
       const h2_t p0 = as_h2(byte_pair(q6)) - bias, p1 = as_h2(byte_pair(q6 >> 8)) - bias;
-      f.b16[t] = h4_t{p0.x, p0.y, p1.x, p1.y};
-      f.sc[t] = fmul_rn(d, (float)(int8_t)((r.sc >> (8 * (2 * s + t))) & 0xff));
+      hi[2 * t] = p0 * sc2;
+      lo[2 * t] = __builtin_elementwise_fma(p0, sc2, -hi[2 * t]);
+      hi[2 * t + 1] = p1 * sc2;
+      lo[2 * t + 1] = __builtin_elementwise_fma(p1, sc2, -hi[2 * t + 1]);
     }
+    f.b = cat8(hi[0], hi[1], hi[2], hi[3]);
+    f.blo = cat8(lo[0], lo[1], lo[2], lo[3]);
+    f.sc[0] = h2f((uint16_t)r.d);
   }
 }
 
@@ -372,10 +381,8 @@ constexpr int PF_WAVES = 4;   // waves per block, side by side along N
 #define UAII_PF_KS_BPC 4
 #endif
 #ifndef UAII_PF_K6TILE
-// Q6_K takes the 64 x 32 wave tile where the grid allows (0: always 32 x 32).
-// Its residual-add and SwiGLU launches then spill ~28 VGPRs at two waves per
-// SIMD and still measured faster: 1B down 14.3 -> 11.3 ms per prompt, prefill
-// 54.8k -> 61.2k tok/s
+// Q6_K takes the 64 x 32 wave tile where the grid allows (0: always 32 x 32):
+// 1B down 14.3 -> 11.3 ms per prompt with the former 16x16x16 decode
 #define UAII_PF_K6TILE 1
 #endif
 #ifndef UAII_PF_DW
@@ -428,7 +435,6 @@ __device__ inline int64_t pf_arow(const PfGemmArgs& a, const PfRange& r, int64_t
 template <int FMT, int EPI, int MT, int NT>
 __global__ void __launch_bounds__(PF_WAVES * 64, 2) k_pf_gemm(PfGemmArgs a) {
   constexpr int BM = 16 * MT;
-  constexpr int KS = pf_ksub<FMT>();
   constexpr bool OFF = pf_offset<FMT>();
   constexpr int NQ = (EPI == EPI_SWIGLU) ? NT / 2 : NT;  // distinct row subtiles
   __shared__ _Float16 lds[pf_lds_halfs<MT>()];
@@ -544,28 +550,15 @@ __global__ void __launch_bounds__(PF_WAVES * 64, 2) k_pf_gemm(PfGemmArgs a) {
           const float4 s4 = *reinterpret_cast<const float4*>(sxs + (buf * 2 + s) * BM + 16 * i + 4 * g);
           sxv = f4_t{s4.x, s4.y, s4.z, s4.w};
         }
-        if constexpr (KS == 32) {
-          const h8_t ahi = *reinterpret_cast<const h8_t*>(ph + 8 * g);
-          const h8_t alo = *reinterpret_cast<const h8_t*>(pl + 8 * g);
+        const h8_t ahi = *reinterpret_cast<const h8_t*>(ph + 8 * g);
+        const h8_t alo = *reinterpret_cast<const h8_t*>(pl + 8 * g);
 #pragma unroll
-          for (int j = 0; j < NT; ++j) {
-            f4_t p = mfma32(ahi, fr[j].b, f4_t{0.0f, 0.0f, 0.0f, 0.0f});
-            p = mfma32(alo, fr[j].b, p);
-            acc[i][j] += fr[j].sc[0] * p;
-            if constexpr (OFF) acc[i][j] -= fr[j].off * sxv;
-          }
-        } else {
-#pragma unroll
-          for (int t = 0; t < 2; ++t) {
-            const h4_t ahi = *reinterpret_cast<const h4_t*>(ph + 16 * t + 4 * g);
-            const h4_t alo = *reinterpret_cast<const h4_t*>(pl + 16 * t + 4 * g);
-#pragma unroll
-            for (int j = 0; j < NT; ++j) {
-              f4_t p = mfma16(ahi, fr[j].b16[t], f4_t{0.0f, 0.0f, 0.0f, 0.0f});
-              p = mfma16(alo, fr[j].b16[t], p);
-              acc[i][j] += fr[j].sc[t] * p;
-            }
-          }
+        for (int j = 0; j < NT; ++j) {
+          f4_t p = mfma32(ahi, fr[j].b, f4_t{0.0f, 0.0f, 0.0f, 0.0f});
+          p = mfma32(alo, fr[j].b, p);
+          if constexpr (pf_split_b<FMT>()) p = mfma32(ahi, fr[j].blo, p);  // (hi, lo) x lo: ~2^-21
+          acc[i][j] += fr[j].sc[0] * p;
+          if constexpr (OFF) acc[i][j] -= fr[j].off * sxv;
         }
       }
     }
@@ -1503,8 +1496,9 @@ hipError_t pf_gemm_dma_go(PfGemmArgs a, hipStream_t s) {
 
 // Wave tile per launch: 64 x 32 (measured best at M = 512 for the 8B shapes,
 // ahead of 64 x 64 and 32 x 32; for Q4_K 232 against 196 TFLOP/s on the 1B
-// gate/up; for Q6_K 85 against 67 TFLOP/s on the 1B down, register spills
-// included) unless that leaves the grid under one block per CU; then 32 x 32.
+// gate/up; for Q6_K 85 against 67 TFLOP/s on the 1B down with the former
+// 16x16x16 decode) unless that leaves the grid under one block per CU; then
+// 32 x 32.
 template <int FMT, int EPI>
 hipError_t pf_gemm_tile(const PfGemmArgs& a, hipStream_t s) {
   int64_t rows = 0;
