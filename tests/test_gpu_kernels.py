@@ -97,7 +97,44 @@ def test_gemv_small_all_formats(hip, t):
     assert maxrel(got, want) < 2e-5
 
 
-@pytest.mark.parametrize("t", [uaii_amd.Q4_0, uaii_amd.Q8_0, uaii_amd.Q4_K],
+def positive_scales(t, p, rows, cols):
+    """The same blocks with every scale made non-negative (and the Q4_K mins
+    zeroed), so all of a row's weights share a sign per block: rounding errors of
+    the kernel's partial sums then add up coherently across the row instead of
+    averaging out over random-sign scales."""
+    be, bb = uaii_amd.BLOCK[t]
+    b = p.reshape(-1, bb).copy()
+    if t == uaii_amd.Q4_0:
+        b[:, 1] &= 0x7f                       # d
+    elif t == uaii_amd.Q4_K:
+        b[:, 1] &= 0x7f                       # d
+        b[:, 2:4] = 0                         # dmin
+    elif t == uaii_amd.Q6_K:
+        b[:, 192:208] &= 0x7f                 # int8 sub-block scales
+        b[:, 209] &= 0x7f                     # d
+    return b.reshape(-1)
+
+
+@pytest.mark.parametrize("t", [uaii_amd.Q4_0, uaii_amd.Q4_K, uaii_amd.Q6_K],
+                         ids=lambda t: uaii_amd.TYPE_NAMES[t])
+def test_gemv_pair_formats_unbiased(hip, t):
+    """The f16-pair GEMV (v_dot2 on nibbles as f16 subnormals) against the oracle
+    on same-sign scales. With the activation's hi part rounded to f16 alone, the
+    hi partial sums rounded in the dot instruction's accumulator, biased
+    downward; on Q4_K's positive scales every row was off by the same ~3e-5
+    (relative), with random-sign scales the error looked like noise. Both the
+    largest error and the mean error over rows are bounded."""
+    rows, cols = 256, 4096
+    p = positive_scales(t, random_packed(t, rows, cols, seed=41), rows, cols)
+    x = synth.normals(42, 1, 0, cols, 1.0)
+    got = run_gemv(hip, t, rows, cols, x, p).astype(np.float64)
+    want = oracle.quant_gemm(t, x, p, rows)[0].astype(np.float64)
+    scale = np.abs(want).max()
+    assert maxrel(got, want) < 4e-6
+    assert abs((got - want).mean()) / scale < 1e-6
+
+
+@pytest.mark.parametrize("t", [uaii_amd.Q4_0, uaii_amd.Q8_0, uaii_amd.Q4_K, uaii_amd.Q6_K],
                          ids=lambda t: uaii_amd.TYPE_NAMES[t])
 @pytest.mark.parametrize("shape", [(4096, 4096), (4096, 14336), (14336, 4096)],
                          ids=lambda s: f"{s[0]}x{s[1]}")

@@ -408,27 +408,55 @@ __device__ inline int64_t qkv_phys(int64_t L, int mode, int hd) {
   return h * hd + p + (L & 1) * (hd / 2);
 }
 
-// ---- f16-pair dot for the 4-bit block formats (Q4_0, Q4_1) ------------------------
+// ---- f16-pair dot for the 4-bit and 6-bit formats (Q4_0, Q4_1, Q4_K, Q6_K) --------
 //
-// The dot runs on v_dot2_f32_f16. A payload word q (bytes 4i..4i+3 of a block)
+// The dot runs on v_dot2_f32_f16. A payload word q (bytes 4i..4i+3 of a chunk)
 // gives four f16 pairs by masking alone: q & 0x000F000F holds the low nibbles of
 // bytes 0 and 2 as the subnormal halves n * 2^-24 (exact), q & 0x00F000F0 their
 // high nibbles as n * 2^-20, and the same masks on q >> 8 give bytes 1 and 3.
-// The input is scaled per chunk by a power of two S (the chunk's largest |x| * S
-// in [2^14, 2^15); the high-nibble entries by S / 16) and split into f16 hi + lo
-// parts, so every x keeps about 22 significant bits relative to its chunk; both
-// products per element are exact and the sums are f32. A chunk's sum of n * x is
-// then (acc_hi + acc_lo) * c with c = 2^24 / S.
+// For Q6_K the two high bits of each 6-bit value are OR-ed in above the nibble
+// (bits 4-5 of a low-nibble half, bits 8-9 of a high-nibble half), still an
+// exact subnormal. Every chunk covers two runs of 16 inputs, run 0 against the
+// low nibbles and run 1 against the high nibbles. The input is scaled per chunk
+// by a power of two S (the chunk's largest |x| * S in [2^14, 2^15); run 1 by
+// S / 16) and split into f16 hi (on a grid of 2^-10 of the chunk's largest
+// value) + lo (the rest), so every x keeps about 22 significant bits relative
+// to its chunk; both products per element are exact, the hi sums are exact in
+// f32 and the lo sums round. A run's sum of n * x is then (acc_hi + acc_lo) * c
+// with c = 2^24 / S.
 //
 // LDS: 8 uint4 planes indexed by chunk (word i: plane 2i = hi pairs, 2i+1 = lo
-// pairs, in the order (x[4i], x[4i+2]), (x[16+4i], x[16+4i+2]) / 16,
-// (x[4i+1], x[4i+3]), (x[16+4i+1], x[16+4i+3]) / 16), then one float2 per chunk:
-// (sum of the block's 32 unscaled inputs, c).
+// pairs, in the order (r0[4i], r0[4i+2]), (r1[4i], r1[4i+2]) / 16,
+// (r0[4i+1], r0[4i+3]), (r1[4i+1], r1[4i+3]) / 16 for runs r0, r1), then the
+// chunk's side data: float2 (sum of both runs' unscaled inputs, c) for the
+// single-scale formats, float4 (sum of run 0, sum of run 1, c, 0) for the
+// K-quants, whose two runs carry their own scales.
+
+#ifndef UAII_GEMV_KPAIR
+#define UAII_GEMV_KPAIR 1  // 0: Q4_K / Q6_K on the f32 cvt + FMA path
+#endif
 
 typedef _Float16 h2v __attribute__((ext_vector_type(2)));
 
 template <int FMT>
-__host__ __device__ constexpr bool pair_fmt() { return FMT == T_Q4_0 || FMT == T_Q4_1; }
+__host__ __device__ constexpr bool pair_fmt() {
+  return FMT == T_Q4_0 || FMT == T_Q4_1 || (UAII_GEMV_KPAIR && (FMT == T_Q4_K || FMT == T_Q6_K));
+}
+
+// f32 slots of side data per chunk in the LDS staging.
+template <int FMT>
+__host__ __device__ constexpr int pair_side() { return (FMT == T_Q4_0 || FMT == T_Q4_1) ? 2 : 4; }
+
+// float4 index of run 0 of chunk t in the input (x_runs in float4 units) and
+// the float4 offset of run 1 from it.
+template <int FMT>
+__device__ inline int64_t pair_run0(int64_t t) {
+  if constexpr (FMT == T_Q4_K) return 64 * (t >> 3) + 16 * ((t & 7) >> 1) + 4 * (t & 1);
+  else if constexpr (FMT == T_Q6_K) return 64 * (t >> 3) + 32 * ((t & 7) >> 2) + 4 * (t & 3);
+  else return 8 * t;
+}
+template <int FMT>
+__host__ __device__ constexpr int pair_run1() { return FMT == T_Q4_K ? 8 : (FMT == T_Q6_K ? 16 : 4); }
 
 __device__ inline float dot2(uint32_t a, uint32_t b, float c) {
   return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2v, a), __builtin_bit_cast(h2v, b), c, false);
@@ -439,40 +467,121 @@ __device__ inline float pow2f(int k) { return __uint_as_float((uint32_t)(k + 127
 
 __device__ inline uint32_t hbits(_Float16 h) { return (uint32_t)__builtin_bit_cast(uint16_t, h); }
 
-// (a, b) -> f16 pairs hi = (f16(a), f16(b)), lo = (f16(a - hi.a), f16(b - hi.b)).
+// (a, b) -> f16 pairs hi = (A, B), lo = (f16(a - A), f16(b - B)) with A, B the
+// nearest multiples of the grid G. The callers pass G = |max| * 2^-10
+// (rounded down to a power of two), so |A| / g <= 2048 is exact in f16, and every
+// partial sum of nibble * hi products over a chunk is a multiple of g * 2^-24
+// below 2^24 of them: exact in f32, whatever rounding v_dot2_f32_f16 applies to
+// its accumulator. (With hi = f16(a) those sums round, and the accumulator's
+// rounding was measured to bias them downward: on positive-scale formats such
+// as Q4_K a row-wide offset of ~3e-5 relative.) Only the lo sums, ~2^-11 of the
+// total, round.
+template <int G>
+__device__ inline float grid_round(float a) {
+  static_assert(G == 1 || G == 16, "grid 1 or 16");
+  if constexpr (G == 1) return rintf(a);
+  // nearest multiple of 16 for |a| < 2^26: the ulp of 1.5 * 2^27 is 16
+  else return (a + 201326592.0f) - 201326592.0f;
+}
+
+template <int G>
 __device__ inline void split2(float a, float b, uint32_t& hi, uint32_t& lo) {
-  const _Float16 ah = (_Float16)a, bh = (_Float16)b;
-  const _Float16 al = (_Float16)(a - (float)ah), bl = (_Float16)(b - (float)bh);
+  const float ar = grid_round<G>(a), br = grid_round<G>(b);
+  const _Float16 ah = (_Float16)ar, bh = (_Float16)br;
+  const _Float16 al = (_Float16)(a - ar), bl = (_Float16)(b - br);
   hi = hbits(ah) | (hbits(bh) << 16);
   lo = hbits(al) | (hbits(bl) << 16);
 }
 
+// The chunk's x pairs and side data: xc = (sum of both runs, -, c, -) for the
+// single-scale formats, (sum of run 0, sum of run 1, c, -) for the K-quants.
+template <int FMT>
 __device__ inline void load_xpairs(const float* __restrict__ xsm, int64_t nch, int64_t t, uint4* xp,
-                                   float2& xc) {
+                                   float4& xc) {
   const uint4* pl = reinterpret_cast<const uint4*>(xsm);
 #pragma unroll
   for (int g = 0; g < 8; ++g) xp[g] = pl[(int64_t)g * nch + t];
-  xc = reinterpret_cast<const float2*>(pl + 8 * nch)[t];
+  if constexpr (pair_side<FMT>() == 2) {
+    const float2 v = reinterpret_cast<const float2*>(pl + 8 * nch)[t];
+    xc = make_float4(v.x, 0.0f, v.y, 0.0f);
+  } else {
+    xc = reinterpret_cast<const float4*>(pl + 8 * nch)[t];
+  }
+}
+
+// Q4_K (scale, min) 6-bit pairs of sub-blocks 2cc and 2cc + 1 (kscale_reg for
+// j = 2cc, 2cc + 1 on whole words): sc / mn hold the two scales / mins in bytes
+// 0 and 1.
+__device__ inline void kscale_pair(int cc, const uint4& meta, uint32_t& sc, uint32_t& mn) {
+  const int sh = 16 * (cc & 1);
+  const uint32_t a = meta.y >> sh, b = meta.z >> sh, c = meta.w >> sh;
+  if (cc < 2) {
+    sc = a & 0x3f3fu;
+    mn = b & 0x3f3fu;
+  } else {
+    sc = (c & 0x0f0fu) | ((a >> 2) & 0x3030u);
+    mn = ((c >> 4) & 0x0f0fu) | ((b >> 2) & 0x3030u);
+  }
 }
 
 template <int FMT>
-__device__ inline float chunk_dot_pairs(const Raw& o, const uint4* xp, float2 xc) {
-  const float xs = xc.x, c = xc.y;
-  float sh = 0.0f, sl = 0.0f;
+__device__ inline float chunk_dot_pairs(const Raw& o, int64_t t, const uint4* xp, float4 xc) {
+  const float c = xc.z;
+  if constexpr (FMT == T_Q4_0 || FMT == T_Q4_1) {
+    float sh = 0.0f, sl = 0.0f;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint32_t q = word(o.q, i), q8 = q >> 8;
-    const uint32_t p0 = q & 0x000F000Fu, p1 = q & 0x00F000F0u;
-    const uint32_t p2 = q8 & 0x000F000Fu, p3 = q8 & 0x00F000F0u;
-    const uint4 H = xp[2 * i], L = xp[2 * i + 1];
-    sh = dot2(p0, H.x, sh); sl = dot2(p0, L.x, sl);
-    sh = dot2(p1, H.y, sh); sl = dot2(p1, L.y, sl);
-    sh = dot2(p2, H.z, sh); sl = dot2(p2, L.z, sl);
-    sh = dot2(p3, H.w, sh); sl = dot2(p3, L.w, sl);
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t q = word(o.q, i), q8 = q >> 8;
+      const uint32_t p0 = q & 0x000F000Fu, p1 = q & 0x00F000F0u;
+      const uint32_t p2 = q8 & 0x000F000Fu, p3 = q8 & 0x00F000F0u;
+      const uint4 H = xp[2 * i], L = xp[2 * i + 1];
+      sh = dot2(p0, H.x, sh); sl = dot2(p0, L.x, sl);
+      sh = dot2(p1, H.y, sh); sl = dot2(p1, L.y, sl);
+      sh = dot2(p2, H.z, sh); sl = dot2(p2, L.z, sl);
+      sh = dot2(p3, H.w, sh); sl = dot2(p3, L.w, sl);
+    }
+    const float s = (sh + sl) * c;  // sum of n * x
+    if constexpr (FMT == T_Q4_0) return lo_h(o.s) * (s - 8.0f * xc.x);
+    else return lo_h(o.s) * s + hi_h(o.s) * xc.x;
+  } else {
+    // K-quants: run 0 (low nibbles) and run 1 (high nibbles) summed apart, hi
+    // and lo parts in their own accumulators (the hi sums stay exact)
+    float s0 = 0.0f, s1 = 0.0f, l0 = 0.0f, l1 = 0.0f;
+    const int qsh = 2 * (int)((t & 3) >> 1);  // Q6_K: qh bit pair of the chunk's runs
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t q = word(o.q, i), q8 = q >> 8;
+      uint32_t p0 = q & 0x000F000Fu, p1 = q & 0x00F000F0u;
+      uint32_t p2 = q8 & 0x000F000Fu, p3 = q8 & 0x00F000F0u;
+      if constexpr (FMT == T_Q6_K) {
+        // bits qsh, qsh+1 (run 0) and qsh+4, qsh+5 (run 1) of each qh byte to
+        // bits 4-5 and 8-9 of its f16 half
+        const uint32_t h = word(o.aux, i);
+        const uint32_t hs = h << (4 - qsh), h8 = h >> (4 + qsh);
+        p0 |= hs & 0x00300030u; p1 |= hs & 0x03000300u;
+        p2 |= h8 & 0x00300030u; p3 |= h8 & 0x03000300u;
+      }
+      const uint4 H = xp[2 * i], L = xp[2 * i + 1];
+      s0 = dot2(p0, H.x, s0); l0 = dot2(p0, L.x, l0);
+      s1 = dot2(p1, H.y, s1); l1 = dot2(p1, L.y, l1);
+      s0 = dot2(p2, H.z, s0); l0 = dot2(p2, L.z, l0);
+      s1 = dot2(p3, H.w, s1); l1 = dot2(p3, L.w, l1);
+    }
+    s0 += l0;
+    s1 += l1;
+    if constexpr (FMT == T_Q4_K) {
+      const float d = lo_h(o.aux.x), dmin = hi_h(o.aux.x);
+      uint32_t sc, mn;
+      kscale_pair((int)((t & 7) >> 1), o.aux, sc, mn);
+      const float dc = d * c;
+      return (dc * (float)(sc & 0xffu)) * s0 - (dmin * (float)(mn & 0xffu)) * xc.x +
+             (dc * (float)(sc >> 8)) * s1 - (dmin * (float)(mn >> 8)) * xc.y;
+    } else {
+      float a0, a1;
+      raw_scales<FMT>(o, t, a0, a1);
+      return a0 * (s0 * c - 32.0f * xc.x) + a1 * (s1 * c - 32.0f * xc.y);
+    }
   }
-  const float s = (sh + sl) * c;  // sum of n * x
-  if constexpr (FMT == T_Q4_0) return lo_h(o.s) * (s - 8.0f * xs);
-  else return lo_h(o.s) * s + hi_h(o.s) * xs;
 }
 
 // ---- walk over row groups ------------------------------------------------------------
@@ -588,11 +697,11 @@ __device__ inline void compute_unit(const Walk& wk, int step, int lane, const fl
       const int64_t t = t0 < wk.nch ? t0 : wk.nch - 1;
       if constexpr (pair_fmt<FMT>()) {
         uint4 xp[8];
-        float2 xc;
-        load_xpairs(xsm, wk.nch, t, xp, xc);
+        float4 xc;
+        load_xpairs<FMT>(xsm, wk.nch, t, xp, xc);
 #pragma unroll
         for (int r = 0; r < rpw_of(FMT); ++r) {
-          const float v = chunk_dot_pairs<FMT>(U.r[j][r], xp, xc);
+          const float v = chunk_dot_pairs<FMT>(U.r[j][r], t, xp, xc);
           acc[r] += ok ? v : 0.0f;
         }
       } else {
@@ -714,9 +823,9 @@ __device__ inline void stage_x(const GemvArgs& a, const float* xin, int64_t nch,
   __syncthreads();
 }
 
-// Staging of a pair format. Item (t, w) is the float4s x[8t + w] and x[8t + 4 + w]
-// (elements 32t+4w.. and 32t+16+4w..); the four items of chunk t sit on four
-// consecutive lanes. The first PB items per thread are loaded into registers by
+// Staging of a pair format. Item (t, w) is float4 w of each of chunk t's two runs
+// (x4[pair_run0(t) + w] and x4[pair_run0(t) + pair_run1 + w]); the four items of
+// chunk t sit on four consecutive lanes. The first PB items per thread are loaded into registers by
 // stage_pairs_issue, before the block's first weight loads, so waiting for them
 // never waits for the weights.
 constexpr int PB = 4;   // items per thread in the register batch
@@ -729,6 +838,7 @@ struct PairStage {
 
 template <int FMT>
 __device__ inline void stage_pairs_issue(const GemvArgs& a, const float* xin, int64_t nch, PairStage& ps) {
+  constexpr int R1 = pair_run1<FMT>();
   const int tid = threadIdx.x, nt = blockDim.x;
   const int64_t items = nch * 4;
   const float4* x4 = reinterpret_cast<const float4*>(xin);
@@ -737,9 +847,9 @@ __device__ inline void stage_pairs_issue(const GemvArgs& a, const float* xin, in
   for (int k = 0; k < PB; ++k) {
     const int64_t it = (int64_t)k * nt + tid;
     if (it < items) {
-      const int64_t i0 = 8 * (it >> 2) + (it & 3);
+      const int64_t i0 = pair_run0<FMT>(it >> 2) + (it & 3);
       ps.xa[k] = x4[i0];
-      ps.xb[k] = x4[i0 + 4];
+      ps.xb[k] = x4[i0 + R1];
     }
   }
   if (w4 && items <= (int64_t)PBW * nt) {
@@ -747,9 +857,9 @@ __device__ inline void stage_pairs_issue(const GemvArgs& a, const float* xin, in
     for (int k = 0; k < PBW; ++k) {
       const int64_t it = (int64_t)k * nt + tid;
       if (it < items) {
-        const int64_t i0 = 8 * (it >> 2) + (it & 3);
+        const int64_t i0 = pair_run0<FMT>(it >> 2) + (it & 3);
         ps.wa[k] = w4[i0];
-        ps.wb[k] = w4[i0 + 4];
+        ps.wb[k] = w4[i0 + R1];
       }
     }
   }
@@ -757,7 +867,8 @@ __device__ inline void stage_pairs_issue(const GemvArgs& a, const float* xin, in
 
 // One item: RMSNorm (two roundings, norm.cpp:122-127), the optional tap, the
 // chunk's power-of-two scale (max over the chunk's four lanes), the hi/lo split
-// into the planes, and the chunk's (sum, c) from the lane holding word 0.
+// into the planes, and the chunk's side data from the lane holding word 0.
+template <int FMT>
 __device__ inline void emit_pair_item(const GemvArgs& a, int64_t nch, int64_t it, bool valid, float4 u,
                                       float4 v, float4 uw, float4 vw, bool norm, float inv, bool tap,
                                       float* xsm) {
@@ -769,22 +880,29 @@ __device__ inline void emit_pair_item(const GemvArgs& a, int64_t nch, int64_t it
     v.x = fmul_rn(fmul_rn(v.x, inv), vw.x); v.y = fmul_rn(fmul_rn(v.y, inv), vw.y);
     v.z = fmul_rn(fmul_rn(v.z, inv), vw.z); v.w = fmul_rn(fmul_rn(v.w, inv), vw.w);
   }
-  float m = 0.0f, psum = 0.0f;
+  constexpr bool two = pair_side<FMT>() == 4;  // the runs' sums kept apart
+  float m = 0.0f, pu = 0.0f, pv = 0.0f;
   if (valid) {
     m = fmaxf(fmaxf(fmaxf(fabsf(u.x), fabsf(u.y)), fmaxf(fabsf(u.z), fabsf(u.w))),
               fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
-    psum = ((u.x + u.y) + (u.z + u.w)) + ((v.x + v.y) + (v.z + v.w));
+    pu = (u.x + u.y) + (u.z + u.w);
+    pv = (v.x + v.y) + (v.z + v.w);
+    if constexpr (!two) { pu += pv; pv = 0.0f; }
   }
   // the chunk's four lanes (quad xor 1, 2) on DPP moves, not LDS permutes
   m = fmaxf(m, dpp_mov<0xB1>(m));
   m = fmaxf(m, dpp_mov<0x4E>(m));
-  psum += dpp_mov<0xB1>(psum);
-  psum += dpp_mov<0x4E>(psum);
+  pu += dpp_mov<0xB1>(pu);
+  pu += dpp_mov<0x4E>(pu);
+  if constexpr (two) {
+    pv += dpp_mov<0xB1>(pv);
+    pv += dpp_mov<0x4E>(pv);
+  }
   if (!valid) return;
-  const int64_t i0 = 8 * t + w;
+  const int64_t i0 = pair_run0<FMT>(t) + w;
   if (tap) {
     reinterpret_cast<float4*>(a.xtap)[i0] = u;
-    reinterpret_cast<float4*>(a.xtap)[i0 + 4] = v;
+    reinterpret_cast<float4*>(a.xtap)[i0 + pair_run1<FMT>()] = v;
   }
   // S = 2^sh with m * S in [2^14, 2^15) (m = m' * 2^e, m' in [0.5, 1), read from
   // the bits; the small margin covers rounding); c = 2^24 / S
@@ -792,19 +910,24 @@ __device__ inline void emit_pair_item(const GemvArgs& a, int64_t nch, int64_t it
   const int sh = (m > 0.0f) ? max(-100, min(100, 15 - e)) : 0;
   const float sl_ = pow2f(sh), sh_ = pow2f(sh - 4);
   uint32_t h0, l0, h1, l1, h2, l2, h3, l3;
-  split2(u.x * sl_, u.z * sl_, h0, l0);
-  split2(v.x * sh_, v.z * sh_, h1, l1);
-  split2(u.y * sl_, u.w * sl_, h2, l2);
-  split2(v.y * sh_, v.w * sh_, h3, l3);
+  // grids: run 0 scaled below 2^15 -> 16; run 1 (a further / 16) -> 1
+  split2<16>(u.x * sl_, u.z * sl_, h0, l0);
+  split2<1>(v.x * sh_, v.z * sh_, h1, l1);
+  split2<16>(u.y * sl_, u.w * sl_, h2, l2);
+  split2<1>(v.y * sh_, v.w * sh_, h3, l3);
   uint4* pl = reinterpret_cast<uint4*>(xsm);
   pl[(int64_t)(2 * w) * nch + t] = make_uint4(h0, h1, h2, h3);
   pl[(int64_t)(2 * w + 1) * nch + t] = make_uint4(l0, l1, l2, l3);
-  if (w == 0) reinterpret_cast<float2*>(pl + 8 * nch)[t] = make_float2(psum, pow2f(24 - sh));
+  if (w == 0) {
+    if constexpr (two) reinterpret_cast<float4*>(pl + 8 * nch)[t] = make_float4(pu, pv, pow2f(24 - sh), 0.0f);
+    else reinterpret_cast<float2*>(pl + 8 * nch)[t] = make_float2(pu, pow2f(24 - sh));
+  }
 }
 
 template <int FMT>
 __device__ inline void stage_pairs_finish(const GemvArgs& a, const float* xin, int64_t nch, const PairStage& ps,
                                           float* xsm, float* red) {
+  constexpr int R1 = pair_run1<FMT>();
   const int tid = threadIdx.x, nt = blockDim.x;
   const int64_t items = nch * 4;
   const float4* x4 = reinterpret_cast<const float4*>(xin);
@@ -827,8 +950,8 @@ __device__ inline void stage_pairs_finish(const GemvArgs& a, const float* xin, i
       }
     } else {
       for (int64_t it = tid; it < items; it += nt) {
-        const int64_t i0 = 8 * (it >> 2) + (it & 3);
-        const float4 u = x4[i0], v = x4[i0 + 4];
+        const int64_t i0 = pair_run0<FMT>(it >> 2) + (it & 3);
+        const float4 u = x4[i0], v = x4[i0 + R1];
         ss += (u.x * u.x + u.y * u.y) + (u.z * u.z + u.w * u.w) + (v.x * v.x + v.y * v.y) +
               (v.z * v.z + v.w * v.w);
       }
@@ -849,11 +972,11 @@ __device__ inline void stage_pairs_finish(const GemvArgs& a, const float* xin, i
       if (norm) {
         if (k < PBW && wregs) { uw = ps.wa[k < PBW ? k : 0]; vw = ps.wb[k < PBW ? k : 0]; }
         else if (it < items) {
-          const int64_t i0 = 8 * (it >> 2) + (it & 3);
-          uw = w4[i0]; vw = w4[i0 + 4];
+          const int64_t i0 = pair_run0<FMT>(it >> 2) + (it & 3);
+          uw = w4[i0]; vw = w4[i0 + R1];
         }
       }
-      emit_pair_item(a, nch, it, it < items, ps.xa[k], ps.xb[k], uw, vw, norm, inv, tap, xsm);
+      emit_pair_item<FMT>(a, nch, it, it < items, ps.xa[k], ps.xb[k], uw, vw, norm, inv, tap, xsm);
     }
   }
   // the rest (rows longer than PB * 4 * 32 * nt / 4 elements)
@@ -862,11 +985,11 @@ __device__ inline void stage_pairs_finish(const GemvArgs& a, const float* xin, i
     const bool valid = it < items;
     float4 u = one, v = one, uw = one, vw = one;
     if (valid) {
-      const int64_t i0 = 8 * (it >> 2) + (it & 3);
-      u = x4[i0]; v = x4[i0 + 4];
-      if (norm) { uw = w4[i0]; vw = w4[i0 + 4]; }
+      const int64_t i0 = pair_run0<FMT>(it >> 2) + (it & 3);
+      u = x4[i0]; v = x4[i0 + R1];
+      if (norm) { uw = w4[i0]; vw = w4[i0 + R1]; }
     }
-    emit_pair_item(a, nch, it, valid, u, v, uw, vw, norm, inv, tap, xsm);
+    emit_pair_item<FMT>(a, nch, it, valid, u, v, uw, vw, norm, inv, tap, xsm);
   }
   __syncthreads();
 }
@@ -1009,7 +1132,7 @@ __global__ void __launch_bounds__(W * 64) k_gemv(GemvArgs a) {
   const int pos = epi_pos<EPI>(a);
   const int g0 = (int)blockIdx.x - (PAIR ? 0 : seg.block0);
   // this half's staged input (the LDS holds one region per segment for EPI_ADD2)
-  const int64_t region = pair_fmt<FMT>() ? wk.nch * 34 : a.K;
+  const int64_t region = pair_fmt<FMT>() ? wk.nch * (32 + pair_side<FMT>()) : a.K;
   float* const xs = xsm + (PAIR ? half * region : 0);
   // groups g0, g0 + nblk, ... below ngroups (counts computed on the host)
   const int mine = (g0 < seg.ngroups) ? seg.gq + (g0 < seg.gr ? 1 : 0) : 0;
@@ -1343,9 +1466,10 @@ int pick_ksplit(const DevWeight& w) {
 }
 
 // Dynamic LDS of one block: the staged input (f32 planes, or f16 hi/lo pair
-// planes plus (sum, scale) per chunk for the pair formats).
+// planes plus side data per chunk for the pair formats).
 size_t lds_bytes(int type, int64_t K) {
   if (type == T_Q4_0 || type == T_Q4_1) return (size_t)(K / 32) * (128 + 8);
+  if (UAII_GEMV_KPAIR && (type == T_Q4_K || type == T_Q6_K)) return (size_t)(K / 32) * (128 + 16);
   return (size_t)K * sizeof(float);
 }
 

@@ -139,9 +139,26 @@ __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
 }
 __device__ __forceinline__ float pow2f(int k) { return __uint_as_float((uint32_t)(k + 127) << 23); }
 __device__ __forceinline__ uint32_t hbits(_Float16 h) { return (uint32_t)__builtin_bit_cast(uint16_t, h); }
+// (a, b) -> hi = (f16(a), f16(b)), lo = the rest in f16 (attention's q)
 __device__ __forceinline__ void split2(float a, float b, uint32_t& hi, uint32_t& lo) {
   const _Float16 ah = (_Float16)a, bh = (_Float16)b;
   const _Float16 al = (_Float16)(a - (float)ah), bl = (_Float16)(b - (float)bh);
+  hi = hbits(ah) | (hbits(bh) << 16);
+  lo = hbits(al) | (hbits(bl) << 16);
+}
+// hi = the nearest multiples of the grid G (|hi| / G <= 2048, exact in f16, so
+// the nibble * hi sums of a chunk are exact in f32), lo = the rest in f16
+template <int G>
+__device__ __forceinline__ float grid_round(float a) {
+  static_assert(G == 1 || G == 16, "grid 1 or 16");
+  if constexpr (G == 1) return rintf(a);
+  else return (a + 201326592.0f) - 201326592.0f;  // |a| < 2^26: the ulp of 1.5 * 2^27 is 16
+}
+template <int G>
+__device__ __forceinline__ void split2(float a, float b, uint32_t& hi, uint32_t& lo) {
+  const float ar = grid_round<G>(a), br = grid_round<G>(b);
+  const _Float16 ah = (_Float16)ar, bh = (_Float16)br;
+  const _Float16 al = (_Float16)(a - ar), bl = (_Float16)(b - br);
   hi = hbits(ah) | (hbits(bh) << 16);
   lo = hbits(al) | (hbits(bl) << 16);
 }
@@ -393,10 +410,10 @@ __device__ __forceinline__ void make_pairs(const float* v, XP& xp) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     uint32_t h0, l0, h1, l1, h2, l2, h3, l3;
-    split2(v[4 * i] * S, v[4 * i + 2] * S, h0, l0);
-    split2(v[16 + 4 * i] * S16, v[16 + 4 * i + 2] * S16, h1, l1);
-    split2(v[4 * i + 1] * S, v[4 * i + 3] * S, h2, l2);
-    split2(v[16 + 4 * i + 1] * S16, v[16 + 4 * i + 3] * S16, h3, l3);
+    split2<16>(v[4 * i] * S, v[4 * i + 2] * S, h0, l0);
+    split2<1>(v[16 + 4 * i] * S16, v[16 + 4 * i + 2] * S16, h1, l1);
+    split2<16>(v[4 * i + 1] * S, v[4 * i + 3] * S, h2, l2);
+    split2<1>(v[16 + 4 * i + 1] * S16, v[16 + 4 * i + 3] * S16, h3, l3);
     xp.p[2 * i] = make_uint4(h0, h1, h2, h3);
     xp.p[2 * i + 1] = make_uint4(l0, l1, l2, l3);
   }
