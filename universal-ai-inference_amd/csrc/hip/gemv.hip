@@ -722,12 +722,12 @@ __device__ inline void compute_unit(const Walk& wk, int step, int lane, const fl
 
 // Stage x (optionally RMS-normalised: x * (1/sqrt(mean(x^2)+eps)) * w, two
 // roundings per element as in norm.cpp:122-127) into LDS.
-template <int FMT>
+template <int FMT, int NT>
 __device__ inline void stage_x(const GemvArgs& a, const float* xin, int64_t nch, float* xsm, float* red) {
   // Loads are issued in unrolled batches of 4 float4 per thread so a block pays
   // one memory round trip per batch (a plain strided loop serialises them).
   constexpr int B = 4;
-  const int tid = threadIdx.x, nt = blockDim.x;
+  const int tid = threadIdx.x, nt = NT;  // threads per block
   const int nv = (int)(a.K / 4);
   const float4* x4 = reinterpret_cast<const float4*>(xin);
   const float4* w4 = reinterpret_cast<const float4*>(a.norm_w);
@@ -791,7 +791,7 @@ __device__ inline void stage_x(const GemvArgs& a, const float* xin, int64_t nch,
     __syncthreads();
     return;
   }
-  // RMSNorm with K > 4 * 4 * blockDim: second pass over LDS with batched weight loads
+  // RMSNorm with K > 4 * 4 * NT: second pass over LDS with batched weight loads
   ss = wave_sum_dpp(ss);
   if ((tid & 63) == 0) red[tid >> 6] = ss;
   __syncthreads();
@@ -836,10 +836,10 @@ struct PairStage {
   float4 wa[PBW], wb[PBW];
 };
 
-template <int FMT>
+template <int FMT, int NT>
 __device__ inline void stage_pairs_issue(const GemvArgs& a, const float* xin, int64_t nch, PairStage& ps) {
   constexpr int R1 = pair_run1<FMT>();
-  const int tid = threadIdx.x, nt = blockDim.x;
+  const int tid = threadIdx.x, nt = NT;  // threads per block
   const int64_t items = nch * 4;
   const float4* x4 = reinterpret_cast<const float4*>(xin);
   const float4* w4 = reinterpret_cast<const float4*>(a.norm_w);
@@ -924,11 +924,11 @@ __device__ inline void emit_pair_item(const GemvArgs& a, int64_t nch, int64_t it
   }
 }
 
-template <int FMT>
+template <int FMT, int NT>
 __device__ inline void stage_pairs_finish(const GemvArgs& a, const float* xin, int64_t nch, const PairStage& ps,
                                           float* xsm, float* red) {
   constexpr int R1 = pair_run1<FMT>();
-  const int tid = threadIdx.x, nt = blockDim.x;
+  const int tid = threadIdx.x, nt = NT;  // threads per block
   const int64_t items = nch * 4;
   const float4* x4 = reinterpret_cast<const float4*>(xin);
   const float4* w4 = reinterpret_cast<const float4*>(a.norm_w);
@@ -1081,9 +1081,9 @@ __device__ inline void epilogue(const GemvArgs& a, const GemvSeg& seg, int64_t l
   }
 }
 
+// The whole kernel for one format (the dynamic LDS, xsm, holds the staged input).
 template <int FMT, int EPI, int W>
-__global__ void __launch_bounds__(W * 64) k_gemv(GemvArgs a) {
-  extern __shared__ float xsm[];
+__device__ __forceinline__ void gemv_body(GemvArgs a, float* xsm) {
   __shared__ float red[2 * W];
   __shared__ float kred[2][W][RPW_MAX];
   __shared__ float bval[W];
@@ -1101,7 +1101,7 @@ __global__ void __launch_bounds__(W * 64) k_gemv(GemvArgs a) {
   // (for a pair format a row of K values is K / 32 chunks): the launch's input
   // is its first memory request, before the segment and group setup below.
   PairStage ps0;
-  if constexpr (pair_fmt<FMT>() && !PAIR) stage_pairs_issue<FMT>(a, a.x, a.K >> 5, ps0);
+  if constexpr (pair_fmt<FMT>() && !PAIR) stage_pairs_issue<FMT, W * 64>(a, a.x, a.K >> 5, ps0);
 
   // segment lookup (uniform per block; per half for EPI_ADD2)
   int si = 0;
@@ -1156,10 +1156,10 @@ __global__ void __launch_bounds__(W * 64) k_gemv(GemvArgs a) {
     for (int h = 0; h < 2; ++h) {
       if constexpr (pair_fmt<FMT>()) {
         PairStage ps;
-        stage_pairs_issue<FMT>(a, a.seg[h].x, wk.nch, ps);
-        stage_pairs_finish<FMT>(a, a.seg[h].x, wk.nch, ps, xsm + h * region, red);
+        stage_pairs_issue<FMT, W * 64>(a, a.seg[h].x, wk.nch, ps);
+        stage_pairs_finish<FMT, W * 64>(a, a.seg[h].x, wk.nch, ps, xsm + h * region, red);
       } else {
-        stage_x<FMT>(a, a.seg[h].x, wk.nch, xsm + h * region, red);
+        stage_x<FMT, W * 64>(a, a.seg[h].x, wk.nch, xsm + h * region, red);
       }
     }
     if constexpr (pair_fmt<FMT>())
@@ -1173,16 +1173,16 @@ __global__ void __launch_bounds__(W * 64) k_gemv(GemvArgs a) {
     // the launch against ~3 us, measured by per-wave clock stamps on the 8B
     // decode (gate/up 19.3 -> 17.9 us, LM head 61 -> 55 us, QKV unchanged;
     // 461 -> 471 tok/s).
-    stage_pairs_finish<FMT>(a, xin, wk.nch, ps0, xsm, red);
+    stage_pairs_finish<FMT, W * 64>(a, xin, wk.nch, ps0, xsm, red);
     if (nunits > 0) load_unit<FMT, EPI>(a, seg, ebase, wk, unit_l0(0), 0, lane, pos, U0);
   } else if constexpr (FMT == T_Q8_0) {
     // input first here too: 8B Q8_0 decode 368.4 -> 372.2 tok/s (QKV 13.0 -> 12.0
     // us); the same order for the K-quants measured slower (1B 935 -> 917 tok/s)
-    stage_x<FMT>(a, xin, wk.nch, xsm, red);
+    stage_x<FMT, W * 64>(a, xin, wk.nch, xsm, red);
     if (nunits > 0) load_unit<FMT, EPI>(a, seg, ebase, wk, unit_l0(0), 0, lane, pos, U0);
   } else {
     if (nunits > 0) load_unit<FMT, EPI>(a, seg, ebase, wk, unit_l0(0), 0, lane, pos, U0);
-    stage_x<FMT>(a, xin, wk.nch, xsm, red);
+    stage_x<FMT, W * 64>(a, xin, wk.nch, xsm, red);
   }
 
   float best_v = -INFINITY;
@@ -1298,6 +1298,25 @@ __global__ void __launch_bounds__(W * 64) k_gemv(GemvArgs a) {
   }
 }
 
+template <int FMT, int EPI, int W>
+__global__ void __launch_bounds__(W * 64) k_gemv(GemvArgs a) {
+  extern __shared__ float xsm[];
+  gemv_body<FMT, EPI, W>(a, xsm);
+}
+
+// Segments of two formats in one launch (a QKV whose V projection is stored in
+// another format, as in Q4_K_M files: Q4_K Q/K, Q6_K V). Blocks belong to one
+// segment, so each block stages and walks in its own segment's format; the
+// per-format launches this replaces each paid their own ramp and input staging.
+template <int FA, int FB, int EPI, int W>
+__global__ void __launch_bounds__(W * 64) k_gemv_mix(GemvArgs a) {
+  extern __shared__ float xsm[];
+  int si = 0;
+  for (int k = 1; k < a.nseg; ++k) if ((int)blockIdx.x >= a.seg[k].block0) si = k;
+  if (a.seg[si].w.type == FB) gemv_body<FB, EPI, W>(a, xsm);
+  else gemv_body<FA, EPI, W>(a, xsm);
+}
+
 // Final greedy argmax over the LM-head block partials (lowest index wins ties,
 // sampling.cpp:38-50), then the token advance: inside the prompt the next token
 // is the prompt's, afterwards the argmax (session.cpp:1006-1044).
@@ -1392,6 +1411,12 @@ KernelFn pick(int epi, int type, int w) {
   }
 }
 
+// The two-format kernel: QKV with Q4_K and Q6_K segments.
+KernelFn pick_mix(int epi, int w) {
+  if (epi == EPI_QKV && w == WPB_QKV) return k_gemv_mix<T_Q4_K, T_Q6_K, EPI_QKV, WPB_QKV>;
+  return nullptr;
+}
+
 // Waves per block for a launch of epilogue `epi` whose rows split K over `ks` waves.
 int pick_waves(int epi, int ks) {
   if (epi == EPI_ADD2) return WPB_LONG;
@@ -1411,10 +1436,14 @@ hipError_t prepare_gemv() {
                        T_Q5_1, T_Q5_K, T_Q2_K, T_Q3_K, T_F32,  T_F16};
   const int lim = lds_limit();
   for (int e : epis) {
-    for (int t : types) {
-      for (int w : {WPB, WPB_QKV, WPB_SWIGLU, WPB_LONG}) {
+    for (int w : {WPB, WPB_QKV, WPB_SWIGLU, WPB_LONG}) {
+      for (int t : types) {
         const KernelFn fn = pick(e, t, w);
         if (!fn) continue;
+        (void)hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, lim - 1024);
+        (void)hipGetLastError();
+      }
+      if (const KernelFn fn = pick_mix(e, w)) {
         (void)hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, lim - 1024);
         (void)hipGetLastError();
       }
@@ -1484,13 +1513,22 @@ struct Plan {
 
 // Blocks per segment: one per row group, capped at what stays resident (the
 // rest loop), shared out by group count.
+// Segments of a run in more than one format (the two-format kernel's case).
+bool mixed_run(const GemvArgs& a) {
+  for (int k = 1; k < a.nseg; ++k)
+    if (a.seg[k].w.type != a.seg[0].w.type) return true;
+  return false;
+}
+
 Plan make_plan(const GemvArgs& a) {
   Plan p;
   const bool pair = a.epi == EPI_ADD2;  // two segments over the same rows, one staged input each
+  const bool mix = mixed_run(a);
   p.lds = (pair ? 2 : 1) * lds_bytes(a.seg[0].w.type, a.K);
+  for (int k = 1; k < a.nseg; ++k) p.lds = std::max(p.lds, lds_bytes(a.seg[k].w.type, a.K));
   p.ks = pick_ksplit(a.seg[0].w);
   p.waves = pick_waves(a.epi, p.ks);
-  p.fn = pick(a.epi, a.seg[0].w.type, p.waves);
+  p.fn = mix ? pick_mix(a.epi, p.waves) : pick(a.epi, a.seg[0].w.type, p.waves);
   if (!p.fn) return p;
   const int rpg = (p.waves / (pair ? 2 : 1) / p.ks) * rpw_of(a.seg[0].w.type);
   if (pair) {
@@ -1521,14 +1559,26 @@ Plan make_plan(const GemvArgs& a) {
   return p;
 }
 
+// Whether segments of types ta and tb (the same K) share the two-format kernel:
+// Q4_K and Q6_K, whose chunks (16 payload bytes, 32 inputs), rows per wave and
+// staged-input side data agree.
+bool mix_pair(int epi, int ta, int tb) {
+  auto kq = [](int t) { return t == T_Q4_K || t == T_Q6_K; };
+  return UAII_GEMV_KPAIR && epi == EPI_QKV && kq(ta) && kq(tb);
+}
+
 // Runs of consecutive segments sharing a weight type: one launch each (the
-// kernel is specialised per type), so QKV with mixed types takes several.
+// kernel is specialised per type), so QKV with mixed types takes several, apart
+// from the mixes the two-format kernel covers.
 template <typename F>
 hipError_t for_each_run(const GemvArgs& in, F&& f) {
   int k0 = 0;
   while (k0 < in.nseg) {
     int k1 = k0 + 1;
-    while (k1 < in.nseg && in.seg[k1].w.type == in.seg[k0].w.type) ++k1;
+    while (k1 < in.nseg && (in.seg[k1].w.type == in.seg[k0].w.type ||
+                            (mix_pair(in.epi, in.seg[k0].w.type, in.seg[k1].w.type) &&
+                             in.seg[k1].w.a_row == in.seg[k0].w.a_row)))
+      ++k1;
     GemvArgs a = in;
     a.nseg = k1 - k0;
     for (int k = 0; k < a.nseg; ++k) a.seg[k] = in.seg[k0 + k];
