@@ -1382,38 +1382,52 @@ __global__ void __launch_bounds__(256) k_pf_moe_route(const float* __restrict__ 
   }
 }
 
-// One block. Thread e counts and lists expert e's (token, slot) entries in
-// token order; thread 0 forms the prefix sums between the two passes.
+// One block lists each expert's (token, slot) entries in entry order (entry
+// i = token * k + slot): counts[e], offsets[e] (exclusive prefix), list[pos] =
+// token and inv[i] = pos. Wave w owns the entry range [w n / 4, (w + 1) n / 4):
+// range counts by LDS atomics, then each wave walks its range 64 entries at a
+// time, a lane's position within its expert being the number of same-expert
+// lanes below it (ballot + popcount) past the range's running base.
 __global__ void __launch_bounds__(256) k_pf_moe_lists(const int32_t* __restrict__ ids, int64_t M, int k,
                                                       int E, int32_t* counts, int32_t* offsets,
                                                       int32_t* list, int32_t* inv) {
-  __shared__ int32_t cnt[256], off[256];
-  const int e = threadIdx.x;
+  __shared__ int32_t cnt[4][256], base[4][256];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t n = M * k;
-  if (e < E) {
-    int32_t c = 0;
-    for (int64_t i = 0; i < n; ++i) c += (ids[i] == e) ? 1 : 0;
-    cnt[e] = c;
-  }
+  const int64_t per = (n + 3) / 4;
+  const int64_t r0 = min(n, (int64_t)wave * per), r1 = min(n, r0 + per);
+  for (int j = tid; j < 4 * 256; j += 256) cnt[j >> 8][j & 255] = 0;
   __syncthreads();
-  if (e == 0) {
+  for (int64_t i = r0 + lane; i < r1; i += 64) atomicAdd(&cnt[wave][ids[i]], 1);
+  __syncthreads();
+  if (tid == 0) {
     int32_t acc = 0;
-    for (int j = 0; j < E; ++j) {
-      off[j] = acc;
-      acc += cnt[j];
+    for (int e = 0; e < E; ++e) {
+      counts[e] = cnt[0][e] + cnt[1][e] + cnt[2][e] + cnt[3][e];
+      offsets[e] = acc;
+      for (int r = 0; r < 4; ++r) {
+        base[r][e] = acc;
+        acc += cnt[r][e];
+      }
     }
   }
   __syncthreads();
-  if (e < E) {
-    counts[e] = cnt[e];
-    offsets[e] = off[e];
-    int32_t pos = off[e];
-    for (int64_t i = 0; i < n; ++i) {
-      if (ids[i] == e) {
+  for (int64_t g = r0; g < r1; g += 64) {
+    const int64_t i = g + lane;
+    const bool act = i < r1;
+    const int x = act ? ids[i] : -1;
+    uint64_t pending = __ballot(act);
+    while (pending) {
+      const int e0 = __shfl(x, __ffsll((long long)pending) - 1, 64);  // wave-uniform
+      const uint64_t m = __ballot(x == e0) & pending;
+      const int32_t b = base[wave][e0];
+      if (x == e0) {
+        const int32_t pos = b + __popcll(m & ((1ull << lane) - 1ull));
         list[pos] = (int32_t)(i / k);
         inv[i] = pos;
-        ++pos;
       }
+      if (lane == 0) base[wave][e0] = b + __popcll(m);
+      pending &= ~m;
     }
   }
 }
