@@ -1253,6 +1253,67 @@ __global__ void __launch_bounds__(256, 2) k_pf_attn(PfAttnArgs a) {
 
 // ---- MoE over prompt rows ----------------------------------------------------------------
 
+// Routing of token t on one wave from its E router logits (LDS): softmax
+// (exp(l - max) * 1/sum), k rounds of the largest remaining probability (ties:
+// the lower expert), weights renormalised over the chosen k
+// (transformer.cpp:446-481, :565-580).
+__device__ inline void moe_topk(const float* logit, int E, int k, int32_t* __restrict__ ids,
+                                float* __restrict__ wout, int64_t t, int lane) {
+  float p[4];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int e = lane + 64 * j;
+    p[j] = e < E ? logit[e] : -INFINITY;
+    mx = fmaxf(mx, p[j]);
+  }
+  mx = wave_max(mx);
+  float sum = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int e = lane + 64 * j;
+    p[j] = e < E ? expf(p[j] - mx) : 0.0f;
+    sum += p[j];
+  }
+  sum = wave_sum(sum);
+  const float isum = sum > 0.0f ? 1.0f / sum : 0.0f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) p[j] = (lane + 64 * j < E) ? p[j] * isum : -1.0f;
+  float mass = 0.0f;
+  float wsel[8];
+  int32_t esel[8];
+  for (int q = 0; q < k; ++q) {
+    float bv = -1.0f;
+    int be = 0x7fffffff;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (p[j] > bv) { bv = p[j]; be = lane + 64 * j; }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const float ov = __shfl_xor(bv, o, 64);
+      const int oe = __shfl_xor(be, o, 64);
+      if (ov > bv || (ov == bv && oe < be)) { bv = ov; be = oe; }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (lane + 64 * j == be) p[j] = -1.0f;  // taken
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (j == q) { wsel[j] = bv; esel[j] = (be >= 0 && be < E) ? be : 0; }
+    mass += bv;
+  }
+  if (!(mass > 0.0f)) mass = 1.0f;
+  if (lane == 0) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if (j < k) {
+        ids[t * k + j] = esel[j];
+        wout[t * k + j] = wsel[j] / mass;
+      }
+    }
+  }
+}
+
 // One block per token: RMSNorm of x[t] (the k_pf_prep arithmetic), router
 // logits against F32 / F16 rows, then the routing of k_moe_route on wave 0:
 // softmax (exp(l - max) * 1/sum), k rounds of the largest remaining probability
@@ -1326,60 +1387,101 @@ __global__ void __launch_bounds__(256) k_pf_moe_route(const float* __restrict__ 
     if (lane == 0) logit[e] = acc;
   }
   __syncthreads();
-  if (wave != 0) return;
-  float p[4];
-  float mx = -INFINITY;
+  if (wave == 0) moe_topk(logit, E, k, ids, wout, t, lane);
+}
+
+// The same routing for one token (the decode step) on a 16-wave block: the
+// router row of expert e is cut into P parts of up to 512 float4 (8 per lane),
+// wave w takes the parts w, w + 16, ..., and its first part's router loads are
+// issued before the RMSNorm, so the weight fetch overlaps the input's. The
+// parts' sums are added in part order. dynamic LDS: K normalised inputs, then
+// the E * P part sums.
+template <int RT>
+__global__ void __launch_bounds__(1024) k_moe_route_dec(const float* __restrict__ x, int64_t K,
+                                                        const float* __restrict__ norm_w, float eps,
+                                                        DevWeight router, int E, int k,
+                                                        int32_t* __restrict__ ids, float* __restrict__ wout) {
+  extern __shared__ float row[];
+  __shared__ float red[16];
+  __shared__ float logit[256];
+  constexpr int RB = 8;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nv = (int)(K / 4);
+  const int P = (nv + 64 * RB - 1) / (64 * RB);
+  const int items = E * P;
+  float* psum = row + K;
+  using Raw = typename std::conditional<RT == T_F32, float4, uint2>::type;
+  auto load_item = [&](int it, Raw (&wv)[RB]) __attribute__((always_inline)) {
+    const int e = it / P, part = it % P;
+    const Raw* wr = reinterpret_cast<const Raw*>(router.a + (int64_t)e * router.a_row);
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int e = lane + 64 * j;
-    p[j] = e < E ? logit[e] : -INFINITY;
-    mx = fmaxf(mx, p[j]);
-  }
-  mx = wave_max(mx);
-  float sum = 0.0f;
+    for (int j = 0; j < RB; ++j) wv[j] = wr[min(part * 64 * RB + 64 * j + lane, nv - 1)];
+  };
+  auto dot_item = [&](int it, const Raw (&wv)[RB]) __attribute__((always_inline)) {
+    const int part = it % P;
+    const float4* r4 = reinterpret_cast<const float4*>(row);
+    float acc = 0.0f;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int e = lane + 64 * j;
-    p[j] = e < E ? expf(p[j] - mx) : 0.0f;
-    sum += p[j];
-  }
-  sum = wave_sum(sum);
-  const float isum = sum > 0.0f ? 1.0f / sum : 0.0f;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) p[j] = (lane + 64 * j < E) ? p[j] * isum : -1.0f;
-  float mass = 0.0f;
-  float wsel[8];
-  int32_t esel[8];
-  for (int q = 0; q < k; ++q) {
-    float bv = -1.0f;
-    int be = 0x7fffffff;
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      if (p[j] > bv) { bv = p[j]; be = lane + 64 * j; }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      const float ov = __shfl_xor(bv, o, 64);
-      const int oe = __shfl_xor(be, o, 64);
-      if (ov > bv || (ov == bv && oe < be)) { bv = ov; be = oe; }
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      if (lane + 64 * j == be) p[j] = -1.0f;  // taken
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-      if (j == q) { wsel[j] = bv; esel[j] = (be >= 0 && be < E) ? be : 0; }
-    mass += bv;
-  }
-  if (!(mass > 0.0f)) mass = 1.0f;
-  if (lane == 0) {
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      if (j < k) {
-        ids[t * k + j] = esel[j];
-        wout[t * k + j] = wsel[j] / mass;
+    for (int j = 0; j < RB; ++j) {
+      const int i = part * 64 * RB + 64 * j + lane;
+      if (i < nv) {
+        float4 w;
+        if constexpr (RT == T_F32) {
+          w = wv[j];
+        } else {
+          w = make_float4(h2f((uint16_t)(wv[j].x & 0xffff)), h2f((uint16_t)(wv[j].x >> 16)),
+                          h2f((uint16_t)(wv[j].y & 0xffff)), h2f((uint16_t)(wv[j].y >> 16)));
+        }
+        const float4 xv = r4[i];
+        acc += xv.x * w.x + xv.y * w.y + xv.z * w.z + xv.w * w.w;
       }
     }
+    acc = wave_sum(acc);
+    if (lane == 0) psum[it] = acc;
+  };
+  Raw w0[RB];
+  if (wave < items) load_item(wave, w0);
+  // RMSNorm (the k_pf_prep arithmetic) into LDS
+  float4* r4 = reinterpret_cast<float4*>(row);
+  const float4* x4 = reinterpret_cast<const float4*>(x);
+  float ss = 0.0f;
+  for (int i = tid; i < nv; i += 1024) {
+    const float4 v = x4[i];
+    r4[i] = v;
+    ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
   }
+  ss = wave_sum(ss);
+  if (lane == 0) red[wave] = ss;
+  __syncthreads();
+  float tot = 0.0f;
+#pragma unroll
+  for (int w = 0; w < 16; ++w) tot += red[w];
+  const float inv = 1.0f / sqrtf(tot / (float)K + eps);
+  const float4* n4 = reinterpret_cast<const float4*>(norm_w);
+  for (int i = tid; i < nv; i += 1024) {
+    float4 v = r4[i];
+    const float4 w = n4[i];
+    v.x = fmul_rn(fmul_rn(v.x, inv), w.x);
+    v.y = fmul_rn(fmul_rn(v.y, inv), w.y);
+    v.z = fmul_rn(fmul_rn(v.z, inv), w.z);
+    v.w = fmul_rn(fmul_rn(v.w, inv), w.w);
+    r4[i] = v;
+  }
+  __syncthreads();
+  if (wave < items) dot_item(wave, w0);
+  for (int it = wave + 16; it < items; it += 16) {
+    Raw wv[RB];
+    load_item(it, wv);
+    dot_item(it, wv);
+  }
+  __syncthreads();
+  if (wave != 0) return;
+  for (int e = lane; e < E; e += 64) {
+    float l = 0.0f;
+    for (int q = 0; q < P; ++q) l += psum[e * P + q];
+    logit[e] = l;
+  }
+  moe_topk(logit, E, k, ids, wout, 0, lane);
 }
 
 // One block lists each expert's (token, slot) entries in entry order (entry
@@ -1667,6 +1769,23 @@ hipError_t launch_pf_moe_route(const float* x, int64_t M, int64_t K, const float
   if (M <= 0 || K % 4 || !norm_w || E < 1 || E > 256 || k < 1 || k > 8 || k > E ||
       router.rows < E || router.cols != K || !pf_router_supported(router.type))
     return hipErrorInvalidValue;
+  if (M == 1) {
+    // the decode step: the 16-wave kernel
+    const int64_t P = (K / 4 + 511) / 512;
+    const size_t lds1 = (size_t)(K + E * P) * 4;
+    if ((int64_t)lds1 > lds_limit()) return hipErrorInvalidValue;
+    const void* fn = router.type == T_F32 ? reinterpret_cast<const void*>(&k_moe_route_dec<T_F32>)
+                                          : reinterpret_cast<const void*>(&k_moe_route_dec<T_F16>);
+    if (lds1 > 64 * 1024) {
+      const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds1);
+      if (e != hipSuccess) return e;
+    }
+    if (router.type == T_F32)
+      UAII_LAUNCH(k_moe_route_dec<T_F32>, dim3(1), dim3(1024), lds1, s, x, K, norm_w, eps, router, E, k, ids, w);
+    else
+      UAII_LAUNCH(k_moe_route_dec<T_F16>, dim3(1), dim3(1024), lds1, s, x, K, norm_w, eps, router, E, k, ids, w);
+    return hipGetLastError();
+  }
   const size_t lds = (size_t)K * 4;
   if ((int64_t)lds > lds_limit()) return hipErrorInvalidValue;
   if (router.type == T_F32) {
