@@ -1298,8 +1298,12 @@ __device__ __forceinline__ void gemv_body(GemvArgs a, float* xsm) {
   }
 }
 
+// 8-wave blocks (QKV) ask for 4 waves per SIMD, i.e. two blocks per CU: Q4_K
+// took 130 VGPRs and held one block per CU; capped at 128 (2 spilled) the
+// Mixtral-shape QKV ran 12.8 -> 9.6 us. The two-format kernel keeps its 132:
+// capped, its 6 spills made the 1B QKV slower.
 template <int FMT, int EPI, int W>
-__global__ void __launch_bounds__(W * 64) k_gemv(GemvArgs a) {
+__global__ void __launch_bounds__(W * 64, W == 8 ? 4 : 1) k_gemv(GemvArgs a) {
   extern __shared__ float xsm[];
   gemv_body<FMT, EPI, W>(a, xsm);
 }
