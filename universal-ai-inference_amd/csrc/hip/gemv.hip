@@ -9,8 +9,10 @@
 //
 // Work decomposition: a block is WPB waves; each wave owns RPW output rows and
 // walks their split-layout payload in 16-byte chunks, lane l taking chunks
-// l, l+64, ... . The input vector is staged once per block in LDS as f32 (after
-// the optional RMSNorm), each lane reads the x values of its chunk once and
+// l, l+64, ... . The input vector is staged once per block in LDS (after the
+// optional RMSNorm): as f32, or for the f16-pair formats (Q4_0, Q4_1, Q4_K,
+// Q6_K) as f16 hi/lo pairs in the order the nibble masks produce, with a
+// power-of-two scale per chunk. Each lane reads the x values of its chunk once and
 // reuses them for all RPW rows, and the per-chunk sum of x folds the
 // quantization offsets/mins out of the inner loop. Partial dots are reduced with
 // 64-lane xor shuffles (DPP on CDNA4).
