@@ -240,6 +240,11 @@ PREFILL_CFGS = {
                                     vocab=700, ctx_len=512, type_default=uaii_amd.Q4_0,
                                     n_experts=8, top_k=2, router_std=1.0 / 16, shared_ffn=192,
                                     seed=46),
+    # MoE 32 experts top-4: a 64-entry group of the token lists spans many
+    # experts, so the per-expert ranking takes several rounds per group
+    "moe_wide": synth.ModelConfig(n_layers=2, dim=256, n_heads=4, n_kv_heads=2, ffn=128,
+                                  vocab=700, ctx_len=512, type_default=uaii_amd.Q4_0,
+                                  n_experts=32, top_k=4, router_std=1.0 / 16, seed=47),
 }
 
 
@@ -263,7 +268,7 @@ def test_generate_with_prefill(name):
         assert maxrel(r2[li], want["resid2"][li]) < 2e-3
 
 
-@pytest.mark.parametrize("name", ["moe_k", "moe_shared"])
+@pytest.mark.parametrize("name", ["moe_k", "moe_shared", "moe_wide"])
 def test_moe_prefill_long_prompt(name):
     """A 400-token prompt: each expert's gathered rows span several row tiles
     of the grouped expert GEMMs, the last one partial."""
