@@ -134,6 +134,29 @@ def test_gemv_pair_formats_unbiased(hip, t):
     assert abs((got - want).mean()) / scale < 1e-6
 
 
+@pytest.mark.parametrize("t", [uaii_amd.Q4_0, uaii_amd.Q4_1, uaii_amd.Q4_K, uaii_amd.Q6_K],
+                         ids=lambda t: uaii_amd.TYPE_NAMES[t])
+def test_gemv_pair_formats_chunk_scales(hip, t):
+    """The f16-pair GEMV scales each 32-input chunk by its own power of two: chunks
+    from 1e-20 to 1e20 and all-zero chunks in one input (no chunk's scale may
+    overflow, underflow or poison the sum). The error is measured against the
+    largest output, which the 1e20 chunks dominate, so the small chunks are only
+    held to finiteness here; their own precision is what the other GEMV tests
+    check at unit scale."""
+    rows, cols = 64, 2048
+    p = random_packed(t, rows, cols, seed=51)
+    x = synth.normals(52, 1, 0, cols, 1.0).astype(np.float64)
+    rng = np.random.default_rng(53)
+    expo = rng.integers(-20, 21, cols // 32)
+    expo[::7] = -99  # all-zero chunks
+    scale = np.where(expo == -99, 0.0, 10.0 ** expo.astype(np.float64))
+    x = (x.reshape(-1, 32) * scale[:, None]).reshape(-1).astype(np.float32)
+    got = run_gemv(hip, t, rows, cols, x, p)
+    want = oracle.quant_gemm(t, x, p, rows)[0]
+    assert np.all(np.isfinite(got))
+    assert maxrel(got, want) < 2e-5
+
+
 @pytest.mark.parametrize("t", [uaii_amd.Q4_0, uaii_amd.Q8_0, uaii_amd.Q4_K, uaii_amd.Q6_K],
                          ids=lambda t: uaii_amd.TYPE_NAMES[t])
 @pytest.mark.parametrize("shape", [(4096, 4096), (4096, 14336), (14336, 4096)],
