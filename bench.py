@@ -266,7 +266,10 @@ def main() -> int:
         sess.step_async(True)
         sess.sync()
         prefill_s = time.perf_counter() - t0
-        prefill["method"] = "matrix cores (MFMA), 1024-token chunks"
+        # the chunk DecoderProgram::prefill uses: 1024 rows, or UAII_PREFILL_CHUNK (at least 16)
+        env_chunk = os.environ.get("UAII_PREFILL_CHUNK")
+        chunk = max(16, int(env_chunk)) if env_chunk else 1024
+        prefill["method"] = f"matrix cores (MFMA), {min(chunk, n_prompt - 1)}-token chunks"
         if not args.no_profile:
             # the same prefill profiled per kernel; it rebuilds the same KV state
             sess.begin(prompt, ctx)

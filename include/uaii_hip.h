@@ -79,7 +79,9 @@ UAII_HIP_API int uaii_hip_gemv_swiglu(const uaii_hip_weight* wg, const uaii_hip_
 /* M > 1: y[i][:] = W . x[i][:] for i < m (x [m][cols], y [m][rows]). Q4_0, Q8_0,
  * Q4_K and Q6_K run on the matrix cores (weights decoded to their exact small
  * integers, x split into f16 hi + lo, block scales applied to the f32 partials);
- * other formats run one GEMV per row. */
+ * other formats run one GEMV per row. Q4_0 and Q8_0 need m (rounded up to 64)
+ * * cols * 2 < 2^31 (their kernels address the f16 activation rows by 32-bit
+ * byte offsets); larger calls return hipErrorInvalidValue. */
 UAII_HIP_API int uaii_hip_gemm(const uaii_hip_weight* w, const float* x, int64_t m, float* y,
                                void* stream);
 UAII_HIP_API int uaii_hip_gemm_rmsnorm(const uaii_hip_weight* w, const float* x, int64_t m,

@@ -10,6 +10,9 @@ restatement; it is optional at run time.
 
 Parity status per oracle function (what pins it):
   orc_half_to_float      exhaustive 65536-value check vs numpy float16 + _ref
+  orc_float_to_half      every float32 bit pattern vs numpy float16 (IEEE round to
+                         nearest even), closed-form ties / subnormals / overflow;
+                         with orc_half_to_float this pins orc_generate's kv_f16 mode
   orc_dequant_row        reference Q4_0 known-answer block, hand-built closed-form
                          blocks for every format, synth round-trip bounds, _ref
   orc_load_row_f32       _ref's gguf_load_tensor_f32 (the reference loader itself)
@@ -58,6 +61,10 @@ def oracle():
         vp, i64, f = C.c_void_p, C.c_int64, C.POINTER(C.c_float)
         L.orc_half_to_float.restype = C.c_float
         L.orc_half_to_float.argtypes = [C.c_uint16]
+        L.orc_float_to_half.restype = C.c_uint16
+        L.orc_float_to_half.argtypes = [C.c_float]
+        L.orc_float_to_half_n.restype = None
+        L.orc_float_to_half_n.argtypes = [vp, vp, i64]
         L.orc_row_bytes.restype = C.c_size_t
         L.orc_row_bytes.argtypes = [C.c_int, i64]
         L.orc_dequant_row.restype = C.c_int
@@ -142,6 +149,8 @@ def ref():
                                     C.POINTER(i64), f, f]
         L.uref_generate_path_a.restype = C.c_int
         L.uref_generate_path_a.argtypes = L.uref_generate.argtypes
+        L.uref_generate_kv16.restype = C.c_int
+        L.uref_generate_kv16.argtypes = L.uref_generate.argtypes
         L.uref_load_tensor_f32.restype = C.c_int
         L.uref_load_tensor_f32.argtypes = [C.c_char_p, C.c_char_p, f, i64, C.POINTER(i64)]
         _r = L
@@ -266,9 +275,11 @@ class Model:
 
 
 def ref_generate(path: str, prompt, max_new: int, max_layers: int = 0, n_layers: int = 0,
-                 dim: int = 0, vocab: int = 0, path_a: bool = False):
+                 dim: int = 0, vocab: int = 0, path_a: bool = False, kv_f16: bool = False):
     """Greedy generate through the reference's compiled kernels (needs _ref);
-    path_a=True loads every weight with the reference's gguf_load_tensor_f32."""
+    path_a=True loads every weight with the reference's gguf_load_tensor_f32;
+    kv_f16=True rounds K and V to fp16 (the CPU's F16C conversion) before the
+    reference's attention and cache append."""
     import numpy as np
     R = ref()
     if R is None:
@@ -278,7 +289,7 @@ def ref_generate(path: str, prompt, max_new: int, max_layers: int = 0, n_layers:
     n = C.c_int64()
     logits = np.zeros(max(vocab, 1), np.float32)
     resid2 = np.zeros(max(n_layers * dim, 1), np.float32)
-    fn = R.uref_generate_path_a if path_a else R.uref_generate
+    fn = R.uref_generate_path_a if path_a else (R.uref_generate_kv16 if kv_f16 else R.uref_generate)
     rc = fn(str(path).encode(), max_layers, p.ctypes.data_as(C.POINTER(C.c_int64)),
                          len(p), max_new, out.ctypes.data_as(C.POINTER(C.c_int64)), C.byref(n),
                          _fp(logits) if vocab else None, _fp(resid2) if n_layers else None)

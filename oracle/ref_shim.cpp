@@ -20,6 +20,8 @@
 #include "uaii/kernels/quant_gemm.hpp"
 #include "uaii/quant/gguf_dequant.hpp"
 #include "uaii/runtime/kv_cache.hpp"
+
+#include <immintrin.h>
 #include "uaii/runtime/sampling.hpp"
 
 extern "C" {
@@ -252,12 +254,20 @@ Error matmul(const TensorView& x, const Weight& w, TensorView* y) {
 // gguf.cpp:935-1209.
 constexpr int NW = 19;  // weights per layer bound by RefRunner
 
+// Each value through IEEE binary16 and back, round to nearest even, on the
+// CPU's own conversion instructions (F16C, compiled for this function only):
+// the fp16 KV cache mirror, independent of the oracle's integer conversion.
+__attribute__((target("f16c"))) void round_f16_hw(float* p, std::int64_t n) {
+  for (std::int64_t i = 0; i < n; ++i) p[i] = _cvtsh_ss(_cvtss_sh(p[i], _MM_FROUND_TO_NEAREST_INT));
+}
+
 struct RefRunner {
   orc_model* m = nullptr;
   std::int64_t L = 0, D = 0, H = 0, HKV = 0, hd = 0, V = 0, E = 0, topk = 0, rope_mode = 0,
                ctx = 0, qd = 0, kvd = 0, ff = 1;
   float theta = 0.f, eps = 0.f;
   bool path_a = false;
+  bool kv_f16 = false;  // K (after RoPE) and V rounded to fp16 before attention and the append
   loaders::GgufFile gf;
   Weight emb, onorm, lm;
   std::vector<Weight> W;
@@ -355,6 +365,11 @@ struct RefRunner {
                                     static_cast<int>(rope_mode))).ok()) return err;
       if (!(err = kernels::rope_f32(kk, nullptr, &kr->view, theta, hd,
                                     static_cast<int>(rope_mode))).ok()) return err;
+      if (kv_f16) {
+        // the fp16 cache holds the current token's K and V as every past one's
+        round_f16_hw(kr->f32.data(), kvd);
+        round_f16_hw(static_cast<float*>(vv.data), kvd);
+      }
       // Attention with the active KV cache (dispatch.cpp:219-231)
       TensorView pk = kv.k_view(li), pv = kv.v_view(li);
       err = kernels::attention_kv_f32(qr->view, kr->view, vv, &att->view, static_cast<int>(H), 0.0f,
@@ -435,10 +450,11 @@ namespace {
 int generate_with(const char* path, int max_layers, const std::int64_t* prompt,
                   std::int64_t n_prompt, std::int64_t max_new, const runtime::SampleParams& sp,
                   std::int64_t* out, std::int64_t* out_n, float* taps_logits, float* taps_resid2,
-                  bool path_a = false) {
+                  bool path_a = false, bool kv_f16 = false) {
   RefRunner R;
   Error err = R.open(path, max_layers, 0, n_prompt + max_new, n_prompt, path_a);
   if (!err.ok()) { g_err = err.message(); return -1; }
+  R.kv_f16 = kv_f16;
   std::vector<std::int64_t> hist;
   std::mt19937_64 rng{0};
   if (sp.has_seed) rng.seed(sp.seed);
@@ -494,6 +510,16 @@ int uref_generate_path_a(const char* path, int max_layers, const std::int64_t* p
                          std::int64_t* out_n, float* taps_logits, float* taps_resid2) {
   return generate_with(path, max_layers, prompt, n_prompt, max_new, runtime::SampleParams{}, out,
                        out_n, taps_logits, taps_resid2, true);
+}
+
+// Greedy generate through the reference kernels with K and V rounded to fp16
+// (hardware conversion) before attention and the cache append: the reference's
+// own attention and cache over the values an fp16 KV cache holds.
+int uref_generate_kv16(const char* path, int max_layers, const std::int64_t* prompt,
+                       std::int64_t n_prompt, std::int64_t max_new, std::int64_t* out,
+                       std::int64_t* out_n, float* taps_logits, float* taps_resid2) {
+  return generate_with(path, max_layers, prompt, n_prompt, max_new, runtime::SampleParams{}, out,
+                       out_n, taps_logits, taps_resid2, false, true);
 }
 
 // One whole GGUF tensor through the reference's f32 load (gguf.cpp:445-556).

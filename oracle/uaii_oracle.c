@@ -975,8 +975,12 @@ typedef struct {
   float *x, *n1, *q, *k, *v, *att, *tmp, *g, *u, *hid, *logits, *probs, *eout;
 } orc_state;
 
-static float round_f16(float f) {
-  /* float -> half (round to nearest even) -> float, for the fp16 cache mirror */
+/* float -> half bits, round to nearest even (IEEE 754 binary16): the value the
+ * fp16 KV cache holds for each cached K/V element. Overflow goes to +-inf, values
+ * below half the smallest subnormal to a signed zero, NaN stays NaN (quiet, sign
+ * kept). Pinned by tests/test_oracle_f16.py against numpy's IEEE conversion on
+ * every float32 bit pattern and by closed-form ties, subnormals and overflows. */
+uint16_t orc_float_to_half(float f) {
   uint32_t b;
   memcpy(&b, &f, 4);
   uint32_t sign = (b >> 16) & 0x8000u;
@@ -1004,8 +1008,15 @@ static float round_f16(float f) {
     if (rem > 0x1000u || (rem == 0x1000u && (hm & 1))) hv++;
     h = (uint16_t)hv;
   }
-  return orc_half_to_float(h);
+  return h;
 }
+
+void orc_float_to_half_n(const float* in, uint16_t* out, int64_t n) {
+  for (int64_t i = 0; i < n; i++) out[i] = orc_float_to_half(in[i]);
+}
+
+/* float -> half -> float, for the fp16 cache mirror */
+static float round_f16(float f) { return orc_half_to_float(orc_float_to_half(f)); }
 
 static void state_free(orc_state* s) {
   free(s->kc); free(s->vc); free(s->x); free(s->n1); free(s->q); free(s->k); free(s->v);

@@ -31,6 +31,14 @@ enum {
  * Pinned: exhaustive 65536-value check against numpy float16 and oracle/_ref. */
 float orc_half_to_float(uint16_t h);
 
+/* float -> IEEE half bits, round to nearest even; overflow to +-inf, NaN stays a
+ * quiet NaN. The fp16 KV cache mode of orc_generate stores every cached K/V
+ * element as orc_half_to_float(orc_float_to_half(x)).
+ * Pinned: every float32 bit pattern against numpy float16, closed-form ties,
+ * subnormals and overflows (tests/test_oracle_f16.py). */
+uint16_t orc_float_to_half(float f);
+void orc_float_to_half_n(const float* in, uint16_t* out, int64_t n);
+
 /* Bytes of one packed row of `cols` values (include/uaii/quant/formats.hpp:81-102). */
 size_t orc_row_bytes(int type, int64_t cols);
 

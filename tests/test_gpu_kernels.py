@@ -142,19 +142,52 @@ def test_gemv_pair_formats_chunk_scales(hip, t):
     overflow, underflow or poison the sum). The error is measured against the
     largest output, which the 1e20 chunks dominate, so the small chunks are only
     held to finiteness here; their own precision is what the other GEMV tests
-    check at unit scale."""
+    check at unit scale. A kernel chunk is 32 consecutive inputs for Q4_0/Q4_1,
+    but two 16-input runs 32 (Q4_K) or 64 (Q6_K) apart, so the scales are set
+    per aligned span of 32, 64 or 128 inputs: every format then gets chunks
+    that are all zero and chunks under one scale."""
     rows, cols = 64, 2048
+    span = {uaii_amd.Q4_0: 32, uaii_amd.Q4_1: 32, uaii_amd.Q4_K: 64, uaii_amd.Q6_K: 128}[t]
     p = random_packed(t, rows, cols, seed=51)
     x = synth.normals(52, 1, 0, cols, 1.0).astype(np.float64)
     rng = np.random.default_rng(53)
-    expo = rng.integers(-20, 21, cols // 32)
-    expo[::7] = -99  # all-zero chunks
+    expo = rng.integers(-20, 21, cols // span)
+    expo[::7] = -99  # all-zero spans
     scale = np.where(expo == -99, 0.0, 10.0 ** expo.astype(np.float64))
-    x = (x.reshape(-1, 32) * scale[:, None]).reshape(-1).astype(np.float32)
+    x = (x.reshape(-1, span) * scale[:, None]).reshape(-1).astype(np.float32)
     got = run_gemv(hip, t, rows, cols, x, p)
     want = oracle.quant_gemm(t, x, p, rows)[0]
     assert np.all(np.isfinite(got))
     assert maxrel(got, want) < 2e-5
+
+
+@pytest.mark.parametrize("t", [uaii_amd.Q4_0, uaii_amd.Q4_K, uaii_amd.Q6_K],
+                         ids=lambda t: uaii_amd.TYPE_NAMES[t])
+def test_gemv_pair_formats_outlier_channels(hip, t):
+    """Inputs with a few 30-100x channels per 64 (as after an RMSNorm with large
+    norm weights). A kernel chunk's power-of-two scale follows its largest input,
+    so unit-scale inputs that share a chunk with an outlier are held on a coarser
+    hi grid and rely on the lo part; each row's error is bounded against that
+    row's non-outlier contribution (sum of |w x| over the unit channels), against
+    the exact product of the dequantized weights in f64."""
+    rows, cols = 512, 4096
+    p = random_packed(t, rows, cols, seed=61)
+    rng = np.random.default_rng(62)
+    x = rng.standard_normal(cols)
+    out_idx = np.concatenate([64 * g + rng.choice(64, 3, replace=False) for g in range(cols // 64)])
+    x[out_idx] = rng.choice([-1.0, 1.0], out_idx.size) * rng.uniform(30.0, 100.0, out_idx.size)
+    x = x.astype(np.float32)
+    got = run_gemv(hip, t, rows, cols, x, p).astype(np.float64)
+    w = oracle.dequant(t, p, rows, cols).astype(np.float64)
+    exact = w @ x.astype(np.float64)
+    rest = np.ones(cols, bool)
+    rest[out_idx] = False
+    l1_rest = np.abs(w[:, rest]) @ np.abs(x[rest].astype(np.float64))
+    err = np.abs(got - exact) / l1_rest
+    assert err.max() < 2e-5, f"worst row error {err.max():.3e} of its unit-channel L1"
+    # the oracle (sequential f32) is held to the same bar, so the device is no worse
+    want = oracle.quant_gemm(t, x, p, rows)[0].astype(np.float64)
+    assert (np.abs(want - exact) / l1_rest).max() < 2e-5
 
 
 @pytest.mark.parametrize("t", [uaii_amd.Q4_0, uaii_amd.Q8_0, uaii_amd.Q4_K, uaii_amd.Q6_K],

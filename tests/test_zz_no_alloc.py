@@ -79,3 +79,10 @@ def test_noalloc_refuses_partials_beyond_its_array(hip):
                                                buf.ptr, None)
     assert rc == -3
     assert b"scratch" in hip.uaii_hip_error_string(rc)
+    # key positions are 32-bit in the kernels: a cache of 2^31 or more positions
+    # (or 2^32 keys, which a 32-bit count would read as 0) is refused by both
+    # entry points before any launch
+    for max_seq, n_keys in ((1 << 31, 1), (1 << 32, 1 << 32)):
+        for fn in (hip.uaii_hip_attention_decode_noalloc, hip.uaii_hip_attention_decode):
+            rc = fn(buf.ptr, buf.ptr, buf.ptr, 1, max_seq, 8, 8, 64, n_keys, buf.ptr, None)
+            assert rc == -1, (fn.__name__, max_seq, n_keys, rc)

@@ -120,11 +120,13 @@ __device__ __forceinline__ void wait_vm() {
   cfence();
 }
 
+// LDS DMA: the LDS address is the asm's M0 operand (the compiler writes M0);
+// s_nop 0 is the wait state an LDS DMA needs after an M0 write.
 __device__ __forceinline__ void dma16(const void* g, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(g) : "memory", "m0");
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"{m0}"(lds), "v"(g) : "memory");
 }
 __device__ __forceinline__ void dma4(const void* g, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, off" ::"s"(lds), "v"(g) : "memory", "m0");
+  asm volatile("s_nop 0\n\tglobal_load_lds_dword %1, off" ::"{m0}"(lds), "v"(g) : "memory");
 }
 // LDS byte address of a pointer into LDS: the low half of its generic address
 // (the LDS aperture base is the high half); no address-space cast, whose null

@@ -640,18 +640,22 @@ __global__ void __launch_bounds__(PF_WAVES * 64, 2) k_pf_gemm(PfGemmArgs a) {
 // SQ_LDS_BANK_CONFLICT: unpermuted rows cost 4 conflict cycles per 16-byte
 // activation read and 2 (Q4_0) or 6 (Q8_0) per 8-byte weight read, as does
 // the permutation p ^ (((r >> 1) ^ (r >> 3)) & 3) for the activations.
+//
+// The LDS address goes to the asm as an M0 operand ("{m0}"), so the compiler
+// writes M0 itself and knows it holds that value; the s_nop gives the one wait
+// state an LDS DMA needs after an M0 write.
 
 __device__ inline void dma16(const void* g, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(g) : "memory", "m0");
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"{m0}"(lds), "v"(g) : "memory");
 }
 __device__ inline void dma4(const void* g, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, off" ::"s"(lds), "v"(g) : "memory", "m0");
+  asm volatile("s_nop 0\n\tglobal_load_lds_dword %1, off" ::"{m0}"(lds), "v"(g) : "memory");
 }
 // The same 16-byte copy from a wave-uniform base (scalar registers) plus the
 // lane's 32-bit byte offset: no per-lane 64-bit address arithmetic per stage.
 __device__ inline void dma16s(const void* sbase, uint32_t voff, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds), "v"(voff), "s"(sbase)
-               : "memory", "m0");
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %1, %2" ::"{m0}"(lds), "v"(voff), "s"(sbase)
+               : "memory");
 }
 // A pointer the wave holds in common, made visibly uniform so that it lives in
 // scalar registers.
@@ -1696,8 +1700,6 @@ hipError_t launch_pf_gemm(PfGemmArgs a, hipStream_t s) {
   if (!a.arow && !a.gtab && a.sx_ld != a.mpad) return hipErrorInvalidValue;
   if (a.nseg < 1 || a.nseg > 3 || a.M <= 0 || a.M > a.mpad || a.mpad % 64 || a.K % 64)
     return hipErrorInvalidValue;
-  // the direct-to-LDS kernels address activation rows by 32-bit byte offsets
-  if (a.sx_ld * a.K * 2 >= (int64_t(1) << 31)) return hipErrorInvalidValue;
   if (a.gtab) {
     // every table entry lies inside [0, M) and names an expert below ngroups (the
     // caller builds it on the host); here the launch itself is checked
@@ -1710,6 +1712,10 @@ hipError_t launch_pf_gemm(PfGemmArgs a, hipStream_t s) {
   }
   const int type = a.seg[0].w.type;
   if (!pf_supported(type)) return hipErrorInvalidValue;
+  // the direct-to-LDS kernels (Q4_0, Q8_0) address activation rows by 32-bit
+  // byte offsets: their activation arrays must span under 2^31 bytes
+  if ((type == T_Q4_0 || type == T_Q8_0) && UAII_PF_DMA && a.sx_ld * a.K * 2 >= (int64_t(1) << 31))
+    return hipErrorInvalidValue;
   if (a.hi16 && !pf_hi16_supported(type)) return hipErrorInvalidValue;
   const int64_t kq = (type == T_Q4_K || type == T_Q6_K) ? 256 : 64;  // K granule of a block's range
   if (a.K % (kq * a.ksplit)) return hipErrorInvalidValue;

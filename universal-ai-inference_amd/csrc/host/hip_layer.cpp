@@ -312,7 +312,8 @@ int uaii_hip_attention_decode(const float* q, const void* kcache, const void* vc
                               int64_t max_seq, int n_heads, int n_kv_heads, int head_dim,
                               int64_t n_keys, float* out, void* stream) {
   if (!q || !kcache || !vcache || !out || n_heads <= 0 || n_kv_heads <= 0 ||
-      n_heads % n_kv_heads || head_dim <= 0 || n_keys <= 0 || n_keys > max_seq)
+      n_heads % n_kv_heads || head_dim <= 0 || n_keys <= 0 || n_keys > max_seq ||
+      max_seq > INT32_MAX)  // key positions are 32-bit in the kernels
     return kErrArg;
   std::lock_guard<std::mutex> lk(g_scratch_mu);
   const int splits = uaii_hip::attention_splits(max_seq);

@@ -910,6 +910,16 @@ Error DecoderProgram::read_ids(int64_t* out, int64_t n) {
   return Error::success();
 }
 
+Error DecoderProgram::read_id(int64_t index, int64_t* id) {
+  if (index < 0 || index > max_ctx_) return Error::make(ErrorCode::InvalidArgument, "read_id beyond capacity");
+  int32_t v = 0;
+  UAII_HIP(hipStreamSynchronize(stream_));
+  UAII_TRY(check_layers_fail());
+  UAII_HIP(hipMemcpy(&v, ids_ + index, 4, hipMemcpyDeviceToHost));
+  *id = v;
+  return Error::success();
+}
+
 Error DecoderProgram::collect_timings() {
   if (!opts_.profile) return Error::success();
   UAII_HIP(hipStreamSynchronize(stream_));

@@ -81,6 +81,8 @@ class DecoderProgram {
   Error synchronize();
   // Copy ids[0..n) (prompt + generated) to the host.
   Error read_ids(int64_t* out, int64_t n);
+  // one id of the history (the id generated at position index - 1 for index >= n_prompt)
+  Error read_id(int64_t index, int64_t* id);
   Error read_state(uaii_hip::StepState* st);
   // Run the n tokens ids[pos .. pos + n) through every layer as M-row matrix
   // products on the matrix cores (K/V appended for each position, no logits),

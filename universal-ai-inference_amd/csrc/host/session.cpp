@@ -130,9 +130,9 @@ Error Session::generate(const std::vector<int64_t>& prompt, int64_t max_new,
   }
   out->assign(prompt.begin(), prompt.end());
   for (int64_t t = 0; t < max_new; ++t) {
-    std::vector<int64_t> ids((size_t)(n_prompt + t + 1));
-    UAII_TRY(p.read_ids(ids.data(), n_prompt + t + 1));
-    const int64_t next = ids.back();
+    // one 4-byte id per token: the one this step's argmax appended
+    int64_t next = 0;
+    UAII_TRY(p.read_id(n_prompt + t, &next));
     out->push_back(next);
     if (on_new_token && !on_new_token(next)) return Error::success();
     if (is_stop(next)) return Error::success();
