@@ -24,6 +24,8 @@ Parity status per oracle function (what pins it):
   orc_softmax/argmax     sum-to-1, lowest-index tie rule, _ref
   orc_moe_router/topk    numpy f64 softmax/top-k, renormalised weights sum to 1
   orc_generate           _ref end-to-end greedy ids + taps (reference kernels)
+  orc_generate_ex        layer-major prompt blocks: bit-identical ids and taps to
+                         orc_generate on every architecture variant and both caches
 """
 from __future__ import annotations
 
@@ -106,6 +108,9 @@ def oracle():
         L.orc_generate.restype = C.c_int
         L.orc_generate.argtypes = [vp, C.POINTER(i64), i64, i64, C.c_int, C.c_int, C.POINTER(i64),
                                    C.POINTER(i64), C.POINTER(Taps)]
+        L.orc_generate_ex.restype = C.c_int
+        L.orc_generate_ex.argtypes = [vp, C.POINTER(i64), i64, i64, C.c_int, C.c_int, i64,
+                                      C.POINTER(i64), C.POINTER(i64), C.POINTER(Taps)]
         L.orc_time_decode_window.restype = C.c_double
         L.orc_time_decode_window.argtypes = [vp, i64, i64, C.c_int]
         _o = L
@@ -221,7 +226,10 @@ class Model:
          self.n_experts, self.top_k, self.rope_mode, self.ctx, self.tied) = list(hp)
 
     def generate(self, prompt, max_new: int, kv_f16: bool = False, nthreads: int = 0,
-                 taps: bool = True):
+                 taps: bool = True, prompt_block: int = 0):
+        """Greedy generate; prompt_block > 0 runs the prompt (all but its last
+        token) layer by layer in blocks of that many tokens, with the same result
+        bit for bit (faster for long prompts)."""
         import numpy as np
         p = np.ascontiguousarray(prompt, dtype=np.int64)
         out = np.zeros(len(p) + max_new + 1, dtype=np.int64)
@@ -236,9 +244,10 @@ class Model:
                     "logits": np.zeros(self.vocab, np.float32),
                     "probs": np.zeros(self.vocab, np.float32)}
             t = Taps(*[_fp(bufs[k]) for k in ("hidden", "resid1", "resid2", "normed", "logits", "probs")])
-        rc = oracle().orc_generate(self.h, p.ctypes.data_as(C.POINTER(C.c_int64)), len(p), max_new,
-                                   int(kv_f16), nthreads, out.ctypes.data_as(C.POINTER(C.c_int64)),
-                                   C.byref(n), C.byref(t) if t is not None else None)
+        rc = oracle().orc_generate_ex(self.h, p.ctypes.data_as(C.POINTER(C.c_int64)), len(p), max_new,
+                                      int(kv_f16), nthreads, prompt_block,
+                                      out.ctypes.data_as(C.POINTER(C.c_int64)),
+                                      C.byref(n), C.byref(t) if t is not None else None)
         if rc != 0:
             raise OracleError(oracle().orc_last_error().decode())
         return out[: n.value], bufs

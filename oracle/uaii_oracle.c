@@ -443,7 +443,13 @@ void orc_rope(float* x, int64_t dim, int64_t head_dim, float pos, float theta, i
 }
 
 /* transformer.cpp:332-374 specialised to q_seq=1: scores, softmax with the max
- * subtracted, probabilities normalised, then P.V summed key by key. */
+ * subtracted, probabilities normalised, then P.V summed key by key. Each score is
+ * one left-to-right sum over d (four keys' sums advance together: independent
+ * chains), and each output element one left-to-right sum over the keys (taken
+ * key-outer across a head's elements), so the values are those of the plain
+ * loops in the reference's order. */
+typedef float orc_v4a __attribute__((vector_size(16), aligned(4)));
+
 void orc_attention_decode(const float* q, const float* kc, const float* vc, int64_t past,
                           const float* kn, const float* vn, float* out, int n_heads,
                           int n_kv_heads, int hd) {
@@ -452,31 +458,53 @@ void orc_attention_decode(const float* q, const float* kc, const float* vc, int6
   int group = n_heads / n_kv_heads;
   float scale = 1.0f / sqrtf((float)hd);
   float* p = (float*)malloc((size_t)n * 4);
+  float* acc = (float*)malloc((size_t)hd * 4);
   for (int h = 0; h < n_heads; h++) {
     int kh = h / group;
     const float* qh = q + (int64_t)h * hd;
     float mx = -INFINITY;
-    for (int64_t j = 0; j < n; j++) {
-      const float* kr = (j < past) ? kc + j * kvd + kh * hd : kn + kh * hd;
+#define ORC_KROW(j) (((j) < past) ? kc + (j) * kvd + kh * hd : kn + kh * hd)
+    int64_t j = 0;
+    for (; j + 4 <= n; j += 4) {
+      const float *k0 = ORC_KROW(j), *k1 = ORC_KROW(j + 1), *k2 = ORC_KROW(j + 2), *k3 = ORC_KROW(j + 3);
+      float d0 = 0.0f, d1 = 0.0f, d2 = 0.0f, d3 = 0.0f;
+      for (int d = 0; d < hd; d++) {
+        d0 += qh[d] * k0[d];
+        d1 += qh[d] * k1[d];
+        d2 += qh[d] * k2[d];
+        d3 += qh[d] * k3[d];
+      }
+      p[j] = d0 * scale; p[j + 1] = d1 * scale; p[j + 2] = d2 * scale; p[j + 3] = d3 * scale;
+    }
+    for (; j < n; j++) {
+      const float* kr = ORC_KROW(j);
       float dot = 0.0f;
       for (int d = 0; d < hd; d++) dot += qh[d] * kr[d];
-      dot *= scale;
-      p[j] = dot;
-      if (dot > mx) mx = dot;
+      p[j] = dot * scale;
     }
+#undef ORC_KROW
+    for (j = 0; j < n; j++) if (p[j] > mx) mx = p[j];
     float sum = 0.0f;
-    for (int64_t j = 0; j < n; j++) { p[j] = expf(p[j] - mx); sum += p[j]; }
+    for (j = 0; j < n; j++) { p[j] = expf(p[j] - mx); sum += p[j]; }
     float inv = sum > 0 ? 1.0f / sum : 0.0f;
-    for (int64_t j = 0; j < n; j++) p[j] *= inv;
-    for (int d = 0; d < hd; d++) {
-      float acc = 0.0f;
-      for (int64_t j = 0; j < n; j++) {
-        const float* vr = (j < past) ? vc + j * kvd + kh * hd : vn + kh * hd;
-        acc += p[j] * vr[d];
+    for (j = 0; j < n; j++) p[j] *= inv;
+    for (int d = 0; d < hd; d++) acc[d] = 0.0f;
+    for (j = 0; j < n; j++) {
+      const float* vr = (j < past) ? vc + j * kvd + kh * hd : vn + kh * hd;
+      const float pj = p[j];
+      int d = 0;
+      if ((hd & 3) == 0) {
+        const orc_v4a pb = {pj, pj, pj, pj};
+        for (; d < hd; d += 4) {
+          orc_v4a a = *(const orc_v4a*)(acc + d), b = *(const orc_v4a*)(vr + d);
+          *(orc_v4a*)(acc + d) = a + pb * b;
+        }
       }
-      out[(int64_t)h * hd + d] = acc;
+      for (; d < hd; d++) acc[d] += pj * vr[d];
     }
+    for (int d = 0; d < hd; d++) out[(int64_t)h * hd + d] = acc[d];
   }
+  free(acc);
   free(p);
 }
 
@@ -1184,8 +1212,220 @@ static int forward(orc_state* s, int64_t token, int64_t pos, int nthreads, orc_t
   return 0;
 }
 
+/* ---------------------------------------------------------- layer-major prompt */
+
+/* Y[i][j] = W_j . X_i for M rows of X at once, in tiles of 4 weight rows x 16
+ * rows of X: the 4 weight rows are dequantized once per tile, X is held
+ * transposed in groups of 16 rows ([group][k][16]), and the 64 sums of a tile
+ * advance together over k in 4-wide vectors. Each vector lane is one (row of X,
+ * weight row) sum taken left to right as s = s + x[k] * w[k] (a product rounded
+ * to f32, then the add: no contraction), the order of qg_row's loop, so every
+ * output equals the M = 1 call's bit for bit. Path A / F32 / F16 weights:
+ * dot_tiled64 per (row of X, weight row), as mv_row_a. */
+typedef float orc_v4 __attribute__((vector_size(16)));
+
+typedef struct {
+  const orc_model* m;
+  const orc_w* w;
+  const float* AT;  /* [ceil(M/16)][K][16] */
+  const float* A;   /* [M][K] (f32-weight path) */
+  int64_t M, K, N;
+  float* Y;         /* [M][N] */
+} mm_ctx;
+
+#define MM_ROWS 4
+#define MM_COLS 16
+
+static void mm_tile(void* v, int64_t tile, float* rows) {
+  mm_ctx* c = (mm_ctx*)v;
+  const orc_w* w = c->w;
+  const int64_t K = c->K;
+  const int64_t j0 = tile * MM_ROWS;
+  const int nr = (int)(c->N - j0 < MM_ROWS ? c->N - j0 : MM_ROWS);
+  if (c->m->path_a || w->type == ORC_F32 || w->type == ORC_F16) {
+    for (int r = 0; r < nr; r++) {
+      const float* wr = w->f32 + (j0 + r) * w->cols;
+      for (int64_t i = 0; i < c->M; i++) c->Y[i * c->N + j0 + r] = dot_tiled64(c->A + i * K, wr, K);
+    }
+    return;
+  }
+  size_t rb = orc_row_bytes(w->type, w->cols);
+  for (int r = 0; r < MM_ROWS; r++) {
+    if (r < nr) {
+      if (orc_dequant_row(w->type, w->data + (size_t)(j0 + r) * rb, K, rows + r * K) != 0) return;
+    } else {
+      memset(rows + r * K, 0, (size_t)K * 4);
+    }
+  }
+  for (int64_t g = 0; g * MM_COLS < c->M; g++) {
+    const orc_v4* at = (const orc_v4*)(c->AT + g * K * MM_COLS);
+    orc_v4 acc[MM_ROWS][MM_COLS / 4];
+    for (int r = 0; r < MM_ROWS; r++)
+      for (int q = 0; q < MM_COLS / 4; q++) acc[r][q] = (orc_v4){0.0f, 0.0f, 0.0f, 0.0f};
+    for (int64_t k = 0; k < K; k++) {
+      const orc_v4 a0 = at[k * 4 + 0], a1 = at[k * 4 + 1], a2 = at[k * 4 + 2], a3 = at[k * 4 + 3];
+      for (int r = 0; r < MM_ROWS; r++) {
+        const float wv = rows[r * K + k];
+        const orc_v4 wb = {wv, wv, wv, wv};
+        acc[r][0] = acc[r][0] + a0 * wb;
+        acc[r][1] = acc[r][1] + a1 * wb;
+        acc[r][2] = acc[r][2] + a2 * wb;
+        acc[r][3] = acc[r][3] + a3 * wb;
+      }
+    }
+    for (int r = 0; r < nr; r++)
+      for (int ii = 0; ii < MM_COLS && g * MM_COLS + ii < c->M; ii++)
+        c->Y[(g * MM_COLS + ii) * c->N + j0 + r] = acc[r][ii / 4][ii % 4];
+  }
+}
+
+static void matmat(const orc_model* m, const orc_w* w, const float* X, int64_t M, float* Y,
+                   float* at_buf, int nthreads) {
+  int64_t K = w->cols;
+  if (!(m->path_a || w->type == ORC_F32 || w->type == ORC_F16)) {
+    for (int64_t g = 0; g * MM_COLS < M; g++)
+      for (int64_t k = 0; k < K; k++)
+        for (int ii = 0; ii < MM_COLS; ii++) {
+          int64_t i = g * MM_COLS + ii;
+          at_buf[(g * K + k) * MM_COLS + ii] = i < M ? X[i * K + k] : 0.0f;
+        }
+  } else if (!w->f32) {
+    return;
+  }
+  mm_ctx c = {m, w, at_buf, X, M, K, w->rows, Y};
+  parallel_for((w->rows + MM_ROWS - 1) / MM_ROWS, nthreads, (size_t)(MM_ROWS * K), mm_tile, &c);
+}
+
+typedef struct {
+  const float *Q, *K, *V, *kc, *vc;
+  float* ATT;
+  int64_t p0, qd, kvd;
+  int nh, nkv, hd;
+} att_ctx;
+
+static void att_row(void* v, int64_t b, float* scratch) {
+  (void)scratch;
+  att_ctx* c = (att_ctx*)v;
+  orc_attention_decode(c->Q + b * c->qd, c->kc, c->vc, c->p0 + b, c->K + b * c->kvd,
+                       c->V + b * c->kvd, c->ATT + b * c->qd, c->nh, c->nkv, c->hd);
+}
+
+/* Prompt tokens at positions p0 .. p0+nb-1 run layer by layer: per layer the
+ * block's rows go through each projection together (matmat), and the block's K/V
+ * are appended before its attentions, where token b reads positions < p0+b from
+ * the cache and its own K/V, as forward() does. Every value equals what nb calls of
+ * forward() (without the LM head, whose values are not read for these tokens)
+ * give, bit for bit; tests/test_oracle_prompt.py checks that on every variant. */
+static int forward_block(orc_state* s, const int64_t* tokens, int64_t nb, int64_t p0,
+                         int nthreads) {
+  orc_model* m = s->m;
+  int64_t D = m->dim, hd = m->head_dim, qd = m->n_heads * hd, kvd = m->n_kv * hd;
+  int64_t ff = m->ffn > 0 ? m->ffn : 4 * m->dim;
+  for (int64_t li = 0; li < m->n_layers; li++) {
+    const orc_layer* L = &m->L[li];
+    if (L->has_ffn && L->w_up.rows > ff) ff = L->w_up.rows;
+    if (L->shared && L->up_sh.rows > ff) ff = L->up_sh.rows;
+  }
+  int64_t kmax = D > qd ? D : qd;
+  if (ff > kmax) kmax = ff;
+  if (p0 + nb > s->max_seq) { set_err("KvCache capacity exceeded"); return -1; }
+  size_t nbz = (size_t)nb;
+  float* X = (float*)malloc(nbz * (size_t)D * 4);
+  float* N1 = (float*)malloc(nbz * (size_t)D * 4);
+  float* Q = (float*)malloc(nbz * (size_t)qd * 4);
+  float* K = (float*)malloc(nbz * (size_t)kvd * 4);
+  float* V = (float*)malloc(nbz * (size_t)kvd * 4);
+  float* ATT = (float*)malloc(nbz * (size_t)qd * 4);
+  float* T = (float*)malloc(nbz * (size_t)D * 4);
+  float* G = (float*)malloc(nbz * (size_t)ff * 4);
+  float* U = (float*)malloc(nbz * (size_t)ff * 4);
+  float* H = (float*)malloc(nbz * (size_t)ff * 4);
+  float* AT = (float*)malloc(((nbz + MM_COLS - 1) / MM_COLS * MM_COLS) * (size_t)kmax * 4);
+  int rc = -1;
+  if (!X || !N1 || !Q || !K || !V || !ATT || !T || !G || !U || !H || !AT) { set_err("oom"); goto done; }
+  size_t erb = orc_row_bytes(m->tok_embd.type, D);
+  for (int64_t b = 0; b < nb; b++) {
+    int64_t token = tokens[b];
+    if (token < 0 || token >= m->tok_embd.rows) { set_err("embedding token id out of range"); goto done; }
+    if (m->path_a) orc_load_row_f32(m->tok_embd.type, m->tok_embd.data + token * erb, D, X + b * D);
+    else orc_dequant_row(m->tok_embd.type, m->tok_embd.data + token * erb, D, X + b * D);
+  }
+  for (int64_t li = 0; li < m->n_layers; li++) {
+    orc_layer* L = &m->L[li];
+    for (int64_t b = 0; b < nb; b++) orc_rmsnorm(X + b * D, L->attn_norm.f32, N1 + b * D, D, m->eps);
+    matmat(m, &L->wq, N1, nb, Q, AT, nthreads);
+    matmat(m, &L->wk, N1, nb, K, AT, nthreads);
+    matmat(m, &L->wv, N1, nb, V, AT, nthreads);
+    float* kc = s->kc + (size_t)li * (size_t)s->max_seq * (size_t)kvd;
+    float* vc = s->vc + (size_t)li * (size_t)s->max_seq * (size_t)kvd;
+    for (int64_t b = 0; b < nb; b++) {
+      float *q = Q + b * qd, *k = K + b * kvd, *v = V + b * kvd;
+      if (L->has_bias_q) for (int64_t i = 0; i < qd; i++) q[i] = q[i] + L->bq.f32[i];
+      if (L->has_bias_k) for (int64_t i = 0; i < kvd; i++) k[i] = k[i] + L->bk.f32[i];
+      if (L->has_bias_v) for (int64_t i = 0; i < kvd; i++) v[i] = v[i] + L->bv.f32[i];
+      orc_rope(q, qd, hd, (float)(p0 + b), m->theta, m->rope_mode);
+      orc_rope(k, kvd, hd, (float)(p0 + b), m->theta, m->rope_mode);
+      if (s->kv_f16) {
+        for (int64_t i = 0; i < kvd; i++) { k[i] = round_f16(k[i]); v[i] = round_f16(v[i]); }
+      }
+      memcpy(kc + (p0 + b) * kvd, k, (size_t)kvd * 4);
+      memcpy(vc + (p0 + b) * kvd, v, (size_t)kvd * 4);
+    }
+    att_ctx ac = {Q, K, V, kc, vc, ATT, p0, qd, kvd, (int)m->n_heads, (int)m->n_kv, (int)hd};
+    parallel_for(nb, nthreads, 0, att_row, &ac);
+    matmat(m, &L->wo, ATT, nb, T, AT, nthreads);
+    for (int64_t i = 0; i < nb * D; i++) X[i] = X[i] + T[i];
+    const float* min = X;
+    if (L->has_ffn_norm) {
+      for (int64_t b = 0; b < nb; b++) orc_rmsnorm(X + b * D, L->ffn_norm.f32, N1 + b * D, D, m->eps);
+      min = N1;
+    }
+    if (L->moe) {
+      for (int64_t b = 0; b < nb; b++) {
+        moe_ffn(s, L, min + b * D, s->eout, nthreads);
+        if (L->shared) {
+          int64_t I = L->up_sh.rows;
+          matvec(m, &L->gate_sh, min + b * D, s->g, 0, I, nthreads);
+          matvec(m, &L->up_sh, min + b * D, s->u, 0, I, nthreads);
+          for (int64_t i = 0; i < I; i++) s->hid[i] = orc_silu(s->g[i]) * s->u[i];
+          matvec(m, &L->down_sh, s->hid, s->tmp, 0, D, nthreads);
+          for (int64_t i = 0; i < D; i++) s->eout[i] = s->eout[i] + s->tmp[i];
+        }
+        for (int64_t i = 0; i < D; i++) X[b * D + i] = X[b * D + i] + s->eout[i];
+      }
+    } else if (L->has_ffn && !L->gelu) {
+      int64_t I = L->w_up.rows;
+      matmat(m, &L->w_gate, min, nb, G, AT, nthreads);
+      matmat(m, &L->w_up, min, nb, U, AT, nthreads);
+      for (int64_t i = 0; i < nb * I; i++) H[i] = orc_silu(G[i]) * U[i];
+      matmat(m, &L->w_down, H, nb, T, AT, nthreads);
+      for (int64_t i = 0; i < nb * D; i++) X[i] = X[i] + T[i];
+    } else if (L->gelu) {
+      int64_t I = L->w_up.rows;
+      matmat(m, &L->w_up, min, nb, U, AT, nthreads);
+      for (int64_t i = 0; i < nb * I; i++) {
+        float v = U[i];
+        float uu = 0.7978845608f * (v + 0.044715f * v * v * v);
+        H[i] = 0.5f * v * (1.0f + tanhf(uu));
+      }
+      matmat(m, &L->w_down, H, nb, T, AT, nthreads);
+      for (int64_t i = 0; i < nb * D; i++) X[i] = X[i] + T[i];
+    }
+  }
+  rc = 0;
+done:
+  free(X); free(N1); free(Q); free(K); free(V); free(ATT); free(T); free(G); free(U); free(H); free(AT);
+  return rc;
+}
+
 int orc_generate(orc_model* m, const int64_t* prompt, int64_t n_prompt, int64_t max_new,
                  int kv_f16, int nthreads, int64_t* out, int64_t* out_n, orc_taps* taps) {
+  return orc_generate_ex(m, prompt, n_prompt, max_new, kv_f16, nthreads, 0, out, out_n, taps);
+}
+
+int orc_generate_ex(orc_model* m, const int64_t* prompt, int64_t n_prompt, int64_t max_new,
+                    int kv_f16, int nthreads, int64_t prompt_block, int64_t* out, int64_t* out_n,
+                    orc_taps* taps) {
   if (!m || !out || !out_n) { set_err("null args"); return -1; }
   if (n_prompt <= 0) { set_err("prompt_tokens empty"); return -1; }
   if (max_new < 0) { set_err("max_new_tokens < 0"); return -1; }
@@ -1199,8 +1439,18 @@ int orc_generate(orc_model* m, const int64_t* prompt, int64_t n_prompt, int64_t 
   orc_state s;
   if (state_init(&s, m, kv_max, kv_f16)) return -1;
   int64_t n = 0, pos = 0;
+  /* prompt_block > 0: prompt tokens 0 .. n_prompt-2 layer-major in blocks of that
+   * many tokens (same values as the token steps below) */
+  if (prompt_block > 0) {
+    while (pos < n_prompt - 1) {
+      int64_t nb = n_prompt - 1 - pos < prompt_block ? n_prompt - 1 - pos : prompt_block;
+      if (forward_block(&s, prompt + pos, nb, pos, nthreads)) { state_free(&s); return -1; }
+      for (int64_t b = 0; b < nb; b++) out[n++] = prompt[pos + b];
+      pos += nb;
+    }
+  }
   /* prefill: one run() per prompt token (session.cpp:1006-1016) */
-  for (int64_t i = 0; i < n_prompt; i++) {
+  for (int64_t i = pos; i < n_prompt; i++) {
     int last = (i == n_prompt - 1);
     /* the LM head of the earlier prompt tokens is computed by the reference and
      * never read; skipping it here changes no value that is read */

@@ -143,6 +143,14 @@ typedef struct orc_taps {
 int orc_generate(orc_model* m, const int64_t* prompt, int64_t n_prompt, int64_t max_new,
                  int kv_f16, int nthreads, int64_t* out, int64_t* out_n, orc_taps* taps);
 
+/* orc_generate with prompt_block > 0: prompt tokens 0 .. n_prompt-2 run layer by
+ * layer in blocks of prompt_block tokens (each weight row dequantized once per
+ * block), the last prompt token and the decode as token steps. Same ids and taps
+ * as orc_generate bit for bit (tests/test_oracle_prompt.py); for long prompts. */
+int orc_generate_ex(orc_model* m, const int64_t* prompt, int64_t n_prompt, int64_t max_new,
+                    int kv_f16, int nthreads, int64_t prompt_block, int64_t* out,
+                    int64_t* out_n, orc_taps* taps);
+
 /* Run `n_steps` decode steps feeding `tokens` at positions start_pos.. with a KV
  * cache pre-filled with deterministic values for positions < start_pos (timing
  * window for the CPU baseline). Returns elapsed seconds, <0 on error. */

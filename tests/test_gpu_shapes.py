@@ -12,8 +12,10 @@
   reference's own cache type) over a shorter run.
 * The Llama-3.2-1B shape at full depth (16 layers, Q4_K + Q6_K, tied):
   128-token prompt, 64 greedy tokens.
+* The same two layers at the headline length: a 4032-token prompt on the matrix
+  cores, then 64 greedy tokens to a full 4096-position cache.
 * The Mixtral shape (8 experts, top-2, Q4_K, d 4096, ffn 14336), one layer:
-  64-token prompt, 32 greedy tokens against the oracle's Path A MoE (the only
+  64-token prompt, 64 greedy tokens against the oracle's Path A MoE (the only
   path on which the reference's experts run, transformer.cpp:522-612).
 
 Reference loop for every model: session.cpp:1006-1044 (prompt, then greedy
@@ -119,6 +121,29 @@ def test_8b_shape_two_layers(name):
     check_taps(taps8, want32, 2)
 
 
+def test_8b_shape_headline_context():
+    """The headline length: two 8B-shape layers (Q4_0, vocab 128256), a 4032-token
+    prompt prefilled on the matrix cores (1024-row chunks), then 64 greedy tokens
+    that fill the 4096-position fp16 cache (decode attention over 4033 .. 4096
+    keys, 32 key splits). Against the oracle with an fp16 cache (its prompt run
+    layer by layer, bit-identical to its token steps): all 64 ids identical,
+    logits and every residual tap of the last step within 2e-3."""
+    cfg = SHAPES["8b_q4_0"]
+    path = synth.cached_model(cfg, nthreads=THREADS)
+    n_prompt, n_new = 4032, 64
+    prompt = np.random.default_rng(cfg.seed + 200).integers(0, cfg.vocab, n_prompt).astype(np.int64)
+    print("8b headline context: device", flush=True)
+    ids, taps = run_device(path, prompt, n_new, 2, max_context=4096)
+    print("8b headline context: oracle", flush=True)
+    want_ids, want = oracle.Model(path).generate(prompt, n_new, kv_f16=True, nthreads=THREADS,
+                                                 prompt_block=256)
+    print("8b ctx4096 gpu", ids[n_prompt:].tolist(), flush=True)
+    print("8b ctx4096 cpu", want_ids[n_prompt:].tolist(), flush=True)
+    assert len(ids) == 4096
+    assert np.array_equal(ids, want_ids)
+    check_taps(taps, want, 2)
+
+
 def test_1b_shape_full_depth():
     cfg = SHAPES["1b"]
     path = synth.cached_model(cfg, nthreads=THREADS)
@@ -135,10 +160,10 @@ def test_mixtral_shape_one_layer():
     cfg = SHAPES["mx"]
     path = synth.cached_model(cfg, nthreads=THREADS)
     prompt = np.random.default_rng(cfg.seed + 100).integers(0, cfg.vocab, 64).astype(np.int64)
-    ids, taps = run_device(path, prompt, 32, 1)
+    ids, taps = run_device(path, prompt, 64, 1)
     m = oracle.Model(path)
     assert m.n_experts == 8 and m.top_k == 2 and m.ffn == 14336
-    want_ids, want = m.generate(prompt, 32, kv_f16=True, nthreads=THREADS)
+    want_ids, want = m.generate(prompt, 64, kv_f16=True, nthreads=THREADS, prompt_block=64)
     print("mx gpu", ids[64:].tolist(), flush=True)
     print("mx cpu", want_ids[64:].tolist(), flush=True)
     assert np.array_equal(ids, want_ids)

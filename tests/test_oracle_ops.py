@@ -168,3 +168,25 @@ def test_moe_router_topk():
     order = np.argsort(-ref, kind="stable")[:2]
     assert list(ids) == order.tolist()
     assert abs(float(w.sum()) - 1.0) < 1e-6
+
+
+@pytest.mark.parametrize("nh, nkv, hd, past", [(4, 4, 128, 4095), (8, 2, 128, 96), (6, 3, 6, 13),
+                                               (2, 1, 10, 0), (32, 8, 64, 1)])
+def test_attention_reference_bits_shapes(nh, nkv, hd, past):
+    """orc_attention_decode against the reference's attention_kv_f32 bit for bit
+    at key counts on and off multiples of four, head_dims with and without a
+    multiple of four, and a long context."""
+    if oracle.ref() is None:
+        pytest.skip("reference kernels not built")
+    rng = np.random.default_rng(past + hd)
+    q = rng.standard_normal(nh * hd).astype(np.float32)
+    kc = rng.standard_normal((max(past, 1), nkv * hd)).astype(np.float32)
+    vc = rng.standard_normal((max(past, 1), nkv * hd)).astype(np.float32)
+    kn = rng.standard_normal(nkv * hd).astype(np.float32)
+    vn = rng.standard_normal(nkv * hd).astype(np.float32)
+    out = np.zeros(nh * hd, np.float32)
+    r = np.zeros(nh * hd, np.float32)
+    O().orc_attention_decode(fp(q), fp(kc), fp(vc), past, fp(kn), fp(vn), fp(out), nh, nkv, hd)
+    assert oracle.ref().uref_attention_decode(fp(q), fp(kc), fp(vc), past, fp(kn), fp(vn), fp(r),
+                                              nh, nkv, hd) == 0
+    assert np.array_equal(out.view(np.uint32), r.view(np.uint32))
