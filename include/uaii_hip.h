@@ -14,6 +14,10 @@
  *   uaii_hip_gemv              quant_gemm_f32 at M=1 (libs/uaii-kernels/src/quant_gemm.cpp:22-70)
  *   uaii_hip_gemv_rmsnorm      rmsnorm_f32 (norm.cpp:89-130) feeding quant_gemm_f32
  *   uaii_hip_gemm              quant_gemm_f32 at M>1 (prefill; same file)
+ *   uaii_hip_add / _mul /      add_f32, mul_f32, silu_f32, gelu_f32
+ *   _silu / _gelu              (libs/uaii-kernels/src/elementwise.cpp:56-110)
+ *   uaii_hip_embed             embedding_f32 (libs/uaii-kernels/src/transformer.cpp:61-142)
+ *   uaii_hip_kv_append         KvCache::append_layer (include/uaii/runtime/kv_cache.hpp:80-120)
  *   uaii_hip_rmsnorm           rmsnorm_f32 (libs/uaii-kernels/src/norm.cpp:89-130)
  *   uaii_hip_softmax           softmax_f32 (libs/uaii-kernels/src/softmax.cpp:11-77)
  *   uaii_hip_argmax            greedy sample_token_f32 (libs/uaii-runtime/src/sampling.cpp:38-50)
@@ -96,6 +100,22 @@ UAII_HIP_API int uaii_hip_gemm_swiglu(const uaii_hip_weight* wg, const uaii_hip_
 UAII_HIP_API int uaii_hip_rmsnorm(const float* x, const float* w, float* y, int64_t rows,
                                   int64_t n, float eps, void* stream);
 UAII_HIP_API int uaii_hip_softmax(const float* x, float* y, int64_t n, void* stream);
+/* Elementwise f32 over n values (y may alias an input): add_f32, mul_f32,
+ * silu_f32, gelu_f32 (libs/uaii-kernels/src/elementwise.cpp:56-110). */
+UAII_HIP_API int uaii_hip_add(const float* a, const float* b, float* y, int64_t n, void* stream);
+UAII_HIP_API int uaii_hip_mul(const float* a, const float* b, float* y, int64_t n, void* stream);
+UAII_HIP_API int uaii_hip_silu(const float* x, float* y, int64_t n, void* stream);
+UAII_HIP_API int uaii_hip_gelu(const float* x, float* y, int64_t n, void* stream);
+/* Embedding rows (embedding_f32, libs/uaii-kernels/src/transformer.cpp:61-142):
+ * out[i][:] = dequantized row ids[i] of w; ids are device int32, in range. */
+UAII_HIP_API int uaii_hip_embed(const uaii_hip_weight* w, const int32_t* ids, int64_t n, float* out,
+                                void* stream);
+/* K and V rows ([rows][kv_dim] f32) into the head-major caches of
+ * uaii_hip_attention_decode at positions p0 .. p0 + rows - 1, as f16 (kv_f16 = 1)
+ * or f32 (KvCache::append_layer, include/uaii/runtime/kv_cache.hpp:80-120). */
+UAII_HIP_API int uaii_hip_kv_append(const float* k, const float* v, void* kcache, void* vcache,
+                                    int64_t rows, int64_t kv_dim, int head_dim, int64_t max_seq,
+                                    int64_t p0, int kv_f16, void* stream);
 UAII_HIP_API int uaii_hip_argmax(const float* x, int64_t n, int32_t* out_idx, void* stream);
 /* table: [max_pos][head_dim/2] (cos, sin) float pairs, filled on the host with
  * the reference's angle formula, uploaded to `table_dev`. */

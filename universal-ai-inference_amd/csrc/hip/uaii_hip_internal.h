@@ -116,6 +116,14 @@ hipError_t launch_embed(const DevWeight& w, const StepState* st, float* x, float
 hipError_t launch_embed_rows(const DevWeight& w, const int32_t* ids, int64_t n, float* x,
                              hipStream_t s);
 hipError_t launch_advance(StepState* st, int32_t* ids, hipStream_t s);
+// Elementwise operators of the op-by-op backend: op 0 add, 1 mul (a, b), 2 SiLU,
+// 3 GELU (a only); y may alias a.
+hipError_t launch_elementwise(int op, const float* a, const float* b, float* y, int64_t n,
+                              hipStream_t s);
+// K and V rows [rows][kv_dim] into head-major caches [n_kv][max_seq][hd] at p0..
+hipError_t launch_kv_append(const float* k, const float* v, void* kc, void* vc, int64_t rows,
+                            int64_t kv_dim, int hd, int64_t max_seq, int64_t p0, int f16,
+                            hipStream_t s);
 hipError_t launch_rmsnorm(const float* x, const float* w, float* y, int64_t rows, int64_t n,
                           float eps, hipStream_t s);
 hipError_t launch_softmax(const float* x, float* y, int64_t n, hipStream_t s);

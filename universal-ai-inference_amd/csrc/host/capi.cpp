@@ -45,6 +45,15 @@ struct SessionHandle {
 
 }  // namespace
 
+// The thread's last-error text and the status of an Error, for the other C
+// entry points of this library (uaii_backend.h).
+uaii_status uaii_capi_status(const uaii::Error& err) { return from_error(err); }
+uaii_status uaii_capi_fail(uaii_status st, const char* msg) { return fail(st, msg); }
+
+namespace {
+
+}  // namespace
+
 extern "C" {
 
 void uaii_session_options_init(uaii_session_options* opts) {

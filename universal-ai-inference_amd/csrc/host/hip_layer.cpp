@@ -281,6 +281,41 @@ int uaii_hip_softmax(const float* x, float* y, int64_t n, void* stream) {
   return (int)launch_softmax(x, y, n, S(stream));
 }
 
+int uaii_hip_add(const float* a, const float* b, float* y, int64_t n, void* stream) {
+  if (!a || !b || !y || n < 0) return kErrArg;
+  return (int)launch_elementwise(0, a, b, y, n, S(stream));
+}
+
+int uaii_hip_mul(const float* a, const float* b, float* y, int64_t n, void* stream) {
+  if (!a || !b || !y || n < 0) return kErrArg;
+  return (int)launch_elementwise(1, a, b, y, n, S(stream));
+}
+
+int uaii_hip_silu(const float* x, float* y, int64_t n, void* stream) {
+  if (!x || !y || n < 0) return kErrArg;
+  return (int)launch_elementwise(2, x, nullptr, y, n, S(stream));
+}
+
+int uaii_hip_gelu(const float* x, float* y, int64_t n, void* stream) {
+  if (!x || !y || n < 0) return kErrArg;
+  return (int)launch_elementwise(3, x, nullptr, y, n, S(stream));
+}
+
+int uaii_hip_embed(const uaii_hip_weight* w, const int32_t* ids, int64_t n, float* out, void* stream) {
+  if (!w || !ids || !out || n < 0) return kErrArg;
+  return (int)launch_embed_rows(w->w.view, ids, n, out, S(stream));
+}
+
+int uaii_hip_kv_append(const float* k, const float* v, void* kcache, void* vcache, int64_t rows,
+                       int64_t kv_dim, int head_dim, int64_t max_seq, int64_t p0, int kv_f16,
+                       void* stream) {
+  if (!k || !v || !kcache || !vcache || rows < 0 || head_dim <= 0 || kv_dim <= 0 ||
+      kv_dim % head_dim || p0 < 0 || p0 + rows > max_seq)
+    return kErrArg;
+  return (int)launch_kv_append(k, v, kcache, vcache, rows, kv_dim, head_dim, max_seq, p0, kv_f16 ? 1 : 0,
+                               S(stream));
+}
+
 int uaii_hip_argmax(const float* x, int64_t n, int32_t* out_idx, void* stream) {
   if (!x || !out_idx || n <= 0) return kErrArg;
   return (int)launch_argmax(x, n, out_idx, S(stream));

@@ -60,6 +60,27 @@ class SessionOptions(C.Structure):
 _lib = None
 
 
+class TensorView(C.Structure):
+    """uaii_tensor_view: the fields of the reference's kernels::TensorView
+    (include/uaii/kernels/tensor_view.hpp:12-24)."""
+    _fields_ = [("dtype", C.c_int32), ("shape", C.POINTER(C.c_int64)), ("rank", C.c_size_t),
+                ("data", C.c_void_p), ("nbytes", C.c_size_t), ("quant_format", C.c_int32),
+                ("quant_rows", C.c_int64), ("quant_cols", C.c_int64)]
+
+
+class Attribute(C.Structure):
+    """uaii_attribute: ir::Attribute (include/uaii/ir/attribute.hpp:11-31)."""
+    _fields_ = [("key", C.c_char_p), ("type", C.c_int32), ("i", C.c_int64), ("f", C.c_double),
+                ("s", C.c_char_p)]
+
+
+# uaii::DType and quant::QuantFormat values (include/uaii/interfaces/types.hpp:13-24,
+# include/uaii/quant/formats.hpp:11-30)
+DTYPE_F32, DTYPE_F16 = 1, 2
+QUANT_FORMAT = {F32: 0, F16: 1, Q4_0: 7, Q4_1: 8, Q5_0: 9, Q5_1: 10, Q8_0: 11, Q2_K: 12, Q3_K: 13,
+                Q4_K: 14, Q5_K: 15, Q6_K: 16}
+
+
 class SampleParams(C.Structure):
     """uaii_sample_params (include/uaii/c_api/uaii_ext.h)."""
     _fields_ = [("struct_size", C.c_uint32), ("temperature", C.c_float), ("top_p", C.c_float),
@@ -167,6 +188,29 @@ def lib() -> C.CDLL:
         "uaii_hip_time_gemm": (C.c_int, [vp, vp, i64, vp, C.c_int, f32p]),
         "uaii_hip_time_copy": (C.c_int, [vp, vp, C.c_size_t, C.c_int, f32p]),
         "uaii_hip_time_read": (C.c_int, [vp, C.c_int, C.c_size_t, C.c_int, f32p]),
+        "uaii_hip_add": (C.c_int, [vp, vp, vp, i64, vp]),
+        "uaii_hip_mul": (C.c_int, [vp, vp, vp, i64, vp]),
+        "uaii_hip_silu": (C.c_int, [vp, vp, i64, vp]),
+        "uaii_hip_gelu": (C.c_int, [vp, vp, i64, vp]),
+        "uaii_hip_embed": (C.c_int, [vp, vp, i64, vp, vp]),
+        "uaii_hip_kv_append": (C.c_int, [vp, vp, vp, vp, i64, i64, C.c_int, i64, i64, C.c_int, vp]),
+        "uaii_backend_create": (C.c_int, [C.c_char_p, C.c_int, C.POINTER(vp)]),
+        "uaii_backend_destroy": (None, [vp]),
+        "uaii_backend_initialize": (C.c_int, [vp]),
+        "uaii_backend_details": (C.c_char_p, [vp]),
+        "uaii_backend_uses_host_fallback": (C.c_int, [vp]),
+        "uaii_backend_dispatch": (C.c_int, [vp, C.c_char_p, C.c_char_p, C.POINTER(TensorView),
+                                            C.c_size_t, C.POINTER(TensorView), C.c_size_t,
+                                            C.POINTER(Attribute), C.c_size_t]),
+        "uaii_backend_synchronize": (C.c_int, [vp]),
+        "uaii_backend_allocate": (C.c_int, [vp, C.c_size_t, C.POINTER(vp)]),
+        "uaii_backend_free": (C.c_int, [vp, vp]),
+        "uaii_backend_copy_h2d": (C.c_int, [vp, vp, vp, C.c_size_t]),
+        "uaii_backend_copy_d2h": (C.c_int, [vp, vp, vp, C.c_size_t]),
+        "uaii_backend_configure_kv_cache": (C.c_int, [vp, i64, i64, i64, i64, C.c_int]),
+        "uaii_backend_reset_kv_cache": (C.c_int, [vp]),
+        "uaii_backend_commit_kv_step": (C.c_int, [vp]),
+        "uaii_backend_kv_past_len": (i64, [vp]),
     }
     for name, (res, args) in sig.items():
         try:
@@ -381,6 +425,110 @@ class Session:
     def close(self):
         if self.h:
             lib().uaii_session_destroy(self.h)
+            self.h = C.c_void_p()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Backend:
+    """The ROCm IBackend through uaii_backend.h: dispatch of the reference's
+    operators (libs/uaii-kernels/src/dispatch.cpp:67-272) on the device.
+
+    Tensors are numpy arrays (host memory, staged by the backend, as the
+    reference's Session hands over its host buffers) or DeviceBuffer objects
+    with an explicit shape (device memory, used in place)."""
+
+    def __init__(self, device: int = 0, initialize: bool = True):
+        L = lib()
+        self.h = C.c_void_p()
+        self._ok(L.uaii_backend_create(b"rocm", device, C.byref(self.h)), "uaii_backend_create")
+        if initialize:
+            self._ok(L.uaii_backend_initialize(self.h), "uaii_backend_initialize")
+
+    @staticmethod
+    def _ok(rc, what):
+        if rc != 0:
+            L = lib()
+            raise UaiiError(f"{what}: {L.uaii_status_name(rc).decode()}: {L.uaii_last_error().decode()}")
+
+    @staticmethod
+    def view(t, shape=None, quant=None):
+        """A TensorView of a numpy array or of (DeviceBuffer, shape, dtype);
+        quant = (gguf_type, rows, cols) marks packed GGUF rows (dtype Unknown)."""
+        import numpy as np
+        keep = []
+        if isinstance(t, tuple):  # (DeviceBuffer, shape, numpy dtype)
+            buf, shp, dt = t
+            data, nbytes = buf.ptr.value, buf.nbytes
+            dtype = DTYPE_F32 if np.dtype(dt) == np.float32 else DTYPE_F16 if np.dtype(dt) == np.float16 else 0
+        else:
+            a = np.ascontiguousarray(t)
+            keep.append(a)
+            shp = a.shape if shape is None else shape
+            data, nbytes = a.ctypes.data, a.nbytes
+            dtype = DTYPE_F32 if a.dtype == np.float32 else DTYPE_F16 if a.dtype == np.float16 else 0
+        shape_arr = (C.c_int64 * max(len(shp), 1))(*shp)
+        keep.append(shape_arr)
+        v = TensorView(dtype, C.cast(shape_arr, C.POINTER(C.c_int64)), len(shp), data, nbytes, 0, 0, 0)
+        if quant is not None:
+            gt, rows, cols = quant
+            v.dtype = 0
+            v.quant_format, v.quant_rows, v.quant_cols = QUANT_FORMAT[gt], rows, cols
+        return v, keep
+
+    def dispatch(self, op: str, inputs, outputs, attrs=None):
+        """inputs / outputs: lists of (TensorView, keep) pairs from view();
+        attrs: {key: value} with bool / int / float / str values."""
+        ins = (TensorView * max(len(inputs), 1))(*[v for v, _ in inputs])
+        outs = (TensorView * max(len(outputs), 1))(*[v for v, _ in outputs])
+        al = []
+        for k, val in (attrs or {}).items():
+            a = Attribute(k.encode(), 0, 0, 0.0, None)
+            if isinstance(val, bool):
+                a.type, a.i = 3, int(val)
+            elif isinstance(val, int):
+                a.type, a.i = 1, val
+            elif isinstance(val, float):
+                a.type, a.f = 2, val
+            else:
+                a.type, a.s = 0, str(val).encode()
+            al.append(a)
+        arr = (Attribute * max(len(al), 1))(*al)
+        self._ok(lib().uaii_backend_dispatch(self.h, op.encode(), b"1", ins, len(inputs), outs,
+                                             len(outputs), arr, len(al)), f"dispatch {op}")
+
+    def configure_kv_cache(self, n_layers, max_seq, kv_dim, n_kv_heads, f16=False):
+        self._ok(lib().uaii_backend_configure_kv_cache(self.h, n_layers, max_seq, kv_dim, n_kv_heads,
+                                                       int(f16)), "configure_kv_cache")
+
+    def reset_kv_cache(self):
+        self._ok(lib().uaii_backend_reset_kv_cache(self.h), "reset_kv_cache")
+
+    def commit_kv_step(self):
+        self._ok(lib().uaii_backend_commit_kv_step(self.h), "commit_kv_step")
+
+    def past_len(self) -> int:
+        return lib().uaii_backend_kv_past_len(self.h)
+
+    def synchronize(self):
+        self._ok(lib().uaii_backend_synchronize(self.h), "synchronize")
+
+    def details(self) -> str:
+        return lib().uaii_backend_details(self.h).decode()
+
+    def close(self):
+        if self.h:
+            lib().uaii_backend_destroy(self.h)
             self.h = C.c_void_p()
 
     def __enter__(self):
