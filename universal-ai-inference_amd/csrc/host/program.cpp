@@ -323,6 +323,22 @@ Error DecoderProgram::build(const DecoderSpec& spec, const ProgramOptions& opts)
   UAII_TRY(build_layers(alloc));
   UAII_TRY(alloc(1024, (void**)&ring_pad_));
   {
+    // UAII_ATTN_MERGE=1: the split merge inside the attention kernel when 8 kv
+    // heads meet 8 XCDs with the co-location the probe confirms (the same
+    // results bit for bit). Off by default: on the 8B decode it measured 11.95
+    // against 12.39 us for split + merge kernel and 492.2 against 493.5 tok/s,
+    // the merging block's chain (store completion, ticket, two rounds of L2
+    // loads) costing about what the second launch does.
+    const char* env = std::getenv("UAII_ATTN_MERGE");
+    const bool want = env && std::string(env) == "1";
+    if (want && opts_.kv_f16 && d.n_kv_heads == 8 && (d.head_dim == 64 || d.head_dim == 128) &&
+        xcd_merge_supported()) {
+      constexpr size_t bytes = sizeof(unsigned) * (32 * 64 + 32);
+      UAII_TRY(alloc(bytes, (void**)&attn_sync_));
+      UAII_HIP(hipMemset(attn_sync_, 0, bytes));
+    }
+  }
+  {
     // the ring kernel measures faster for the residual-add GEMVs (O, down) and
     // slower for QKV and gate/up (whose RMSNorm staging the first loads wait
     // behind); UAII_RING=2 takes all four, 0 none
@@ -878,6 +894,20 @@ Error DecoderProgram::seek(int64_t pos) {
 // kernel that timed out leaves the fail word set and the step's results
 // meaningless; report it (once) to whichever read-back comes first.
 Error DecoderProgram::check_layers_fail() {
+  if (attn_sync_) {
+    unsigned afail = 0;
+    UAII_HIP(hipMemcpy(&afail, attn_sync_ + 32 * 64, sizeof(afail), hipMemcpyDeviceToHost));
+    if (afail) {
+      // the split blocks of a kv head ran on more than one XCD: this step's
+      // attention was not merged; later steps use the merge kernel
+      attn_sync_ = nullptr;
+      for (auto& g : graph_) {  // re-captured with the merge kernel
+        if (g) (void)hipGraphExecDestroy(g);
+        g = nullptr;
+      }
+      return Error::make(ErrorCode::Internal, "decode attention: the key splits of a kv head ran on more than one XCD");
+    }
+  }
   if (!lay_sync_) return Error::success();
   unsigned long long fail = 0;
   UAII_HIP(hipMemcpy(&fail, lay_sync_->w, sizeof(fail), hipMemcpyDeviceToHost));
@@ -1051,6 +1081,7 @@ Error DecoderProgram::encode_step(bool want_logits) {
     at.out = attn_;
     at.part = attn_part_;
     at.splits = attn_splits_;
+    at.sync = attn_sync_;
     const double attn_bytes = 2.0 * (double)(pos_host + 1) * (double)d.kv_dim * (double)elem +
                               8.0 * (double)d.q_dim;
     UAII_TRY(timed("attention", attn_bytes, [&] { return launch_attention_decode(at, s); }));

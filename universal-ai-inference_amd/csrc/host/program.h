@@ -168,6 +168,9 @@ class DecoderProgram {
   int32_t* ids_ = nullptr;
   float2* rope_ = nullptr;
   float* attn_part_ = nullptr;
+  // decode attention merged inside the split kernel: tickets + fail word
+  // (AttnArgs::sync), null when the two-launch path runs
+  unsigned* attn_sync_ = nullptr;
   int attn_splits_ = 1;
 
   // all layers of a decode step in one launch (layers.hip): eligibility, the
