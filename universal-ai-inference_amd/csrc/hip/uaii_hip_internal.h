@@ -166,101 +166,35 @@ hipError_t prepare_attention();
 hipError_t prepare_noalloc();
 size_t noalloc_scratch_bytes();
 
-// ---- all transformer layers of one decode step in one persistent launch -----------
-
-// Weights of one dense SwiGLU layer (device copy of the table, one entry per layer).
-struct LayerW {
-  DevWeight wq, wk, wv, wo, gate, up, down;
-  const float* attn_norm;
-  const float* ffn_norm;
-  const float *bq, *bk, *bv;  // optional QKV biases
-};
-
-// Device-wide counters of k_layers (zero before the first launch; every launch
-// leaves them zero again except `fail`). Each counter sits on its own 128-byte line.
-struct LayersSync {
-  unsigned long long w[16 * (16 + 64)];
-};
-
-struct LayersArgs {
-  const LayerW* layers;  // [n_layers], device memory
-  int n_layers;
-  int64_t dim, q_dim, kv_dim, inter;
-  int n_heads, n_kv, head_dim, rope_mode;
-  float eps;
-  float* x;            // residual stream [dim]
-  float* qkv;          // raw projections [q_dim + 2 kv_dim]
-  float* attn;         // attention output [q_dim]
-  float* h;            // SwiGLU activation [inter]
-  float* part;         // attention split partials [n_kv][splits][G][hd + 2]
-  int splits;          // key splits per kv head (set by launch_layers)
-  void* kv;            // f16 cache: layer l K at kv + 2 l layer_bytes, V at + layer_bytes
-  int64_t max_seq;
-  const float2* rope;  // [max_seq][hd / 2]
-  const StepState* state;
-  float* tap_r1;       // [n_layers][dim] residual after attention, or null
-  float* tap_r2;       // [n_layers][dim] residual after the FFN, or null
-  LayersSync* sync;
-  const uint8_t* pad;  // >= 1 KiB of device memory read by the padding DMA lines
-  unsigned long long timeout;  // s_memrealtime ticks a device-wide wait may take
-};
-
-// Whether launch_layers can run a model of this shape (all seven matrices of
-// every layer of one type; see layers.hip for the shape rules).
-bool layers_supported(int type, int n_layers, int64_t dim, int64_t q_dim, int64_t kv_dim, int64_t inter,
-                      int n_heads, int n_kv, int head_dim);
-// Attention splits per kv head the launch uses (partial buffer sizing).
-int layers_splits(int n_kv);
-// Once per process, outside stream capture: the kernel's LDS limit and fit check.
-hipError_t prepare_layers(int head_dim, int G);
-hipError_t launch_layers(const LayersArgs& a, int type, hipStream_t s);
-
 // ---- one decode GEMV with its weights streamed through an LDS ring ----------------
 
 // Loader waves fetch the block's rows global -> LDS while compute waves take
-// stages out of LDS (layers.hip), so the dot products never hold back the next
-// loads. Q4_0 only; see ring_gemv_supported for the shapes.
-// The input fields lead (the kernel loads its input before anything else).
+// stages out of LDS (ring_gemv.hip), so the dot products never hold back the
+// next loads. Q4_0 only, EPI_STORE / EPI_ADD; see ring_gemv_supported for the
+// shapes. The input fields lead (the kernel loads its input before anything else).
 struct RingArgs {
   const float* x;        // input [K]
   const float* norm_w;   // RMSNorm weight or null
   int64_t K;
   float eps;
-  int nseg;
-  int epi;               // EPI_STORE, EPI_ADD, EPI_QKV (RoPE mode 0), EPI_SWIGLU, EPI_LOGITS
+  int epi;               // EPI_STORE or EPI_ADD
   // set by launch_ring_gemv: stages per block (tq, plus one for blocks below tr)
   int32_t tq, tr;
-  DevWeight w[3];        // stacked row segments (Q, K, V), or gate (0) / up (1) for EPI_SWIGLU
-  int64_t rows[3];       // rows per segment (EPI_SWIGLU: rows[0] = output size)
-  float* y;              // output (EPI_QKV: q)
+  DevWeight w;
+  int64_t rows;          // output rows (<= w.rows)
+  float* y;              // output
   float* tap;            // EPI_ADD: copy of each written value, or null
-  // EPI_QKV
-  const float* bias[3];
-  void* kcache;          // layer base [n_kv][max_seq][hd]
-  void* vcache;
-  int kv_f16;
-  int64_t max_seq;
-  int head_dim;
-  const float2* rope;    // [max_seq][hd / 2]
-  const StepState* state;
   const uint8_t* pad;    // >= 1 KiB of device memory read by the padding DMA lines
-  // EPI_LOGITS: the staged (normed) input copied to xtap by block 0 when set, and
-  // per compute wave a (max, lowest index) partial of the greedy argmax at
-  // part_val/part_idx[block * 8 + wave] (ring_logits_parts() entries)
-  float* xtap;
-  float* part_val;
-  int32_t* part_idx;
 };
-
-// Argmax partials a ring EPI_LOGITS launch writes (one per compute wave).
-int ring_logits_parts();
-// The final argmax + token advance over `nparts` partials (k_argmax_final).
-hipError_t launch_argmax_final(float* part_val, int32_t* part_idx, int nparts, StepState* state,
-                               int32_t* ids, hipStream_t s);
 
 bool ring_gemv_supported(const RingArgs& a);
 hipError_t prepare_ring_gemv();
 hipError_t launch_ring_gemv(const RingArgs& a, hipStream_t s);
+
+// The final argmax + token advance over `nparts` partials (k_argmax_final).
+hipError_t launch_argmax_final(float* part_val, int32_t* part_idx, int nparts, StepState* state,
+                               int32_t* ids, hipStream_t s);
+
 
 // ---- prefill (M > 1 prompt tokens, matrix cores) ---------------------------------------
 

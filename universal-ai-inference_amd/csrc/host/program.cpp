@@ -286,7 +286,7 @@ Error DecoderProgram::build(const DecoderSpec& spec, const ProgramOptions& opts)
   lm.K = d.dim;
   lm.seg[0].w = d.tied ? tok_embd_.view : output_.view;
   lm.seg[0].rows = d.vocab;
-  lm_blocks_ = std::max(gemv_grid(lm), ring_logits_parts());  // either LM-head route's partials
+  lm_blocks_ = gemv_grid(lm);
   const int lm_blocks = lm_blocks_;
   UAII_TRY(alloc(4 * (size_t)lm_blocks, (void**)&lm_part_val_));
   UAII_TRY(alloc(4 * (size_t)lm_blocks, (void**)&lm_part_idx_));
@@ -320,7 +320,6 @@ Error DecoderProgram::build(const DecoderSpec& spec, const ProgramOptions& opts)
   // Q4_0 GEMMs take their high nibbles in place (PfAct::hi16) where every
   // consumer of a prep is one; UAII_PF_H16=0 keeps the shifted decode
   if (const char* env = std::getenv("UAII_PF_H16")) pf_h16_ = std::string(env) != "0";
-  UAII_TRY(build_layers(alloc));
   UAII_TRY(alloc(1024, (void**)&ring_pad_));
   {
     // UAII_ATTN_MERGE=1: the split merge inside the attention kernel when 8 kv
@@ -339,65 +338,15 @@ Error DecoderProgram::build(const DecoderSpec& spec, const ProgramOptions& opts)
     }
   }
   {
-    // the ring kernel measures faster for the residual-add GEMVs (O, down) and
-    // slower for QKV and gate/up (whose RMSNorm staging the first loads wait
-    // behind); UAII_RING=2 takes all four, 0 none
+    // the ring kernel measures faster for the residual-add GEMVs (O, down; the
+    // QKV and gate/up GEMVs measured slower on it, their RMSNorm staging waiting
+    // behind the first loads, as did the LM head); UAII_RING=0 keeps every
+    // projection on gemv.hip
     const char* env = std::getenv("UAII_RING");
     ring_mode_ = env ? std::atoi(env) : 1;
     if (prepare_ring_gemv() != hipSuccess) ring_mode_ = 0;
     (void)hipGetLastError();
-    // the LM head on the ring (argmax partials per compute wave) measured 66.8
-    // against 63.6 us for the GEMV on the 8B decode; UAII_RING_LM=1 opts in
-    const char* lm = std::getenv("UAII_RING_LM");
-    ring_lm_ = ring_mode_ >= 1 && lm && std::string(lm) == "1";
   }
-  return Error::success();
-}
-
-// The one-launch layer kernel (UAII_LAYERS=1; off by default: on the 8B
-// decode it measures 362 tok/s against 428 for the per-layer launches) takes
-// dense SwiGLU models whose seven layer matrices share one block format, with
-// an f16 KV cache.
-template <class Alloc>
-Error DecoderProgram::build_layers(Alloc&& alloc) {
-  const DecoderSpec& d = spec_;
-  const char* env = std::getenv("UAII_LAYERS");
-  lay_ok_ = env && std::string(env) == "1" && opts_.kv_f16 && !moe_ && d.n_layers > 0;
-  if (!lay_ok_) return Error::success();
-  const int64_t inter = d.layers[0].inter;
-  lay_type_ = layers_[0]->wq.view.type;
-  for (int64_t li = 0; lay_ok_ && li < d.n_layers; ++li) {
-    const Layer& L = *layers_[(size_t)li];
-    const LayerSpec& ls = d.layers[(size_t)li];
-    if (ls.ffn != LayerSpec::kSwiGLU || ls.inter != inter || !L.attn_norm || !L.ffn_norm) lay_ok_ = false;
-    for (const DeviceWeight* w : {&L.wq, &L.wk, &L.wv, &L.wo, &L.gate, &L.up, &L.down})
-      if (w->view.type != lay_type_) lay_ok_ = false;
-  }
-  lay_ok_ = lay_ok_ && layers_supported(lay_type_, (int)d.n_layers, d.dim, d.q_dim, d.kv_dim, inter,
-                                        (int)d.n_heads, (int)d.n_kv_heads, (int)d.head_dim);
-  if (!lay_ok_) return Error::success();
-  std::vector<LayerW> tab((size_t)d.n_layers);
-  lay_wbytes_ = 0.0;
-  for (int64_t li = 0; li < d.n_layers; ++li) {
-    const Layer& L = *layers_[(size_t)li];
-    LayerW& t = tab[(size_t)li];
-    t.wq = L.wq.view; t.wk = L.wk.view; t.wv = L.wv.view; t.wo = L.wo.view;
-    t.gate = L.gate.view; t.up = L.up.view; t.down = L.down.view;
-    t.attn_norm = L.attn_norm; t.ffn_norm = L.ffn_norm;
-    t.bq = L.bq; t.bk = L.bk; t.bv = L.bv;
-    for (const DeviceWeight* w : {&L.wq, &L.wk, &L.wv, &L.wo, &L.gate, &L.up, &L.down})
-      lay_wbytes_ += gemv_bytes(w->view);
-  }
-  UAII_TRY(alloc(sizeof(LayerW) * tab.size(), (void**)&lay_tab_));
-  UAII_HIP(hipMemcpy(lay_tab_, tab.data(), sizeof(LayerW) * tab.size(), hipMemcpyHostToDevice));
-  UAII_TRY(alloc(sizeof(LayersSync), (void**)&lay_sync_));
-  UAII_TRY(alloc(1024, (void**)&lay_pad_));
-  UAII_TRY(alloc(4 * (size_t)(d.q_dim + 2 * d.kv_dim), (void**)&lay_qkv_));
-  const int G = (int)(d.n_heads / d.n_kv_heads);
-  const size_t part = (size_t)d.n_kv_heads * (size_t)layers_splits((int)d.n_kv_heads) * (size_t)G *
-                      (size_t)(d.head_dim + 2);
-  UAII_TRY(alloc(4 * part, (void**)&lay_part_));
-  UAII_HIP(prepare_layers((int)d.head_dim, G));
   return Error::success();
 }
 
@@ -890,10 +839,9 @@ Error DecoderProgram::seek(int64_t pos) {
   return Error::success();
 }
 
-// After the stream has drained: a device-wide wait of the one-launch layer
-// kernel that timed out leaves the fail word set and the step's results
-// meaningless; report it (once) to whichever read-back comes first.
-Error DecoderProgram::check_layers_fail() {
+// After the stream has drained: a fail word a kernel set leaves the step's
+// results meaningless; report it (once) to whichever read-back comes first.
+Error DecoderProgram::check_device_fail() {
   if (attn_sync_) {
     unsigned afail = 0;
     UAII_HIP(hipMemcpy(&afail, attn_sync_ + 32 * 64, sizeof(afail), hipMemcpyDeviceToHost));
@@ -908,33 +856,26 @@ Error DecoderProgram::check_layers_fail() {
       return Error::make(ErrorCode::Internal, "decode attention: the key splits of a kv head ran on more than one XCD");
     }
   }
-  if (!lay_sync_) return Error::success();
-  unsigned long long fail = 0;
-  UAII_HIP(hipMemcpy(&fail, lay_sync_->w, sizeof(fail), hipMemcpyDeviceToHost));
-  if (fail) {
-    UAII_HIP(hipMemset(lay_sync_, 0, sizeof(LayersSync)));
-    return Error::make(ErrorCode::Internal, "decode layer kernel: a device-wide wait timed out");
-  }
   return Error::success();
 }
 
 Error DecoderProgram::read_state(StepState* st) {
   UAII_HIP(hipStreamSynchronize(stream_));
-  UAII_TRY(check_layers_fail());
+  UAII_TRY(check_device_fail());
   UAII_HIP(hipMemcpy(st, state_, sizeof(StepState), hipMemcpyDeviceToHost));
   return Error::success();
 }
 
 Error DecoderProgram::synchronize() {
   UAII_HIP(hipStreamSynchronize(stream_));
-  return check_layers_fail();
+  return check_device_fail();
 }
 
 Error DecoderProgram::read_ids(int64_t* out, int64_t n) {
   if (n > max_ctx_ + 1) return Error::make(ErrorCode::InvalidArgument, "read_ids beyond capacity");
   std::vector<int32_t> ids((size_t)n);
   UAII_HIP(hipStreamSynchronize(stream_));
-  UAII_TRY(check_layers_fail());
+  UAII_TRY(check_device_fail());
   UAII_HIP(hipMemcpy(ids.data(), ids_, (size_t)n * 4, hipMemcpyDeviceToHost));
   for (int64_t i = 0; i < n; ++i) out[i] = ids[(size_t)i];
   return Error::success();
@@ -944,7 +885,7 @@ Error DecoderProgram::read_id(int64_t index, int64_t* id) {
   if (index < 0 || index > max_ctx_) return Error::make(ErrorCode::InvalidArgument, "read_id beyond capacity");
   int32_t v = 0;
   UAII_HIP(hipStreamSynchronize(stream_));
-  UAII_TRY(check_layers_fail());
+  UAII_TRY(check_device_fail());
   UAII_HIP(hipMemcpy(&v, ids_ + index, 4, hipMemcpyDeviceToHost));
   *id = v;
   return Error::success();
@@ -986,37 +927,7 @@ Error DecoderProgram::encode_step(bool want_logits) {
   if (opts_.profile) {
     UAII_HIP(hipMemcpy(&pos_host, &state_->pos, 4, hipMemcpyDeviceToHost));
   }
-  if (lay_ok_) {
-    LayersArgs la{};
-    la.layers = lay_tab_;
-    la.n_layers = (int)d.n_layers;
-    la.dim = d.dim;
-    la.q_dim = d.q_dim;
-    la.kv_dim = d.kv_dim;
-    la.inter = d.layers[0].inter;
-    la.n_heads = (int)d.n_heads;
-    la.n_kv = (int)d.n_kv_heads;
-    la.head_dim = (int)d.head_dim;
-    la.rope_mode = d.rope_mode;
-    la.eps = d.rms_eps;
-    la.x = x_;
-    la.qkv = lay_qkv_;
-    la.attn = attn_;
-    la.h = h_;
-    la.part = lay_part_;
-    la.kv = kv_;
-    la.max_seq = max_ctx_;
-    la.rope = rope_;
-    la.state = state_;
-    la.tap_r1 = tap_r1_;
-    la.tap_r2 = tap_r2_;
-    la.sync = lay_sync_;
-    la.pad = lay_pad_;
-    la.timeout = 20000000ull;  // 0.2 s of the 100 MHz s_memrealtime clock per wait
-    const double kv_read = 2.0 * (double)pos_host * (double)d.kv_dim * (double)elem * (double)d.n_layers;
-    UAII_TRY(timed("layers", lay_wbytes_ + kv_read, [&] { return launch_layers(la, lay_type_, s); }));
-  }
-  for (int64_t li = 0; !lay_ok_ && li < d.n_layers; ++li) {
+  for (int64_t li = 0; li < d.n_layers; ++li) {
     const Layer& L = *layers_[(size_t)li];
     const LayerSpec& ls = d.layers[(size_t)li];
     uint8_t* kbase = static_cast<uint8_t*>(kv_) + (size_t)li * 2 * layer_kv;
@@ -1042,30 +953,7 @@ Error DecoderProgram::encode_step(bool want_logits) {
     a.rope = rope_;
     a.state = state_;
     const double qkv_bytes = gemv_bytes(L.wq.view) + gemv_bytes(L.wk.view) + gemv_bytes(L.wv.view);
-    RingArgs rq{};
-    rq.w[0] = L.wq.view; rq.w[1] = L.wk.view; rq.w[2] = L.wv.view;
-    rq.rows[0] = d.q_dim; rq.rows[1] = d.kv_dim; rq.rows[2] = d.kv_dim;
-    rq.nseg = 3;
-    rq.epi = EPI_QKV;
-    rq.K = d.dim;
-    rq.x = x_;
-    rq.norm_w = L.attn_norm;
-    rq.eps = d.rms_eps;
-    rq.y = q_;
-    rq.bias[0] = L.bq; rq.bias[1] = L.bk; rq.bias[2] = L.bv;
-    rq.kcache = kbase;
-    rq.vcache = vbase;
-    rq.kv_f16 = opts_.kv_f16 ? 1 : 0;
-    rq.max_seq = max_ctx_;
-    rq.head_dim = (int)d.head_dim;
-    rq.rope = rope_;
-    rq.state = state_;
-    rq.pad = ring_pad_;
-    if (ring_mode_ >= 2 && d.rope_mode == 0 && ring_gemv_supported(rq)) {
-      UAII_TRY(timed("gemv_qkv", qkv_bytes, [&] { return launch_ring_gemv(rq, s); }));
-    } else {
-      UAII_TRY(timed("gemv_qkv", qkv_bytes, [&] { return launch_gemv(a, s); }));
-    }
+    UAII_TRY(timed("gemv_qkv", qkv_bytes, [&] { return launch_gemv(a, s); }));
 
     AttnArgs at{};
     at.q = q_;
@@ -1097,9 +985,8 @@ Error DecoderProgram::encode_step(bool want_logits) {
     o.seg[0].rows = d.dim;
     o.state = state_;
     RingArgs ro{};
-    ro.w[0] = L.wo.view;
-    ro.rows[0] = d.dim;
-    ro.nseg = 1;
+    ro.w = L.wo.view;
+    ro.rows = d.dim;
     ro.epi = EPI_ADD;
     ro.K = d.q_dim;
     ro.x = attn_;
@@ -1125,24 +1012,8 @@ Error DecoderProgram::encode_step(bool want_logits) {
       g.seg[0].w2 = L.up.view;
       g.seg[0].rows = 2 * ls.inter;
       g.state = state_;
-      RingArgs rg{};
-      rg.w[0] = L.gate.view;
-      rg.w[1] = L.up.view;
-      rg.rows[0] = ls.inter;
-      rg.nseg = 2;
-      rg.epi = EPI_SWIGLU;
-      rg.K = d.dim;
-      rg.x = x_;
-      rg.norm_w = L.ffn_norm;
-      rg.eps = d.rms_eps;
-      rg.y = h_;
-      rg.pad = ring_pad_;
       const double gu_bytes = gemv_bytes(L.gate.view) + gemv_bytes(L.up.view);
-      if (ring_mode_ >= 2 && ring_gemv_supported(rg)) {
-        UAII_TRY(timed("gemv_gate_up", gu_bytes, [&] { return launch_ring_gemv(rg, s); }));
-      } else {
-        UAII_TRY(timed("gemv_gate_up", gu_bytes, [&] { return launch_gemv(g, s); }));
-      }
+      UAII_TRY(timed("gemv_gate_up", gu_bytes, [&] { return launch_gemv(g, s); }));
       GemvArgs dn{};
       dn.nseg = 1;
       dn.epi = EPI_ADD;
@@ -1154,9 +1025,8 @@ Error DecoderProgram::encode_step(bool want_logits) {
       dn.seg[0].rows = d.dim;
       dn.state = state_;
       RingArgs rd{};
-      rd.w[0] = L.down.view;
-      rd.rows[0] = d.dim;
-      rd.nseg = 1;
+      rd.w = L.down.view;
+      rd.rows = d.dim;
       rd.epi = EPI_ADD;
       rd.K = ls.inter;
       rd.x = h_;
@@ -1321,29 +1191,7 @@ Error DecoderProgram::encode_step(bool want_logits) {
     lm.part_cap = lm_blocks_;
     lm.ids = ids_;
     lm.state = state_;
-    RingArgs rl{};
-    rl.w[0] = lm.seg[0].w;
-    rl.rows[0] = d.vocab;
-    rl.nseg = 1;
-    rl.epi = EPI_LOGITS;
-    rl.K = d.dim;
-    rl.x = x_;
-    rl.norm_w = out_norm_;
-    rl.eps = d.rms_eps;
-    rl.y = logits_;
-    rl.xtap = tap_normed_;
-    rl.part_val = lm_part_val_;
-    rl.part_idx = lm_part_idx_;
-    rl.pad = ring_pad_;
-    if (ring_lm_ && ring_gemv_supported(rl) && ring_logits_parts() <= lm_blocks_) {
-      UAII_TRY(timed("gemv_lm_head", gemv_bytes(lm.seg[0].w), [&] {
-        hipError_t e = launch_ring_gemv(rl, s);
-        if (e == hipSuccess) e = launch_argmax_final(lm_part_val_, lm_part_idx_, ring_logits_parts(), state_, ids_, s);
-        return e;
-      }));
-    } else {
-      UAII_TRY(timed("gemv_lm_head", gemv_bytes(lm.seg[0].w), [&] { return launch_gemv(lm, s); }));
-    }
+    UAII_TRY(timed("gemv_lm_head", gemv_bytes(lm.seg[0].w), [&] { return launch_gemv(lm, s); }));
   } else {
     UAII_TRY(timed("advance", 0.0, [&] { return launch_advance(state_, ids_, s); }));
   }
@@ -1395,7 +1243,7 @@ Error DecoderProgram::read_tap(const std::string& name, std::vector<float>* out)
   }
   out->resize(n);
   UAII_HIP(hipStreamSynchronize(stream_));
-  UAII_TRY(check_layers_fail());
+  UAII_TRY(check_device_fail());
   UAII_HIP(hipMemcpy(out->data(), src, n * 4, hipMemcpyDeviceToHost));
   return Error::success();
 }

@@ -120,7 +120,7 @@ class DecoderProgram {
   template <class F>
   Error timed(const char* name, double bytes, double flops, F&& launch);
   Error collect_timings();
-  Error check_layers_fail();
+  Error check_device_fail();
   Error ensure_prefill_buffers(int64_t chunk);
   Error pf_gemm(const DeviceWeight* w[3], const int64_t cols0[3], int nw, const DeviceWeight* w2,
                 int epi, int64_t m, float* y, int64_t ldy, int store_split = 1);
@@ -129,8 +129,6 @@ class DecoderProgram {
   template <class Prep, class Gemm>
   Error prefill_moe(const Layer& L, const LayerSpec& ls, int64_t m, Prep&& prep, Gemm&& gemm);
   Error encode_step(bool want_logits);
-  template <class Alloc>
-  Error build_layers(Alloc&& alloc);
   void free_dynamic();
 
   DecoderSpec spec_;
@@ -150,7 +148,6 @@ class DecoderProgram {
   int32_t* lm_part_idx_ = nullptr;
   int lm_blocks_ = 0;  // capacity of the LM-head partial buffers
   bool pf_h16_ = true;    // Q4_0 prefill GEMMs on PfAct::hi16 activations (UAII_PF_H16=0: off)
-  bool ring_lm_ = false;  // the LM head on the ring GEMV (UAII_RING_LM=1; off by default)
   // profiling mode: start/stop event pairs and their (kernel name, bytes) per launch group
   struct ProfTag {
     std::string name;
@@ -173,18 +170,8 @@ class DecoderProgram {
   unsigned* attn_sync_ = nullptr;
   int attn_splits_ = 1;
 
-  // all layers of a decode step in one launch (layers.hip): eligibility, the
-  // device layer table, device-wide counters and the launch's own buffers
-  bool lay_ok_ = false;
-  int lay_type_ = 0;
-  uaii_hip::LayerW* lay_tab_ = nullptr;
-  uaii_hip::LayersSync* lay_sync_ = nullptr;
-  uint8_t* lay_pad_ = nullptr;
-  float* lay_qkv_ = nullptr;
-  float* lay_part_ = nullptr;
-  double lay_wbytes_ = 0.0;  // weight bytes the launch streams
-  // decode GEMVs through the LDS ring (layers.hip) where the shapes allow:
-  // 0 none, 1 the residual-add GEMVs (O, down), 2 also QKV and gate/up
+  // the residual-add GEMVs (O, down) through the LDS ring (ring_gemv.hip) where
+  // the shapes allow: 1 (default) or 0 none
   int ring_mode_ = 0;
   uint8_t* ring_pad_ = nullptr;
 
