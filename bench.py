@@ -201,6 +201,41 @@ def parity_check(path: str, n_prompt: int, n_new: int, layers: int, threads: int
             "ids_match": bool(np.array_equal(got, want)), "against": "oracle (f16 KV)"}
 
 
+def sampled_rates(uaii_amd, sess, prompt, ctx: int, K: int):
+    """Sampled decode rate at the headline context, host sampler (the
+    reference's method: the logits row to the host each token, session.cpp:974-978)
+    and device sampler (uaii_session_set_device_sampler): two seeded
+    generate_sampled runs of `base` and `base + K` new tokens over the same
+    prompt; K over the difference of their wall times is the per-token rate with
+    the prefill cancelled out."""
+    base = 8
+    pr = prompt[: ctx - base - K]
+    out = {"method": f"{K} tokens: wall time of generate_sampled(+{base + K}) minus (+{base}), "
+                     f"prompt {len(pr)}"}
+    for name, (t, tp, tk, rp) in (("T0.8_p0.9_k40", (0.8, 0.9, 40, 1.0)), ("T1_p0.9", (1.0, 0.9, 0, 1.0))):
+        res, ids = {}, {}
+        for mode in ("host", "device"):
+            sess.set_device_sampler(mode == "device")
+            prm = uaii_amd.sample_params(t, tp, tk, rp, seed=1234)
+            sess.generate_sampled(pr, base, prm)  # graphs captured, buffers sized
+            t0 = time.perf_counter()
+            sess.generate_sampled(pr, base, prm)
+            ta = time.perf_counter() - t0
+            t0 = time.perf_counter()
+            ids[mode] = sess.generate_sampled(pr, base + K, prm)
+            tb = time.perf_counter() - t0
+            res[f"{mode}_tok_s"] = round(K / (tb - ta), 1)
+        sess.set_device_sampler(False)
+        gh, gd = ids["host"][len(pr):].tolist(), ids["device"][len(pr):].tolist()
+        same = 0
+        while same < min(len(gh), len(gd)) and gh[same] == gd[same]:
+            same += 1
+        res["equal_leading_ids"] = same
+        res["tokens"] = base + K
+        out[name] = res
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -214,6 +249,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-profile", action="store_true")
     ap.add_argument("--no-parity", action="store_true")
+    ap.add_argument("--no-sampled", action="store_true")
+    ap.add_argument("--sampled-steps", type=int, default=128)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); "
@@ -358,6 +395,14 @@ def main() -> int:
                     "gemv_attn_frac": round(agg_b / (agg_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                     "kernel_ms_per_step": round(step_ms, 4),
                     "profiled_steps": P, "profiled_replay_ids_match": replay_ok}
+    sampled = None
+    if not args.no_sampled:
+        try:
+            sampled = sampled_rates(uaii_amd, sess, prompt, ctx, args.sampled_steps)
+            log(f"sampled decode {sampled}")
+        except Exception as e:
+            log(f"sampled decode unavailable: {e}")
+            sampled = {"error": str(e)}
     sess.close()
 
     parity = None
@@ -401,6 +446,7 @@ def main() -> int:
         "kernels": {n: {"avg_us": round(v["avg_us"], 2), "gbps": round(v["gbps"], 1),
                         "launches_per_step": v["launches"] / max(1, P)}
                     for n, v in kernels.items()},
+        "sampled_tok_s": sampled,
         "parity": parity,
         "cpu_baseline": cpu,
     }

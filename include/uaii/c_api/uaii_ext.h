@@ -85,6 +85,18 @@ UAII_CAPI_API uaii_status uaii_session_generate_sampled(uaii_session* session,
                                                         int64_t* out_tokens, size_t capacity,
                                                         size_t* out_n);
 
+/** Non-greedy draws of uaii_session_generate_sampled on the device (on != 0)
+ * instead of on the host: the same parameters, penalty history and generator
+ * draws (one uniform per generated token, taken from the seeded mt19937_64
+ * before the run), with the pick made where the logits are, so only token ids
+ * cross PCIe. The reference samples on the host; this switch has no
+ * counterpart there. Ids equal the host sampler's except where a draw lands
+ * within float rounding of a cumulative boundary, on tied scores, or with
+ * top_k alone (walked in descending order rather than std::nth_element's, the
+ * same distribution). UAII_ERR_NOT_IMPLEMENTED for vocabularies above 262144.
+ * UAII_DEVICE_SAMPLER=1 in the environment turns it on for new sessions. */
+UAII_CAPI_API uaii_status uaii_session_set_device_sampler(uaii_session* session, int on);
+
 /** One draw of the sampler (sampling.cpp:22-125) over row[0..vocab) with a fresh
  * mt19937_64(params->seed); penalty ids as the reference's history. Host only. */
 UAII_CAPI_API uaii_status uaii_sample_token(const float* row, size_t vocab,

@@ -21,6 +21,7 @@
  *   uaii_hip_rmsnorm           rmsnorm_f32 (libs/uaii-kernels/src/norm.cpp:89-130)
  *   uaii_hip_softmax           softmax_f32 (libs/uaii-kernels/src/softmax.cpp:11-77)
  *   uaii_hip_argmax            greedy sample_token_f32 (libs/uaii-runtime/src/sampling.cpp:38-50)
+ *   uaii_hip_sample            non-greedy sample_token_f32 (sampling.cpp:53-125) on the device
  *   uaii_hip_rope              rope_f32 (libs/uaii-kernels/src/transformer.cpp:144-220)
  *   uaii_hip_attention_decode  attention_kv_f32, q_seq=1 (transformer.cpp:222-433)
  *   uaii_hip_gemv_add          quant_gemm_f32 + residual add_f32 (elementwise.cpp:86-97)
@@ -122,6 +123,25 @@ UAII_HIP_API int uaii_hip_kv_append(const float* k, const float* v, void* kcache
                                     int64_t rows, int64_t kv_dim, int head_dim, int64_t max_seq,
                                     int64_t p0, int kv_f16, void* stream);
 UAII_HIP_API int uaii_hip_argmax(const float* x, int64_t n, int32_t* out_idx, void* stream);
+/* Device sampling: one draw of sample_token_f32's non-greedy path
+ * (libs/uaii-runtime/src/sampling.cpp:53-125) from a device logits row of
+ * `vocab` floats (at most 262144), with the reference's temperature, top_p,
+ * top_k and repetition penalty over the `n_pen` device ids `pen`, and the draw
+ * `r` in [0, 1] that the reference takes from its generator (uaii_sample_uniforms
+ * gives the same sequence). The reference samples on the host; this entry has no
+ * counterpart there and serves token loops that keep the logits on the device.
+ * workspace: device memory of uaii_hip_sample_workspace_bytes(vocab) bytes,
+ * 256-byte aligned; calls sharing one workspace must not overlap. The id is
+ * written to the device int32 at out_idx. */
+UAII_HIP_API int64_t uaii_hip_sample_workspace_bytes(int64_t vocab);
+UAII_HIP_API int uaii_hip_sample(const float* logits, int64_t vocab, float temperature, float top_p,
+                                 int top_k, float repetition_penalty, const int32_t* pen,
+                                 int64_t n_pen, float r, int32_t* out_idx, void* workspace,
+                                 void* stream);
+/* Host: n draws of std::uniform_real_distribution<float>(0, 1) from
+ * std::mt19937_64(seed), the per-token draws of sample_token_f32
+ * (sampling.cpp:111-112) in order. */
+UAII_HIP_API int uaii_sample_uniforms(uint64_t seed, int64_t n, float* out);
 /* table: [max_pos][head_dim/2] (cos, sin) float pairs, filled on the host with
  * the reference's angle formula, uploaded to `table_dev`. */
 UAII_HIP_API int uaii_hip_rope_table(float theta, int head_dim, int64_t max_pos,

@@ -194,6 +194,60 @@ def test_generate_sampled_matches_reference(prm):
     assert len(set(ids[12:].tolist())) > 1
 
 
+@pytest.mark.parametrize("prm", [(0.8, 0.9, 40, 1.1), (1.0, 0.9, 0, 1.0), (0.7, 1.0, 0, 1.3)],
+                         ids=lambda p: f"T{p[0]}_p{p[1]}_k{p[2]}_r{p[3]}")
+def test_device_sampler_generate_matches_host(prm):
+    """The device sampler (uaii_session_set_device_sampler) picks the ids the host
+    sampler picks from the same logits, seed and history, with top_p or with
+    neither top_k nor top_p (walks in the reference's order). Where a run
+    differs, the first differing token must be a boundary case: on that step's
+    logits row and history, the device's picks at r -/+ (2e-4 + 6e-8 * vocab)
+    bracket the host's (the reference's float prefix sums against exact integer
+    ones). Afterwards greedy generation on the same session is unchanged."""
+    import test_gpu_sampler as ts
+    cfg = SMALL["gqa_q4_0"]
+    path = synth.cached_model(cfg)
+    prompt = prompt_for(cfg, 12, 99)
+    n_new = 24
+    t, tp, tk, rp = prm
+    descending = tk > 0 or tp < 1.0 - 1e-6
+    with uaii_amd.Session(path) as s:
+        greedy = s.generate(prompt, 16)
+        runs = {}
+        for seed in (11, 12, 13):
+            prms = uaii_amd.sample_params(t, tp, tk, rp, seed=seed)
+            s.set_device_sampler(False)
+            host = s.generate_sampled(prompt, n_new, prms)
+            s.set_device_sampler(True)
+            dev = s.generate_sampled(prompt, n_new, prms)
+            assert np.array_equal(s.generate_sampled(prompt, n_new, prms), dev)  # replayable
+            runs[seed] = (host, dev)
+        assert np.array_equal(s.generate(prompt, 16), greedy)
+        s.set_device_sampler(False)
+        equal = 0
+        sampler = ts.DevSampler(cfg.vocab)
+        for seed, (host, dev) in runs.items():
+            assert len(set(dev[12:].tolist())) > 1
+            if np.array_equal(host, dev):
+                equal += 1
+                continue
+            f = int(np.nonzero(host != dev)[0][0])  # first differing position
+            s.generate_sampled(prompt, f - len(prompt) + 1, uaii_amd.sample_params(t, tp, tk, rp, seed=seed))
+            row = np.asarray(s.get("logits"), np.float32)
+            hist = host[:f].tolist()
+            r = float(uaii_amd.sample_uniforms(seed, f - len(prompt) + 1)[-1])
+            sampler.load(row, hist)
+            d = 2e-4 + 6e-8 * cfg.vocab
+            lo, hi = sampler(prm, max(r - d, 0.0)), sampler(prm, min(r + d, 1.0))
+            if descending:
+                sc = ts.scores(row, prm, hist)
+                tol = 4e-7 * (1.0 + abs(float(sc.max()) - float(sc[host[f]])))
+                assert sc[hi] - tol <= sc[host[f]] <= sc[lo] + tol, (seed, f)
+            else:
+                assert lo <= host[f] <= hi, (seed, f, lo, host[f], hi)
+        assert equal >= 1
+
+
 @pytest.mark.parametrize("prm", [(0.05, 1.0, 0, 1.0), (0.7, 0.9, 0, 1.3)], ids=lambda p: f"T{p[0]}_p{p[1]}_r{p[3]}")
 def test_generate_sampled_draws_from_logits(prm):
     """The first sampled token is the reference sampler's draw over the device's

@@ -69,3 +69,29 @@ def test_sampler_distribution_follows_softmax_of_logits():
     flat = np.exp(logits - logits.max()) / np.exp(logits - logits.max()).sum()
     resoft = np.exp(flat) / np.exp(flat).sum()
     assert abs(resoft[0] - 0.84) > 0.3  # the probs-reading mistake is far outside the bar
+
+
+def test_uniforms_are_the_reference_draws():
+    """uaii_sample_uniforms(seed, n) gives the r the reference's sampler draws
+    (sampling.cpp:111-112) from mt19937_64(seed): over a flat-ish row walked in
+    index order (no top-k / top-p) the reference picks the first id whose
+    cumulative probability reaches r, which fixes r to within one id's mass."""
+    if oracle.ref() is None:
+        pytest.skip("reference kernels not built (make -C oracle ref needs /root/reference)")
+    V = 1000
+    row = np.random.default_rng(3).normal(0, 0.5, V).astype(np.float32)
+    e = np.exp(row.astype(np.float64) - row.max())
+    cum = np.cumsum(e / e.sum())
+    checked = 0
+    for seed in range(150):
+        r = float(uaii_amd.sample_uniforms(seed, 1)[0])
+        want = oracle.ref_sample_token(row, 1.0, 1.0, 0, 1.0, seed, [])
+        if np.abs(cum - r).min() < 1e-6:
+            continue  # within float rounding of a boundary
+        assert want == int(np.searchsorted(cum, r)), (seed, r)
+        checked += 1
+    assert checked >= 140
+    # a sequence is the generator's successive draws: the first of n equals n = 1
+    seq = uaii_amd.sample_uniforms(77, 5)
+    assert seq[0] == uaii_amd.sample_uniforms(77, 1)[0] and len(set(seq.tolist())) == 5
+    assert np.all((seq >= 0) & (seq < 1))

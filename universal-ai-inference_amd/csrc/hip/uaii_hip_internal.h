@@ -191,6 +191,34 @@ bool ring_gemv_supported(const RingArgs& a);
 hipError_t prepare_ring_gemv();
 hipError_t launch_ring_gemv(const RingArgs& a, hipStream_t s);
 
+// ---- sampling (sample.hip) ------------------------------------------------------------
+
+// One draw from the logits row (sample_token_f32's non-greedy path,
+// libs/uaii-runtime/src/sampling.cpp:53-125). With `state`, the penalised ids are
+// ids[0 .. pos], the draw is rbuf[pos + 1 - n_prompt] and the pick kernel
+// advances the token as k_argmax_final does; without it, pen[0 .. n_pen) and
+// r_fixed. `ws`: sample_workspace_bytes(V), 256-byte aligned.
+struct SampleArgs {
+  const float* logits;
+  int64_t V;
+  float inv_t;           // 1 / max(temperature, 1e-5)
+  float top_p;           // active when 0 < top_p < 1 - 1e-6
+  int32_t top_k;         // active when 0 < top_k < V
+  float rep;             // repetition penalty, active when > 1 + 1e-6
+  StepState* state;
+  int32_t* ids;          // history [max_seq + 2]
+  const float* rbuf;     // uniform draws, one per generated token
+  int64_t nr;
+  const int32_t* pen;    // standalone: penalised ids
+  int64_t n_pen;
+  float r_fixed;         // standalone: the draw
+  int32_t* out;          // the sampled id, or null
+  void* ws;
+};
+int sample_max_vocab();
+size_t sample_workspace_bytes(int64_t V);
+hipError_t launch_sample(const SampleArgs& a, hipStream_t s);
+
 // The final argmax + token advance over `nparts` partials (k_argmax_final).
 hipError_t launch_argmax_final(float* part_val, int32_t* part_idx, int nparts, StepState* state,
                                int32_t* ids, hipStream_t s);

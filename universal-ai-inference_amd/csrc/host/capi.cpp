@@ -368,6 +368,17 @@ uaii_status uaii_session_set_profiling(uaii_session* session, int on) {
   return UAII_OK;
 }
 
+uaii_status uaii_session_set_device_sampler(uaii_session* session, int on) {
+  if (session == nullptr) return fail(UAII_ERR_INVALID_ARGUMENT, "session null");
+  auto& sess = reinterpret_cast<SessionHandle*>(session)->session;
+  auto* p = sess.program();
+  if (!p) return fail(UAII_ERR_INVALID_ARGUMENT, "session not ready");
+  if (on && !p->sampler_supported())
+    return fail(UAII_ERR_NOT_IMPLEMENTED, "device sampler: vocabulary too large");
+  sess.set_device_sampler(on != 0);
+  return UAII_OK;
+}
+
 uaii_status uaii_session_last_margin(uaii_session* session, float* best, float* second) {
   if (session == nullptr || best == nullptr || second == nullptr)
     return fail(UAII_ERR_INVALID_ARGUMENT, "null args");

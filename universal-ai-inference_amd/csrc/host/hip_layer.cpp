@@ -5,6 +5,7 @@
 
 #include <cmath>
 #include <mutex>
+#include <random>
 #include <vector>
 
 using namespace uaii_hip;
@@ -325,6 +326,41 @@ int uaii_hip_kv_append(const float* k, const float* v, void* kcache, void* vcach
 int uaii_hip_argmax(const float* x, int64_t n, int32_t* out_idx, void* stream) {
   if (!x || !out_idx || n <= 0) return kErrArg;
   return (int)launch_argmax(x, n, out_idx, S(stream));
+}
+
+int64_t uaii_hip_sample_workspace_bytes(int64_t vocab) {
+  return (int64_t)sample_workspace_bytes(vocab);
+}
+
+int uaii_hip_sample(const float* logits, int64_t vocab, float temperature, float top_p, int top_k,
+                    float repetition_penalty, const int32_t* pen, int64_t n_pen, float r, int32_t* out_idx,
+                    void* workspace, void* stream) {
+  if (!logits || !out_idx || !workspace || vocab <= 0 || vocab > sample_max_vocab() || n_pen < 0 ||
+      (n_pen > 0 && !pen) || !(r >= 0.0f && r <= 1.0f))
+    return kErrArg;
+  SampleArgs a{};
+  a.logits = logits;
+  a.V = vocab;
+  a.inv_t = 1.0f / std::max(temperature, 1e-5f);  // sampling.cpp:63
+  a.top_p = top_p;
+  a.top_k = top_k;
+  a.rep = repetition_penalty;
+  a.pen = pen;
+  a.n_pen = n_pen;
+  a.r_fixed = r;
+  a.out = out_idx;
+  a.ws = workspace;
+  return (int)launch_sample(a, S(stream));
+}
+
+int uaii_sample_uniforms(uint64_t seed, int64_t n, float* out) {
+  if (n < 0 || (n > 0 && !out)) return kErrArg;
+  // the per-token draw of sample_token_f32 (sampling.cpp:111-112) from a seeded
+  // mt19937_64 (session.cpp:989-995)
+  std::mt19937_64 rng(seed);
+  std::uniform_real_distribution<float> dist(0.0f, 1.0f);
+  for (int64_t i = 0; i < n; ++i) out[i] = dist(rng);
+  return 0;
 }
 
 int uaii_hip_rope_table(float theta, int head_dim, int64_t max_pos, float* table_dev) {

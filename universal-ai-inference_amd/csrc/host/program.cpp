@@ -96,6 +96,7 @@ Error upload_weight(int type, const uint8_t* host, int64_t rows, int64_t cols, h
 
 DecoderProgram::~DecoderProgram() {
   free_dynamic();
+  if (samp_r_) (void)hipFree(samp_r_);
   for (void* p : pf_allocs_) (void)hipFree(p);
   for (void* p : allocs_) (void)hipFree(p);
   if (ev0_) (void)hipEventDestroy(ev0_);
@@ -791,6 +792,40 @@ Error DecoderProgram::ensure_capacity(int64_t max_seq) {
   return Error::success();
 }
 
+Error DecoderProgram::arm_sampler(const SamplerParams& prm, const float* r, int64_t n) {
+  if (!sampler_supported())
+    return Error::make(ErrorCode::NotImplemented, "device sampler: vocabulary above " +
+                                                      std::to_string(sample_max_vocab()));
+  if (n < 0 || (n > 0 && !r)) return Error::make(ErrorCode::InvalidArgument, "device sampler: draws");
+  UAII_HIP(hipStreamSynchronize(stream_));
+  if (!samp_ws_) {
+    const size_t b = sample_workspace_bytes(spec_.vocab);
+    UAII_TRY(charge(used_static_, b));
+    UAII_HIP(hipMalloc(&samp_ws_, b));
+    allocs_.push_back(samp_ws_);
+  }
+  if (n > samp_r_cap_) {
+    if (samp_r_) (void)hipFree(samp_r_);
+    samp_r_ = nullptr;
+    samp_r_cap_ = 0;
+    UAII_HIP(hipMalloc((void**)&samp_r_, sizeof(float) * (size_t)n));
+    samp_r_cap_ = n;
+    // the graph holds the old buffer's address
+    if (graph_[2]) (void)hipGraphExecDestroy(graph_[2]);
+    graph_[2] = nullptr;
+  }
+  if (n > 0) UAII_HIP(hipMemcpy(samp_r_, r, sizeof(float) * (size_t)n, hipMemcpyHostToDevice));
+  if (graph_[2] && !(prm == samp_graph_ && n == samp_n_)) {
+    (void)hipGraphExecDestroy(graph_[2]);
+    graph_[2] = nullptr;
+  }
+  samp_ = prm;
+  samp_graph_ = prm;
+  samp_n_ = n;
+  sampler_on_ = true;
+  return Error::success();
+}
+
 Error DecoderProgram::begin(const int64_t* prompt, int64_t n_prompt) {
   if (n_prompt <= 0) return Error::make(ErrorCode::InvalidArgument, "prompt_tokens empty");
   if (n_prompt > max_ctx_) return Error::make(ErrorCode::InvalidArgument, "prompt exceeds KV capacity");
@@ -1174,7 +1209,34 @@ Error DecoderProgram::encode_step(bool want_logits) {
       UAII_HIP(hipMemcpyAsync(tap_r2_ + li * d.dim, x_, 4 * (size_t)d.dim, hipMemcpyDeviceToDevice, s));
     }
   }
-  if (want_logits) {
+  if (want_logits && sampler_on_) {
+    // the normalised LM head into logits_, then the draw and the token advance
+    GemvArgs lm{};
+    lm.nseg = 1;
+    lm.epi = EPI_STORE;
+    lm.K = d.dim;
+    lm.x = x_;
+    lm.norm_w = out_norm_;
+    lm.eps = d.rms_eps;
+    lm.y = logits_;
+    lm.xtap = tap_normed_;
+    lm.seg[0].w = d.tied ? tok_embd_.view : output_.view;
+    lm.seg[0].rows = d.vocab;
+    UAII_TRY(timed("gemv_lm_head", gemv_bytes(lm.seg[0].w), [&] { return launch_gemv(lm, s); }));
+    SampleArgs sa{};
+    sa.logits = logits_;
+    sa.V = d.vocab;
+    sa.inv_t = samp_.inv_t;
+    sa.top_p = samp_.top_p;
+    sa.top_k = samp_.top_k;
+    sa.rep = samp_.rep;
+    sa.state = state_;
+    sa.ids = ids_;
+    sa.rbuf = samp_r_;
+    sa.nr = samp_n_;
+    sa.ws = samp_ws_;
+    UAII_TRY(timed("sample", 0.0, [&] { return launch_sample(sa, s); }));
+  } else if (want_logits) {
     GemvArgs lm{};
     lm.nseg = 1;
     lm.epi = EPI_LOGITS;
@@ -1201,7 +1263,7 @@ Error DecoderProgram::encode_step(bool want_logits) {
 Error DecoderProgram::step(bool want_logits) {
   if (!kv_) return Error::make(ErrorCode::InvalidArgument, "KvCache not configured");
   if (opts_.profile || !opts_.use_graph) return encode_step(want_logits);
-  hipGraphExec_t& ex = graph_[want_logits ? 1 : 0];
+  hipGraphExec_t& ex = graph_[want_logits ? (sampler_on_ ? 2 : 1) : 0];
   if (!ex) {
     hipGraph_t g = nullptr;
     UAII_HIP(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal));

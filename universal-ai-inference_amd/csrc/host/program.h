@@ -94,6 +94,21 @@ class DecoderProgram {
   Error set_token(int64_t token);
   // Rewind to `pos` (ids and KV below it are kept; ids[pos] is fed next).
   Error seek(int64_t pos);
+  // Token draws on the device (sample.hip) in place of the greedy argmax for the
+  // steps that compute logits: the reference's sampler parameters, and r[t], the
+  // uniform for the token generated at position n_prompt + t.
+  struct SamplerParams {
+    float inv_t = 1.0f;  // 1 / max(temperature, 1e-5)
+    float top_p = 1.0f;
+    int32_t top_k = 0;
+    float rep = 1.0f;
+    bool operator==(const SamplerParams& o) const {
+      return inv_t == o.inv_t && top_p == o.top_p && top_k == o.top_k && rep == o.rep;
+    }
+  };
+  bool sampler_supported() const { return spec_.vocab <= uaii_hip::sample_max_vocab(); }
+  Error arm_sampler(const SamplerParams& p, const float* r, int64_t n);
+  void disarm_sampler() { sampler_on_ = false; }
   void set_profile(bool on) { opts_.profile = on; }
   Error read_tap(const std::string& name, std::vector<float>* out);
   std::string profile_summary() const;
@@ -175,7 +190,13 @@ class DecoderProgram {
   int ring_mode_ = 0;
   uint8_t* ring_pad_ = nullptr;
 
-  hipGraphExec_t graph_[2] = {nullptr, nullptr};
+  // step graphs: no logits, greedy logits, sampled logits
+  hipGraphExec_t graph_[3] = {nullptr, nullptr, nullptr};
+  bool sampler_on_ = false;
+  SamplerParams samp_{}, samp_graph_{};  // armed; baked into graph_[2]
+  float* samp_r_ = nullptr;              // the draws
+  int64_t samp_r_cap_ = 0, samp_n_ = 0;
+  void* samp_ws_ = nullptr;              // sample_workspace_bytes(vocab)
   std::map<std::string, KernelTiming> timing_;
   hipEvent_t ev0_ = nullptr, ev1_ = nullptr;
   int64_t hid_max_ = 0;  // floats of the FFN hidden buffer (gate/up output)

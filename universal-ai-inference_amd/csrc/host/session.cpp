@@ -41,6 +41,7 @@ Error Session::create(const std::string& gguf_path, SessionOptions options) {
   po.profile = options_.enable_profiler;
   po.max_context = options_.max_context;
   po.budget_bytes = options_.budget_bytes;
+  if (const char* ds = std::getenv("UAII_DEVICE_SAMPLER")) options_.device_sampler = ds[0] == '1';
   program_ = std::make_unique<DecoderProgram>();
   UAII_TRY(program_->build(spec_, po));
   ready_ = true;
@@ -80,6 +81,39 @@ Error Session::generate(const std::vector<int64_t>& prompt, int64_t max_new,
   UAII_TRY(p.begin(prompt.data(), n_prompt));
   run_started_ = true;
 
+  // Non-greedy draws use a seeded mt19937_64 (session.cpp:989-995), one uniform
+  // per generated token (sampling.cpp:111-112).
+  std::mt19937_64 rng;
+  if (!sample.greedy()) {
+    if (sample.has_seed) {
+      rng.seed(sample.seed);
+    } else {
+      std::random_device rd;
+      rng.seed((static_cast<uint64_t>(rd()) << 32) ^ static_cast<uint64_t>(rd()));
+    }
+  }
+  // The device sampler takes the draws up front and picks each token where its
+  // logits are: only the ids come back, as on the greedy path.
+  const bool dev_sample = !sample.greedy() && options_.device_sampler && p.sampler_supported();
+  struct Disarm {
+    DecoderProgram* p;
+    ~Disarm() {
+      if (p) p->disarm_sampler();
+    }
+  } disarm{nullptr};
+  if (dev_sample) {
+    std::uniform_real_distribution<float> dist(0.0f, 1.0f);
+    std::vector<float> r((size_t)std::max<int64_t>(max_new, 1));
+    for (auto& v : r) v = dist(rng);
+    DecoderProgram::SamplerParams sp;
+    sp.inv_t = 1.0f / std::max(sample.temperature, 1e-5f);
+    sp.top_p = sample.top_p;
+    sp.top_k = sample.top_k;
+    sp.rep = sample.repetition_penalty;
+    UAII_TRY(p.arm_sampler(sp, r.data(), (int64_t)r.size()));
+    disarm.p = &p;
+  }
+
   out->clear();
   // Prefill. The reference runs one step per prompt token; here all prompt
   // tokens but the last go through the matrix-core path as M-row products when
@@ -93,19 +127,12 @@ Error Session::generate(const std::vector<int64_t>& prompt, int64_t max_new,
   }
   const bool per_token = (bool)on_new_token || !stop_ids.empty();
   auto is_stop = [&](int64_t t) { return std::find(stop_ids.begin(), stop_ids.end(), t) != stop_ids.end(); };
-  if (!sample.greedy()) {
-    // Non-greedy: the reference samples the pre-softmax `logits` row on the host
-    // (want_logits = !sample.greedy(), session.cpp:974-978) with a seeded
-    // mt19937_64 (:989-995, :1018-1026); each step's logits come back from the
-    // device and the chosen id is fed to the next step. The sampler applies its
-    // own softmax, so the device's softmax kernel does not run on this path.
-    std::mt19937_64 rng;
-    if (sample.has_seed) {
-      rng.seed(sample.seed);
-    } else {
-      std::random_device rd;
-      rng.seed((static_cast<uint64_t>(rd()) << 32) ^ static_cast<uint64_t>(rd()));
-    }
+  if (!sample.greedy() && !dev_sample) {
+    // Non-greedy on the host: the reference samples the pre-softmax `logits` row
+    // (want_logits = !sample.greedy(), session.cpp:974-978) with the seeded
+    // generator (:1018-1026); each step's logits come back from the device and
+    // the chosen id is fed to the next step. The sampler applies its own
+    // softmax, so the device's softmax kernel does not run on this path.
     out->assign(prompt.begin(), prompt.end());
     std::vector<float> logits;
     for (int64_t t = 0; t < max_new; ++t) {
@@ -122,7 +149,7 @@ Error Session::generate(const std::vector<int64_t>& prompt, int64_t max_new,
     return Error::success();
   }
   if (!per_token) {
-    // Whole decode on the device: every step's argmax feeds the next step.
+    // Whole decode on the device: every step's argmax (or draw) feeds the next step.
     for (int64_t t = 0; t + 1 < max_new; ++t) UAII_TRY(p.step(true));
     out->resize((size_t)total);
     UAII_TRY(p.read_ids(out->data(), total));
@@ -130,7 +157,7 @@ Error Session::generate(const std::vector<int64_t>& prompt, int64_t max_new,
   }
   out->assign(prompt.begin(), prompt.end());
   for (int64_t t = 0; t < max_new; ++t) {
-    // one 4-byte id per token: the one this step's argmax appended
+    // one 4-byte id per token: the one this step's argmax (or draw) appended
     int64_t next = 0;
     UAII_TRY(p.read_id(n_prompt + t, &next));
     out->push_back(next);

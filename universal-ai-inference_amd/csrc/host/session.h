@@ -41,6 +41,9 @@ struct SessionOptions {
   int64_t max_context = 0;
   uint64_t budget_bytes = 0;
   bool use_graph = true;             // replay captured step graphs
+  // non-greedy draws on the device (sample.hip) instead of the host sampler;
+  // UAII_DEVICE_SAMPLER=1 also turns it on
+  bool device_sampler = false;
 };
 
 
@@ -71,6 +74,8 @@ class Session {
   // Prompt tokens [pos, pos + n) through the matrix-core path (no logits).
   Error prefill(int64_t n);
   DecoderProgram* program() { return program_.get(); }
+  void set_device_sampler(bool on) { options_.device_sampler = on; }
+  bool device_sampler() const { return options_.device_sampler; }
   const DecoderSpec& spec() const { return spec_; }
 
  private:

@@ -97,6 +97,18 @@ def sample_params(temperature=0.0, top_p=1.0, top_k=0, repetition_penalty=1.0, s
     return p
 
 
+def sample_uniforms(seed: int, n: int):
+    """The first n draws of uniform_real_distribution<float>(0, 1) over
+    mt19937_64(seed): the uniforms the reference's sampler takes, in order."""
+    import numpy as np
+    out = np.zeros(max(n, 1), dtype=np.float32)
+    rc = lib().uaii_sample_uniforms(C.c_uint64(seed % (1 << 64)), n,
+                                    out.ctypes.data_as(C.POINTER(C.c_float)))
+    if rc != 0:
+        raise UaiiError(f"uaii_sample_uniforms: {rc}")
+    return out[:n]
+
+
 def sample_token(row, params: "SampleParams", penalty=()):
     """One host draw of the sampler (fresh mt19937_64(params.seed))."""
     import numpy as np
@@ -144,6 +156,7 @@ def lib() -> C.CDLL:
         "uaii_session_seek": (C.c_int, [vp, i64]),
         "uaii_session_set_profiling": (C.c_int, [vp, C.c_int]),
         "uaii_session_last_margin": (C.c_int, [vp, f32p, f32p]),
+        "uaii_session_set_device_sampler": (C.c_int, [vp, C.c_int]),
         "uaii_sample_params_init": (None, [C.POINTER(SampleParams)]),
         "uaii_session_generate_sampled": (C.c_int, [vp, C.POINTER(i64), C.c_size_t, i64,
                                                     C.POINTER(SampleParams), C.POINTER(i64),
@@ -178,6 +191,10 @@ def lib() -> C.CDLL:
         "uaii_hip_rmsnorm": (C.c_int, [vp, vp, vp, i64, i64, C.c_float, vp]),
         "uaii_hip_softmax": (C.c_int, [vp, vp, i64, vp]),
         "uaii_hip_argmax": (C.c_int, [vp, i64, vp, vp]),
+        "uaii_hip_sample_workspace_bytes": (i64, [i64]),
+        "uaii_hip_sample": (C.c_int, [vp, i64, C.c_float, C.c_float, C.c_int, C.c_float, vp, i64,
+                                      C.c_float, vp, vp, vp]),
+        "uaii_sample_uniforms": (C.c_int, [C.c_uint64, i64, f32p]),
         "uaii_hip_rope_table": (C.c_int, [C.c_float, C.c_int, i64, vp]),
         "uaii_hip_rope": (C.c_int, [vp, i64, i64, C.c_int, C.c_int, vp, vp, vp]),
         "uaii_hip_attention_decode": (C.c_int, [vp, vp, vp, C.c_int, i64, C.c_int, C.c_int, C.c_int,
@@ -407,6 +424,10 @@ class Session:
 
     def seek(self, pos: int):
         self._ok(lib().uaii_session_seek(self.h, pos), "seek")
+
+    def set_device_sampler(self, on: bool):
+        """generate_sampled's non-greedy draws on the device (True) or the host."""
+        self._ok(lib().uaii_session_set_device_sampler(self.h, int(on)), "set_device_sampler")
 
     def set_profiling(self, on: bool):
         self._ok(lib().uaii_session_set_profiling(self.h, int(on)), "set_profiling")
