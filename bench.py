@@ -37,15 +37,22 @@ def log(*a):
 
 
 def measured_traffic(kernel: str, algo_bytes: float):
-    """HBM bytes per launch of `kernel` from the committed counter runs
-    (profiles/traffic_*.json: FETCH_SIZE + WRITE_SIZE, scaled by the copy
-    kernel), when they were taken on the same kernel and shape; else None."""
-    for f in sorted((ROOT / "profiles").glob("traffic_*.json")):
+    """HBM bytes per launch of the step role `kernel` from the committed counter
+    runs (profiles/traffic_<role>_*.json: FETCH_SIZE + WRITE_SIZE, scaled by the
+    copy kernel), when they were taken on the same shape and on kernel sources
+    identical to this tree's (sha1 of the role's sources); else None."""
+    from uaii_amd import pmc
+    try:
+        sha = pmc.source_sha(kernel)
+    except OSError:
+        return None
+    for f in sorted((ROOT / "profiles").glob(f"traffic_{kernel}_*.json")):
         try:
             t = json.loads(f.read_text())
         except (OSError, ValueError):
             continue
-        if t.get("bench_kernel") == kernel and abs(t["algorithmic_bytes"] - algo_bytes) <= 1e-3 * algo_bytes:
+        if (t.get("bench_kernel") == kernel and t.get("source_sha1") == sha
+                and abs(t["algorithmic_bytes"] - algo_bytes) <= 1e-3 * algo_bytes):
             return round(t["traffic_bytes"])
     return None
 
@@ -394,7 +401,9 @@ def main() -> int:
                     "gemv_attn_achieved": round(agg_b / (agg_ms * 1e-3) / 1e9, 1),
                     "gemv_attn_frac": round(agg_b / (agg_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                     "kernel_ms_per_step": round(step_ms, 4),
-                    "profiled_steps": P, "profiled_replay_ids_match": replay_ok}
+                    "profiled_steps": P, "profiled_replay_ids_match": replay_ok,
+                    "traffic_by_role": {n: measured_traffic(n, v["bytes"] / v["launches"])
+                                        for n, v in kernels.items() if v["bytes"] > 0}}
     sampled = None
     if not args.no_sampled:
         try:
@@ -444,6 +453,7 @@ def main() -> int:
         "argmax_margin_last": round(best - second, 6),
         "roofline": roofline,
         "kernels": {n: {"avg_us": round(v["avg_us"], 2), "gbps": round(v["gbps"], 1),
+                        "bytes_per_launch": round(v["bytes"] / max(1, v["launches"])),
                         "launches_per_step": v["launches"] / max(1, P)}
                     for n, v in kernels.items()},
         "sampled_tok_s": sampled,

@@ -42,9 +42,10 @@ def main(argv=None) -> int:
                     help="activation rows: 1 = decode GEMV, > 1 = prefill MFMA GEMM (TFLOP/s)")
     ap.add_argument("--floor", action="store_true",
                     help="plain-read per-launch floor over the 8B decode kernels' byte counts")
+    ap.add_argument("--floor-case", help="with --floor: only the case of this name (e.g. 'LM head')")
     a = ap.parse_args(argv)
     if a.floor:
-        return floor(a.iters)
+        return floor(a.iters, a.floor_case)
     names = {v.lower(): k for k, v in TYPE_NAMES.items()}
     t = names[a.type.lower()]
     L = lib()
@@ -113,7 +114,7 @@ FLOOR_CASES = [("O", 9.44e6), ("QKV", 14.17e6), ("attention K+V", 16.8e6), ("dow
                ("gate+up", 66.1e6), ("LM head", 295.5e6)]
 
 
-def floor(iters: int) -> int:
+def floor(iters: int, only: str | None = None) -> int:
     """Average time of a plain read of each case's bytes, one launch after
     another, rotating over enough buffers (> 320 MiB) that every launch reads
     HBM. Prints one line per case and the per-token sum (32 layers of the five
@@ -122,6 +123,8 @@ def floor(iters: int) -> int:
     check_hip(L.uaii_hip_init(0), "init")
     total_us = 0.0
     for name, nbytes in FLOOR_CASES:
+        if only and name != only:
+            continue
         nb = int(nbytes) // 16 * 16
         copies = max(2, int(np.ceil(320 * 2 ** 20 / nb)))
         bufs = [DeviceBuffer(nb) for _ in range(copies)]
