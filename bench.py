@@ -107,6 +107,58 @@ PUBLISHED_GEMV = {"shape": "Q4_0 M=1 N=2048 K=4096", "median_ms": 4.495, "trials
                   "source": "benchmarks/results/local_wsl.json:103-111 (uaii_bench.cpp:494-566)"}
 
 
+def cpu_prompt_window(path: str, prompt, n_tokens: int, threads: int, report_every: int = 0):
+    """Window (i): the first n prompt tokens fed one at a time through the
+    reference's compiled kernels from an empty cache (session.cpp:1006-1016)."""
+    sys.path.insert(0, str(ROOT))
+    import numpy as np
+    import oracle  # baseline only
+    import ctypes as C
+    os.environ["UAII_NUM_THREADS"] = str(threads)
+    R = oracle.ref()
+    if R is None:
+        raise RuntimeError("reference kernels not built")
+    R.uref_time_prompt_window.restype = C.c_double
+    R.uref_time_prompt_window.argtypes = [C.c_char_p, C.POINTER(C.c_int64), C.c_int64, C.c_int]
+    p = np.ascontiguousarray(prompt[:n_tokens], dtype=np.int64)
+    secs = R.uref_time_prompt_window(path.encode(), p.ctypes.data_as(C.POINTER(C.c_int64)), len(p),
+                                     report_every)
+    if secs <= 0:
+        raise RuntimeError("cpu prompt window failed")
+    return {"tokens": len(p), "seconds": round(secs, 2), "tok_s": round(len(p) / secs, 4),
+            "sample": f"prompt tokens 0..{len(p) - 1} of the benchmark prompt, one run() each from an "
+                      f"empty cache (the reference's prefill), of the 256 BASELINE.md plans"}
+
+
+def cpu_full_runs(uaii_amd, threads: int, lengths):
+    """Whole greedy generate runs (prompt, then decode) on the small configs: the
+    reference's compiled kernels on the host cores and this build on the GPU,
+    same GGUF file and prompt, ids compared."""
+    sys.path.insert(0, str(ROOT))
+    import numpy as np
+    import oracle  # baseline only
+    from uaii_amd import synth
+    os.environ["UAII_NUM_THREADS"] = str(threads)
+    out = {}
+    for name, (n_prompt, n_new) in lengths.items():
+        cfg = synth.PRESETS[name]
+        path = synth.cached_model(cfg, nthreads=16)
+        prompt = np.random.default_rng(cfg.seed + 1).integers(0, cfg.vocab, n_prompt).astype(np.int64)
+        t0 = time.perf_counter()
+        want, _ = oracle.ref_generate(path, prompt, n_new)
+        cpu_s = time.perf_counter() - t0
+        with uaii_amd.Session(path) as sess:
+            sess.generate(prompt, n_new)  # graphs captured
+            t0 = time.perf_counter()
+            got = sess.generate(prompt, n_new)
+            gpu_s = time.perf_counter() - t0
+        out[name] = {"prompt": n_prompt, "new": n_new, "cpu_s": round(cpu_s, 3),
+                     "cpu_tok_s": round((n_prompt + n_new) / cpu_s, 2), "gpu_s": round(gpu_s, 4),
+                     "gpu_tok_s": round((n_prompt + n_new) / gpu_s, 1),
+                     "ids_match": bool(np.array_equal(np.asarray(got), np.asarray(want)))}
+    return out
+
+
 def published_gemv_inputs(np):
     """The inputs of the reference's quant GEMV benchmark (uaii_bench.cpp:505-518):
     Q4_0 blocks in row-major order with d = 1.0 (0x3c00) and qs[i] = (i + block) & 0xff,
@@ -257,6 +309,11 @@ def main() -> int:
     ap.add_argument("--no-profile", action="store_true")
     ap.add_argument("--no-parity", action="store_true")
     ap.add_argument("--no-sampled", action="store_true")
+    ap.add_argument("--cpu-prompt-tokens", type=int, default=8,
+                    help="window (i): the first N prompt tokens through the reference CPU kernels")
+    ap.add_argument("--cpu-1b", default="16,16", help="prompt,new tokens of the full 1B CPU run (0 skips)")
+    ap.add_argument("--cpu-only", action="store_true",
+                    help="only the CPU baseline windows (with --cpu-prompt-tokens / --cpu-steps)")
     ap.add_argument("--sampled-steps", type=int, default=128)
     args = ap.parse_args()
     if args.gpus != 1:
@@ -278,6 +335,14 @@ def main() -> int:
     t = time.time()
     path = synth.cached_model(cfg, nthreads=16)
     log(f"model {path} ready in {time.time() - t:.1f}s")
+    if args.cpu_only:
+        prompt = np.random.default_rng(cfg.seed + 1).integers(0, cfg.vocab, n_prompt)
+        res = {"decode_window": cpu_baseline(path, n_prompt + W + K // 2, args.cpu_steps, args.cpu_threads)}
+        log(f"cpu decode window {res['decode_window']}")
+        res["prompt_window"] = cpu_prompt_window(path, prompt, args.cpu_prompt_tokens, args.cpu_threads,
+                                                 report_every=16)
+        print(json.dumps(res), flush=True)
+        return 0
 
     # device copy rate (HBM read+write) for context
     L = uaii_amd.lib()
@@ -430,6 +495,22 @@ def main() -> int:
             log(f"cpu baseline {cpu}")
         except Exception as e:  # the GPU figure stands on its own
             log(f"cpu baseline unavailable: {e}")
+        if cpu is not None and args.cpu_prompt_tokens > 0:
+            try:
+                cpu["prompt_window"] = cpu_prompt_window(path, prompt, args.cpu_prompt_tokens, args.cpu_threads)
+                log(f"cpu prompt window {cpu['prompt_window']}")
+            except Exception as e:
+                log(f"cpu prompt window unavailable: {e}")
+        if cpu is not None:
+            lengths = {"tiny": (32, 64)}
+            if args.cpu_1b and args.cpu_1b != "0":
+                p1, n1 = (int(v) for v in args.cpu_1b.split(","))
+                lengths["1b"] = (p1, n1)
+            try:
+                cpu["full_runs"] = cpu_full_runs(uaii_amd, args.cpu_threads, lengths)
+                log(f"cpu full runs {cpu['full_runs']}")
+            except Exception as e:
+                log(f"cpu full runs unavailable: {e}")
         try:
             pub["cpu_reference_here"] = published_gemv_cpu(np, args.cpu_threads)
             log(f"published GEMV shape on this host {pub['cpu_reference_here']}")

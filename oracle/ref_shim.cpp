@@ -29,6 +29,7 @@ extern "C" {
 }
 
 #include <chrono>
+#include <cstdio>
 #include <cstring>
 #include <memory>
 #include <random>
@@ -591,6 +592,30 @@ double uref_time_decode_window(const char* path, std::int64_t start_pos, std::in
     std::mt19937_64 rng{0};
     (void)runtime::sample_token_f32(R.probs->f32.data(), static_cast<std::size_t>(R.V), greedy, {},
                                     &rng, &tok);
+  }
+  const auto t1 = std::chrono::steady_clock::now();
+  return std::chrono::duration<double>(t1 - t0).count();
+}
+
+// CPU baseline window (i): the first n prompt tokens fed one at a time through
+// the reference kernels from an empty cache, as the reference prefills
+// (session.cpp:1006-1016: one run() per prompt token). Returns the wall seconds
+// of the n runs, or < 0 on error. report_every > 0 prints progress to stderr.
+double uref_time_prompt_window(const char* path, const std::int64_t* prompt, std::int64_t n,
+                               int report_every) {
+  RefRunner R;
+  Error err = R.open(path, 0, n + 1, 0, n);
+  if (!err.ok()) { g_err = err.message(); return -1.0; }
+  const auto t0 = std::chrono::steady_clock::now();
+  for (std::int64_t i = 0; i < n; ++i) {
+    err = R.run(prompt[i], nullptr);
+    if (!err.ok()) { g_err = err.message(); return -1.0; }
+    if (report_every > 0 && (i + 1) % report_every == 0) {
+      const double s = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+      std::fprintf(stderr, "cpu prompt window: %lld/%lld tokens, %.1f s\n", (long long)(i + 1),
+                   (long long)n, s);
+      std::fflush(stderr);
+    }
   }
   const auto t1 = std::chrono::steady_clock::now();
   return std::chrono::duration<double>(t1 - t0).count();
