@@ -36,6 +36,24 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+def traffic_record(kernel: str):
+    """The committed counter record of a step role, when it was taken on kernel
+    sources identical to this tree's (sha1 of the role's sources); else None."""
+    from uaii_amd import pmc
+    try:
+        sha = pmc.source_sha(kernel)
+    except OSError:
+        return None
+    for f in sorted((ROOT / "profiles").glob(f"traffic_{kernel}_*.json")):
+        try:
+            t = json.loads(f.read_text())
+        except (OSError, ValueError):
+            continue
+        if t.get("bench_kernel") == kernel and t.get("source_sha1") == sha:
+            return t
+    return None
+
+
 def measured_traffic(kernel: str, algo_bytes: float):
     """HBM bytes per launch of the step role `kernel` from the committed counter
     runs (profiles/traffic_<role>_*.json: FETCH_SIZE + WRITE_SIZE, scaled by the
@@ -145,7 +163,7 @@ def cpu_full_runs(uaii_amd, threads: int, lengths):
         path = synth.cached_model(cfg, nthreads=16)
         prompt = np.random.default_rng(cfg.seed + 1).integers(0, cfg.vocab, n_prompt).astype(np.int64)
         t0 = time.perf_counter()
-        want, _ = oracle.ref_generate(path, prompt, n_new)
+        want = oracle.ref_generate(path, prompt, n_new)[0]
         cpu_s = time.perf_counter() - t0
         with uaii_amd.Session(path) as sess:
             sess.generate(prompt, n_new)  # graphs captured
@@ -467,8 +485,9 @@ def main() -> int:
                     "gemv_attn_frac": round(agg_b / (agg_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                     "kernel_ms_per_step": round(step_ms, 4),
                     "profiled_steps": P, "profiled_replay_ids_match": replay_ok,
-                    "traffic_by_role": {n: measured_traffic(n, v["bytes"] / v["launches"])
-                                        for n, v in kernels.items() if v["bytes"] > 0}}
+                    "traffic_over_algorithmic_by_role": {
+                        n: (round(t["traffic_over_algorithmic"], 4) if t else None)
+                        for n, t in ((n, traffic_record(n)) for n, v in kernels.items() if v["bytes"] > 0)}}
     sampled = None
     if not args.no_sampled:
         try:
