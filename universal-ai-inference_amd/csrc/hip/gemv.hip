@@ -1551,8 +1551,10 @@ Plan make_plan(const GemvArgs& a) {
   // The LM head streams 296 MB (8B shape) through one launch: with every
   // resident block (5 per CU) its loads queue in the per-CU memory path (the
   // address unit waits on the cache 5x as long as a plain read's); 3 blocks per
-  // CU measured 61.4 us against 65.0 (1: 95.6, 2: 67.7, 4: 64.1).
-  const int cap_cu = a.epi == EPI_LOGITS ? std::min(per_cu, 3) : per_cu;
+  // CU measured 61.4 us against 65.0 with the argmax epilogue (1: 95.6, 2: 67.7,
+  // 4: 64.1), 55.0 against 56.5 storing the logits for the device sampler.
+  const bool lm_head = a.epi == EPI_LOGITS || (a.epi == EPI_STORE && a.nseg == 1 && a.seg[0].rows >= 65536);
+  const int cap_cu = lm_head ? std::min(per_cu, 3) : per_cu;
   const int64_t cap = (int64_t)cu_count() * cap_cu;
   for (int k = 0; k < a.nseg; ++k) {
     const int64_t g = (a.seg[k].rows + rpg - 1) / rpg;
