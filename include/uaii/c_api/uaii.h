@@ -63,7 +63,7 @@ typedef struct uaii_session_options {
   uint32_t struct_size;          /* sizeof(uaii_session_options) */
   const char* backend;           /* "rocm" (only backend of this library) */
   const char* weights_dir;       /* prefix for relative model paths (may be NULL) */
-  uaii_weight_init weight_init;  /* accepted; every weight of a GGUF decoder must load */
+  uaii_weight_init weight_init;  /* a weight whose bytes the file lacks: NONE fails the create (NOT_FOUND); ZEROS / ONES / SEQUENCE fill its f32 values (Path A; packed Path B weights cannot be filled) */
   int enable_fusion;             /* accepted; the device program is always fused */
   int enable_memory_reuse;       /* non-zero (default): weights take the values of the
                                     reference's f32 weight load (its Path A: Q4_0 nibbles

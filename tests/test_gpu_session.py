@@ -274,3 +274,36 @@ def test_generate_sampled_draws_from_logits(prm):
         assert drawn.count(int(np.argmax(logits))) >= 16
     else:
         assert len(set(drawn)) > 1
+
+
+def test_weight_init_fills_unreadable_weight(tmp_path):
+    """A weight whose bytes the file does not hold (the tiny file cut one byte
+    short, inside its last tensor, output.weight): the reference's header still
+    parses and the load fails (session.cpp:510-544). weight_init NONE: create
+    fails with NOT_FOUND naming the weight; ZEROS / ONES / SEQUENCE fill the
+    weight's f32 buffer on Path A (element i of the row-major [32000][512] buffer
+    = i * 0.01f for SEQUENCE); a packed Path B buffer cannot be filled."""
+    cfg = synth.PRESETS["tiny"]
+    data = Path(synth.cached_model(cfg)).read_bytes()
+    cut = tmp_path / "cut.gguf"
+    cut.write_bytes(data[:-1])
+    prompt = prompt_for(cfg, 8, 3)
+    with pytest.raises(uaii_amd.UaiiError, match="not_found.*failed to load required weight 'output.weight'"):
+        uaii_amd.Session(cut, memory_reuse=True)
+    with pytest.raises(uaii_amd.UaiiError, match="not_found.*failed to load weight 'output.weight'"):
+        uaii_amd.Session(cut, memory_reuse=True, allow_missing_weights=True)
+    with pytest.raises(uaii_amd.UaiiError, match="not_found.*failed to load packed weight 'output.weight'"):
+        uaii_amd.Session(cut, memory_reuse=False, keep_quantized=True, weight_init=1)
+    with uaii_amd.Session(cut, memory_reuse=True, weight_init=1) as s:
+        ids = s.generate(prompt, 4)
+        assert ids[:8].tolist() == prompt.tolist() and ids[8:].tolist() == [0, 0, 0, 0]
+        assert not np.any(s.get("logits"))
+    with uaii_amd.Session(cut, memory_reuse=True, weight_init=2) as s:
+        s.generate(prompt, 1)
+        lg, xn = s.get("logits"), s.get("normed").astype(np.float64)
+        assert maxrel(lg, np.full(cfg.vocab, xn.sum())) < 2e-3
+    with uaii_amd.Session(cut, memory_reuse=True, weight_init=3) as s:
+        s.generate(prompt, 1)
+        lg, xn = s.get("logits"), s.get("normed").astype(np.float64)
+        w = (np.arange(cfg.vocab * cfg.dim, dtype=np.float32) * np.float32(0.01)).reshape(cfg.vocab, cfg.dim)
+        assert maxrel(lg, w.astype(np.float64) @ xn) < 2e-3

@@ -188,9 +188,10 @@ Error GgufFile::open(const std::string& path) {
     }
     if (wrap || n > (uint64_t)INT64_MAX)
       return Error::make(ErrorCode::InvalidArgument, "tensor " + t.name + " size overflows");
-    if (t.offset > (uint64_t)len_ || (be && end > (uint64_t)len_))
-      return Error::make(ErrorCode::InvalidArgument, "tensor " + t.name + " extends past end of file");
-    t.data = map_ + data_off + t.offset;
+    // bytes past the end of the file: left unreadable (data null) for the load
+    // to report, as the reference reads tensors only when it loads them
+    const bool readable = be && data_off + t.offset <= (uint64_t)len_ && end <= (uint64_t)len_;
+    t.data = readable ? map_ + data_off + t.offset : nullptr;
     index_[t.name] = i;
   }
   return Error::success();

@@ -27,6 +27,9 @@ struct GgufTensor {
   int type = 0;
   std::vector<uint64_t> ne;  // GGUF order (ne[0] = row length)
   uint64_t offset = 0;
+  // null when the file ends before the tensor's bytes do: the header still
+  // parses (as gguf_read_header, gguf.cpp:374-443) and the load fails, or takes
+  // the session's weight_init fill (session.cpp:510-544)
   const uint8_t* data = nullptr;
   uint64_t nbytes = 0;
   // row-major view after the reference's dims reversal (gguf.cpp:272-280)

@@ -127,6 +127,31 @@ Error DecoderProgram::charge(uint64_t& pool, uint64_t bytes) {
   return Error::success();
 }
 
+// The load of a weight whose bytes the file does not hold fails as the
+// reference's load_or_init_weights does (session.cpp:510-544): an error unless
+// weight_init asks for a synthetic fill of the f32 buffer (zeros, ones, or
+// element i = i * 0.01 in row-major order); a packed buffer (Path B) has no f32
+// values to fill.
+Error DecoderProgram::missing_weight(const GgufTensor* t, bool packed, std::vector<float>* fill) {
+  const std::string ref = opts_.weight_source + "#" + t->name;
+  if (opts_.weight_init == 0) {
+    if (!opts_.allow_missing_weights)
+      return Error::make(ErrorCode::NotFound, "failed to load required weight '" + t->name + "' from '" + ref +
+                                                  "': the file ends before the tensor's data");
+    return Error::make(ErrorCode::NotFound, "failed to load weight '" + t->name + "' from '" + ref + "'");
+  }
+  if (packed) return Error::make(ErrorCode::NotFound, "failed to load packed weight '" + t->name + "'");
+  uint64_t n = 1;
+  for (auto d : t->ne) n *= d;
+  fill->assign(n, 0.0f);
+  if (opts_.weight_init == 2) {
+    for (auto& v : *fill) v = 1.0f;
+  } else if (opts_.weight_init == 3) {
+    for (uint64_t i = 0; i < n; ++i) (*fill)[i] = static_cast<float>(i) * 0.01f;
+  }
+  return Error::success();
+}
+
 Error DecoderProgram::upload_f32(const GgufTensor* t, float** out) {
   *out = nullptr;
   if (!t) return Error::success();
@@ -134,7 +159,9 @@ Error DecoderProgram::upload_f32(const GgufTensor* t, float** out) {
   for (auto d : t->ne) n *= d;
   UAII_TRY(charge(used_static_, n * 4));
   std::vector<float> h(n);
-  if (t->type == T_F32) {
+  if (!t->data) {
+    UAII_TRY(missing_weight(t, false, &h));
+  } else if (t->type == T_F32) {
     std::memcpy(h.data(), t->data, n * 4);
   } else if (t->type == T_F16) {
     for (uint64_t i = 0; i < n; ++i) {
@@ -184,10 +211,20 @@ Error DecoderProgram::build(const DecoderSpec& spec, const ProgramOptions& opts)
   for (const LayerSpec& s : d.layers) moe_model = moe_model || s.ffn == LayerSpec::kMoE;
   const bool f32_load = opts_.f32_weight_load || moe_model;
   auto up = [&](const GgufTensor* t, DeviceWeight* w) -> Error {
+    if (t->cols() <= 0 || t->rows() <= 0)
+      return Error::make(ErrorCode::InvalidArgument, "tensor " + t->name + " has no elements");
+    if (!t->data) {
+      // bytes past the end of the file: the reference's failed load or its fill
+      std::vector<float> fill;
+      const bool packed = !f32_load && t->type != T_F32 && t->type != T_F16;
+      UAII_TRY(missing_weight(t, packed, &fill));
+      UAII_TRY(upload_weight(T_F32, reinterpret_cast<const uint8_t*>(fill.data()), t->rows(), t->cols(), stream_, w,
+                             f32_load));
+      return charge(used_static_, w->bytes);
+    }
     // the rows the upload copies must be exactly the bytes the file holds for
     // this tensor (the parser bounded those by the end of the mapping)
-    if (t->cols() <= 0 || t->rows() <= 0 ||
-        (uint64_t)t->rows() * gguf_nbytes(t->type, (uint64_t)t->cols()) != t->nbytes)
+    if ((uint64_t)t->rows() * gguf_nbytes(t->type, (uint64_t)t->cols()) != t->nbytes)
       return Error::make(ErrorCode::InvalidArgument, "tensor " + t->name + " shape does not match its bytes");
     UAII_TRY(upload_weight(t->type, t->data, t->rows(), t->cols(), stream_, w, f32_load));
     return charge(used_static_, w->bytes);

@@ -52,6 +52,12 @@ struct ProgramOptions {
   // buffers); 0 = unlimited. Exceeding it is InvalidArgument "memory budget
   // exceeded", as the reference's MemoryBudget::reserve (libs/uaii-memory/src/budget.cpp:6-19).
   uint64_t budget_bytes = 0;
+  // A weight whose bytes the file does not hold (session.cpp:510-544): with
+  // weight_init 0 (None) the build fails; 1 zeros, 2 ones, 3 i * 0.01 fill the
+  // weight's f32 values (packed Path B buffers cannot be filled).
+  int weight_init = 0;
+  bool allow_missing_weights = false;
+  std::string weight_source;  // the file, for the reference's messages
 };
 
 struct KernelTiming {
@@ -126,6 +132,7 @@ class DecoderProgram {
   };
 
   Error upload_f32(const GgufTensor* t, float** out);
+  Error missing_weight(const GgufTensor* t, bool packed, std::vector<float>* fill);
   // Count `bytes` against the device budget in `pool` (static, dynamic or prompt buffers).
   Error charge(uint64_t& pool, uint64_t bytes);
   uint64_t used_static_ = 0, used_dyn_ = 0, used_pf_ = 0;

@@ -41,6 +41,9 @@ Error Session::create(const std::string& gguf_path, SessionOptions options) {
   po.profile = options_.enable_profiler;
   po.max_context = options_.max_context;
   po.budget_bytes = options_.budget_bytes;
+  po.weight_init = static_cast<int>(options_.weight_init);
+  po.allow_missing_weights = options_.allow_missing_weights;
+  po.weight_source = path;
   if (const char* ds = std::getenv("UAII_DEVICE_SAMPLER")) options_.device_sampler = ds[0] == '1';
   program_ = std::make_unique<DecoderProgram>();
   UAII_TRY(program_->build(spec_, po));

@@ -318,7 +318,8 @@ class Session:
 
     def __init__(self, path: str, *, kv_f16: bool = False, max_context: int = 0,
                  profile: bool = False, backend: str = "rocm", memory_reuse: bool = False,
-                 keep_quantized: bool = True, budget_bytes: int = 0):
+                 keep_quantized: bool = True, budget_bytes: int = 0, weight_init: int = 0,
+                 allow_missing_weights: bool = False):
         """memory_reuse / keep_quantized select the reference's weight path: the
         defaults here (memory_reuse off, quantized weights kept) are its packed
         Path B, the quant_gemm path; memory_reuse=True (the C ABI's default, as in
@@ -332,6 +333,8 @@ class Session:
         opts.enable_memory_reuse = 1 if memory_reuse else 0
         opts.keep_quantized_weights = 1 if keep_quantized else 0
         opts.budget_bytes = budget_bytes
+        opts.weight_init = weight_init  # 0 none, 1 zeros, 2 ones, 3 sequence (uaii_weight_init)
+        opts.allow_missing_weights = 1 if allow_missing_weights else 0
         opts.compute_dtype = 1 if kv_f16 else 0
         opts.max_context = max_context
         opts.enable_profiler = 1 if profile else 0
