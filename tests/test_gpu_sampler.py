@@ -100,7 +100,7 @@ ORDERED = [(0.8, 0.9, 40, 1.0), (1.0, 0.9, 0, 1.0), (0.7, 1.0, 0, 1.0), (0.9, 0.
            (1.5, 0.5, 5, 1.0), (0.0, 1.0, 0, 1.3), (1.0, 1.0, 0, 1.0)]
 
 
-@pytest.mark.parametrize("vocab", [50, 3000, 32000, 128256])
+@pytest.mark.parametrize("vocab", [50, 3000, 32000, 128256, 151937])
 @pytest.mark.parametrize("prm", ORDERED, ids=lambda p: f"T{p[0]}_p{p[1]}_k{p[2]}_r{p[3]}")
 def test_device_ids_match_host_sampler(vocab, prm):
     t, tp, tk, rp = prm
@@ -142,7 +142,7 @@ def test_device_ids_match_host_sampler(vocab, prm):
     assert same >= floor * total, (same, total)
 
 
-@pytest.mark.parametrize("vocab", [50, 3000, 128256])
+@pytest.mark.parametrize("vocab", [50, 3000, 128256, 151937])
 @pytest.mark.parametrize("prm", [(1.0, 1.0, 40, 1.0), (0.7, 1.0, 5, 1.3), (0.8, 0.9, 40, 1.0),
                                  (1.0, 0.9, 0, 1.0), (2.0, 1.0, 0, 1.0)],
                          ids=lambda p: f"T{p[0]}_p{p[1]}_k{p[2]}_r{p[3]}")
@@ -204,3 +204,33 @@ def test_device_sampler_arguments():
     assert rc == -1  # r outside [0, 1]
     # a flat row: every id equally likely, in index order
     assert [dev((1.0, 1.0, 0, 1.0), (j + 0.5) / 64) for j in range(64)] == list(range(64))
+
+
+def test_device_sampler_long_history_and_large_k():
+    """The penalty over a history longer than a slice's share of threads (5000
+    ids, repeats included), and top-k above the LDS list (3000 kept ids: the
+    top-p and draw selects run over the grouped copy instead)."""
+    V = 32000
+    dev = DevSampler(V)
+    rng = np.random.default_rng(21)
+    row = rng.normal(0, 2, V).astype(np.float32)
+    pen = rng.integers(0, V, 5000).tolist()
+    dev.load(row, pen)
+    for prm in [(0.9, 0.95, 3000, 1.3), (1.0, 1.0, 3000, 1.2), (0.8, 0.9, 0, 1.3)]:
+        t, tp, tk, rp = prm
+        order, p = kept_probs(row, prm, pen)
+        n = 3000
+        counts = {}
+        for j in range(n):
+            got = dev(prm, (j + 0.5) / n)
+            counts[got] = counts.get(got, 0) + 1
+        assert set(counts) <= set(order.tolist()), prm
+        for i, pi in zip(order.tolist(), p):
+            assert abs(counts.get(i, 0) - n * pi) <= 2.0, (prm, i, counts.get(i, 0), n * pi)
+        same = 0
+        for seed in range(10):
+            r = float(uaii_amd.sample_uniforms(seed, 1)[0])
+            host = uaii_amd.sample_token(row, uaii_amd.sample_params(t, tp, tk, rp, seed=seed), pen)
+            same += dev(prm, r) == host
+        if tp < 1.0:
+            assert same >= 8, (prm, same)
