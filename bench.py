@@ -145,7 +145,7 @@ def cpu_prompt_window(path: str, prompt, n_tokens: int, threads: int, report_eve
         raise RuntimeError("cpu prompt window failed")
     return {"tokens": len(p), "seconds": round(secs, 2), "tok_s": round(len(p) / secs, 4),
             "sample": f"prompt tokens 0..{len(p) - 1} of the benchmark prompt, one run() each from an "
-                      f"empty cache (the reference's prefill), of the 256 BASELINE.md plans"}
+                      f"empty cache (the reference's prefill), the start of the 256-token window (i)"}
 
 
 def cpu_full_runs(uaii_amd, threads: int, lengths):

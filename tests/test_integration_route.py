@@ -1,10 +1,11 @@
-"""The C++ Session route documented in INTEGRATION.md builds and links.
+"""The C++ Session route of the repository's integration notes builds and links.
 
-INTEGRATION.md section 3 gives the branch a maintainer would add to the
-reference's `Session::generate` (include/uaii/runtime/session.hpp:131-136,
-routing `backend_name == "rocm"`, session.hpp:50) so that it calls this build's
-`uaii_session_generate`. This test takes that snippet out of INTEGRATION.md,
-so the document and the test cannot drift apart. It compiles the snippet with
+Section 3 of the integration notes at the repository root gives the branch a
+maintainer would add to the reference's `Session::generate`
+(include/uaii/runtime/session.hpp:131-136, routing `backend_name == "rocm"`,
+session.hpp:50) so that it calls this build's `uaii_session_generate`. This test
+takes that snippet out of the notes themselves, so the document and the test
+cannot drift apart. It compiles the snippet with
 g++ against the reference's own headers, links it against libuaii_amd.so and
 runs it on the CPU:
 * with `backend_name = "cpu"` the branch is skipped (the driver then returns
@@ -65,7 +66,7 @@ def snippet() -> str:
     text = (ROOT / "INTEGRATION.md").read_text()
     sec = text.split("## 3.", 1)[1].split("\n## 4.", 1)[0]
     m = re.search(r"```cpp\n(.*?)```", sec, re.S)
-    assert m, "INTEGRATION.md section 3 holds no cpp block"
+    assert m, "section 3 of the integration notes holds no cpp block"
     return m.group(1)
 
 
