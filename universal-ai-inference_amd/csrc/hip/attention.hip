@@ -436,26 +436,33 @@ __global__ void __launch_bounds__(NW * 64) k_attn_h16(AttnArgs a) {
   const int kq = lane % LK, kk = lane / LK;   // scores: dims [32 kq, 32 kq + 32) of key kk + KPI j
   const int vd = lane % LV, vk = lane / LV;   // P.V: dims [8 vd, 8 vd + 8) of key vk + VPI j
 
-  uint4 kr[KJ][4], vr[VJ];
-  auto load_tile = [&](int t0) {
+  // Two register sets, used in turn: a wave's next tile is in flight while it
+  // computes one, and every load stays on a straight line. (A loop that loads
+  // its tile at the top for every pass but the first joins two load paths at
+  // the loop head, and the compiler then waited there for the whole first tile,
+  // K and V, before the first score: with one tile per wave, as at 4096
+  // positions, this form measured attention + merge 12.1 against 12.7 us on the
+  // 8B decode, the waits for V now falling inside the score and softmax work.)
+  uint4 kr[KJ][4], vr[VJ], kn[KJ][4], vn[VJ];
+  auto load_tile = [&](int t0, uint4 (&K)[KJ][4], uint4 (&V)[VJ]) __attribute__((always_inline)) {
 #pragma unroll
     for (int j = 0; j < KJ; ++j) {
       int key = t0 + kk + KPI * j;
       key = key < b1 ? key : b1 - 1;  // in bounds; masked below
       const uint4* src = reinterpret_cast<const uint4*>(kc + (int64_t)key * HD + 32 * kq);
 #pragma unroll
-      for (int c = 0; c < 4; ++c) kr[j][c] = src[c];
+      for (int c = 0; c < 4; ++c) K[j][c] = src[c];
     }
 #pragma unroll
     for (int j = 0; j < VJ; ++j) {
       int key = t0 + vk + VPI * j;
       key = key < b1 ? key : b1 - 1;
-      vr[j] = *reinterpret_cast<const uint4*>(vc + (int64_t)key * HD + 8 * vd);
+      V[j] = *reinterpret_cast<const uint4*>(vc + (int64_t)key * HD + 8 * vd);
     }
   };
 
   const int first = b0 + wave * TK;
-  if (first < b1) load_tile(first);
+  if (first < b1) load_tile(first, kr, vr);
 
   // q * scale -> f16 (hi, lo) pairs in LDS
 #pragma unroll
@@ -480,8 +487,7 @@ __global__ void __launch_bounds__(NW * 64) k_attn_h16(AttnArgs a) {
     for (int e = 0; e < 8; ++e) o[g][e] = 0.0f;
   }
 
-  for (int t0 = first; t0 < b1; t0 += NW * TK) {
-    if (t0 != first) load_tile(t0);
+  auto tile = [&](int t0, const uint4 (&K)[KJ][4], const uint4 (&V)[VJ]) __attribute__((always_inline)) {
     // scores
     float sc[KJ][G];
 #pragma unroll
@@ -496,10 +502,10 @@ __global__ void __launch_bounds__(NW * 64) k_attn_h16(AttnArgs a) {
 #pragma unroll
         for (int j = 0; j < KJ; ++j) {
           float t = sc[j][g];
-          t = adot2(kr[j][c].x, qh.x, t); t = adot2(kr[j][c].x, ql.x, t);
-          t = adot2(kr[j][c].y, qh.y, t); t = adot2(kr[j][c].y, ql.y, t);
-          t = adot2(kr[j][c].z, qh.z, t); t = adot2(kr[j][c].z, ql.z, t);
-          t = adot2(kr[j][c].w, qh.w, t); t = adot2(kr[j][c].w, ql.w, t);
+          t = adot2(K[j][c].x, qh.x, t); t = adot2(K[j][c].x, ql.x, t);
+          t = adot2(K[j][c].y, qh.y, t); t = adot2(K[j][c].y, ql.y, t);
+          t = adot2(K[j][c].z, qh.z, t); t = adot2(K[j][c].z, ql.z, t);
+          t = adot2(K[j][c].w, qh.w, t); t = adot2(K[j][c].w, ql.w, t);
           sc[j][g] = t;
         }
       }
@@ -543,7 +549,7 @@ __global__ void __launch_bounds__(NW * 64) k_attn_h16(AttnArgs a) {
 #pragma unroll
     for (int j = 0; j < VJ; ++j) {
       float vf[8];
-      const uint32_t w4[4] = {vr[j].x, vr[j].y, vr[j].z, vr[j].w};
+      const uint32_t w4[4] = {V[j].x, V[j].y, V[j].z, V[j].w};
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         vf[2 * e] = __half2float(__ushort_as_half((uint16_t)(w4[e] & 0xffffu)));
@@ -557,6 +563,15 @@ __global__ void __launch_bounds__(NW * 64) k_attn_h16(AttnArgs a) {
       }
     }
     __builtin_amdgcn_wave_barrier();
+  };
+
+  const int step = NW * TK;
+  for (int t0 = first; t0 < b1; t0 += 2 * step) {
+    if (t0 + step < b1) load_tile(t0 + step, kn, vn);
+    tile(t0, kr, vr);
+    if (t0 + step >= b1) break;
+    if (t0 + 2 * step < b1) load_tile(t0 + 2 * step, kr, vr);
+    tile(t0 + step, kn, vn);
   }
 
   // reduce the key groups of P.V (lanes vd, vd + LV, ...)
@@ -620,32 +635,43 @@ bool launch_h16(const AttnArgs& a, int G, hipStream_t s) {
 }
 
 
-// Merge the SB block partials of every query head (one block per head):
-// out = sum_s w_s o_s / sum_s w_s l_s with w_s = exp(m_s - max_s m_s).
+// Merge the SB (<= 64) block partials of every query head (one block per head,
+// one thread per output dim): out = sum_s w_s o_s / sum_s w_s l_s with
+// w_s = exp(m_s - max_s m_s). Split s's m and l sit on lane s of every wave,
+// which derives the weights itself (DPP max and sum) and reads w_s from lane s
+// with readlane; a thread's dims of the first 32 splits' o are loaded together
+// with them, before any arithmetic, so the merge costs one memory round trip
+// (where loading the weights first, through LDS, and then the o values cost
+// three). The sums and their order are those of a loop s = 0 .. SB-1 (the
+// in-kernel merge, merge_tail, relies on it).
 __global__ void __launch_bounds__(256) k_attn_merge(AttnArgs a) {
-  __shared__ float w[64];
-  __shared__ float inv_den;
+  constexpr int CH = 32;  // splits per chunk (the lanes holding m, l)
   const int hq = blockIdx.x, hd = a.hd, G = a.n_heads / a.n_kv, SB = a.splits;
-  const int kvh = hq / G, g = hq % G;
-  const int64_t pstride = hd + 2;
-  const float* hp = a.part + ((int64_t)kvh * SB * G + g) * pstride;  // split k at + k*G*pstride
-  if (threadIdx.x < 64) {
-    const int k = threadIdx.x;
-    const float mk = (k < SB) ? hp[(int64_t)k * G * pstride + hd] : -INFINITY;
-    const float M = wave_max_dpp(mk);
-    const float wk = (k < SB && mk != -INFINITY) ? expf(mk - M) : 0.0f;
-    const float lk = (k < SB) ? hp[(int64_t)k * G * pstride + hd + 1] : 0.0f;
-    const float den = wave_sum_dpp(wk * lk);
-    w[k] = wk;
-    if (k == 0) inv_den = den > 0.0f ? 1.0f / den : 0.0f;
+  const int kvh = hq / G, g = hq % G, lane = threadIdx.x & 63;
+  const int d = threadIdx.x < hd ? (int)threadIdx.x : hd - 1;  // lanes past hd repeat the last dim
+  const int64_t ks = (int64_t)G * (hd + 2);                      // split stride
+  const float* hp = a.part + ((int64_t)kvh * SB * G + g) * (hd + 2);
+  const int kl = lane < SB ? lane : SB - 1;
+  const float mk = hp[kl * ks + hd], lk = hp[kl * ks + hd + 1];
+  float ov[CH];
+#pragma unroll
+  for (int c = 0; c < CH; ++c) ov[c] = hp[(c < SB ? c : SB - 1) * ks + d];
+  const float mv = lane < SB ? mk : -INFINITY;
+  const float M = wave_max_dpp(mv);
+  const float wk = (lane < SB && mv != -INFINITY) ? expf(mv - M) : 0.0f;
+  const float den = wave_sum_dpp(wk * (lane < SB ? lk : 0.0f));
+  // splits past SB weigh 0 (their loads repeat split SB - 1): adding 0 * o
+  // leaves the sum as it is, and the FMAs stay on a straight line
+  float num = 0.0f;
+#pragma unroll
+  for (int c = 0; c < CH; ++c) num += lane_val(wk, c) * ov[c];
+  if (SB > CH) {  // 33 .. 64 splits: lanes 32 .. 63 hold their weights
+#pragma unroll
+    for (int c = 0; c < CH; ++c) ov[c] = hp[(CH + c < SB ? CH + c : SB - 1) * ks + d];
+#pragma unroll
+    for (int c = 0; c < CH; ++c) num += lane_val(wk, CH + c) * ov[c];
   }
-  __syncthreads();
-  for (int d = threadIdx.x; d < hd; d += blockDim.x) {
-    float num = 0.0f;
-#pragma unroll 16
-    for (int k = 0; k < SB; ++k) num += w[k] * hp[(int64_t)k * G * pstride + d];
-    a.out[(int64_t)hq * hd + d] = num * inv_den;
-  }
+  if ((int)threadIdx.x < hd) a.out[(int64_t)hq * hd + d] = num * (den > 0.0f ? 1.0f / den : 0.0f);
 }
 
 
@@ -720,7 +746,7 @@ hipError_t launch_attention_decode(const AttnArgs& a, hipStream_t s) {
     if (ok) {
       const hipError_t st = hipGetLastError();
       if (st != hipSuccess) return st;
-      UAII_LAUNCH(k_attn_merge, dim3(a.n_heads), dim3(256), 0, s, a);
+      UAII_LAUNCH(k_attn_merge, dim3(a.n_heads), dim3((a.hd + 63) / 64 * 64), 0, s, a);
       return hipGetLastError();
     }
   }
@@ -737,7 +763,7 @@ hipError_t launch_attention_decode(const AttnArgs& a, hipStream_t s) {
   }
   const hipError_t st = hipGetLastError();
   if (st != hipSuccess) return st;
-  UAII_LAUNCH(k_attn_merge, dim3(a.n_heads), dim3(256), 0, s, a);
+  UAII_LAUNCH(k_attn_merge, dim3(a.n_heads), dim3((a.hd + 63) / 64 * 64), 0, s, a);
   return hipGetLastError();
 }
 
