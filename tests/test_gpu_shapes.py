@@ -47,13 +47,10 @@ def maxrel(a, b):
     return float(np.abs(np.asarray(a, np.float64) - b).max() / max(np.abs(b).max(), 1e-30))
 
 
-@pytest.mark.parametrize("kv_f16", [1, 0])
-@pytest.mark.parametrize("heads", [(32, 8, 128), (64, 8, 128), (32, 8, 64)], ids=str)
-@pytest.mark.parametrize("n_keys", [1, 2049, 4090, 4096])
-def test_attention_decode_32_splits(hip, kv_f16, heads, n_keys):
-    nh, nkv, hd = heads
-    max_seq = 4096
-    rng = np.random.default_rng(n_keys * 13 + nh + hd)
+def check_attention_decode(hip, nh, nkv, hd, kv_f16, max_seq, n_keys, seed):
+    """uaii_hip_attention_decode on seeded q, K, V against the oracle's
+    attention_kv_f32 restatement (the past n_keys - 1 keys, then the current one)."""
+    rng = np.random.default_rng(seed)
     q = rng.standard_normal(nh * hd).astype(np.float32)
     k = rng.standard_normal((nkv, max_seq, hd)).astype(np.float32)
     v = rng.standard_normal((nkv, max_seq, hd)).astype(np.float32)
@@ -76,6 +73,24 @@ def test_attention_decode_32_splits(hip, kv_f16, heads, n_keys):
     assert maxrel(got, want) < 1e-5
     if n_keys == 1:
         assert maxrel(got, np.repeat(vf[0].reshape(nkv, hd), nh // nkv, axis=0).reshape(-1)) < 1e-6
+
+
+@pytest.mark.parametrize("kv_f16", [1, 0])
+@pytest.mark.parametrize("heads", [(32, 8, 128), (64, 8, 128), (32, 8, 64)], ids=str)
+@pytest.mark.parametrize("n_keys", [1, 2049, 4090, 4096])
+def test_attention_decode_32_splits(hip, kv_f16, heads, n_keys):
+    nh, nkv, hd = heads
+    check_attention_decode(hip, nh, nkv, hd, kv_f16, 4096, n_keys, n_keys * 13 + nh + hd)
+
+
+@pytest.mark.parametrize("heads", [(32, 8, 128), (32, 8, 64)], ids=str)
+@pytest.mark.parametrize("n_keys", [4097, 4224, 6000, 8192, 12289])
+def test_attention_decode_several_tiles_per_wave(hip, heads, n_keys):
+    """A cache past 4096 positions (12800): 32 splits of 129 .. 385 keys, so the
+    f16 kernel's waves walk 2 to 4 tiles with their two register sets in turn
+    (odd and even tile counts, a last pass with a single key)."""
+    nh, nkv, hd = heads
+    check_attention_decode(hip, nh, nkv, hd, 1, 12800, n_keys, n_keys * 13 + nh + hd + 1)
 
 
 def run_device(path, prompt, n_new, n_layers, kv_f16=True, max_context=0):

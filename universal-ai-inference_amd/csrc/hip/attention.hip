@@ -437,12 +437,12 @@ __global__ void __launch_bounds__(NW * 64) k_attn_h16(AttnArgs a) {
   const int vd = lane % LV, vk = lane / LV;   // P.V: dims [8 vd, 8 vd + 8) of key vk + VPI j
 
   // Two register sets, used in turn: a wave's next tile is in flight while it
-  // computes one, and every load stays on a straight line. (A loop that loads
-  // its tile at the top for every pass but the first joins two load paths at
-  // the loop head, and the compiler then waited there for the whole first tile,
-  // K and V, before the first score: with one tile per wave, as at 4096
-  // positions, this form measured attention + merge 12.1 against 12.7 us on the
-  // 8B decode, the waits for V now falling inside the score and softmax work.)
+  // computes one. (A loop that loads its tile at the top of every pass but the
+  // first joins two load paths at the loop head, and the compiler then waited
+  // there for the whole first tile, K and V, before the first score. With one
+  // tile per wave, as at 4096 positions, the straight-line path below measured
+  // attention + merge 12.1 against 12.7 us on the 8B decode, the waits for V
+  // falling inside the score and softmax work.)
   uint4 kr[KJ][4], vr[VJ], kn[KJ][4], vn[VJ];
   auto load_tile = [&](int t0, uint4 (&K)[KJ][4], uint4 (&V)[VJ]) __attribute__((always_inline)) {
 #pragma unroll
@@ -566,12 +566,18 @@ __global__ void __launch_bounds__(NW * 64) k_attn_h16(AttnArgs a) {
   };
 
   const int step = NW * TK;
-  for (int t0 = first; t0 < b1; t0 += 2 * step) {
-    if (t0 + step < b1) load_tile(t0 + step, kn, vn);
-    tile(t0, kr, vr);
-    if (t0 + step >= b1) break;
-    if (t0 + 2 * step < b1) load_tile(t0 + 2 * step, kr, vr);
-    tile(t0 + step, kn, vn);
+  if (b1 - b0 <= step) {
+    // at most one tile per wave (every split of a cache up to 4096 positions):
+    // no next-tile code ahead of the first scores
+    if (first < b1) tile(first, kr, vr);
+  } else {
+    for (int t0 = first; t0 < b1; t0 += 2 * step) {
+      if (t0 + step < b1) load_tile(t0 + step, kn, vn);
+      tile(t0, kr, vr);
+      if (t0 + step >= b1) break;
+      if (t0 + 2 * step < b1) load_tile(t0 + 2 * step, kr, vr);
+      tile(t0 + step, kn, vn);
+    }
   }
 
   // reduce the key groups of P.V (lanes vd, vd + LV, ...)
