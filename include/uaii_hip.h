@@ -50,11 +50,6 @@ typedef struct uaii_hip_weight uaii_hip_weight;
 /* ---- device and memory ---------------------------------------------------- */
 UAII_HIP_API int uaii_hip_init(int device);
 UAII_HIP_API int uaii_hip_device_count(int* count);
-/* *supported = 1 when a grid (8, 32) places all blocks (h, s) of one h on one XCD
- * of the current device (probed once with HW_REG_XCC_ID): the condition under which decode
- * attention over 8 kv heads merges its key splits inside the split kernel
- * instead of a second launch. No reference counterpart. */
-UAII_HIP_API int uaii_hip_xcd_merge_supported(int* supported);
 UAII_HIP_API const char* uaii_hip_error_string(int code);
 UAII_HIP_API int uaii_hip_malloc(void** ptr, size_t bytes);
 UAII_HIP_API int uaii_hip_free(void* ptr);

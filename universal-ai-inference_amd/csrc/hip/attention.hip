@@ -14,7 +14,8 @@
 // costs more than the extra launch: with a device-scope release per block, an L2
 // write-back on CDNA4; with write-through (sc1) partial stores and sc1 loads in
 // the merging block, 409 against 451 tok/s on the 8B decode, the merge code
-// raising the kernel to 214 VGPRs.)
+// raising the kernel to 214 VGPRs; with the splits of a kv head on one XCD and
+// the ticket and partials in its L2, 518 against 526 tok/s.)
 
 #include "common.h"
 #include "uaii_hip_internal.h"
@@ -296,86 +297,6 @@ __global__ void __launch_bounds__(256) k_attn_fast(AttnArgs a) {
   }
 }
 
-// ---- the split merge inside the split kernel, through one XCD's L2 ------------------
-//
-// With 8 kv heads the grid (8, S) puts block (h, s), linear id h + 8 s, on XCD
-// (h + c) mod 8 under the round-robin dispatch of workgroups to the 8 XCDs (c,
-// where the round robin starts, depends on the launches before), so every
-// split of a kv head shares one L2. The last of them to finish merges the S
-// partials there instead of a second kernel (k_attn_merge): each block waits
-// until its partial stores are in the L2 (vmcnt 0: stores complete at the L2,
-// the L1 being write-through), then takes a ticket with an atomic add of
-// 2^(8 x) for its XCD x; the block that brings the total to S reads the
-// partials with L1-bypassing (sc0) loads, which hit that L2, and resets the
-// ticket. No device-scope release is needed because no partial leaves the XCD
-// (a device-scope fence would write the whole L2 back). prepare_attention checks
-// the co-location once with HW_REG_XCC_ID (xcd_merge_supported); the ticket
-// checks it again on every launch: unless all S arrivals counted in the
-// merging block's own XCD field, the merge is skipped and the fail word set,
-// which the host reports. The merge's arithmetic and order are
-// k_attn_merge's, so the output is the same bit for bit.
-
-constexpr unsigned kXccReg = (3u << 11) | 20u;  // hwreg(HW_REG_XCC_ID, 0, 4)
-
-__device__ inline float ld_l2(const float* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);  // global_load sc0
-}
-
-template <int HD, int G, int NT>
-__device__ inline void merge_tail(const AttnArgs& a, int h, int SB) {
-  __shared__ int s_last;
-  __shared__ float s_w[G][64];
-  __shared__ float s_inv[G];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this thread's partial stores are in the L2
-  __syncthreads();
-  if (tid == 0) {
-    const unsigned xcc = __builtin_amdgcn_s_getreg(kXccReg) & 7u;
-    const unsigned long long inc = 1ull << (8 * xcc);
-    unsigned long long* ticket = reinterpret_cast<unsigned long long*>(a.sync + 32 * h);
-    const unsigned long long now =
-        __hip_atomic_fetch_add(ticket, inc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) + inc;
-    unsigned total = 0;
-#pragma unroll
-    for (int x = 0; x < 8; ++x) total += (unsigned)((now >> (8 * x)) & 0xffu);
-    int last = 0;
-    if (total == (unsigned)SB) {
-      last = (now == (unsigned long long)SB << (8 * xcc)) ? 1 : -1;
-      __hip_atomic_store(ticket, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-      if (last < 0) __hip_atomic_store(a.sync + 32 * 64, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    s_last = last;
-  }
-  __syncthreads();
-  if (s_last != 1) return;
-  const int64_t pstride = HD + 2;
-  const float* hp0 = a.part + (int64_t)h * SB * G * pstride;  // split k, head g at + (k * G + g) * pstride
-  for (int g = wave; g < G; g += NT / 64) {
-    const float* hp = hp0 + (int64_t)g * pstride;
-    const int k = lane;
-    const float mk = (k < SB) ? ld_l2(hp + (int64_t)k * G * pstride + HD) : -INFINITY;
-    const float M = wave_max_dpp(mk);
-    const float wk = (k < SB && mk != -INFINITY) ? expf(mk - M) : 0.0f;
-    const float lk = (k < SB) ? ld_l2(hp + (int64_t)k * G * pstride + HD + 1) : 0.0f;
-    const float den = wave_sum_dpp(wk * lk);
-    s_w[g][k] = wk;
-    if (k == 0) s_inv[g] = den > 0.0f ? 1.0f / den : 0.0f;
-  }
-  __syncthreads();
-  for (int i = tid; i < G * HD; i += NT) {
-    const int g = i / HD, d = i % HD;
-    const float* hp = hp0 + (int64_t)g * pstride;
-    float num = 0.0f;
-#pragma unroll 16
-    for (int k = 0; k < SB; ++k) num += s_w[g][k] * ld_l2(hp + (int64_t)k * G * pstride + d);
-    a.out[((int64_t)h * G + g) * HD + d] = num * s_inv[g];
-  }
-}
-
-__global__ void k_xcc_probe(unsigned* out) {
-  if (threadIdx.x == 0) out[blockIdx.y * gridDim.x + blockIdx.x] = __builtin_amdgcn_s_getreg(kXccReg);
-}
-
 // ---- f16 KV, head_dim 64 / 128: one memory round trip per 32-key tile ---------------
 //
 // A wave takes tiles of TK = 32 keys. All K and V loads of a tile are issued
@@ -395,7 +316,7 @@ __device__ inline float adot2(uint32_t a, uint32_t b, float c) {
 
 __device__ inline uint32_t ah_bits(_Float16 h) { return (uint32_t)__builtin_bit_cast(uint16_t, h); }
 
-template <int HD, int G, int TK, int NW, bool MERGE>
+template <int HD, int G, int TK, int NW>
 __global__ void __launch_bounds__(NW * 64) k_attn_h16(AttnArgs a) {
   static_assert(TK == 16 || TK == 32, "tile of 16 or 32 keys");
   static_assert(TK >= 64 / (HD / 32), "at least one key per lane group in the scores");
@@ -620,22 +541,21 @@ __global__ void __launch_bounds__(NW * 64) k_attn_h16(AttnArgs a) {
       part[g * pstride + HD + 1] = den;
     }
   }
-  if constexpr (MERGE) merge_tail<HD, G, NT>(a, h, SB);
 }
 
 // Tiles of 32 keys per wave: a block covers 128 keys per pass. (16-key tiles
 // with twice the splits measured slower end to end: more blocks and a wider
 // merge cost more than the shorter per-block chain saves.)
 // (Eight waves of 16-key tiles per block measured within 2 % of this.)
-template <int HD, bool MERGE>
+template <int HD>
 bool launch_h16(const AttnArgs& a, int G, hipStream_t s) {
   constexpr int TK = 32, NW = 4;
   dim3 grid(a.n_kv, a.splits);
   switch (G) {
-    case 1: UAII_LAUNCH((k_attn_h16<HD, 1, TK, NW, MERGE>), grid, dim3(NW * 64), 0, s, a); return true;
-    case 2: UAII_LAUNCH((k_attn_h16<HD, 2, TK, NW, MERGE>), grid, dim3(NW * 64), 0, s, a); return true;
-    case 4: UAII_LAUNCH((k_attn_h16<HD, 4, TK, NW, MERGE>), grid, dim3(NW * 64), 0, s, a); return true;
-    case 8: UAII_LAUNCH((k_attn_h16<HD, 8, TK, NW, MERGE>), grid, dim3(NW * 64), 0, s, a); return true;
+    case 1: UAII_LAUNCH((k_attn_h16<HD, 1, TK, NW>), grid, dim3(NW * 64), 0, s, a); return true;
+    case 2: UAII_LAUNCH((k_attn_h16<HD, 2, TK, NW>), grid, dim3(NW * 64), 0, s, a); return true;
+    case 4: UAII_LAUNCH((k_attn_h16<HD, 4, TK, NW>), grid, dim3(NW * 64), 0, s, a); return true;
+    case 8: UAII_LAUNCH((k_attn_h16<HD, 8, TK, NW>), grid, dim3(NW * 64), 0, s, a); return true;
     default: return false;
   }
 }
@@ -648,8 +568,7 @@ bool launch_h16(const AttnArgs& a, int G, hipStream_t s) {
 // with readlane; a thread's dims of the first 32 splits' o are loaded together
 // with them, before any arithmetic, so the merge costs one memory round trip
 // (where loading the weights first, through LDS, and then the o values cost
-// three). The sums and their order are those of a loop s = 0 .. SB-1 (the
-// in-kernel merge, merge_tail, relies on it).
+// three). The sums and their order are those of a loop s = 0 .. SB-1.
 __global__ void __launch_bounds__(256) k_attn_merge(AttnArgs a) {
   constexpr int CH = 32;  // splits per chunk (the lanes holding m, l)
   const int hq = blockIdx.x, hd = a.hd, G = a.n_heads / a.n_kv, SB = a.splits;
@@ -713,40 +632,13 @@ int attention_splits(int64_t max_seq) {
   return (int)(s < 1 ? 1 : (s > 32 ? 32 : s));
 }
 
-bool xcd_merge_supported() {
-  static int cached = -1;
-  if (cached >= 0) return cached == 1;
-  cached = 0;
-  unsigned* d = nullptr;
-  constexpr int NB = 8 * 32;
-  if (hipMalloc(&d, NB * sizeof(unsigned)) != hipSuccess) {
-    (void)hipGetLastError();
-    return false;
-  }
-  unsigned h[NB];
-  hipLaunchKernelGGL(k_xcc_probe, dim3(8, 32), dim3(64), 0, nullptr, d);
-  bool ok = hipGetLastError() == hipSuccess && hipDeviceSynchronize() == hipSuccess &&
-            hipMemcpy(h, d, sizeof(h), hipMemcpyDeviceToHost) == hipSuccess;
-  // co-location: every block of one kv head (same blockIdx.x) on one XCD
-  for (int i = 8; ok && i < NB; ++i) ok = (h[i] & 7u) == (h[i % 8] & 7u);
-  (void)hipFree(d);
-  (void)hipGetLastError();
-  cached = ok ? 1 : 0;
-  return ok;
-}
-
 hipError_t launch_attention_decode(const AttnArgs& a, hipStream_t s) {
   const int G = a.n_heads / a.n_kv;
   if (G < 1 || G > MAXG || a.hd > 256 || a.hd % 2 || a.n_heads % a.n_kv) return hipErrorInvalidValue;
   if (a.splits < 1 || a.splits > 64) return hipErrorInvalidValue;
   if ((a.hd == 64 || a.hd == 128) && (G == 1 || G == 2 || G == 4 || G == 8)) {
     bool ok;
-    if (a.kv_f16 && a.sync && a.n_kv == 8 && a.splits <= 64) {
-      // the split merge in the split kernel (one launch): see merge_tail
-      ok = (a.hd == 64) ? launch_h16<64, true>(a, G, s) : launch_h16<128, true>(a, G, s);
-      if (ok) return hipGetLastError();
-    }
-    if (a.kv_f16) ok = (a.hd == 64) ? launch_h16<64, false>(a, G, s) : launch_h16<128, false>(a, G, s);
+    if (a.kv_f16) ok = (a.hd == 64) ? launch_h16<64>(a, G, s) : launch_h16<128>(a, G, s);
     else if (a.hd == 64) ok = launch_fast_hd<false, 64>(a, G, s);
     else ok = launch_fast_hd<false, 128>(a, G, s);
     if (ok) {

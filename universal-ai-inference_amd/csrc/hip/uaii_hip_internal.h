@@ -151,15 +151,9 @@ struct AttnArgs {
   int splits;
   float* out;            // [n_heads * hd]
   float* part;           // [n_kv][splits][group][hd + 2]
-  // non-null: merge the splits in the split kernel (8 kv heads, f16 cache);
-  // 64-bit tickets at sync[32 h] (zero between launches), fail word at sync[32 * 64]
-  unsigned* sync;
 };
 
 int attention_splits(int64_t max_seq);
-// Whether the grid (8, 32) puts all blocks (h, s) of one h on one XCD (probed
-// once with HW_REG_XCC_ID): the condition of the in-kernel split merge.
-bool xcd_merge_supported();
 hipError_t launch_attention_decode(const AttnArgs& a, hipStream_t s);
 hipError_t prepare_attention();
 // Resolves the allocation-free attention scratch of the current device (noalloc.hip).

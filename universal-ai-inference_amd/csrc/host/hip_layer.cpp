@@ -57,12 +57,6 @@ int uaii_hip_init(int device) {
   return (int)prepare_noalloc();
 }
 
-int uaii_hip_xcd_merge_supported(int* supported) {
-  if (!supported) return kErrArg;
-  *supported = uaii_hip::xcd_merge_supported() ? 1 : 0;
-  return 0;
-}
-
 int uaii_hip_device_count(int* count) {
   if (!count) return kErrArg;
   return (int)hipGetDeviceCount(count);

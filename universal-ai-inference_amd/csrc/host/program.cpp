@@ -360,22 +360,6 @@ Error DecoderProgram::build(const DecoderSpec& spec, const ProgramOptions& opts)
   if (const char* env = std::getenv("UAII_PF_H16")) pf_h16_ = std::string(env) != "0";
   UAII_TRY(alloc(1024, (void**)&ring_pad_));
   {
-    // UAII_ATTN_MERGE=1: the split merge inside the attention kernel when 8 kv
-    // heads meet 8 XCDs with the co-location the probe confirms (the same
-    // results bit for bit). Off by default: on the 8B decode it measured 11.95
-    // against 12.39 us for split + merge kernel and 492.2 against 493.5 tok/s,
-    // the merging block's chain (store completion, ticket, two rounds of L2
-    // loads) costing about what the second launch does.
-    const char* env = std::getenv("UAII_ATTN_MERGE");
-    const bool want = env && std::string(env) == "1";
-    if (want && opts_.kv_f16 && d.n_kv_heads == 8 && (d.head_dim == 64 || d.head_dim == 128) &&
-        xcd_merge_supported()) {
-      constexpr size_t bytes = sizeof(unsigned) * (32 * 64 + 32);
-      UAII_TRY(alloc(bytes, (void**)&attn_sync_));
-      UAII_HIP(hipMemset(attn_sync_, 0, bytes));
-    }
-  }
-  {
     // the ring kernel measures faster for the residual-add GEMVs (O, down; the
     // QKV and gate/up GEMVs measured slower on it, their RMSNorm staging waiting
     // behind the first loads, as did the LM head); UAII_RING=0 keeps every
@@ -911,43 +895,21 @@ Error DecoderProgram::seek(int64_t pos) {
   return Error::success();
 }
 
-// After the stream has drained: a fail word a kernel set leaves the step's
-// results meaningless; report it (once) to whichever read-back comes first.
-Error DecoderProgram::check_device_fail() {
-  if (attn_sync_) {
-    unsigned afail = 0;
-    UAII_HIP(hipMemcpy(&afail, attn_sync_ + 32 * 64, sizeof(afail), hipMemcpyDeviceToHost));
-    if (afail) {
-      // the split blocks of a kv head ran on more than one XCD: this step's
-      // attention was not merged; later steps use the merge kernel
-      attn_sync_ = nullptr;
-      for (auto& g : graph_) {  // re-captured with the merge kernel
-        if (g) (void)hipGraphExecDestroy(g);
-        g = nullptr;
-      }
-      return Error::make(ErrorCode::Internal, "decode attention: the key splits of a kv head ran on more than one XCD");
-    }
-  }
-  return Error::success();
-}
-
 Error DecoderProgram::read_state(StepState* st) {
   UAII_HIP(hipStreamSynchronize(stream_));
-  UAII_TRY(check_device_fail());
   UAII_HIP(hipMemcpy(st, state_, sizeof(StepState), hipMemcpyDeviceToHost));
   return Error::success();
 }
 
 Error DecoderProgram::synchronize() {
   UAII_HIP(hipStreamSynchronize(stream_));
-  return check_device_fail();
+  return Error::success();
 }
 
 Error DecoderProgram::read_ids(int64_t* out, int64_t n) {
   if (n > max_ctx_ + 1) return Error::make(ErrorCode::InvalidArgument, "read_ids beyond capacity");
   std::vector<int32_t> ids((size_t)n);
   UAII_HIP(hipStreamSynchronize(stream_));
-  UAII_TRY(check_device_fail());
   UAII_HIP(hipMemcpy(ids.data(), ids_, (size_t)n * 4, hipMemcpyDeviceToHost));
   for (int64_t i = 0; i < n; ++i) out[i] = ids[(size_t)i];
   return Error::success();
@@ -957,7 +919,6 @@ Error DecoderProgram::read_id(int64_t index, int64_t* id) {
   if (index < 0 || index > max_ctx_) return Error::make(ErrorCode::InvalidArgument, "read_id beyond capacity");
   int32_t v = 0;
   UAII_HIP(hipStreamSynchronize(stream_));
-  UAII_TRY(check_device_fail());
   UAII_HIP(hipMemcpy(&v, ids_ + index, 4, hipMemcpyDeviceToHost));
   *id = v;
   return Error::success();
@@ -1041,7 +1002,6 @@ Error DecoderProgram::encode_step(bool want_logits) {
     at.out = attn_;
     at.part = attn_part_;
     at.splits = attn_splits_;
-    at.sync = attn_sync_;
     const double attn_bytes = 2.0 * (double)(pos_host + 1) * (double)d.kv_dim * (double)elem +
                               8.0 * (double)d.q_dim;
     UAII_TRY(timed("attention", attn_bytes, [&] { return launch_attention_decode(at, s); }));
@@ -1342,7 +1302,6 @@ Error DecoderProgram::read_tap(const std::string& name, std::vector<float>* out)
   }
   out->resize(n);
   UAII_HIP(hipStreamSynchronize(stream_));
-  UAII_TRY(check_device_fail());
   UAII_HIP(hipMemcpy(out->data(), src, n * 4, hipMemcpyDeviceToHost));
   return Error::success();
 }

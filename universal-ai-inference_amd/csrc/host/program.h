@@ -142,7 +142,6 @@ class DecoderProgram {
   template <class F>
   Error timed(const char* name, double bytes, double flops, F&& launch);
   Error collect_timings();
-  Error check_device_fail();
   Error ensure_prefill_buffers(int64_t chunk);
   Error pf_gemm(const DeviceWeight* w[3], const int64_t cols0[3], int nw, const DeviceWeight* w2,
                 int epi, int64_t m, float* y, int64_t ldy, int store_split = 1);
@@ -189,7 +188,6 @@ class DecoderProgram {
   float* attn_part_ = nullptr;
   // decode attention merged inside the split kernel: tickets + fail word
   // (AttnArgs::sync), null when the two-launch path runs
-  unsigned* attn_sync_ = nullptr;
   int attn_splits_ = 1;
 
   // the residual-add GEMVs (O, down) through the LDS ring (ring_gemv.hip) where

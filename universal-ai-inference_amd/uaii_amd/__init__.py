@@ -166,7 +166,6 @@ def lib() -> C.CDLL:
         "uaii_model_describe": (C.c_int, [C.c_char_p, C.c_char_p, C.c_size_t]),
         "uaii_hip_init": (C.c_int, [C.c_int]),
         "uaii_hip_device_count": (C.c_int, [C.POINTER(C.c_int)]),
-        "uaii_hip_xcd_merge_supported": (C.c_int, [C.POINTER(C.c_int)]),
         "uaii_hip_error_string": (C.c_char_p, [C.c_int]),
         "uaii_hip_malloc": (C.c_int, [C.POINTER(vp), C.c_size_t]),
         "uaii_hip_free": (C.c_int, [vp]),
