@@ -24,6 +24,9 @@
  *   uaii_hip_sample            non-greedy sample_token_f32 (sampling.cpp:53-125) on the device
  *   uaii_hip_rope              rope_f32 (libs/uaii-kernels/src/transformer.cpp:144-220)
  *   uaii_hip_attention_decode  attention_kv_f32, q_seq=1 (transformer.cpp:222-433)
+ *   uaii_hip_attention_o       attention_kv_f32 + quant_gemm_f32 of the attention
+ *                              output + residual add_f32 (quant_gemm.cpp:22-70,
+ *                              elementwise.cpp:99-110), the decode layer's attention half
  *   uaii_hip_gemv_add          quant_gemm_f32 + residual add_f32 (elementwise.cpp:86-97)
  *   uaii_hip_gemv_swiglu       two quant_gemm_f32 + silu_f32 * mul_f32
  *                              (elementwise.cpp:73-110), the graph's FFN gate/up
@@ -149,6 +152,21 @@ UAII_HIP_API int uaii_hip_attention_decode(const float* q, const void* kcache,
                                            const void* vcache, int kv_f16, int64_t max_seq,
                                            int n_heads, int n_kv_heads, int head_dim,
                                            int64_t n_keys, float* out, void* stream);
+
+/* uaii_hip_attention_decode, then y += W_o . out (residual add), in two
+ * launches: the key-split kernel, then one launch that merges the splits of
+ * 256 / head_dim heads per block, writes them to `out` and adds its share of
+ * the W_o product into y with float atomics. out is the same bits as
+ * uaii_hip_attention_decode's; each y row is a sum whose adds arrive in an
+ * order the hardware picks, so runs can differ in its last bits. W_o: Q4_0,
+ * [rows][n_heads * head_dim] with n_heads * head_dim a multiple of 256,
+ * head_dim 64 or 128, rows (y's length) a multiple of 32; other shapes return
+ * -1 and launch nothing. */
+UAII_HIP_API int uaii_hip_attention_o(const float* q, const void* kcache, const void* vcache,
+                                      int kv_f16, int64_t max_seq, int n_heads,
+                                      int n_kv_heads, int head_dim, int64_t n_keys,
+                                      const uaii_hip_weight* wo, float* out, float* y,
+                                      void* stream);
 
 /* uaii_hip_attention_decode without any allocation. No counterpart in the
  * reference: it is for callers that cannot allocate device memory (code under

@@ -5,6 +5,10 @@
   attention_kv_f32 restatement (transformer.cpp:222-433) at 1, 2049, 4090 and
   4096 keys, 32 or 64 query heads over 8 kv heads, head_dim 64 / 128, f16 and
   f32 caches.
+* The split merge fused with the O projection and residual add
+  (uaii_hip_attention_o) at the 8B, 1B and wider shapes: the merged output the
+  same bits as the two-launch attention's, y within 1e-5 of the oracle's
+  quant_gemm_f32 of it plus the residual.
 * The Llama-3-8B shape (Q4_0 and Q8_0), two layers of it at full width with a
   4096-position KV cache: a 96-token prompt on the matrix cores, then 64 greedy
   tokens; ids identical to the oracle with an fp16 cache, logits and the
@@ -91,6 +95,75 @@ def test_attention_decode_several_tiles_per_wave(hip, heads, n_keys):
     (odd and even tile counts, a last pass with a single key)."""
     nh, nkv, hd = heads
     check_attention_decode(hip, nh, nkv, hd, 1, 12800, n_keys, n_keys * 13 + nh + hd + 1)
+
+
+def check_attention_o(hip, nh, nkv, hd, kv_f16, max_seq, n_keys, rows, seed):
+    """uaii_hip_attention_o: its attention output the same bits as
+    uaii_hip_attention_decode's, and y = y0 + W_o . out within 1e-5 of the
+    oracle's quant_gemm_f32 of that output plus y0 (quant_gemm.cpp:22-70,
+    elementwise.cpp:99-110). A second call from the same y0 agrees with the
+    first to 1e-6 (its float atomics add in arrival order)."""
+    rng = np.random.default_rng(seed)
+    q = rng.standard_normal(nh * hd).astype(np.float32)
+    k = rng.standard_normal((nkv, max_seq, hd)).astype(np.float32)
+    v = rng.standard_normal((nkv, max_seq, hd)).astype(np.float32)
+    if kv_f16:
+        k, v = k.astype(np.float16), v.astype(np.float16)
+    packed = synth.quantize(uaii_amd.Q4_0, synth.normals(seed, 0, 0, rows * nh * hd, 0.02))
+    w = uaii_amd.DeviceWeight(uaii_amd.Q4_0, packed, rows, nh * hd)
+    y0 = rng.standard_normal(rows).astype(np.float32)
+    dq, dk, dv = DeviceBuffer.from_array(q), DeviceBuffer.from_array(k), DeviceBuffer.from_array(v)
+    do, do2 = DeviceBuffer(nh * hd * 4), DeviceBuffer(nh * hd * 4)
+    ys = []
+    for _ in range(2):
+        dy = DeviceBuffer.from_array(y0)
+        check_hip(hip.uaii_hip_attention_o(dq.ptr, dk.ptr, dv.ptr, kv_f16, max_seq, nh, nkv, hd, n_keys,
+                                           w.h, do.ptr, dy.ptr, None), "attention_o")
+        ys.append(dy.to_array(np.float32, rows))
+    check_hip(hip.uaii_hip_attention_decode(dq.ptr, dk.ptr, dv.ptr, kv_f16, max_seq, nh, nkv, hd,
+                                            n_keys, do2.ptr, None), "attention_decode")
+    out, out2 = do.to_array(np.float32, nh * hd), do2.to_array(np.float32, nh * hd)
+    assert np.array_equal(out.view(np.uint32), out2.view(np.uint32))
+    want = y0 + oracle.quant_gemm(uaii_amd.Q4_0, out2, packed, rows, nthreads=THREADS)[0]
+    assert maxrel(ys[0], want) < 1e-5
+    assert maxrel(ys[1], ys[0]) < 1e-6
+
+
+@pytest.mark.parametrize("case", [
+    (32, 8, 128, 1, 4096, 4096, 4096),     # 8B: 16 slices of 2 heads, 128-row blocks
+    (32, 8, 128, 1, 4096, 1, 4096),        # one key: the merge of a single split
+    (32, 8, 64, 1, 4096, 4090, 2048),      # 1B: 8 slices of 4 heads, 32-row blocks
+    (64, 8, 128, 0, 4096, 2049, 8192),     # G = 8, f32 cache, q_dim 8192
+    (8, 8, 128, 1, 12800, 12289, 96),      # G = 1, 4 slices, 3 row blocks
+    (16, 2, 128, 1, 640, 300, 160),        # G = 8 over 5 splits, 5 row blocks
+], ids=str)
+def test_attention_o(hip, case):
+    nh, nkv, hd, kv_f16, max_seq, n_keys, rows = case
+    check_attention_o(hip, nh, nkv, hd, kv_f16, max_seq, n_keys, rows, nh * 7 + hd + n_keys + rows)
+
+
+def test_attention_o_refuses_unsupported_shapes(hip):
+    """W_o other than Q4_0, rows not a multiple of 32, head_dim other than 64
+    or 128, or n_heads * head_dim not a multiple of 256: -1 before any launch."""
+    nh, nkv, hd, max_seq = 32, 8, 128, 256
+    buf = DeviceBuffer(nkv * max_seq * hd * 4)
+    out, y = DeviceBuffer(nh * hd * 4), DeviceBuffer(8192 * 4)
+    x = synth.normals(3, 0, 0, 96 * nh * hd, 0.02)
+    bad = [uaii_amd.DeviceWeight(uaii_amd.Q4_K, synth.quantize(uaii_amd.Q4_K, x[: 64 * nh * hd]), 64, nh * hd),
+           uaii_amd.DeviceWeight(uaii_amd.Q4_0, synth.quantize(uaii_amd.Q4_0, x[: 48 * nh * hd]), 48, nh * hd)]
+    for w in bad:
+        assert hip.uaii_hip_attention_o(buf.ptr, buf.ptr, buf.ptr, 1, max_seq, nh, nkv, hd, 10, w.h, out.ptr,
+                                        y.ptr, None) == -1
+    w96 = uaii_amd.DeviceWeight(uaii_amd.Q4_0, synth.quantize(uaii_amd.Q4_0, x[: 32 * 24 * 96]), 32, 24 * 96)
+    assert hip.uaii_hip_attention_o(buf.ptr, buf.ptr, buf.ptr, 1, max_seq, 24, 8, 96, 10, w96.h, out.ptr,
+                                    y.ptr, None) == -1  # head_dim 96
+    w4 = uaii_amd.DeviceWeight(uaii_amd.Q4_0, synth.quantize(uaii_amd.Q4_0, x[: 32 * 6 * 64]), 32, 6 * 64)
+    assert hip.uaii_hip_attention_o(buf.ptr, buf.ptr, buf.ptr, 1, max_seq, 6, 2, 64, 10, w4.h, out.ptr,
+                                    y.ptr, None) == -1  # q_dim 384
+    w256 = uaii_amd.DeviceWeight(uaii_amd.Q4_0, synth.quantize(uaii_amd.Q4_0, x[: 32 * 4 * 256]), 32, 4 * 256)
+    assert hip.uaii_hip_attention_o(buf.ptr, buf.ptr, buf.ptr, 1, max_seq, 4, 2, 256, 10, w256.h, out.ptr,
+                                    y.ptr, None) == -1  # head_dim 256
+    check_hip(hip.uaii_hip_synchronize())
 
 
 def run_device(path, prompt, n_new, n_layers, kv_f16=True, max_context=0):

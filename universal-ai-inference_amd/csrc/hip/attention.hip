@@ -630,7 +630,7 @@ int attention_splits(int64_t max_seq) {
   return (int)(s < 1 ? 1 : (s > 32 ? 32 : s));
 }
 
-hipError_t launch_attention_decode(const AttnArgs& a, hipStream_t s) {
+hipError_t launch_attention_splits(const AttnArgs& a, hipStream_t s) {
   const int G = a.n_heads / a.n_kv;
   if (G < 1 || G > MAXG || a.hd > 256 || a.hd % 2 || a.n_heads % a.n_kv) return hipErrorInvalidValue;
   if (a.splits < 1 || a.splits > 32) return hipErrorInvalidValue;  // attention_splits: <= 32
@@ -639,12 +639,7 @@ hipError_t launch_attention_decode(const AttnArgs& a, hipStream_t s) {
     if (a.kv_f16) ok = (a.hd == 64) ? launch_h16<64>(a, G, s) : launch_h16<128>(a, G, s);
     else if (a.hd == 64) ok = launch_fast_hd<false, 64>(a, G, s);
     else ok = launch_fast_hd<false, 128>(a, G, s);
-    if (ok) {
-      const hipError_t st = hipGetLastError();
-      if (st != hipSuccess) return st;
-      UAII_LAUNCH(k_attn_merge, dim3(a.n_heads), dim3((a.hd + 63) / 64 * 64), 0, s, a);
-      return hipGetLastError();
-    }
+    if (ok) return hipGetLastError();
   }
   const int tile = a.hd > 64 ? 32 : 64;
   const size_t lds = sizeof(float) * ((size_t)G * a.hd + 2 * tile * (size_t)(a.hd + 1) + (size_t)G * tile);
@@ -657,7 +652,11 @@ hipError_t launch_attention_decode(const AttnArgs& a, hipStream_t s) {
     if (a.kv_f16) UAII_LAUNCH((k_attn<true, 32>), grid, dim3(NT), lds, s, a);
     else UAII_LAUNCH((k_attn<false, 32>), grid, dim3(NT), lds, s, a);
   }
-  const hipError_t st = hipGetLastError();
+  return hipGetLastError();
+}
+
+hipError_t launch_attention_decode(const AttnArgs& a, hipStream_t s) {
+  const hipError_t st = launch_attention_splits(a, s);
   if (st != hipSuccess) return st;
   UAII_LAUNCH(k_attn_merge, dim3(a.n_heads), dim3((a.hd + 63) / 64 * 64), 0, s, a);
   return hipGetLastError();

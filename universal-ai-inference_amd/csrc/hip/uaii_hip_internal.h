@@ -155,6 +155,20 @@ struct AttnArgs {
 
 int attention_splits(int64_t max_seq);
 hipError_t launch_attention_decode(const AttnArgs& a, hipStream_t s);
+// The split kernel alone: partials into a.part, a.out untouched (a.splits <= 32).
+hipError_t launch_attention_splits(const AttnArgs& a, hipStream_t s);
+
+// ---- split merge + output projection + residual add (attn_out.hip) -----------------
+
+struct MergeOArgs {
+  AttnArgs at;      // the split partials (part, splits, heads, hd); merged values also to at.out
+  DevWeight w;      // W_o [rows][n_heads * hd], Q4_0
+  int64_t rows;     // output rows
+  float* y;         // residual stream: y[r] += W_o[r] . merged
+};
+
+bool merge_o_supported(const MergeOArgs& p);  // shapes and weight layout (not the pointers)
+hipError_t launch_merge_o(const MergeOArgs& p, hipStream_t s);
 hipError_t prepare_attention();
 // Resolves the allocation-free attention scratch of the current device (noalloc.hip).
 hipError_t prepare_noalloc();
@@ -178,6 +192,7 @@ struct RingArgs {
   int64_t rows;          // output rows (<= w.rows)
   float* y;              // output
   float* tap;            // EPI_ADD: copy of each written value, or null
+  float* tap0;           // EPI_ADD: copy of the residual before the add, or null
   const uint8_t* pad;    // >= 1 KiB of device memory read by the padding DMA lines
 };
 

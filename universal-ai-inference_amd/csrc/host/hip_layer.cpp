@@ -409,6 +409,44 @@ int uaii_hip_attention_decode(const float* q, const void* kcache, const void* vc
   return (int)launch_attention_decode(a, S(stream));
 }
 
+int uaii_hip_attention_o(const float* q, const void* kcache, const void* vcache, int kv_f16,
+                         int64_t max_seq, int n_heads, int n_kv_heads, int head_dim,
+                         int64_t n_keys, const uaii_hip_weight* wo, float* out, float* y,
+                         void* stream) {
+  if (!q || !kcache || !vcache || !out || !y || !wo || n_heads <= 0 || n_kv_heads <= 0 ||
+      n_heads % n_kv_heads || head_dim <= 0 || n_keys <= 0 || n_keys > max_seq ||
+      max_seq > INT32_MAX)
+    return kErrArg;
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  const int splits = uaii_hip::attention_splits(max_seq);
+  const int G = n_heads / n_kv_heads;
+  MergeOArgs m{};
+  AttnArgs& a = m.at;
+  a.q = q;
+  a.kcache = kcache;
+  a.vcache = vcache;
+  a.kv_f16 = kv_f16;
+  a.max_seq = max_seq;
+  a.n_heads = n_heads;
+  a.n_kv = n_kv_heads;
+  a.hd = head_dim;
+  a.state = nullptr;
+  a.fixed_len = (int)n_keys;
+  a.out = out;
+  a.splits = splits;
+  m.w = wo->w.view;
+  m.rows = wo->w.view.rows;
+  m.y = y;
+  if (!uaii_hip::merge_o_supported(m)) return kErrArg;
+  const size_t part = (size_t)n_kv_heads * splits * G * (size_t)(head_dim + 2) * 4;
+  int rc = grow_scratch(part);
+  if (rc) return rc;
+  a.part = static_cast<float*>(g_scratch);
+  const hipError_t st = launch_attention_splits(a, S(stream));
+  if (st != hipSuccess) return (int)st;
+  return (int)launch_merge_o(m, S(stream));
+}
+
 int uaii_hip_time_gemv(const uaii_hip_weight* w, const float* x, float* y, int iters,
                        float* avg_ms) {
   if (!w || !x || !y || iters <= 0 || !avg_ms) return kErrArg;

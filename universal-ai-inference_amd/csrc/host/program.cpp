@@ -369,6 +369,12 @@ Error DecoderProgram::build(const DecoderSpec& spec, const ProgramOptions& opts)
     if (prepare_ring_gemv() != hipSuccess) ring_mode_ = 0;
     (void)hipGetLastError();
   }
+  // The attention's split merge runs inside the O projection's launch
+  // (attn_out.hip: split kernel + merge/O 13.6 us against 18.0 us for split,
+  // merge and ring O on the 8B decode). Its residual adds are float atomics in
+  // arrival order; UAII_MERGE_O=0 keeps the merge kernel and the ring O
+  // projection, whose residual is the same bits on every run.
+  if (const char* env = std::getenv("UAII_MERGE_O")) merge_o_ = std::string(env) != "0";
   return Error::success();
 }
 
@@ -1004,7 +1010,32 @@ Error DecoderProgram::encode_step(bool want_logits) {
     at.splits = attn_splits_;
     const double attn_bytes = 2.0 * (double)(pos_host + 1) * (double)d.kv_dim * (double)elem +
                               8.0 * (double)d.q_dim;
-    UAII_TRY(timed("attention", attn_bytes, [&] { return launch_attention_decode(at, s); }));
+    // merge + O + residual in one launch, with the residual tap taken by the
+    // down projection's epilogue (the value it adds to)
+    MergeOArgs mo{};
+    mo.at = at;
+    mo.w = L.wo.view;
+    mo.rows = d.dim;
+    mo.y = x_;
+    RingArgs rd{};
+    bool fuse_o = false;
+    if (merge_o_ && ls.ffn == LayerSpec::kSwiGLU && ring_mode_ >= 1 && merge_o_supported(mo)) {
+      rd.w = L.down.view;
+      rd.rows = d.dim;
+      rd.epi = EPI_ADD;
+      rd.K = ls.inter;
+      rd.x = h_;
+      rd.y = x_;
+      rd.tap = tap_r2_ + li * d.dim;
+      rd.tap0 = tap_r1_ + li * d.dim;
+      rd.pad = ring_pad_;
+      fuse_o = ring_gemv_supported(rd);
+    }
+    if (fuse_o) {
+      UAII_TRY(timed("attention", attn_bytes, [&] { return launch_attention_splits(at, s); }));
+    } else {
+      UAII_TRY(timed("attention", attn_bytes, [&] { return launch_attention_decode(at, s); }));
+    }
 
     GemvArgs o{};
     o.nseg = 1;
@@ -1025,7 +1056,9 @@ Error DecoderProgram::encode_step(bool want_logits) {
     ro.y = x_;
     ro.tap = o.tap;
     ro.pad = ring_pad_;
-    if (ring_mode_ >= 1 && ring_gemv_supported(ro)) {
+    if (fuse_o) {
+      UAII_TRY(timed("gemv_o", gemv_bytes(L.wo.view), [&] { return launch_merge_o(mo, s); }));
+    } else if (ring_mode_ >= 1 && ring_gemv_supported(ro)) {
       UAII_TRY(timed("gemv_o", gemv_bytes(L.wo.view), [&] { return launch_ring_gemv(ro, s); }));
     } else {
       UAII_TRY(timed("gemv_o", gemv_bytes(L.wo.view), [&] { return launch_gemv(o, s); }));
@@ -1056,16 +1089,17 @@ Error DecoderProgram::encode_step(bool want_logits) {
       dn.seg[0].w = L.down.view;
       dn.seg[0].rows = d.dim;
       dn.state = state_;
-      RingArgs rd{};
-      rd.w = L.down.view;
-      rd.rows = d.dim;
-      rd.epi = EPI_ADD;
-      rd.K = ls.inter;
-      rd.x = h_;
-      rd.y = x_;
-      rd.tap = dn.tap;
-      rd.pad = ring_pad_;
-      if (ring_mode_ >= 1 && ring_gemv_supported(rd)) {
+      if (!fuse_o) {
+        rd.w = L.down.view;
+        rd.rows = d.dim;
+        rd.epi = EPI_ADD;
+        rd.K = ls.inter;
+        rd.x = h_;
+        rd.y = x_;
+        rd.tap = dn.tap;
+        rd.pad = ring_pad_;
+      }
+      if (fuse_o || (ring_mode_ >= 1 && ring_gemv_supported(rd))) {
         UAII_TRY(timed("gemv_down", gemv_bytes(L.down.view), [&] { return launch_ring_gemv(rd, s); }));
       } else {
         UAII_TRY(timed("gemv_down", gemv_bytes(L.down.view), [&] { return launch_gemv(dn, s); }));
