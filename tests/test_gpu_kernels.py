@@ -331,6 +331,48 @@ def test_gemv_add_epilogue(hip, t, rows, cols, norm):
     assert maxrel(got, want) < 1e-4
 
 
+@pytest.mark.parametrize("rows,cols", [
+    (4096, 14336),   # the 8B down projection: 14 slices x 64 row blocks of 64 rows
+    (2048, 8192),    # 8 slices, 32-row blocks
+    (4096, 4096),
+    (48, 1024),      # one slice, 16-row blocks
+], ids=lambda v: str(v))
+def test_gemv_add_atomic(hip, rows, cols):
+    """y += W . x split along K with float-atomic adds (the residual add of the
+    graph, elementwise.cpp:86-97, on quant_gemm_f32, quant_gemm.cpp:22-70):
+    within 1e-5 of the oracle, within 1e-6 of the whole-row kernel, and two
+    calls from the same y0 within 1e-6 of each other (the adds land in arrival
+    order)."""
+    p = random_packed(uaii_amd.Q4_0, rows, cols, seed=rows + cols + 1)
+    x = synth.normals(92, 1, 0, cols, 1.0)
+    y0 = synth.normals(91, 1, 0, rows, 1.0)
+    w = DeviceWeight(uaii_amd.Q4_0, p, rows, cols)
+    dx = DeviceBuffer.from_array(x)
+    got = []
+    for _ in range(2):
+        dy = DeviceBuffer.from_array(y0)
+        check_hip(hip.uaii_hip_gemv_add_atomic(w.h, dx.ptr, dy.ptr, None), "gemv_add_atomic")
+        got.append(dy.to_array(np.float32, rows))
+    dy = DeviceBuffer.from_array(y0)
+    check_hip(hip.uaii_hip_gemv_add(w.h, dx.ptr, None, 1e-5, dy.ptr, None), "gemv_add")
+    whole = dy.to_array(np.float32, rows)
+    want = y0 + oracle.quant_gemm(uaii_amd.Q4_0, x, p, rows, nthreads=0)[0]
+    assert maxrel(got[0], want) < 1e-5
+    assert maxrel(got[0], whole) < 1e-6
+    assert maxrel(got[1], got[0]) < 1e-6
+
+
+def test_gemv_add_atomic_refuses_unsupported_shapes(hip):
+    """Types other than Q4_0, columns not a multiple of 1024 and rows not a
+    multiple of 16 return -1 before any launch."""
+    x, y = DeviceBuffer(4 * 4096), DeviceBuffer(4 * 4096)
+    for t, rows, cols in [(uaii_amd.Q4_K, 64, 1024), (uaii_amd.Q8_0, 64, 1024), (uaii_amd.Q4_0, 64, 1536),
+                          (uaii_amd.Q4_0, 24, 1024)]:
+        w = DeviceWeight(t, random_packed(t, rows, cols, seed=7), rows, cols)
+        assert hip.uaii_hip_gemv_add_atomic(w.h, x.ptr, y.ptr, None) == -1, (t, rows, cols)
+    check_hip(hip.uaii_hip_synchronize())
+
+
 @pytest.mark.parametrize("t", [uaii_amd.Q4_0, uaii_amd.Q8_0, uaii_amd.Q4_K, uaii_amd.Q6_K],
                          ids=lambda t: uaii_amd.TYPE_NAMES[t])
 def test_gemv_swiglu_epilogue(hip, t):

@@ -25,6 +25,7 @@
 // every other value is computed in a fixed order.
 
 #include "common.h"
+#include "q4_dot.h"
 #include "uaii_hip_internal.h"
 
 namespace uaii_hip {
@@ -85,8 +86,7 @@ __global__ void __launch_bounds__(NW * 64) k_merge_o(MergeOArgs p) {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
   __builtin_amdgcn_sched_barrier(0);
 
-  // block b's 32 inputs: element k is the low nibble of payload byte k, element
-  // k + 16 its high nibble; value (nibble - 8) * scale
+  // block b's 32 inputs
   float xv[32];
 #pragma unroll
   for (int k = 0; k < 32; k += 4) {
@@ -100,19 +100,7 @@ __global__ void __launch_bounds__(NW * 64) k_merge_o(MergeOArgs p) {
   float rs[J];
 #pragma unroll
   for (int j = 0; j < J; ++j) {
-    const uint32_t q4[4] = {qv[j].x, qv[j].y, qv[j].z, qv[j].w};
-    float acc = 0.0f;
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const uint32_t lo = q4[t] & 0x0F0F0F0Fu, hi = (q4[t] >> 4) & 0x0F0F0F0Fu;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        acc = fmaf((float)((lo >> (8 * e)) & 0xFFu), xv[4 * t + e], acc);
-        acc = fmaf((float)((hi >> (8 * e)) & 0xFFu), xv[16 + 4 * t + e], acc);
-      }
-    }
-    const float sc = __half2float(__ushort_as_half((unsigned short)sv[j]));
-    float v = sc * (acc - 8.0f * sx);
+    float v = q4_0_dot(qv[j], sv[j], xv, sx);
     // the row's eight blocks: lanes b = 0..7 of the row group
     v += dpp_mov<0xB1>(v);   // quad_perm [1,0,3,2]
     v += dpp_mov<0x4E>(v);   // quad_perm [2,3,0,1]

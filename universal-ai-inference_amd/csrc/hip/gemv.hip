@@ -735,6 +735,7 @@ __device__ inline void stage_x(const GemvArgs& a, const float* xin, int64_t nch,
   const float4* w4 = reinterpret_cast<const float4*>(a.norm_w);
   float4* s4 = reinterpret_cast<float4*>(xsm);
   const bool tap = a.xtap && blockIdx.x == 0;
+  const bool rtap = a.rtap && blockIdx.x == 0;
   const bool norm = a.norm_w != nullptr;
   const bool w_in_regs = norm && nv <= B * nt;
   float4 wr[B];
@@ -755,6 +756,7 @@ __device__ inline void stage_x(const GemvArgs& a, const float* xin, int64_t nch,
       if (i < nv) {
         const float4 v = xr[j];
         ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+        if (rtap) reinterpret_cast<float4*>(a.rtap)[i] = v;
         if (!w_in_regs) {
           s4[plane_index<FMT>(i, nch)] = v;
           if (!norm && tap) reinterpret_cast<float4*>(a.xtap)[i] = v;
@@ -873,9 +875,14 @@ __device__ inline void stage_pairs_issue(const GemvArgs& a, const float* xin, in
 template <int FMT>
 __device__ inline void emit_pair_item(const GemvArgs& a, int64_t nch, int64_t it, bool valid, float4 u,
                                       float4 v, float4 uw, float4 vw, bool norm, float inv, bool tap,
-                                      float* xsm) {
+                                      bool rtap, float* xsm) {
   const int64_t t = it >> 2;
   const int w = (int)(it & 3);
+  if (rtap && valid) {
+    const int64_t r0 = pair_run0<FMT>(t) + w;
+    reinterpret_cast<float4*>(a.rtap)[r0] = u;
+    reinterpret_cast<float4*>(a.rtap)[r0 + pair_run1<FMT>()] = v;
+  }
   if (norm) {
     u.x = fmul_rn(fmul_rn(u.x, inv), uw.x); u.y = fmul_rn(fmul_rn(u.y, inv), uw.y);
     u.z = fmul_rn(fmul_rn(u.z, inv), uw.z); u.w = fmul_rn(fmul_rn(u.w, inv), uw.w);
@@ -937,6 +944,7 @@ __device__ inline void stage_pairs_finish(const GemvArgs& a, const float* xin, i
   const bool norm = w4 != nullptr;
   const bool wregs = items <= (int64_t)PBW * nt;  // norm weights of every item in registers
   const bool tap = a.xtap && blockIdx.x == 0;
+  const bool rtap = a.rtap && blockIdx.x == 0;
   const float4 one = make_float4(1.0f, 1.0f, 1.0f, 1.0f);
   float inv = 1.0f;
   if (norm) {
@@ -978,7 +986,7 @@ __device__ inline void stage_pairs_finish(const GemvArgs& a, const float* xin, i
           uw = w4[i0]; vw = w4[i0 + R1];
         }
       }
-      emit_pair_item<FMT>(a, nch, it, it < items, ps.xa[k], ps.xb[k], uw, vw, norm, inv, tap, xsm);
+      emit_pair_item<FMT>(a, nch, it, it < items, ps.xa[k], ps.xb[k], uw, vw, norm, inv, tap, rtap, xsm);
     }
   }
   // the rest (rows longer than PB * 4 * 32 * nt / 4 elements)
@@ -991,7 +999,7 @@ __device__ inline void stage_pairs_finish(const GemvArgs& a, const float* xin, i
       u = x4[i0]; v = x4[i0 + R1];
       if (norm) { uw = w4[i0]; vw = w4[i0 + R1]; }
     }
-    emit_pair_item<FMT>(a, nch, it, valid, u, v, uw, vw, norm, inv, tap, xsm);
+    emit_pair_item<FMT>(a, nch, it, valid, u, v, uw, vw, norm, inv, tap, rtap, xsm);
   }
   __syncthreads();
 }
@@ -1595,7 +1603,7 @@ hipError_t for_each_run(const GemvArgs& in, F&& f) {
     GemvArgs a = in;
     a.nseg = k1 - k0;
     for (int k = 0; k < a.nseg; ++k) a.seg[k] = in.seg[k0 + k];
-    if (k0 > 0) a.xtap = nullptr;
+    if (k0 > 0) a.xtap = a.rtap = nullptr;
     const hipError_t st = f(a);
     if (st != hipSuccess) return st;
     k0 = k1;

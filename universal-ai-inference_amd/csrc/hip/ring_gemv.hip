@@ -444,11 +444,7 @@ __global__ void __launch_bounds__(NTH, 1) k_ring_gemv(RingArgs a) {
     const int i = t / ge.R, r = t % ge.R;
     const int64_t gr = (f + i) * ge.R + r;
     float v = row_sum(part, ge, i, r);
-    if (a.epi == EPI_ADD) {
-      const float y0 = a.y[gr];
-      if (a.tap0) a.tap0[gr] = y0;
-      v = y0 + v;
-    }
+    if (a.epi == EPI_ADD) v = a.y[gr] + v;
     a.y[gr] = v;
     if (a.tap) a.tap[gr] = v;
   }

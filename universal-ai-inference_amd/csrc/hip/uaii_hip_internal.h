@@ -80,6 +80,7 @@ struct GemvArgs {
   float* y;              // EPI_STORE/ADD/QKV(q)/SWIGLU/LOGITS output
   float* tap;            // optional copy of each written value (EPI_ADD)
   float* xtap;           // optional copy of the staged (normalised) input, block 0
+  float* rtap;           // optional copy of the raw input (before any RMSNorm), block 0
   // EPI_QKV
   void* kcache;          // layer base, [n_kv][max_seq][hd] (f16 or f32)
   void* vcache;
@@ -169,6 +170,18 @@ struct MergeOArgs {
 
 bool merge_o_supported(const MergeOArgs& p);  // shapes and weight layout (not the pointers)
 hipError_t launch_merge_o(const MergeOArgs& p, hipStream_t s);
+
+// ---- split-K GEMV with a float-atomic residual add (splitk_gemv.hip) --------------
+
+struct SplitKArgs {
+  DevWeight w;      // Q4_0 [rows][K]
+  int64_t rows;     // output rows
+  const float* x;   // input [K]
+  float* y;         // y[r] += W[r] . x
+};
+
+bool gemv_splitk_supported(const SplitKArgs& p);  // shapes and weight layout (not the pointers)
+hipError_t launch_gemv_splitk(const SplitKArgs& p, hipStream_t s);
 hipError_t prepare_attention();
 // Resolves the allocation-free attention scratch of the current device (noalloc.hip).
 hipError_t prepare_noalloc();
@@ -192,7 +205,6 @@ struct RingArgs {
   int64_t rows;          // output rows (<= w.rows)
   float* y;              // output
   float* tap;            // EPI_ADD: copy of each written value, or null
-  float* tap0;           // EPI_ADD: copy of the residual before the add, or null
   const uint8_t* pad;    // >= 1 KiB of device memory read by the padding DMA lines
 };
 

@@ -409,6 +409,17 @@ int uaii_hip_attention_decode(const float* q, const void* kcache, const void* vc
   return (int)launch_attention_decode(a, S(stream));
 }
 
+int uaii_hip_gemv_add_atomic(const uaii_hip_weight* w, const float* x, float* y, void* stream) {
+  if (!w || !x || !y) return kErrArg;
+  SplitKArgs p{};
+  p.w = w->w.view;
+  p.rows = w->w.view.rows;
+  p.x = x;
+  p.y = y;
+  if (!uaii_hip::gemv_splitk_supported(p)) return kErrArg;
+  return (int)launch_gemv_splitk(p, S(stream));
+}
+
 int uaii_hip_attention_o(const float* q, const void* kcache, const void* vcache, int kv_f16,
                          int64_t max_seq, int n_heads, int n_kv_heads, int head_dim,
                          int64_t n_keys, const uaii_hip_weight* wo, float* out, float* y,

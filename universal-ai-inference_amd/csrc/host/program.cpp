@@ -369,12 +369,14 @@ Error DecoderProgram::build(const DecoderSpec& spec, const ProgramOptions& opts)
     if (prepare_ring_gemv() != hipSuccess) ring_mode_ = 0;
     (void)hipGetLastError();
   }
-  // The attention's split merge runs inside the O projection's launch
-  // (attn_out.hip: split kernel + merge/O 13.6 us against 18.0 us for split,
-  // merge and ring O on the 8B decode). Its residual adds are float atomics in
-  // arrival order; UAII_MERGE_O=0 keeps the merge kernel and the ring O
-  // projection, whose residual is the same bits on every run.
-  if (const char* env = std::getenv("UAII_MERGE_O")) merge_o_ = std::string(env) != "0";
+  // The projections that add into the residual stream run split along K, each
+  // block adding its partial row sums with float atomics: the attention output
+  // projection with the merge of the attention's key splits in its launch
+  // (attn_out.hip; attention + merge + O 13.6 us against 18.0 us on the 8B
+  // decode) and the FFN down projection (splitk_gemv.hip; 9.4 against 12.3 us).
+  // The adds land in arrival order; UAII_SPLITK=0 keeps the merge kernel and the
+  // whole-row O and down kernels, whose residual is the same bits on every run.
+  if (const char* env = std::getenv("UAII_SPLITK")) splitk_ = std::string(env) != "0";
   return Error::success();
 }
 
@@ -966,6 +968,9 @@ Error DecoderProgram::encode_step(bool want_logits) {
   if (opts_.profile) {
     UAII_HIP(hipMemcpy(&pos_host, &state_->pos, 4, hipMemcpyDeviceToHost));
   }
+  // A residual written by atomic adds has no launch that sees its final value,
+  // so its tap (resid2) is written by the next GEMV's input staging.
+  float* r2_pending = nullptr;
   for (int64_t li = 0; li < d.n_layers; ++li) {
     const Layer& L = *layers_[(size_t)li];
     const LayerSpec& ls = d.layers[(size_t)li];
@@ -991,6 +996,8 @@ Error DecoderProgram::encode_step(bool want_logits) {
     a.rope_mode = d.rope_mode;
     a.rope = rope_;
     a.state = state_;
+    a.rtap = r2_pending;
+    r2_pending = nullptr;
     const double qkv_bytes = gemv_bytes(L.wq.view) + gemv_bytes(L.wk.view) + gemv_bytes(L.wv.view);
     UAII_TRY(timed("gemv_qkv", qkv_bytes, [&] { return launch_gemv(a, s); }));
 
@@ -1010,27 +1017,15 @@ Error DecoderProgram::encode_step(bool want_logits) {
     at.splits = attn_splits_;
     const double attn_bytes = 2.0 * (double)(pos_host + 1) * (double)d.kv_dim * (double)elem +
                               8.0 * (double)d.q_dim;
-    // merge + O + residual in one launch, with the residual tap taken by the
-    // down projection's epilogue (the value it adds to)
+    // merge + O + residual in one launch (dense FFN layers, whose first FFN GEMV
+    // records the residual tap resid1 from its input)
     MergeOArgs mo{};
     mo.at = at;
     mo.w = L.wo.view;
     mo.rows = d.dim;
     mo.y = x_;
-    RingArgs rd{};
-    bool fuse_o = false;
-    if (merge_o_ && ls.ffn == LayerSpec::kSwiGLU && ring_mode_ >= 1 && merge_o_supported(mo)) {
-      rd.w = L.down.view;
-      rd.rows = d.dim;
-      rd.epi = EPI_ADD;
-      rd.K = ls.inter;
-      rd.x = h_;
-      rd.y = x_;
-      rd.tap = tap_r2_ + li * d.dim;
-      rd.tap0 = tap_r1_ + li * d.dim;
-      rd.pad = ring_pad_;
-      fuse_o = ring_gemv_supported(rd);
-    }
+    const bool fuse_o = splitk_ && (ls.ffn == LayerSpec::kSwiGLU || ls.ffn == LayerSpec::kGelu) &&
+                        merge_o_supported(mo);
     if (fuse_o) {
       UAII_TRY(timed("attention", attn_bytes, [&] { return launch_attention_splits(at, s); }));
     } else {
@@ -1077,6 +1072,7 @@ Error DecoderProgram::encode_step(bool want_logits) {
       g.seg[0].w2 = L.up.view;
       g.seg[0].rows = 2 * ls.inter;
       g.state = state_;
+      if (fuse_o) g.rtap = tap_r1_ + li * d.dim;
       const double gu_bytes = gemv_bytes(L.gate.view) + gemv_bytes(L.up.view);
       UAII_TRY(timed("gemv_gate_up", gu_bytes, [&] { return launch_gemv(g, s); }));
       GemvArgs dn{};
@@ -1089,17 +1085,24 @@ Error DecoderProgram::encode_step(bool want_logits) {
       dn.seg[0].w = L.down.view;
       dn.seg[0].rows = d.dim;
       dn.state = state_;
-      if (!fuse_o) {
-        rd.w = L.down.view;
-        rd.rows = d.dim;
-        rd.epi = EPI_ADD;
-        rd.K = ls.inter;
-        rd.x = h_;
-        rd.y = x_;
-        rd.tap = dn.tap;
-        rd.pad = ring_pad_;
-      }
-      if (fuse_o || (ring_mode_ >= 1 && ring_gemv_supported(rd))) {
+      RingArgs rd{};
+      rd.w = L.down.view;
+      rd.rows = d.dim;
+      rd.epi = EPI_ADD;
+      rd.K = ls.inter;
+      rd.x = h_;
+      rd.y = x_;
+      rd.tap = dn.tap;
+      rd.pad = ring_pad_;
+      SplitKArgs sk{};
+      sk.w = L.down.view;
+      sk.rows = d.dim;
+      sk.x = h_;
+      sk.y = x_;
+      if (splitk_ && gemv_splitk_supported(sk)) {
+        UAII_TRY(timed("gemv_down", gemv_bytes(L.down.view), [&] { return launch_gemv_splitk(sk, s); }));
+        r2_pending = dn.tap;
+      } else if (ring_mode_ >= 1 && ring_gemv_supported(rd)) {
         UAII_TRY(timed("gemv_down", gemv_bytes(L.down.view), [&] { return launch_ring_gemv(rd, s); }));
       } else {
         UAII_TRY(timed("gemv_down", gemv_bytes(L.down.view), [&] { return launch_gemv(dn, s); }));
@@ -1116,6 +1119,7 @@ Error DecoderProgram::encode_step(bool want_logits) {
       g.seg[0].w = L.up.view;
       g.seg[0].rows = ls.inter;
       g.state = state_;
+      if (fuse_o) g.rtap = tap_r1_ + li * d.dim;
       UAII_TRY(timed("gemv_up_gelu", gemv_bytes(L.up.view), [&] { return launch_gemv(g, s); }));
       GemvArgs dn{};
       dn.nseg = 1;
@@ -1127,7 +1131,17 @@ Error DecoderProgram::encode_step(bool want_logits) {
       dn.seg[0].w = L.down.view;
       dn.seg[0].rows = d.dim;
       dn.state = state_;
-      UAII_TRY(timed("gemv_down", gemv_bytes(L.down.view), [&] { return launch_gemv(dn, s); }));
+      SplitKArgs sk{};
+      sk.w = L.down.view;
+      sk.rows = d.dim;
+      sk.x = h_;
+      sk.y = x_;
+      if (splitk_ && gemv_splitk_supported(sk)) {
+        UAII_TRY(timed("gemv_down", gemv_bytes(L.down.view), [&] { return launch_gemv_splitk(sk, s); }));
+        r2_pending = dn.tap;
+      } else {
+        UAII_TRY(timed("gemv_down", gemv_bytes(L.down.view), [&] { return launch_gemv(dn, s); }));
+      }
     } else if (ls.ffn == LayerSpec::kMoE) {
       // router logits on the ffn_norm'd input, then softmax / top-k / weights on
       // the device (transformer.cpp:446-481)
@@ -1251,6 +1265,7 @@ Error DecoderProgram::encode_step(bool want_logits) {
     lm.eps = d.rms_eps;
     lm.y = logits_;
     lm.xtap = tap_normed_;
+    lm.rtap = r2_pending;
     lm.seg[0].w = d.tied ? tok_embd_.view : output_.view;
     lm.seg[0].rows = d.vocab;
     UAII_TRY(timed("gemv_lm_head", gemv_bytes(lm.seg[0].w), [&] { return launch_gemv(lm, s); }));
@@ -1277,6 +1292,7 @@ Error DecoderProgram::encode_step(bool want_logits) {
     lm.eps = d.rms_eps;
     lm.y = logits_;
     lm.xtap = tap_normed_;
+    lm.rtap = r2_pending;
     lm.seg[0].w = d.tied ? tok_embd_.view : output_.view;
     lm.seg[0].rows = d.vocab;
     lm.part_val = lm_part_val_;
@@ -1286,6 +1302,7 @@ Error DecoderProgram::encode_step(bool want_logits) {
     lm.state = state_;
     UAII_TRY(timed("gemv_lm_head", gemv_bytes(lm.seg[0].w), [&] { return launch_gemv(lm, s); }));
   } else {
+    if (r2_pending) UAII_HIP(hipMemcpyAsync(r2_pending, x_, 4 * (size_t)d.dim, hipMemcpyDeviceToDevice, s));
     UAII_TRY(timed("advance", 0.0, [&] { return launch_advance(state_, ids_, s); }));
   }
   return collect();

@@ -193,7 +193,7 @@ class DecoderProgram {
   // the residual-add GEMVs (O, down) through the LDS ring (ring_gemv.hip) where
   // the shapes allow: 1 (default) or 0 none
   int ring_mode_ = 0;
-  bool merge_o_ = true;  // attention split merge fused into the O projection (attn_out.hip)
+  bool splitk_ = true;  // O (with the split merge) and down split along K, atomic residual adds
   uint8_t* ring_pad_ = nullptr;
 
   // step graphs: no logits, greedy logits, sampled logits

@@ -202,6 +202,7 @@ def lib() -> C.CDLL:
                                                         C.c_int, i64, vp, vp]),
         "uaii_hip_attention_o": (C.c_int, [vp, vp, vp, C.c_int, i64, C.c_int, C.c_int, C.c_int,
                                            i64, vp, vp, vp, vp]),
+        "uaii_hip_gemv_add_atomic": (C.c_int, [vp, vp, vp, vp]),
         "uaii_hip_time_gemv": (C.c_int, [vp, vp, vp, C.c_int, f32p]),
         "uaii_hip_time_gemv_rotate": (C.c_int, [vp, C.c_int, vp, vp, C.c_int, f32p]),
         "uaii_hip_time_gemm": (C.c_int, [vp, vp, i64, vp, C.c_int, f32p]),
