@@ -724,7 +724,7 @@ __device__ inline void compute_unit(const Walk& wk, int step, int lane, const fl
 
 // Stage x (optionally RMS-normalised: x * (1/sqrt(mean(x^2)+eps)) * w, two
 // roundings per element as in norm.cpp:122-127) into LDS.
-template <int FMT, int NT>
+template <int FMT, int NT, bool RT>
 __device__ inline void stage_x(const GemvArgs& a, const float* xin, int64_t nch, float* xsm, float* red) {
   // Loads are issued in unrolled batches of 4 float4 per thread so a block pays
   // one memory round trip per batch (a plain strided loop serialises them).
@@ -735,7 +735,7 @@ __device__ inline void stage_x(const GemvArgs& a, const float* xin, int64_t nch,
   const float4* w4 = reinterpret_cast<const float4*>(a.norm_w);
   float4* s4 = reinterpret_cast<float4*>(xsm);
   const bool tap = a.xtap && blockIdx.x == 0;
-  const bool rtap = a.rtap && blockIdx.x == 0;
+  const bool rtap = RT && a.rtap && blockIdx.x == 0;
   const bool norm = a.norm_w != nullptr;
   const bool w_in_regs = norm && nv <= B * nt;
   float4 wr[B];
@@ -872,13 +872,13 @@ __device__ inline void stage_pairs_issue(const GemvArgs& a, const float* xin, in
 // One item: RMSNorm (two roundings, norm.cpp:122-127), the optional tap, the
 // chunk's power-of-two scale (max over the chunk's four lanes), the hi/lo split
 // into the planes, and the chunk's side data from the lane holding word 0.
-template <int FMT>
+template <int FMT, bool RT>
 __device__ inline void emit_pair_item(const GemvArgs& a, int64_t nch, int64_t it, bool valid, float4 u,
                                       float4 v, float4 uw, float4 vw, bool norm, float inv, bool tap,
                                       bool rtap, float* xsm) {
   const int64_t t = it >> 2;
   const int w = (int)(it & 3);
-  if (rtap && valid) {
+  if (RT && rtap && valid) {
     const int64_t r0 = pair_run0<FMT>(t) + w;
     reinterpret_cast<float4*>(a.rtap)[r0] = u;
     reinterpret_cast<float4*>(a.rtap)[r0 + pair_run1<FMT>()] = v;
@@ -933,7 +933,7 @@ __device__ inline void emit_pair_item(const GemvArgs& a, int64_t nch, int64_t it
   }
 }
 
-template <int FMT, int NT>
+template <int FMT, int NT, bool RT>
 __device__ inline void stage_pairs_finish(const GemvArgs& a, const float* xin, int64_t nch, const PairStage& ps,
                                           float* xsm, float* red) {
   constexpr int R1 = pair_run1<FMT>();
@@ -944,7 +944,7 @@ __device__ inline void stage_pairs_finish(const GemvArgs& a, const float* xin, i
   const bool norm = w4 != nullptr;
   const bool wregs = items <= (int64_t)PBW * nt;  // norm weights of every item in registers
   const bool tap = a.xtap && blockIdx.x == 0;
-  const bool rtap = a.rtap && blockIdx.x == 0;
+  const bool rtap = RT && a.rtap && blockIdx.x == 0;
   const float4 one = make_float4(1.0f, 1.0f, 1.0f, 1.0f);
   float inv = 1.0f;
   if (norm) {
@@ -986,7 +986,7 @@ __device__ inline void stage_pairs_finish(const GemvArgs& a, const float* xin, i
           uw = w4[i0]; vw = w4[i0 + R1];
         }
       }
-      emit_pair_item<FMT>(a, nch, it, it < items, ps.xa[k], ps.xb[k], uw, vw, norm, inv, tap, rtap, xsm);
+      emit_pair_item<FMT, RT>(a, nch, it, it < items, ps.xa[k], ps.xb[k], uw, vw, norm, inv, tap, rtap, xsm);
     }
   }
   // the rest (rows longer than PB * 4 * 32 * nt / 4 elements)
@@ -999,7 +999,7 @@ __device__ inline void stage_pairs_finish(const GemvArgs& a, const float* xin, i
       u = x4[i0]; v = x4[i0 + R1];
       if (norm) { uw = w4[i0]; vw = w4[i0 + R1]; }
     }
-    emit_pair_item<FMT>(a, nch, it, valid, u, v, uw, vw, norm, inv, tap, rtap, xsm);
+    emit_pair_item<FMT, RT>(a, nch, it, valid, u, v, uw, vw, norm, inv, tap, rtap, xsm);
   }
   __syncthreads();
 }
@@ -1092,7 +1092,7 @@ __device__ inline void epilogue(const GemvArgs& a, const GemvSeg& seg, int64_t l
 }
 
 // The whole kernel for one format (the dynamic LDS, xsm, holds the staged input).
-template <int FMT, int EPI, int W>
+template <int FMT, int EPI, int W, bool RT>
 __device__ __forceinline__ void gemv_body(GemvArgs a, float* xsm) {
   __shared__ float red[2 * W];
   __shared__ float kred[2][W][RPW_MAX];
@@ -1167,9 +1167,9 @@ __device__ __forceinline__ void gemv_body(GemvArgs a, float* xsm) {
       if constexpr (pair_fmt<FMT>()) {
         PairStage ps;
         stage_pairs_issue<FMT, W * 64>(a, a.seg[h].x, wk.nch, ps);
-        stage_pairs_finish<FMT, W * 64>(a, a.seg[h].x, wk.nch, ps, xsm + h * region, red);
+        stage_pairs_finish<FMT, W * 64, RT>(a, a.seg[h].x, wk.nch, ps, xsm + h * region, red);
       } else {
-        stage_x<FMT, W * 64>(a, a.seg[h].x, wk.nch, xsm + h * region, red);
+        stage_x<FMT, W * 64, RT>(a, a.seg[h].x, wk.nch, xsm + h * region, red);
       }
     }
     if constexpr (pair_fmt<FMT>())
@@ -1183,16 +1183,16 @@ __device__ __forceinline__ void gemv_body(GemvArgs a, float* xsm) {
     // the launch against ~3 us, measured by per-wave clock stamps on the 8B
     // decode (gate/up 19.3 -> 17.9 us, LM head 61 -> 55 us, QKV unchanged;
     // 461 -> 471 tok/s).
-    stage_pairs_finish<FMT, W * 64>(a, xin, wk.nch, ps0, xsm, red);
+    stage_pairs_finish<FMT, W * 64, RT>(a, xin, wk.nch, ps0, xsm, red);
     if (nunits > 0) load_unit<FMT, EPI>(a, seg, ebase, wk, unit_l0(0), 0, lane, pos, U0);
   } else if constexpr (FMT == T_Q8_0) {
     // input first here too: 8B Q8_0 decode 368.4 -> 372.2 tok/s (QKV 13.0 -> 12.0
     // us); the same order for the K-quants measured slower (1B 935 -> 917 tok/s)
-    stage_x<FMT, W * 64>(a, xin, wk.nch, xsm, red);
+    stage_x<FMT, W * 64, RT>(a, xin, wk.nch, xsm, red);
     if (nunits > 0) load_unit<FMT, EPI>(a, seg, ebase, wk, unit_l0(0), 0, lane, pos, U0);
   } else {
     if (nunits > 0) load_unit<FMT, EPI>(a, seg, ebase, wk, unit_l0(0), 0, lane, pos, U0);
-    stage_x<FMT, W * 64>(a, xin, wk.nch, xsm, red);
+    stage_x<FMT, W * 64, RT>(a, xin, wk.nch, xsm, red);
   }
 
   float best_v = -INFINITY;
@@ -1312,23 +1312,23 @@ __device__ __forceinline__ void gemv_body(GemvArgs a, float* xsm) {
 // took 130 VGPRs and held one block per CU; capped at 128 (2 spilled) the
 // Mixtral-shape QKV ran 12.8 -> 9.6 us. The two-format kernel keeps its 132:
 // capped, its 6 spills made the 1B QKV slower.
-template <int FMT, int EPI, int W>
+template <int FMT, int EPI, int W, bool RT>
 __global__ void __launch_bounds__(W * 64, W == 8 ? 4 : 1) k_gemv(GemvArgs a) {
   extern __shared__ float xsm[];
-  gemv_body<FMT, EPI, W>(a, xsm);
+  gemv_body<FMT, EPI, W, RT>(a, xsm);
 }
 
 // Segments of two formats in one launch (a QKV whose V projection is stored in
 // another format, as in Q4_K_M files: Q4_K Q/K, Q6_K V). Blocks belong to one
 // segment, so each block stages and walks in its own segment's format; the
 // per-format launches this replaces each paid their own ramp and input staging.
-template <int FA, int FB, int EPI, int W>
+template <int FA, int FB, int EPI, int W, bool RT>
 __global__ void __launch_bounds__(W * 64) k_gemv_mix(GemvArgs a) {
   extern __shared__ float xsm[];
   int si = 0;
   for (int k = 1; k < a.nseg; ++k) if ((int)blockIdx.x >= a.seg[k].block0) si = k;
-  if (a.seg[si].w.type == FB) gemv_body<FB, EPI, W>(a, xsm);
-  else gemv_body<FA, EPI, W>(a, xsm);
+  if (a.seg[si].w.type == FB) gemv_body<FB, EPI, W, RT>(a, xsm);
+  else gemv_body<FA, EPI, W, RT>(a, xsm);
 }
 
 // Final greedy argmax over the LM-head block partials (lowest index wins ties,
@@ -1384,50 +1384,68 @@ __global__ void __launch_bounds__(1024) k_argmax_final(GemvArgs a, int nparts) {
 
 using KernelFn = void (*)(GemvArgs);
 
-template <int EPI, int W>
+template <int EPI, int W, bool RT>
 KernelFn pick_fmt(int type) {
   switch (type) {
-    case T_Q4_0: return k_gemv<T_Q4_0, EPI, W>;
-    case T_Q8_0: return k_gemv<T_Q8_0, EPI, W>;
-    case T_Q4_K: return k_gemv<T_Q4_K, EPI, W>;
-    case T_Q6_K: return k_gemv<T_Q6_K, EPI, W>;
-    case T_Q4_1: return k_gemv<T_Q4_1, EPI, W>;
-    case T_Q5_0: return k_gemv<T_Q5_0, EPI, W>;
-    case T_Q5_1: return k_gemv<T_Q5_1, EPI, W>;
-    case T_Q5_K: return k_gemv<T_Q5_K, EPI, W>;
-    case T_Q2_K: return k_gemv<T_Q2_K, EPI, W>;
-    case T_Q3_K: return k_gemv<T_Q3_K, EPI, W>;
-    case T_F32: return k_gemv<T_F32, EPI, W>;
-    case T_F16: return k_gemv<T_F16, EPI, W>;
+    case T_Q4_0: return k_gemv<T_Q4_0, EPI, W, RT>;
+    case T_Q8_0: return k_gemv<T_Q8_0, EPI, W, RT>;
+    case T_Q4_K: return k_gemv<T_Q4_K, EPI, W, RT>;
+    case T_Q6_K: return k_gemv<T_Q6_K, EPI, W, RT>;
+    case T_Q4_1: return k_gemv<T_Q4_1, EPI, W, RT>;
+    case T_Q5_0: return k_gemv<T_Q5_0, EPI, W, RT>;
+    case T_Q5_1: return k_gemv<T_Q5_1, EPI, W, RT>;
+    case T_Q5_K: return k_gemv<T_Q5_K, EPI, W, RT>;
+    case T_Q2_K: return k_gemv<T_Q2_K, EPI, W, RT>;
+    case T_Q3_K: return k_gemv<T_Q3_K, EPI, W, RT>;
+    case T_F32: return k_gemv<T_F32, EPI, W, RT>;
+    case T_F16: return k_gemv<T_F16, EPI, W, RT>;
     default: return nullptr;
   }
 }
 
-// Kernel for (epilogue, format, waves per block): WPB for every epilogue,
-// WPB_QKV for the QKV epilogue, WPB_LONG for the residual add.
-KernelFn pick(int epi, int type, int w) {
-  if (epi == EPI_SWIGLU && w == WPB_SWIGLU) return pick_fmt<EPI_SWIGLU, WPB_SWIGLU>(type);
-  if (epi == EPI_QKV && w == WPB_QKV) return pick_fmt<EPI_QKV, WPB_QKV>(type);
+// Kernel for (epilogue, format, waves per block, raw input tap): WPB for every
+// epilogue, WPB_QKV for the QKV epilogue, WPB_LONG for the residual add. The
+// raw tap (GemvArgs::rtap, the residual a split-K launch left) is compiled into
+// its own instances of the epilogues that take a residual as input: the copy in
+// the staging slowed every launch that carried it, taken or not (1B decode
+// 1220 -> 1193 tok/s).
+KernelFn pick(int epi, int type, int w, bool rt) {
+  if (rt) {
+    if (epi == EPI_SWIGLU && w == WPB_SWIGLU) return pick_fmt<EPI_SWIGLU, WPB_SWIGLU, true>(type);
+    if (epi == EPI_QKV && w == WPB_QKV) return pick_fmt<EPI_QKV, WPB_QKV, true>(type);
+    if (w != WPB) return nullptr;
+    switch (epi) {
+      case EPI_STORE: return pick_fmt<EPI_STORE, WPB, true>(type);
+      case EPI_QKV: return pick_fmt<EPI_QKV, WPB, true>(type);
+      case EPI_SWIGLU: return pick_fmt<EPI_SWIGLU, WPB, true>(type);
+      case EPI_LOGITS: return pick_fmt<EPI_LOGITS, WPB, true>(type);
+      case EPI_GELU: return pick_fmt<EPI_GELU, WPB, true>(type);
+      default: return nullptr;
+    }
+  }
+  if (epi == EPI_SWIGLU && w == WPB_SWIGLU) return pick_fmt<EPI_SWIGLU, WPB_SWIGLU, false>(type);
+  if (epi == EPI_QKV && w == WPB_QKV) return pick_fmt<EPI_QKV, WPB_QKV, false>(type);
   if (w == WPB_LONG) {
-    if (epi == EPI_ADD) return pick_fmt<EPI_ADD, WPB_LONG>(type);
-    if (epi == EPI_ADD2) return pick_fmt<EPI_ADD2, WPB_LONG>(type);
+    if (epi == EPI_ADD) return pick_fmt<EPI_ADD, WPB_LONG, false>(type);
+    if (epi == EPI_ADD2) return pick_fmt<EPI_ADD2, WPB_LONG, false>(type);
     return nullptr;
   }
   if (w != WPB) return nullptr;
   switch (epi) {
-    case EPI_STORE: return pick_fmt<EPI_STORE, WPB>(type);
-    case EPI_ADD: return pick_fmt<EPI_ADD, WPB>(type);
-    case EPI_QKV: return pick_fmt<EPI_QKV, WPB>(type);
-    case EPI_SWIGLU: return pick_fmt<EPI_SWIGLU, WPB>(type);
-    case EPI_LOGITS: return pick_fmt<EPI_LOGITS, WPB>(type);
-    case EPI_GELU: return pick_fmt<EPI_GELU, WPB>(type);
+    case EPI_STORE: return pick_fmt<EPI_STORE, WPB, false>(type);
+    case EPI_ADD: return pick_fmt<EPI_ADD, WPB, false>(type);
+    case EPI_QKV: return pick_fmt<EPI_QKV, WPB, false>(type);
+    case EPI_SWIGLU: return pick_fmt<EPI_SWIGLU, WPB, false>(type);
+    case EPI_LOGITS: return pick_fmt<EPI_LOGITS, WPB, false>(type);
+    case EPI_GELU: return pick_fmt<EPI_GELU, WPB, false>(type);
     default: return nullptr;
   }
 }
 
 // The two-format kernel: QKV with Q4_K and Q6_K segments.
-KernelFn pick_mix(int epi, int w) {
-  if (epi == EPI_QKV && w == WPB_QKV) return k_gemv_mix<T_Q4_K, T_Q6_K, EPI_QKV, WPB_QKV>;
+KernelFn pick_mix(int epi, int w, bool rt) {
+  if (epi == EPI_QKV && w == WPB_QKV)
+    return rt ? k_gemv_mix<T_Q4_K, T_Q6_K, EPI_QKV, WPB_QKV, true> : k_gemv_mix<T_Q4_K, T_Q6_K, EPI_QKV, WPB_QKV, false>;
   return nullptr;
 }
 
@@ -1451,15 +1469,17 @@ hipError_t prepare_gemv() {
   const int lim = lds_limit();
   for (int e : epis) {
     for (int w : {WPB, WPB_QKV, WPB_SWIGLU, WPB_LONG}) {
-      for (int t : types) {
-        const KernelFn fn = pick(e, t, w);
-        if (!fn) continue;
-        (void)hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, lim - 1024);
-        (void)hipGetLastError();
-      }
-      if (const KernelFn fn = pick_mix(e, w)) {
-        (void)hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, lim - 1024);
-        (void)hipGetLastError();
+      for (bool rt : {false, true}) {
+        for (int t : types) {
+          const KernelFn fn = pick(e, t, w, rt);
+          if (!fn) continue;
+          (void)hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, lim - 1024);
+          (void)hipGetLastError();
+        }
+        if (const KernelFn fn = pick_mix(e, w, rt)) {
+          (void)hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, lim - 1024);
+          (void)hipGetLastError();
+        }
       }
     }
   }
@@ -1542,7 +1562,8 @@ Plan make_plan(const GemvArgs& a) {
   for (int k = 1; k < a.nseg; ++k) p.lds = std::max(p.lds, lds_bytes(a.seg[k].w.type, a.K));
   p.ks = pick_ksplit(a.seg[0].w);
   p.waves = pick_waves(a.epi, p.ks);
-  p.fn = mix ? pick_mix(a.epi, p.waves) : pick(a.epi, a.seg[0].w.type, p.waves);
+  const bool rt = a.rtap != nullptr;
+  p.fn = mix ? pick_mix(a.epi, p.waves, rt) : pick(a.epi, a.seg[0].w.type, p.waves, rt);
   if (!p.fn) return p;
   const int rpg = (p.waves / (pair ? 2 : 1) / p.ks) * rpw_of(a.seg[0].w.type);
   if (pair) {

@@ -84,7 +84,6 @@ struct GemvArgs {
   // EPI_QKV
   void* kcache;          // layer base, [n_kv][max_seq][hd] (f16 or f32)
   void* vcache;
-  int kv_f16;
   int64_t max_seq;
   int head_dim;
   int rope_mode;
@@ -93,6 +92,7 @@ struct GemvArgs {
   float* part_val;       // [part_cap] block partials of the argmax
   int32_t* part_idx;
   int part_cap;          // capacity of part_val/part_idx (launch fails if the grid exceeds it)
+  int kv_f16;            // EPI_QKV: f16 cache (beside part_cap: no padding after either)
   int32_t* ids;          // token history [max_seq + 1]
   // shared
   StepState* state;

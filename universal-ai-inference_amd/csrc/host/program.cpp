@@ -325,6 +325,8 @@ Error DecoderProgram::build(const DecoderSpec& spec, const ProgramOptions& opts)
   lm.seg[0].w = d.tied ? tok_embd_.view : output_.view;
   lm.seg[0].rows = d.vocab;
   lm_blocks_ = gemv_grid(lm);
+  lm.rtap = tap_r2_;  // the launch after a split-K down takes the raw-tap kernel: its grid too
+  lm_blocks_ = std::max(lm_blocks_, gemv_grid(lm));
   const int lm_blocks = lm_blocks_;
   UAII_TRY(alloc(4 * (size_t)lm_blocks, (void**)&lm_part_val_));
   UAII_TRY(alloc(4 * (size_t)lm_blocks, (void**)&lm_part_idx_));

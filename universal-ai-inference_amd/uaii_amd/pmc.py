@@ -55,21 +55,22 @@ def per_dispatch_ordered(path: str, counter: str):
 
 # The decode step's roles: (bench.py timing name, kernel symbol patterns, which
 # dispatches of the first pattern). The attention role is the key-split kernel;
-# the split merge runs in the O projection's launch (k_merge_o); the ring kernel
-# runs the down projection.
+# the split merge runs in the O projection's launch (k_merge_o); the down
+# projection is the split-K kernel (k_gemv_splitk).
 DECODE_ROLES = [
     ("gemv_qkv", ["k_gemv<2, 2,"], None),
     ("attention", ["k_attn_h16"], None),
     ("gemv_o", ["k_merge_o"], None),
     ("gemv_gate_up", ["k_gemv<2, 3,"], None),
-    ("gemv_down", ["k_ring_gemv"], None),
+    ("gemv_down", ["k_gemv_splitk"], None),
     ("gemv_lm_head", ["k_gemv<2, 4,"], None),
 ]
 
 # Sources each role's kernels are built from (relative to the package's csrc/hip).
 ROLE_SOURCES = {
     "gemv_qkv": ["gemv.hip"], "gemv_gate_up": ["gemv.hip"], "gemv_lm_head": ["gemv.hip"],
-    "gemv_o": ["attn_out.hip"], "gemv_down": ["ring_gemv.hip"], "attention": ["attention.hip"],
+    "gemv_o": ["attn_out.hip", "q4_dot.h"], "gemv_down": ["splitk_gemv.hip", "q4_dot.h"],
+    "attention": ["attention.hip"],
 }
 
 
