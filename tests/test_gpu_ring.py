@@ -1,11 +1,14 @@
-"""The LDS-ring GEMV (ring_gemv.hip) through the C ABI.
+"""The residual-add projections through the C ABI, on each of their kernels.
 
-By default (UAII_RING=1) the Q4_0 residual-add projections, attention output O
-and FFN down, run on k_ring_gemv where the shapes allow (K a multiple of 2048);
-UAII_RING=0 keeps them on the gemv.hip kernels. Bars as for the other generate
-tests: greedy ids identical to the CPU oracle (fp16-cache flavour) over the
-decoded tokens, logits and per-layer hidden states within 2e-3 max relative
-error; and the two GEMV kernels within 1e-4 of each other.
+By default (UAII_SPLITK=1) the Q4_0 attention output O runs with the merge of
+the attention's key splits in its launch (attn_out.hip) and the FFN down split
+along K (splitk_gemv.hip), both adding into the residual with float atomics.
+UAII_SPLITK=0 keeps the whole-row kernels: the merge kernel, then O and down on
+k_ring_gemv where the shapes allow (K a multiple of 2048; UAII_RING=1) or on
+gemv.hip (UAII_RING=0). Bars as for the other generate tests: greedy ids
+identical to the CPU oracle (fp16-cache flavour) over the decoded tokens,
+logits and per-layer hidden states within 2e-3 max relative error; and the
+kernels within 1e-4 of each other.
 """
 import os
 
@@ -48,9 +51,10 @@ def maxrel(a, b):
     return float(np.abs(np.asarray(a, np.float64) - b).max() / max(np.abs(b).max(), 1e-30))
 
 
-def run(path, cfg, prompt, n_new, ring="1"):
-    saved = os.environ.get("UAII_RING")
-    os.environ["UAII_RING"] = ring
+def run(path, cfg, prompt, n_new, ring="1", splitk="0"):
+    env = {"UAII_RING": ring, "UAII_SPLITK": splitk}
+    saved = {k: os.environ.get(k) for k in env}
+    os.environ.update(env)
     try:
         with uaii_amd.Session(path, kv_f16=True) as s:
             ids = s.generate(prompt, n_new)
@@ -59,21 +63,24 @@ def run(path, cfg, prompt, n_new, ring="1"):
                 taps[f"r1_{li}"] = s.get(f"blk.{li}.resid1")
                 taps[f"r2_{li}"] = s.get(f"blk.{li}.resid2")
     finally:
-        if saved is None:
-            del os.environ["UAII_RING"]
-        else:
-            os.environ["UAII_RING"] = saved
+        for k, v in saved.items():
+            if v is None:
+                del os.environ[k]
+            else:
+                os.environ[k] = v
     return ids, taps
 
 
+@pytest.mark.parametrize("splitk", ["0", "1"], ids=["ring", "splitk"])
 @pytest.mark.parametrize("name", [n for n in CFGS if n != "g1_hd64_long"])
-def test_ring_gemv_match_oracle(name):
-    """Per-layer launches with the O and down projections on the ring kernel."""
+def test_ring_gemv_match_oracle(name, splitk):
+    """Per-layer launches with the O and down projections on the ring kernel
+    (after the merge kernel), or split along K (the merge in O's launch)."""
     cfg = CFGS[name]
     path = synth.cached_model(cfg)
     prompt = np.random.default_rng(cfg.seed + 3).integers(0, cfg.vocab, 40).astype(np.int64)
-    print(name, flush=True)
-    ids, taps = run(path, cfg, prompt, 24)
+    print(name, "splitk", splitk, flush=True)
+    ids, taps = run(path, cfg, prompt, 24, splitk=splitk)
     want_ids, want = oracle.Model(path).generate(prompt, 24, kv_f16=True)
     assert np.array_equal(ids, want_ids)
     assert maxrel(taps["logits"], want["logits"]) < 2e-3
@@ -98,6 +105,22 @@ def test_ring_gemv_long_context():
     ids2, _ = run(path, cfg, short, 8)
     want2, _ = oracle.Model(path).generate(short, 8, kv_f16=True)
     assert np.array_equal(ids2, want2)
+
+
+@pytest.mark.parametrize("name", ["g4_hd128", "g2_hd64_neox_bias"])
+def test_splitk_matches_whole_row(name):
+    """The split-K O (with the merge in its launch) and down against the
+    whole-row kernels (merge kernel, ring O and down) on the same prompt: ids
+    identical, every tap within 1e-4 (the atomic adds change only the order
+    of the residual's f32 sums)."""
+    cfg = CFGS[name]
+    path = synth.cached_model(cfg)
+    prompt = np.random.default_rng(cfg.seed + 17).integers(0, cfg.vocab, 9).astype(np.int64)
+    ids, taps = run(path, cfg, prompt, 40, splitk="1")
+    ids0, taps0 = run(path, cfg, prompt, 40, splitk="0")
+    assert np.array_equal(ids, ids0)
+    for k in taps:
+        assert maxrel(taps[k], taps0[k]) < 1e-4, k
 
 
 @pytest.mark.parametrize("name", ["g4_hd128", "g1_hd128_ffn6144"])
