@@ -97,7 +97,7 @@ def test_attention_decode_several_tiles_per_wave(hip, heads, n_keys):
     check_attention_decode(hip, nh, nkv, hd, 1, 12800, n_keys, n_keys * 13 + nh + hd + 1)
 
 
-def check_attention_o(hip, nh, nkv, hd, kv_f16, max_seq, n_keys, rows, seed):
+def check_attention_o(hip, nh, nkv, hd, kv_f16, max_seq, n_keys, rows, seed, t=uaii_amd.Q4_0):
     """uaii_hip_attention_o: its attention output the same bits as
     uaii_hip_attention_decode's, and y = y0 + W_o . out within 1e-5 of the
     oracle's quant_gemm_f32 of that output plus y0 (quant_gemm.cpp:22-70,
@@ -109,8 +109,8 @@ def check_attention_o(hip, nh, nkv, hd, kv_f16, max_seq, n_keys, rows, seed):
     v = rng.standard_normal((nkv, max_seq, hd)).astype(np.float32)
     if kv_f16:
         k, v = k.astype(np.float16), v.astype(np.float16)
-    packed = synth.quantize(uaii_amd.Q4_0, synth.normals(seed, 0, 0, rows * nh * hd, 0.02))
-    w = uaii_amd.DeviceWeight(uaii_amd.Q4_0, packed, rows, nh * hd)
+    packed = synth.quantize(t, synth.normals(seed, 0, 0, rows * nh * hd, 0.02))
+    w = uaii_amd.DeviceWeight(t, packed, rows, nh * hd)
     y0 = rng.standard_normal(rows).astype(np.float32)
     dq, dk, dv = DeviceBuffer.from_array(q), DeviceBuffer.from_array(k), DeviceBuffer.from_array(v)
     do, do2 = DeviceBuffer(nh * hd * 4), DeviceBuffer(nh * hd * 4)
@@ -124,7 +124,7 @@ def check_attention_o(hip, nh, nkv, hd, kv_f16, max_seq, n_keys, rows, seed):
                                             n_keys, do2.ptr, None), "attention_decode")
     out, out2 = do.to_array(np.float32, nh * hd), do2.to_array(np.float32, nh * hd)
     assert np.array_equal(out.view(np.uint32), out2.view(np.uint32))
-    want = y0 + oracle.quant_gemm(uaii_amd.Q4_0, out2, packed, rows, nthreads=THREADS)[0]
+    want = y0 + oracle.quant_gemm(t, out2, packed, rows, nthreads=THREADS)[0]
     assert maxrel(ys[0], want) < 1e-5
     assert maxrel(ys[1], ys[0]) < 1e-6
 
@@ -142,9 +142,22 @@ def test_attention_o(hip, case):
     check_attention_o(hip, nh, nkv, hd, kv_f16, max_seq, n_keys, rows, nh * 7 + hd + n_keys + rows)
 
 
+@pytest.mark.parametrize("case", [
+    (32, 8, 128, 1, 4096, 4096, 4096),     # the 8B shape with Q8_0 weights
+    (32, 8, 64, 1, 4096, 2049, 2048),      # 4 heads per slice
+    (32, 8, 128, 0, 4096, 300, 96),        # f32 cache, 3 row blocks
+], ids=str)
+def test_attention_o_q8_0(hip, case):
+    """uaii_hip_attention_o with a Q8_0 W_o (32 payload bytes per block)."""
+    nh, nkv, hd, kv_f16, max_seq, n_keys, rows = case
+    check_attention_o(hip, nh, nkv, hd, kv_f16, max_seq, n_keys, rows, nh * 5 + hd + n_keys + rows,
+                      t=uaii_amd.Q8_0)
+
+
 def test_attention_o_refuses_unsupported_shapes(hip):
-    """W_o other than Q4_0, rows not a multiple of 32, head_dim other than 64
-    or 128, or n_heads * head_dim not a multiple of 256: -1 before any launch."""
+    """W_o other than Q4_0 or Q8_0, rows not a multiple of 32, head_dim other
+    than 64 or 128, or n_heads * head_dim not a multiple of 256: -1 before any
+    launch."""
     nh, nkv, hd, max_seq = 32, 8, 128, 256
     buf = DeviceBuffer(nkv * max_seq * hd * 4)
     out, y = DeviceBuffer(nh * hd * 4), DeviceBuffer(8192 * 4)

@@ -3,13 +3,13 @@
 //
 // Replaces, at M = 1, quant_gemm_f32 of the attention output
 // (libs/uaii-kernels/src/quant_gemm.cpp:22-70) and the residual add_f32
-// (elementwise.cpp:99-110) for Q4_0 weights, together with the second step of
+// (elementwise.cpp:99-110) for Q4_0 and Q8_0 weights, together with the second step of
 // the split-K decode attention: out = sum_s w_s o_s / sum_s w_s l_s with
 // w_s = exp(m_s - max_s m_s), which makes the per-split softmaxes one softmax
 // over all keys as attention_kv_f32 computes it (transformer.cpp:222-433).
 //
 // Split along K by heads: block (r, c) owns column slice c of W_o (SC = 256
-// columns, 8 Q4_0 blocks, 256 / hd query heads, hd 64 or 128) and RB = 32 J
+// columns, 8 blocks of 32, 256 / hd query heads, hd 64 or 128) and RB = 32 J
 // consecutive rows r RB ... The row block is the grid's x index, so the slices
 // of one row block (its blocks r + R c) land on one XCD and their atomic adds
 // to a row meet in that XCD's L2 (13.8 MB fetched per 8B launch against 17.8
@@ -17,7 +17,7 @@
 // then fetched by every XCD).
 // Each wave merges 64 of the slice's dims from the split partials with the
 // arithmetic of k_attn_merge (same bits), the block keeps them in LDS, and lane
-// (g, b) of a wave multiplies Q4_0 block b of rows g, g + 8, ... (J rows) by
+// (g, b) of a wave multiplies weight block b of rows g, g + 8, ... (J rows) by
 // them; the eight blocks of a row are summed with DPP and the row's sum is
 // added into the residual stream with one float atomic. The partial loads are
 // issued first and the weight loads right behind them, so the merge runs while
@@ -29,7 +29,7 @@
 // every other value is computed in a fixed order.
 
 #include "common.h"
-#include "q4_dot.h"
+#include "block_dot.h"
 #include "uaii_hip_internal.h"
 
 namespace uaii_hip {
@@ -39,8 +39,9 @@ constexpr int SC = 256;  // weight columns per block
 constexpr int NW = 4;    // waves per block
 constexpr int CH = 32;   // most key splits (attention_splits)
 
-template <int J>
+template <int FMT, int J>
 __global__ void __launch_bounds__(NW * 64) k_merge_o(MergeOArgs p) {
+  constexpr int QW = FMT == T_Q8_0 ? 2 : 1;  // 16-byte payload words per block
   __shared__ float xs[SC];
   const AttnArgs& a = p.at;
   const int c = blockIdx.y, w = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -58,15 +59,18 @@ __global__ void __launch_bounds__(NW * 64) k_merge_o(MergeOArgs p) {
 #pragma unroll
   for (int s = 0; s < CH; ++s) ov[s] = hp[(s < SB ? s : SB - 1) * ks + d];
 
-  // the lane's weights: Q4_0 block b of rows r0 + 8 j (16 payload bytes, f16 scale)
+  // the lane's weights: block b of rows r0 + 8 j (16 (Q4_0) or 32 (Q8_0) payload
+  // bytes, f16 scale)
   const int b = lane & 7;
   const int64_t r0 = (int64_t)blockIdx.x * (NW * 8 * J) + w * (8 * J) + (lane >> 3);
-  uint4 qv[J];
+  uint4 qv[J][QW];
   uint32_t sv[J];
 #pragma unroll
   for (int j = 0; j < J; ++j) {
     const int64_t r = r0 + 8 * j;
-    qv[j] = *reinterpret_cast<const uint4*>(p.w.a + r * p.w.a_row + c * (SC / 2) + b * 16);
+    const uint4* src = reinterpret_cast<const uint4*>(p.w.a + r * p.w.a_row + (c * SC + b * 32) * QW / 2);
+#pragma unroll
+    for (int k = 0; k < QW; ++k) qv[j][k] = src[k];
     sv[j] = *reinterpret_cast<const uint16_t*>(p.w.b + r * p.w.b_row + c * (SC / 16) + b * 2);
   }
   // every load is issued before the merge waits for the first of them
@@ -104,7 +108,9 @@ __global__ void __launch_bounds__(NW * 64) k_merge_o(MergeOArgs p) {
   float rs[J];
 #pragma unroll
   for (int j = 0; j < J; ++j) {
-    float v = q4_0_dot(qv[j], sv[j], xv, sx);
+    float v;
+    if constexpr (FMT == T_Q8_0) v = q8_0_dot(qv[j], sv[j], xv);
+    else v = q4_0_dot(qv[j][0], sv[j], xv, sx);
     // the row's eight blocks: lanes b = 0..7 of the row group
     v += dpp_mov<0xB1>(v);   // quad_perm [1,0,3,2]
     v += dpp_mov<0x4E>(v);   // quad_perm [2,3,0,1]
@@ -134,7 +140,8 @@ bool merge_o_supported(const MergeOArgs& p) {
   const int64_t K = (int64_t)a.n_heads * a.hd;
   if (K % SC) return false;
   const DevWeight& w = p.w;
-  if (w.type != T_Q4_0 || w.cols != K || w.a_row != K / 2 || w.b_row != K / 16) return false;
+  if (w.cols != K || w.b_row != K / 16) return false;
+  if (!(w.type == T_Q4_0 && w.a_row == K / 2) && !(w.type == T_Q8_0 && w.a_row == K)) return false;
   if (p.rows <= 0 || w.rows < p.rows) return false;
   return pick_j(p) > 0;
 }
@@ -143,10 +150,20 @@ hipError_t launch_merge_o(const MergeOArgs& p, hipStream_t s) {
   if (!merge_o_supported(p) || !p.at.part || !p.at.out || !p.y) return hipErrorInvalidValue;
   const int J = pick_j(p);
   dim3 grid((unsigned)(p.rows / (NW * 8 * J)), (unsigned)((int64_t)p.at.n_heads * p.at.hd / SC));
+  const bool q8 = p.w.type == T_Q8_0;
   switch (J) {
-    case 4: UAII_LAUNCH(k_merge_o<4>, grid, dim3(NW * 64), 0, s, p); break;
-    case 2: UAII_LAUNCH(k_merge_o<2>, grid, dim3(NW * 64), 0, s, p); break;
-    default: UAII_LAUNCH(k_merge_o<1>, grid, dim3(NW * 64), 0, s, p); break;
+    case 4:
+      if (q8) UAII_LAUNCH((k_merge_o<T_Q8_0, 4>), grid, dim3(NW * 64), 0, s, p);
+      else UAII_LAUNCH((k_merge_o<T_Q4_0, 4>), grid, dim3(NW * 64), 0, s, p);
+      break;
+    case 2:
+      if (q8) UAII_LAUNCH((k_merge_o<T_Q8_0, 2>), grid, dim3(NW * 64), 0, s, p);
+      else UAII_LAUNCH((k_merge_o<T_Q4_0, 2>), grid, dim3(NW * 64), 0, s, p);
+      break;
+    default:
+      if (q8) UAII_LAUNCH((k_merge_o<T_Q8_0, 1>), grid, dim3(NW * 64), 0, s, p);
+      else UAII_LAUNCH((k_merge_o<T_Q4_0, 1>), grid, dim3(NW * 64), 0, s, p);
+      break;
   }
   return hipGetLastError();
 }

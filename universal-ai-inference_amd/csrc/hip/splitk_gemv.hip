@@ -23,7 +23,7 @@
 // in a fixed order.
 
 #include "common.h"
-#include "q4_dot.h"
+#include "block_dot.h"
 #include "uaii_hip_internal.h"
 
 namespace uaii_hip {

@@ -69,7 +69,7 @@ DECODE_ROLES = [
 # Sources each role's kernels are built from (relative to the package's csrc/hip).
 ROLE_SOURCES = {
     "gemv_qkv": ["gemv.hip"], "gemv_gate_up": ["gemv.hip"], "gemv_lm_head": ["gemv.hip"],
-    "gemv_o": ["attn_out.hip", "q4_dot.h"], "gemv_down": ["splitk_gemv.hip", "q4_dot.h"],
+    "gemv_o": ["attn_out.hip", "block_dot.h"], "gemv_down": ["splitk_gemv.hip", "block_dot.h"],
     "attention": ["attention.hip"],
 }
 
