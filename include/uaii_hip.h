@@ -168,8 +168,8 @@ UAII_HIP_API int uaii_hip_gemv_add_atomic(const uaii_hip_weight* w, const float*
  * 256 / head_dim heads per block, writes them to `out` and adds its share of
  * the W_o product into y with float atomics. out is the same bits as
  * uaii_hip_attention_decode's; each y row is a sum whose adds arrive in an
- * order the hardware picks, so runs can differ in its last bits. W_o: Q4_0 or
- * Q8_0, [rows][n_heads * head_dim] with n_heads * head_dim a multiple of 256,
+ * order the hardware picks, so runs can differ in its last bits. W_o: Q4_0,
+ * Q8_0 or Q4_K, [rows][n_heads * head_dim] with n_heads * head_dim a multiple of 256,
  * head_dim 64 or 128, rows (y's length) a multiple of 32; other shapes return
  * -1 and launch nothing. */
 UAII_HIP_API int uaii_hip_attention_o(const float* q, const void* kcache, const void* vcache,

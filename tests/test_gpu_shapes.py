@@ -154,15 +154,28 @@ def test_attention_o_q8_0(hip, case):
                       t=uaii_amd.Q8_0)
 
 
+@pytest.mark.parametrize("case", [
+    (32, 8, 64, 1, 2048, 1800, 2048),      # the 1B shape: one super-block per 4-head slice
+    (32, 8, 128, 1, 4096, 4096, 4096),     # 2 heads per super-block
+    (32, 8, 128, 0, 4096, 300, 96),        # f32 cache, 3 row blocks
+], ids=str)
+def test_attention_o_q4_k(hip, case):
+    """uaii_hip_attention_o with a Q4_K W_o: each lane takes one 32-element
+    sub-block (its own 6-bit scale and min) of the slice's super-block."""
+    nh, nkv, hd, kv_f16, max_seq, n_keys, rows = case
+    check_attention_o(hip, nh, nkv, hd, kv_f16, max_seq, n_keys, rows, nh * 3 + hd + n_keys + rows,
+                      t=uaii_amd.Q4_K)
+
+
 def test_attention_o_refuses_unsupported_shapes(hip):
-    """W_o other than Q4_0 or Q8_0, rows not a multiple of 32, head_dim other
-    than 64 or 128, or n_heads * head_dim not a multiple of 256: -1 before any
-    launch."""
+    """W_o other than Q4_0, Q8_0 or Q4_K, rows not a multiple of 32, head_dim
+    other than 64 or 128, or n_heads * head_dim not a multiple of 256: -1 before
+    any launch."""
     nh, nkv, hd, max_seq = 32, 8, 128, 256
     buf = DeviceBuffer(nkv * max_seq * hd * 4)
     out, y = DeviceBuffer(nh * hd * 4), DeviceBuffer(8192 * 4)
     x = synth.normals(3, 0, 0, 96 * nh * hd, 0.02)
-    bad = [uaii_amd.DeviceWeight(uaii_amd.Q4_K, synth.quantize(uaii_amd.Q4_K, x[: 64 * nh * hd]), 64, nh * hd),
+    bad = [uaii_amd.DeviceWeight(uaii_amd.Q6_K, synth.quantize(uaii_amd.Q6_K, x[: 64 * nh * hd]), 64, nh * hd),
            uaii_amd.DeviceWeight(uaii_amd.Q4_0, synth.quantize(uaii_amd.Q4_0, x[: 48 * nh * hd]), 48, nh * hd)]
     for w in bad:
         assert hip.uaii_hip_attention_o(buf.ptr, buf.ptr, buf.ptr, 1, max_seq, nh, nkv, hd, 10, w.h, out.ptr,

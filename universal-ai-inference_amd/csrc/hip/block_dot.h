@@ -1,5 +1,6 @@
-// block_dot.h — one Q4_0 or Q8_0 block dotted with 32 f32 inputs, for the
-// kernels that hold a block's inputs in registers (attn_out.hip, splitk_gemv.hip).
+// block_dot.h — one 32-element block (Q4_0, Q8_0, or a Q4_K sub-block) dotted
+// with 32 f32 inputs, for the kernels that hold a block's inputs in registers
+// (attn_out.hip, splitk_gemv.hip).
 #pragma once
 
 #include "common.h"
@@ -35,6 +36,38 @@ __device__ __forceinline__ float q8_0_dot(const uint4 (&q)[2], uint32_t d16, con
 #pragma unroll
     for (int e = 0; e < 4; ++e) acc = fmaf((float)(int8_t)((w8[t] >> (8 * e)) & 0xFFu), xv[4 * t + e], acc);
   return __half2float(__ushort_as_half((unsigned short)d16)) * acc;
+}
+
+// Sub-block j (0..7) of a Q4_K super-block (gguf_dequant.cpp:308-340): its 32
+// elements are the low (j even) or high (j odd) nibbles of quant bytes
+// 32 (j / 2) .. 32 (j / 2) + 31, here q; value d1 * nibble - m1 with d1 = d * sc,
+// m1 = dmin * mn and (sc, mn) the 6-bit pair j of the 12 scale bytes
+// (get_scale_min_k4, gguf_dequant.cpp:107-115). meta holds the super-block's
+// d, dmin and scale bytes as the file stores them (16 bytes).
+__device__ __forceinline__ float q4_k_dot(const uint4 (&q)[2], const uint4& meta, int j, const float (&xv)[32],
+                                          float sx) {
+  const int sh = 4 * (j & 1);
+  const uint32_t w8[8] = {q[0].x, q[0].y, q[0].z, q[0].w, q[1].x, q[1].y, q[1].z, q[1].w};
+  float acc = 0.0f;
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    const uint32_t n = (w8[t] >> sh) & 0x0F0F0F0Fu;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc = fmaf((float)((n >> (8 * e)) & 0xFFu), xv[4 * t + e], acc);
+  }
+  const uint32_t mw[4] = {meta.x, meta.y, meta.z, meta.w};
+  auto sbyte = [&](int k) { return (int)((mw[(4 + k) >> 2] >> (8 * ((4 + k) & 3))) & 0xFFu); };  // scales[k]
+  int sc, mn;
+  if (j < 4) {
+    sc = sbyte(j) & 63;
+    mn = sbyte(j + 4) & 63;
+  } else {
+    sc = (sbyte(j + 4) & 15) | ((sbyte(j - 4) >> 6) << 4);
+    mn = (sbyte(j + 4) >> 4) | ((sbyte(j) >> 6) << 4);
+  }
+  const float d = __half2float(__ushort_as_half((unsigned short)(meta.x & 0xFFFFu)));
+  const float dmin = __half2float(__ushort_as_half((unsigned short)(meta.x >> 16)));
+  return (d * (float)sc) * acc - (dmin * (float)mn) * sx;
 }
 
 }  // namespace uaii_hip
