@@ -1019,14 +1019,15 @@ Error DecoderProgram::encode_step(bool want_logits) {
     at.splits = attn_splits_;
     const double attn_bytes = 2.0 * (double)(pos_host + 1) * (double)d.kv_dim * (double)elem +
                               8.0 * (double)d.q_dim;
-    // merge + O + residual in one launch (dense FFN layers, whose first FFN GEMV
-    // records the residual tap resid1 from its input)
+    // merge + O + residual in one launch (FFN layers whose first GEMV records
+    // the residual tap resid1 from its input: gate/up, up, the first experts')
     MergeOArgs mo{};
     mo.at = at;
     mo.w = L.wo.view;
     mo.rows = d.dim;
     mo.y = x_;
-    const bool fuse_o = splitk_ && (ls.ffn == LayerSpec::kSwiGLU || ls.ffn == LayerSpec::kGelu) &&
+    const bool fuse_o = splitk_ &&
+                        (ls.ffn == LayerSpec::kSwiGLU || ls.ffn == LayerSpec::kGelu || ls.ffn == LayerSpec::kMoE) &&
                         merge_o_supported(mo);
     if (fuse_o) {
       UAII_TRY(timed("attention", attn_bytes, [&] { return launch_attention_splits(at, s); }));
@@ -1182,6 +1183,7 @@ Error DecoderProgram::encode_step(bool want_logits) {
         g.eps = d.rms_eps;
         g.y = h_;
         g.state = state_;
+        if (fuse_o && t0 == 0) g.rtap = tap_r1_ + li * d.dim;
         double bytes = 0.0;
         for (int t = t0; t < std::min(nsegs, t0 + 3); ++t) {
           GemvSeg& sg = g.seg[g.nseg++];
