@@ -28,7 +28,7 @@
  *                              output + residual add_f32 (quant_gemm.cpp:22-70,
  *                              elementwise.cpp:99-110), the decode layer's attention half
  *   uaii_hip_gemv_add          quant_gemm_f32 + residual add_f32 (elementwise.cpp:86-97)
- *   uaii_hip_gemv_add_atomic   the same, split along K with float-atomic adds (Q4_0)
+ *   uaii_hip_gemv_add_atomic   the same, split along K with float-atomic adds (Q4_0, Q6_K)
  *   uaii_hip_gemv_swiglu       two quant_gemm_f32 + silu_f32 * mul_f32
  *                              (elementwise.cpp:73-110), the graph's FFN gate/up
  *   uaii_hip_gemm_rmsnorm/_add/_swiglu  the same three at M>1 (prefill)
@@ -154,7 +154,7 @@ UAII_HIP_API int uaii_hip_attention_decode(const float* q, const void* kcache,
                                            int n_heads, int n_kv_heads, int head_dim,
                                            int64_t n_keys, float* out, void* stream);
 
-/* y += W . x for Q4_0 W [rows][cols], split along K: each block multiplies a
+/* y += W . x for Q4_0 or Q6_K W [rows][cols], split along K: each block multiplies a
  * 1024-column slice of W by the matching inputs and adds its row sums into y
  * with float atomics, so y's rows take cols / 1024 adds in an order the
  * hardware picks (runs can differ in their last bits). cols a multiple of

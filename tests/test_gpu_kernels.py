@@ -331,22 +331,25 @@ def test_gemv_add_epilogue(hip, t, rows, cols, norm):
     assert maxrel(got, want) < 1e-4
 
 
-@pytest.mark.parametrize("rows,cols", [
-    (4096, 14336),   # the 8B down projection: 14 slices x 64 row blocks of 64 rows
-    (2048, 8192),    # 8 slices, 32-row blocks
-    (4096, 4096),
-    (48, 1024),      # one slice, 16-row blocks
-], ids=lambda v: str(v))
-def test_gemv_add_atomic(hip, rows, cols):
+@pytest.mark.parametrize("t,rows,cols", [
+    (uaii_amd.Q4_0, 4096, 14336),   # the 8B down projection: 14 slices x 64 row blocks of 64 rows
+    (uaii_amd.Q4_0, 2048, 8192),    # 8 slices, 32-row blocks
+    (uaii_amd.Q4_0, 4096, 4096),
+    (uaii_amd.Q4_0, 48, 1024),      # one slice, 16-row blocks
+    (uaii_amd.Q6_K, 2048, 8192),    # the 1B down projection: 4 super-blocks per slice
+    (uaii_amd.Q6_K, 4096, 14336),
+    (uaii_amd.Q6_K, 48, 1024),
+], ids=lambda v: uaii_amd.TYPE_NAMES.get(v, str(v)) if isinstance(v, int) and v in uaii_amd.TYPE_NAMES and v < 64 else str(v))
+def test_gemv_add_atomic(hip, t, rows, cols):
     """y += W . x split along K with float-atomic adds (the residual add of the
     graph, elementwise.cpp:86-97, on quant_gemm_f32, quant_gemm.cpp:22-70):
     within 1e-5 of the oracle, within 1e-6 of the whole-row kernel, and two
     calls from the same y0 within 1e-6 of each other (the adds land in arrival
     order)."""
-    p = random_packed(uaii_amd.Q4_0, rows, cols, seed=rows + cols + 1)
+    p = random_packed(t, rows, cols, seed=rows + cols + 1)
     x = synth.normals(92, 1, 0, cols, 1.0)
     y0 = synth.normals(91, 1, 0, rows, 1.0)
-    w = DeviceWeight(uaii_amd.Q4_0, p, rows, cols)
+    w = DeviceWeight(t, p, rows, cols)
     dx = DeviceBuffer.from_array(x)
     got = []
     for _ in range(2):
@@ -356,15 +359,15 @@ def test_gemv_add_atomic(hip, rows, cols):
     dy = DeviceBuffer.from_array(y0)
     check_hip(hip.uaii_hip_gemv_add(w.h, dx.ptr, None, 1e-5, dy.ptr, None), "gemv_add")
     whole = dy.to_array(np.float32, rows)
-    want = y0 + oracle.quant_gemm(uaii_amd.Q4_0, x, p, rows, nthreads=0)[0]
+    want = y0 + oracle.quant_gemm(t, x, p, rows, nthreads=0)[0]
     assert maxrel(got[0], want) < 1e-5
     assert maxrel(got[0], whole) < 1e-6
     assert maxrel(got[1], got[0]) < 1e-6
 
 
 def test_gemv_add_atomic_refuses_unsupported_shapes(hip):
-    """Types other than Q4_0, columns not a multiple of 1024 and rows not a
-    multiple of 16 return -1 before any launch."""
+    """Types other than Q4_0 and Q6_K, columns not a multiple of 1024 and rows
+    not a multiple of 16 return -1 before any launch."""
     x, y = DeviceBuffer(4 * 4096), DeviceBuffer(4 * 4096)
     for t, rows, cols in [(uaii_amd.Q4_K, 64, 1024), (uaii_amd.Q8_0, 64, 1024), (uaii_amd.Q4_0, 64, 1536),
                           (uaii_amd.Q4_0, 24, 1024)]:

@@ -70,4 +70,29 @@ __device__ __forceinline__ float q4_k_dot(const uint4 (&q)[2], const uint4& meta
   return (d * (float)sc) * acc - (dmin * (float)mn) * sx;
 }
 
+// Elements 32 m .. 32 m + 31 (m = 0..3) of one 128-element half of a Q6_K
+// super-block (gguf_dequant.cpp:381-416): element l takes the low (m < 2) or
+// high (m >= 2) nibble of quant byte 32 (m & 1) + l of the half's 64 (ql) and
+// bits 2m, 2m + 1 of its high-bit byte l (qh), value d * scale * (q - 32), the
+// int8 scale of elements l < 16 in byte 0 of sc2 and of l >= 16 in byte 1.
+__device__ __forceinline__ float q6_k_dot(const uint4 (&ql)[2], const uint4 (&qh)[2], int m, uint32_t sc2,
+                                          uint32_t d16, const float (&xv)[32], float sx0, float sx1) {
+  const int nsh = 4 * (m >> 1), hsh = 2 * m;
+  const uint32_t wl[8] = {ql[0].x, ql[0].y, ql[0].z, ql[0].w, ql[1].x, ql[1].y, ql[1].z, ql[1].w};
+  const uint32_t wh[8] = {qh[0].x, qh[0].y, qh[0].z, qh[0].w, qh[1].x, qh[1].y, qh[1].z, qh[1].w};
+  float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    const uint32_t q = ((wl[t] >> nsh) & 0x0F0F0F0Fu) | (((wh[t] >> hsh) & 0x03030303u) << 4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float v = (float)((q >> (8 * e)) & 0xFFu) * xv[4 * t + e];
+      if (t < 4) a0 += v; else a1 += v;
+    }
+  }
+  const float s0 = (float)(int8_t)(sc2 & 0xFFu), s1 = (float)(int8_t)((sc2 >> 8) & 0xFFu);
+  const float d = __half2float(__ushort_as_half((unsigned short)d16));
+  return d * (s0 * (a0 - 32.0f * sx0) + s1 * (a1 - 32.0f * sx1));
+}
+
 }  // namespace uaii_hip

@@ -2,10 +2,11 @@
 // blocks add their partial row sums into the output with float atomics (gfx950).
 //
 // Replaces quant_gemm_f32 at M = 1 (libs/uaii-kernels/src/quant_gemm.cpp:22-70)
-// plus the residual add_f32 (elementwise.cpp:99-110) for Q4_0 weights: the FFN
-// down projection, y += W_down . h.
+// plus the residual add_f32 (elementwise.cpp:99-110) for Q4_0 and Q6_K weights:
+// the FFN down projection, y += W_down . h.
 //
-// Block (r, c) owns column slice c (SC = 1024 columns, 32 Q4_0 blocks) of
+// Block (r, c) owns column slice c (SC = 1024 columns: 32 Q4_0 blocks, or 4 Q6_K
+// super-blocks of which each lane takes 32 elements) of
 // RB = 8 J consecutive rows r RB ... The row block is the grid's x index, so the
 // slices of one row block land on one XCD and their atomic adds to a row meet
 // in that XCD's L2 (33.6 MB fetched per 8B down launch, 33.1 MB algorithmic,
@@ -34,7 +35,7 @@ constexpr int SC = 32 * LPR;   // columns per slice
 constexpr int RPI = 64 / LPR;  // rows per wave instruction
 constexpr int NW = 4;          // waves per block
 
-template <int J>
+template <int FMT, int J>
 __global__ void __launch_bounds__(NW * 64) k_gemv_splitk(SplitKArgs p) {
   const int c = blockIdx.y, w = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int b = lane % LPR;
@@ -48,24 +49,47 @@ __global__ void __launch_bounds__(NW * 64) k_gemv_splitk(SplitKArgs p) {
     const float4 t = xp[k];
     xv[4 * k] = t.x; xv[4 * k + 1] = t.y; xv[4 * k + 2] = t.z; xv[4 * k + 3] = t.w;
   }
-  uint4 qv[J];
-  uint32_t sv[J];
+  // Q4_0: block b (16 payload bytes, f16 scale). Q6_K: elements 32 m .. 32 m + 31
+  // of half hf of super-block sb (4 per slice): 32 ql and 32 qh bytes, the two
+  // int8 scales and d
+  constexpr int QW = FMT == T_Q6_K ? 2 : 1;
+  const int64_t sb = (int64_t)c * (SC / 256) + (b >> 3);
+  const int hf = (b & 7) >> 2, m = b & 3;
+  uint4 qv[J][QW], hv[J][QW];
+  uint32_t sv[J], dv[J];
 #pragma unroll
   for (int j = 0; j < J; ++j) {
     const int64_t r = r0 + RPI * j;
-    qv[j] = *reinterpret_cast<const uint4*>(p.w.a + r * p.w.a_row + c * (SC / 2) + b * 16);
-    sv[j] = *reinterpret_cast<const uint16_t*>(p.w.b + r * p.w.b_row + c * (SC / 16) + b * 2);
+    if constexpr (FMT == T_Q6_K) {
+      const uint4* ql = reinterpret_cast<const uint4*>(p.w.a + r * p.w.a_row + sb * 128 + hf * 64 + 32 * (m & 1));
+      const uint4* qh = reinterpret_cast<const uint4*>(p.w.b + r * p.w.b_row + sb * 64 + hf * 32);
+#pragma unroll
+      for (int k = 0; k < QW; ++k) {
+        qv[j][k] = ql[k];
+        hv[j][k] = qh[k];
+      }
+      sv[j] = *reinterpret_cast<const uint16_t*>(p.w.c + r * p.w.c_row + sb * 16 + hf * 8 + 2 * m);
+      dv[j] = *reinterpret_cast<const uint16_t*>(p.w.d + r * p.w.d_row + sb * 2);
+    } else {
+      qv[j][0] = *reinterpret_cast<const uint4*>(p.w.a + r * p.w.a_row + c * (SC / 2) + b * 16);
+      sv[j] = *reinterpret_cast<const uint16_t*>(p.w.b + r * p.w.b_row + c * (SC / 16) + b * 2);
+    }
   }
   // every load is issued before the first product waits for the inputs
   __builtin_amdgcn_sched_barrier(0);
 
-  float sx = 0.0f;
+  float sx0 = 0.0f, sx1 = 0.0f;
 #pragma unroll
-  for (int k = 0; k < 32; ++k) sx += xv[k];
+  for (int k = 0; k < 16; ++k) {
+    sx0 += xv[k];
+    sx1 += xv[16 + k];
+  }
   float rs[J];
 #pragma unroll
   for (int j = 0; j < J; ++j) {
-    float v = q4_0_dot(qv[j], sv[j], xv, sx);
+    float v;
+    if constexpr (FMT == T_Q6_K) v = q6_k_dot(qv[j], hv[j], m, sv[j], dv[j], xv, sx0, sx1);
+    else v = q4_0_dot(qv[j][0], sv[j], xv, sx0 + sx1);
     v += dpp_mov<0xB1>(v);   // quad_perm [1,0,3,2]
     v += dpp_mov<0x4E>(v);   // quad_perm [2,3,0,1]
     v += dpp_mov<0x141>(v);  // row_half_mirror
@@ -81,13 +105,14 @@ __global__ void __launch_bounds__(NW * 64) k_gemv_splitk(SplitKArgs p) {
 
 // Rows per lane: the most (fewest blocks, fewest redundant input loads) that
 // still gives 512 blocks; 8 on the 8B down projection (896 blocks; 4 and 16
-// measured slower).
+// measured slower). Q6_K carries four payload words per row: at most 4.
 int pick_j(const SplitKArgs& p) {
   const int64_t slices = p.w.cols / SC;
+  const int most = p.w.type == T_Q6_K ? 4 : 8;
   for (int j : {8, 4, 2})
-    if (p.rows % (NW * RPI * j) == 0 && slices * (p.rows / (NW * RPI * j)) >= 512) return j;
+    if (j <= most && p.rows % (NW * RPI * j) == 0 && slices * (p.rows / (NW * RPI * j)) >= 512) return j;
   for (int j : {8, 4, 2})
-    if (p.rows % (NW * RPI * j) == 0) return j;
+    if (j <= most && p.rows % (NW * RPI * j) == 0) return j;
   return 0;
 }
 
@@ -95,8 +120,11 @@ int pick_j(const SplitKArgs& p) {
 
 bool gemv_splitk_supported(const SplitKArgs& p) {
   const DevWeight& w = p.w;
-  if (w.type != T_Q4_0 || w.cols <= 0 || w.cols % SC) return false;
-  if (w.a_row != w.cols / 2 || w.b_row != w.cols / 16) return false;
+  if (w.cols <= 0 || w.cols % SC) return false;
+  const bool q4 = w.type == T_Q4_0 && w.a_row == w.cols / 2 && w.b_row == w.cols / 16;
+  const bool q6 = w.type == T_Q6_K && w.a_row == w.cols / 2 && w.b_row == w.cols / 4 &&
+                  w.c_row == w.cols / 16 && w.d_row == w.cols / 128;
+  if (!q4 && !q6) return false;
   if (p.rows <= 0 || w.rows < p.rows) return false;
   return pick_j(p) > 0;
 }
@@ -105,10 +133,13 @@ hipError_t launch_gemv_splitk(const SplitKArgs& p, hipStream_t s) {
   if (!gemv_splitk_supported(p) || !p.x || !p.y) return hipErrorInvalidValue;
   const int J = pick_j(p);
   dim3 grid((unsigned)(p.rows / (NW * RPI * J)), (unsigned)(p.w.cols / SC));
-  switch (J) {
-    case 8: UAII_LAUNCH(k_gemv_splitk<8>, grid, dim3(NW * 64), 0, s, p); break;
-    case 4: UAII_LAUNCH(k_gemv_splitk<4>, grid, dim3(NW * 64), 0, s, p); break;
-    default: UAII_LAUNCH(k_gemv_splitk<2>, grid, dim3(NW * 64), 0, s, p); break;
+  if (p.w.type == T_Q6_K) {
+    if (J == 4) UAII_LAUNCH((k_gemv_splitk<T_Q6_K, 4>), grid, dim3(NW * 64), 0, s, p);
+    else UAII_LAUNCH((k_gemv_splitk<T_Q6_K, 2>), grid, dim3(NW * 64), 0, s, p);
+  } else {
+    if (J == 8) UAII_LAUNCH((k_gemv_splitk<T_Q4_0, 8>), grid, dim3(NW * 64), 0, s, p);
+    else if (J == 4) UAII_LAUNCH((k_gemv_splitk<T_Q4_0, 4>), grid, dim3(NW * 64), 0, s, p);
+    else UAII_LAUNCH((k_gemv_splitk<T_Q4_0, 2>), grid, dim3(NW * 64), 0, s, p);
   }
   return hipGetLastError();
 }
