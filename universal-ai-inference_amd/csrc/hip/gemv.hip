@@ -1581,9 +1581,14 @@ Plan make_plan(const GemvArgs& a) {
   // resident block (5 per CU) its loads queue in the per-CU memory path (the
   // address unit waits on the cache 5x as long as a plain read's); 3 blocks per
   // CU measured 61.4 us against 65.0 with the argmax epilogue (1: 95.6, 2: 67.7,
-  // 4: 64.1), 55.0 against 56.5 storing the logits for the device sampler.
+  // 4: 64.1), 55.0 against 56.5 storing the logits for the device sampler;
+  // 101.9 against 107.3 for the 558 MB Q8_0 head. Smaller heads keep every
+  // resident block: 70.7 against 76.7 us for a 148 MB Q4_K head (2048 columns),
+  // 28.7 against 29.4 for a 74 MB one.
+  const DevWeight& w0 = a.seg[0].w;
+  const int64_t head_bytes = w0.rows * (w0.a_row + w0.b_row + w0.c_row + w0.d_row);
   const bool lm_head = a.epi == EPI_LOGITS || (a.epi == EPI_STORE && a.nseg == 1 && a.seg[0].rows >= 65536);
-  const int cap_cu = lm_head ? std::min(per_cu, 3) : per_cu;
+  const int cap_cu = lm_head && head_bytes >= (256ll << 20) ? std::min(per_cu, 3) : per_cu;
   const int64_t cap = (int64_t)cu_count() * cap_cu;
   for (int k = 0; k < a.nseg; ++k) {
     const int64_t g = (a.seg[k].rows + rpg - 1) / rpg;
