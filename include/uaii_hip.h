@@ -148,7 +148,10 @@ UAII_HIP_API int uaii_hip_rope_table(float theta, int head_dim, int64_t max_pos,
 UAII_HIP_API int uaii_hip_rope(float* x, int64_t rows, int64_t dim, int head_dim, int mode,
                                const int32_t* pos_dev, const float* table_dev, void* stream);
 /* kcache/vcache: head-major [n_kv_heads][max_seq][head_dim], f16 (kv_f16=1) or f32;
- * attends over keys 0..n_keys-1. */
+ * attends over keys 0..n_keys-1. The split partials go to one device buffer the
+ * library owns (grown on demand, kept until the process ends; growing it waits
+ * for the device), shared with uaii_hip_attention_o: calls that run at the same
+ * time on different streams race on it, so issue them on one stream. */
 UAII_HIP_API int uaii_hip_attention_decode(const float* q, const void* kcache,
                                            const void* vcache, int kv_f16, int64_t max_seq,
                                            int n_heads, int n_kv_heads, int head_dim,
@@ -171,7 +174,8 @@ UAII_HIP_API int uaii_hip_gemv_add_atomic(const uaii_hip_weight* w, const float*
  * order the hardware picks, so runs can differ in its last bits. W_o: Q4_0,
  * Q8_0 or Q4_K, [rows][n_heads * head_dim] with n_heads * head_dim a multiple of 256,
  * head_dim 64 or 128, rows (y's length) a multiple of 32; other shapes return
- * -1 and launch nothing. */
+ * -1 and launch nothing. Its split partials share uaii_hip_attention_decode's
+ * library-owned buffer (the same one-stream rule applies). */
 UAII_HIP_API int uaii_hip_attention_o(const float* q, const void* kcache, const void* vcache,
                                       int kv_f16, int64_t max_seq, int n_heads,
                                       int n_kv_heads, int head_dim, int64_t n_keys,
