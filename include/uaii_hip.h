@@ -162,7 +162,8 @@ UAII_HIP_API int uaii_hip_attention_decode(const float* q, const void* kcache,
  * with float atomics, so y's rows take cols / 1024 adds in an order the
  * hardware picks (runs can differ in their last bits). cols a multiple of
  * 1024, rows a multiple of 16; other shapes or types return -1 and launch
- * nothing. */
+ * nothing. x and y must not overlap: blocks still reading x run beside blocks
+ * already adding into y. */
 UAII_HIP_API int uaii_hip_gemv_add_atomic(const uaii_hip_weight* w, const float* x, float* y,
                                           void* stream);
 
