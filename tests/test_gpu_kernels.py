@@ -366,13 +366,17 @@ def test_gemv_add_atomic(hip, t, rows, cols):
 
 
 def test_gemv_add_atomic_refuses_unsupported_shapes(hip):
-    """Types other than Q4_0 and Q6_K, columns not a multiple of 1024 and rows
-    not a multiple of 16 return -1 before any launch."""
+    """Types other than Q4_0 and Q6_K, columns not a multiple of 1024, rows not
+    a multiple of 16 and overlapping x and y return -1 before any launch."""
     x, y = DeviceBuffer(4 * 4096), DeviceBuffer(4 * 4096)
     for t, rows, cols in [(uaii_amd.Q4_K, 64, 1024), (uaii_amd.Q8_0, 64, 1024), (uaii_amd.Q4_0, 64, 1536),
                           (uaii_amd.Q4_0, 24, 1024)]:
         w = DeviceWeight(t, random_packed(t, rows, cols, seed=7), rows, cols)
         assert hip.uaii_hip_gemv_add_atomic(w.h, x.ptr, y.ptr, None) == -1, (t, rows, cols)
+    # a supported shape whose x and y overlap (x is read while y takes adds)
+    w = DeviceWeight(uaii_amd.Q4_0, random_packed(uaii_amd.Q4_0, 64, 1024, seed=7), 64, 1024)
+    assert hip.uaii_hip_gemv_add_atomic(w.h, x.ptr, x.ptr, None) == -1
+    assert hip.uaii_hip_gemv_add_atomic(w.h, x.ptr, C.c_void_p(x.ptr.value + 4 * 1000), None) == -1
     check_hip(hip.uaii_hip_synchronize())
 
 

@@ -411,6 +411,12 @@ int uaii_hip_attention_decode(const float* q, const void* kcache, const void* vc
 
 int uaii_hip_gemv_add_atomic(const uaii_hip_weight* w, const float* x, float* y, void* stream) {
   if (!w || !x || !y) return kErrArg;
+  {
+    // x is read while other blocks already add into y: the ranges must not overlap
+    const uintptr_t x0 = (uintptr_t)x, x1 = x0 + (uintptr_t)w->w.view.cols * sizeof(float);
+    const uintptr_t y0 = (uintptr_t)y, y1 = y0 + (uintptr_t)w->w.view.rows * sizeof(float);
+    if (x0 < y1 && y0 < x1) return kErrArg;
+  }
   SplitKArgs p{};
   p.w = w->w.view;
   p.rows = w->w.view.rows;
