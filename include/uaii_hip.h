@@ -175,7 +175,8 @@ UAII_HIP_API int uaii_hip_gemv_add_atomic(const uaii_hip_weight* w, const float*
  * order the hardware picks, so runs can differ in its last bits. W_o: Q4_0,
  * Q8_0 or Q4_K, [rows][n_heads * head_dim] with n_heads * head_dim a multiple of 256,
  * head_dim 64 or 128, rows (y's length) a multiple of 32; other shapes return
- * -1 and launch nothing. Its split partials share uaii_hip_attention_decode's
+ * -1 and launch nothing, as do `out` and y overlapping (merge blocks write
+ * `out` while others add into y). Its split partials share uaii_hip_attention_decode's
  * library-owned buffer (the same one-stream rule applies). */
 UAII_HIP_API int uaii_hip_attention_o(const float* q, const void* kcache, const void* vcache,
                                       int kv_f16, int64_t max_seq, int n_heads,

@@ -25,6 +25,7 @@
 Reference loop for every model: session.cpp:1006-1044 (prompt, then greedy
 argmax over probs, lowest index on ties).
 """
+import ctypes as C
 import dataclasses
 import os
 
@@ -169,8 +170,8 @@ def test_attention_o_q4_k(hip, case):
 
 def test_attention_o_refuses_unsupported_shapes(hip):
     """W_o other than Q4_0, Q8_0 or Q4_K, rows not a multiple of 32, head_dim
-    other than 64 or 128, or n_heads * head_dim not a multiple of 256: -1 before
-    any launch."""
+    other than 64 or 128, n_heads * head_dim not a multiple of 256, or `out`
+    overlapping y: -1 before any launch."""
     nh, nkv, hd, max_seq = 32, 8, 128, 256
     buf = DeviceBuffer(nkv * max_seq * hd * 4)
     out, y = DeviceBuffer(nh * hd * 4), DeviceBuffer(8192 * 4)
@@ -189,6 +190,13 @@ def test_attention_o_refuses_unsupported_shapes(hip):
     w256 = uaii_amd.DeviceWeight(uaii_amd.Q4_0, synth.quantize(uaii_amd.Q4_0, x[: 32 * 4 * 256]), 32, 4 * 256)
     assert hip.uaii_hip_attention_o(buf.ptr, buf.ptr, buf.ptr, 1, max_seq, 4, 2, 256, 10, w256.h, out.ptr,
                                     y.ptr, None) == -1  # head_dim 256
+    # a supported shape whose `out` and y overlap (merge blocks write `out` while
+    # others add into y)
+    wok = uaii_amd.DeviceWeight(uaii_amd.Q4_0, synth.quantize(uaii_amd.Q4_0, x[: 64 * nh * hd]), 64, nh * hd)
+    assert hip.uaii_hip_attention_o(buf.ptr, buf.ptr, buf.ptr, 1, max_seq, nh, nkv, hd, 10, wok.h, y.ptr,
+                                    y.ptr, None) == -1
+    assert hip.uaii_hip_attention_o(buf.ptr, buf.ptr, buf.ptr, 1, max_seq, nh, nkv, hd, 10, wok.h, y.ptr,
+                                    C.c_void_p(y.ptr.value + 4 * 100), None) == -1
     check_hip(hip.uaii_hip_synchronize())
 
 

@@ -455,6 +455,12 @@ int uaii_hip_attention_o(const float* q, const void* kcache, const void* vcache,
   m.rows = wo->w.view.rows;
   m.y = y;
   if (!uaii_hip::merge_o_supported(m)) return kErrArg;
+  {
+    // blocks write `out` while others already add into y: the ranges must not overlap
+    const uintptr_t o0 = (uintptr_t)out, o1 = o0 + (uintptr_t)n_heads * head_dim * sizeof(float);
+    const uintptr_t y0 = (uintptr_t)y, y1 = y0 + (uintptr_t)m.rows * sizeof(float);
+    if (o0 < y1 && y0 < o1) return kErrArg;
+  }
   const size_t part = (size_t)n_kv_heads * splits * G * (size_t)(head_dim + 2) * 4;
   int rc = grow_scratch(part);
   if (rc) return rc;
